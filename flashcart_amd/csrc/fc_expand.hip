@@ -1,0 +1,395 @@
+// Eq. (1) expansion, radial bases, cutoff envelope and the fused edge-geometry pass.
+//
+// Edge-parallel, one thread per edge: each edge reads 12-36 B and writes
+// (L+1)^2 + n_radial + 1 floats, so these kernels are HBM/launch bound; the fusion
+// removes the separate gather / norm / normalise / expand / basis / cutoff passes
+// (and their intermediates) of the reference forward (src/flashcart/model/
+// flashcart.py:268-284) and the matching autograd chain in the backward.
+#include "fc_common.h"
+#include "generated/fc_expand_poly.h"
+
+namespace fc {
+
+constexpr float kMinEdgeLength = 1.0e-4f;  // MIN_EDGE_LENGTH, src/flashcart/model/flashcart.py:22
+constexpr int kMaxRadial = 32;
+
+template <int L>
+__device__ __forceinline__ void expand_all(float x, float y, float z, float* out) {
+  static_for<L + 1>([&](auto ic) {
+    constexpr int l = decltype(ic)::value;
+    Expand<l>::fwd(x, y, z, out + l * l);
+  });
+}
+
+template <int L>
+__device__ __forceinline__ void expand_all_bwd(float x, float y, float z, const float* g, float* gv) {
+  static_for<L + 1>([&](auto ic) {
+    constexpr int l = decltype(ic)::value;
+    if constexpr (l > 0) Expand<l>::bwd(x, y, z, g + l * l, gv);
+  });
+}
+
+// ---------------------------------------------------------------------------
+// Radial basis + envelope (value and derivative with respect to d), following
+// src/flashcart/nn/radial.py. The derivative conventions are those of PyTorch
+// autograd on the reference expressions (clamp passes the gradient on the closed
+// interval, torch.sinc' = 0 at 0).
+// ---------------------------------------------------------------------------
+struct RadialParams {
+  int basis, n_radial, poly_order;
+  float r_min, r_max;
+};
+
+__device__ __forceinline__ void radial_eval(const RadialParams& p, float d, float* feats, float* dfeats) {
+  const int n = p.n_radial;
+  if (p.basis == FC_BASIS_BESSEL) {
+    // sqrt(2/r_max) * w_n * sinc(w_n d / pi), w_n = n pi / r_max
+    const float pre = sqrtf(2.0f / p.r_max);
+    for (int k = 0; k < n; ++k) {
+      const float w = (float)M_PI / p.r_max * (float)(k + 1);
+      const float u = d * w / (float)M_PI;  // argument of torch.sinc
+      const float pu = (float)M_PI * u;
+      float s, ds;
+      if (fabsf(pu) < 0.05f) {
+        // Taylor series of sin(t)/t and of pi * d/dt[sin(t)/t] (the direct forms cancel for small t)
+        const float t2 = pu * pu;
+        s = 1.0f - t2 * (1.0f / 6.0f) * (1.0f - t2 * (1.0f / 20.0f));
+        ds = (float)M_PI * pu * (-1.0f / 3.0f + t2 * (1.0f / 30.0f) * (1.0f - t2 * (1.0f / 28.0f)));
+      } else {
+        const float sn = sinf(pu), cs = cosf(pu);
+        s = sn / pu;
+        ds = (pu * cs - sn) / (pu * u);
+      }
+      feats[k] = pre * w * s;
+      if (dfeats) dfeats[k] = pre * w * ds * (w / (float)M_PI);
+    }
+    return;
+  }
+  // Chebyshev T_k of x(t), t = (d - r_min) / (r_max - r_min)
+  const float span = p.r_max - p.r_min;
+  const float t = (d - p.r_min) / span;
+  float x, dx;
+  if (p.basis == FC_BASIS_CHEBYSHEV_COSINE) {
+    x = cosf(t * (float)M_PI);
+    dx = -sinf(t * (float)M_PI) * (float)M_PI / span;
+  } else {
+    x = 2.0f * t - 1.0f;
+    dx = 2.0f / span;
+  }
+  float tm2 = 1.0f, tm1 = x, dm2 = 0.0f, dm1 = 1.0f;  // T_{k-2}, T_{k-1} and d/dx
+  feats[0] = 1.0f;
+  if (dfeats) dfeats[0] = 0.0f;
+  if (n > 1) {
+    feats[1] = x;
+    if (dfeats) dfeats[1] = dx;
+  }
+  for (int k = 2; k < n; ++k) {
+    const float tk = 2.0f * x * tm1 - tm2;
+    const float dk = 2.0f * tm1 + 2.0f * x * dm1 - dm2;
+    feats[k] = tk;
+    if (dfeats) dfeats[k] = dk * dx;
+    tm2 = tm1; tm1 = tk; dm2 = dm1; dm1 = dk;
+  }
+}
+
+__device__ __forceinline__ float envelope_eval(const RadialParams& p, float d, float* denv) {
+  // clamp(d, 0); t = d / r_max; f(t) = 1 - c1 t^p + c2 t^(p+1) - c3 t^(p+2); * [d < r_max]; clamp [0, 1].
+  // f has a triple root at t = 1 and is evaluated in the exactly equal factored form
+  //   f(t) = (1-t)^3 g(t),  g(t) = sum_{k<p} C(k+2,2) t^k,
+  // which avoids the cancellation of the expanded form near the cutoff (terms ~50 summing to ~1e-4).
+  const int po = p.poly_order;
+  const float dc = fmaxf(d, 0.0f);
+  const float t = dc / p.r_max;
+  float g = 0.0f, dg = 0.0f;  // Horner for g and g'
+  for (int k = po - 1; k >= 0; --k) {
+    dg = fmaf(dg, t, g);
+    g = fmaf(g, t, 0.5f * (float)((k + 1) * (k + 2)));
+  }
+  const float s = 1.0f - t;
+  const float env = s * s * s * g;
+  const float mask = dc < p.r_max ? 1.0f : 0.0f;
+  const float v = env * mask;
+  const float out = fminf(fmaxf(v, 0.0f), 1.0f);
+  if (denv) {
+    const float de = s * s * (s * dg - 3.0f * g) / p.r_max;
+    const bool pass = (v >= 0.0f && v <= 1.0f) && (d >= 0.0f);
+    *denv = pass ? mask * de : 0.0f;
+  }
+  return out;
+}
+
+__host__ __device__ inline RadialParams radial_params(const fc_radial_desc& d) {
+  return RadialParams{d.basis, d.n_radial, d.poly_order, d.r_min, d.r_max};
+}
+
+// ---------------------------------------------------------------------------
+// Irreps (Eq. 1 on given unit vectors)
+// ---------------------------------------------------------------------------
+template <int L>
+__global__ void irreps_fwd_kernel(int64_t n, const float* __restrict__ x, float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float o[ncomp(L)];
+  expand_all<L>(x[3 * i], x[3 * i + 1], x[3 * i + 2], o);
+#pragma unroll
+  for (int k = 0; k < ncomp(L); ++k) out[i * ncomp(L) + k] = o[k];
+}
+
+template <int L>
+__global__ void irreps_bwd_kernel(int64_t n, const float* __restrict__ g, const float* __restrict__ x,
+                                  float* __restrict__ gx) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float gi[ncomp(L)];
+#pragma unroll
+  for (int k = 0; k < ncomp(L); ++k) gi[k] = g[i * ncomp(L) + k];
+  float v[3] = {0.f, 0.f, 0.f};
+  expand_all_bwd<L>(x[3 * i], x[3 * i + 1], x[3 * i + 2], gi, v);
+  gx[3 * i] = v[0];
+  gx[3 * i + 1] = v[1];
+  gx[3 * i + 2] = v[2];
+}
+
+__global__ void radial_fwd_kernel(RadialParams p, int64_t n, const float* __restrict__ d,
+                                  float* __restrict__ feats, float* __restrict__ env) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float di = d[i];
+  if (feats && p.basis != FC_BASIS_NONE) {
+    float f[kMaxRadial];
+    radial_eval(p, di, f, nullptr);
+    for (int k = 0; k < p.n_radial; ++k) feats[i * p.n_radial + k] = f[k];
+  }
+  if (env) env[i] = envelope_eval(p, di, nullptr);
+}
+
+__global__ void radial_bwd_kernel(RadialParams p, int64_t n, const float* __restrict__ d,
+                                  const float* __restrict__ gf, const float* __restrict__ ge,
+                                  float* __restrict__ gd) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float di = d[i];
+  float acc = 0.f;
+  if (gf && p.basis != FC_BASIS_NONE) {
+    float f[kMaxRadial], df[kMaxRadial];
+    radial_eval(p, di, f, df);
+    for (int k = 0; k < p.n_radial; ++k) acc = fmaf(gf[i * p.n_radial + k], df[k], acc);
+  }
+  if (ge) {
+    float de;
+    envelope_eval(p, di, &de);
+    acc = fmaf(ge[i], de, acc);
+  }
+  gd[i] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// Fused edge geometry
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void edge_vector(int64_t e, const float* pos, const float* shift, const int32_t* ii,
+                                            const int32_t* jj, const float* vectors, float* v) {
+  if (pos) {
+    const int64_t i = ii[e], j = jj[e];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) v[k] = pos[3 * j + k] - pos[3 * i + k] + (shift ? shift[3 * e + k] : 0.f);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 3; ++k) v[k] = vectors[3 * e + k];
+  }
+}
+
+template <int L>
+__global__ void edge_fwd_kernel(RadialParams p, int64_t n, const float* __restrict__ pos,
+                                const float* __restrict__ shift, const int32_t* __restrict__ ii,
+                                const int32_t* __restrict__ jj, const float* __restrict__ vectors,
+                                float* __restrict__ attrs, float* __restrict__ feats, float* __restrict__ env) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n) return;
+  float v[3];
+  edge_vector(e, pos, shift, ii, jj, vectors, v);
+  const float d = sqrtf(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
+  const float inv = 1.0f / fmaxf(d, kMinEdgeLength);
+  if (attrs) {
+    float o[ncomp(L)];
+    expand_all<L>(v[0] * inv, v[1] * inv, v[2] * inv, o);
+#pragma unroll
+    for (int k = 0; k < ncomp(L); ++k) attrs[e * ncomp(L) + k] = o[k];
+  }
+  if (feats && p.basis != FC_BASIS_NONE) {
+    float f[kMaxRadial];
+    radial_eval(p, d, f, nullptr);
+    for (int k = 0; k < p.n_radial; ++k) feats[e * p.n_radial + k] = f[k];
+  }
+  if (env) env[e] = p.poly_order > 0 ? envelope_eval(p, d, nullptr) : 1.0f;
+}
+
+template <int L>
+__global__ void edge_bwd_kernel(RadialParams p, int64_t n, const float* __restrict__ pos,
+                                const float* __restrict__ shift, const int32_t* __restrict__ ii,
+                                const int32_t* __restrict__ jj, const float* __restrict__ vectors,
+                                const float* __restrict__ ga, const float* __restrict__ gf,
+                                const float* __restrict__ ge, float* __restrict__ gvec) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n) return;
+  float v[3];
+  edge_vector(e, pos, shift, ii, jj, vectors, v);
+  const float d = sqrtf(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
+  const float dcl = fmaxf(d, kMinEdgeLength);
+  const float inv = 1.0f / dcl;
+  const float r[3] = {v[0] * inv, v[1] * inv, v[2] * inv};
+  float gr[3] = {0.f, 0.f, 0.f};
+  if (ga) {
+    float g[ncomp(L)];
+#pragma unroll
+    for (int k = 0; k < ncomp(L); ++k) g[k] = ga[e * ncomp(L) + k];
+    expand_all_bwd<L>(r[0], r[1], r[2], g, gr);
+  }
+  // direction = v / clamp_min(d, eps): dL/dv += gr / dcl, dL/dd -= (gr . v) / dcl^2 when d >= eps
+  float gd = 0.f;
+  if (gf && p.basis != FC_BASIS_NONE) {
+    float f[kMaxRadial], df[kMaxRadial];
+    radial_eval(p, d, f, df);
+    for (int k = 0; k < p.n_radial; ++k) gd = fmaf(gf[e * p.n_radial + k], df[k], gd);
+  }
+  if (ge && p.poly_order > 0) {
+    float de;
+    envelope_eval(p, d, &de);
+    gd = fmaf(ge[e], de, gd);
+  }
+  if (d >= kMinEdgeLength) gd -= (gr[0] * v[0] + gr[1] * v[1] + gr[2] * v[2]) * inv * inv;
+  const float nd = d > 0.f ? gd / d : 0.f;  // d|v|/dv = v / |v|
+#pragma unroll
+  for (int k = 0; k < 3; ++k) gvec[3 * e + k] = gr[k] * inv + nd * v[k];
+}
+
+template <template <int> class K, class... Args>
+int launch_by_l(int l, int64_t n, hipStream_t s, Args... args) {
+  if (n == 0) return FC_OK;
+  const int bs = 256;
+  dim3 grid((unsigned)((n + bs - 1) / bs)), block(bs);
+  switch (l) {
+    case 0: hipLaunchKernelGGL(K<0>::fn, grid, block, 0, s, n, args...); break;
+    case 1: hipLaunchKernelGGL(K<1>::fn, grid, block, 0, s, n, args...); break;
+    case 2: hipLaunchKernelGGL(K<2>::fn, grid, block, 0, s, n, args...); break;
+    case 3: hipLaunchKernelGGL(K<3>::fn, grid, block, 0, s, n, args...); break;
+    default: return FC_ERR_UNSUPPORTED_L;
+  }
+  FC_LAUNCH_CHECK();
+  return FC_OK;
+}
+
+template <int L> struct IrrepsFwd { static constexpr auto fn = irreps_fwd_kernel<L>; };
+template <int L> struct IrrepsBwd { static constexpr auto fn = irreps_bwd_kernel<L>; };
+
+static int check_radial(const fc_radial_desc* d) {
+  if (!d) return FC_ERR_NULL;
+  if (d->basis < 0 || d->basis > FC_BASIS_NONE) return FC_ERR_BAD_DESC;
+  if (d->basis != FC_BASIS_NONE && (d->n_radial < 1 || d->n_radial > kMaxRadial)) return FC_ERR_BAD_DESC;
+  if (d->poly_order != 0 && d->poly_order < 2) return FC_ERR_BAD_DESC;
+  if (!(d->r_max > d->r_min) || !(d->r_max > 0.f)) return FC_ERR_BAD_DESC;
+  return FC_OK;
+}
+
+template <int L>
+int launch_edge_fwd(const RadialParams& p, int64_t n, const float* pos, const float* shift, const int32_t* ii,
+                    const int32_t* jj, const float* vec, float* attrs, float* feats, float* env, hipStream_t s) {
+  const int bs = 256;
+  hipLaunchKernelGGL(edge_fwd_kernel<L>, dim3((unsigned)((n + bs - 1) / bs)), dim3(bs), 0, s, p, n, pos, shift,
+                     ii, jj, vec, attrs, feats, env);
+  FC_LAUNCH_CHECK();
+  return FC_OK;
+}
+
+template <int L>
+int launch_edge_bwd(const RadialParams& p, int64_t n, const float* pos, const float* shift, const int32_t* ii,
+                    const int32_t* jj, const float* vec, const float* ga, const float* gf, const float* ge,
+                    float* gvec, hipStream_t s) {
+  const int bs = 256;
+  hipLaunchKernelGGL(edge_bwd_kernel<L>, dim3((unsigned)((n + bs - 1) / bs)), dim3(bs), 0, s, p, n, pos, shift,
+                     ii, jj, vec, ga, gf, ge, gvec);
+  FC_LAUNCH_CHECK();
+  return FC_OK;
+}
+
+}  // namespace fc
+
+using namespace fc;
+
+extern "C" int fc_irreps_fwd(int64_t n, int32_t l_max, const float* x, float* out, void* stream) {
+  if (n < 0) return FC_ERR_SHAPE;
+  if (n > 0 && (!x || !out)) return FC_ERR_NULL;
+  return launch_by_l<IrrepsFwd>(l_max, n, (hipStream_t)stream, x, out);
+}
+
+extern "C" int fc_irreps_bwd(int64_t n, int32_t l_max, const float* g, const float* x, float* gx, void* stream) {
+  if (n < 0) return FC_ERR_SHAPE;
+  if (n > 0 && (!g || !x || !gx)) return FC_ERR_NULL;
+  return launch_by_l<IrrepsBwd>(l_max, n, (hipStream_t)stream, g, x, gx);
+}
+
+extern "C" int fc_radial_fwd(const fc_radial_desc* desc, int64_t n, const float* d, float* feats, float* env,
+                             void* stream) {
+  int st = check_radial(desc);
+  if (st != FC_OK) return st;
+  if (n == 0) return FC_OK;
+  if (!d) return FC_ERR_NULL;
+  if (env && desc->poly_order == 0) return FC_ERR_BAD_DESC;
+  const int bs = 256;
+  hipLaunchKernelGGL(radial_fwd_kernel, dim3((unsigned)((n + bs - 1) / bs)), dim3(bs), 0, (hipStream_t)stream,
+                     radial_params(*desc), n, d, feats, env);
+  FC_LAUNCH_CHECK();
+  return FC_OK;
+}
+
+extern "C" int fc_radial_bwd(const fc_radial_desc* desc, int64_t n, const float* d, const float* g_feats,
+                             const float* g_env, float* grad_d, void* stream) {
+  int st = check_radial(desc);
+  if (st != FC_OK) return st;
+  if (n == 0) return FC_OK;
+  if (!d || !grad_d) return FC_ERR_NULL;
+  if (g_env && desc->poly_order == 0) return FC_ERR_BAD_DESC;
+  const int bs = 256;
+  hipLaunchKernelGGL(radial_bwd_kernel, dim3((unsigned)((n + bs - 1) / bs)), dim3(bs), 0, (hipStream_t)stream,
+                     radial_params(*desc), n, d, g_feats, g_env, grad_d);
+  FC_LAUNCH_CHECK();
+  return FC_OK;
+}
+
+extern "C" int fc_edge_geometry_fwd(const fc_edge_desc* desc, int64_t n, const float* pos, const float* shift,
+                                    const int32_t* ii, const int32_t* jj, const float* vectors, float* attrs,
+                                    float* feats, float* env, void* stream) {
+  if (!desc) return FC_ERR_NULL;
+  int st = check_radial(&desc->radial);
+  if (st != FC_OK) return st;
+  if (n == 0) return FC_OK;
+  if (pos ? (!ii || !jj) : !vectors) return FC_ERR_NULL;
+  const RadialParams p = radial_params(desc->radial);
+  hipStream_t s = (hipStream_t)stream;
+  switch (desc->l_max) {
+    case 0: return launch_edge_fwd<0>(p, n, pos, shift, ii, jj, vectors, attrs, feats, env, s);
+    case 1: return launch_edge_fwd<1>(p, n, pos, shift, ii, jj, vectors, attrs, feats, env, s);
+    case 2: return launch_edge_fwd<2>(p, n, pos, shift, ii, jj, vectors, attrs, feats, env, s);
+    case 3: return launch_edge_fwd<3>(p, n, pos, shift, ii, jj, vectors, attrs, feats, env, s);
+  }
+  return FC_ERR_UNSUPPORTED_L;
+}
+
+extern "C" int fc_edge_geometry_bwd(const fc_edge_desc* desc, int64_t n, const float* pos, const float* shift,
+                                    const int32_t* ii, const int32_t* jj, const float* vectors,
+                                    const float* ga, const float* gf, const float* ge, float* gvec,
+                                    void* stream) {
+  if (!desc) return FC_ERR_NULL;
+  int st = check_radial(&desc->radial);
+  if (st != FC_OK) return st;
+  if (n == 0) return FC_OK;
+  if (!gvec || (pos ? (!ii || !jj) : !vectors)) return FC_ERR_NULL;
+  const RadialParams p = radial_params(desc->radial);
+  hipStream_t s = (hipStream_t)stream;
+  switch (desc->l_max) {
+    case 0: return launch_edge_bwd<0>(p, n, pos, shift, ii, jj, vectors, ga, gf, ge, gvec, s);
+    case 1: return launch_edge_bwd<1>(p, n, pos, shift, ii, jj, vectors, ga, gf, ge, gvec, s);
+    case 2: return launch_edge_bwd<2>(p, n, pos, shift, ii, jj, vectors, ga, gf, ge, gvec, s);
+    case 3: return launch_edge_bwd<3>(p, n, pos, shift, ii, jj, vectors, ga, gf, ge, gvec, s);
+  }
+  return FC_ERR_UNSUPPORTED_L;
+}

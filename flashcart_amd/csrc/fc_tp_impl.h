@@ -1,0 +1,273 @@
+// Irreducible Cartesian tensor product kernels (forward and vector-Jacobian product).
+//
+// One template covers the two modes of TensorProduct.forward:
+//   CONV = true  : out[i] = sum_{e in in(i)} sum_p w[e,p,:] (x) contract_p(in1[idx_j[e]], in2[e])
+//                  over a receiver-sorted CSR (rowptr), as in the reference's
+//                  tp_fwd_csr_kernel (src/flashcart/o3/_codegen_tensor_product.py:3245-3311);
+//   CONV = false : independent rows (reference tp_fwd_kernel, :2062-2140).
+// Work decomposition (gfx950, wave64): one workgroup per output row (node), one
+// lane per feature channel; per-path accumulators live in VGPRs and every output
+// element is stored exactly once, so the aggregation needs no atomics. The
+// per-edge coupling matrix A_p[a][b] = sum_c B_p[a,b,c] y_c depends only on the
+// edge when in2 has one channel; it is formed once per edge per lane.
+#pragma once
+#include "fc_common.h"
+#include "generated/fc_tp_paths.h"
+
+namespace fc {
+
+struct TPArgs {
+  const float* in1;
+  const float* in2;
+  const float* w;
+  const int32_t* idx_j;    // conv: sender per edge
+  const int32_t* rowptr;   // conv: receiver CSR, n_rows + 1 entries
+  const float* grad_out;   // bwd only
+  float* out;              // fwd output
+  float* grad_in1;         // bwd: rows mode -> grad wrt in1 rows; conv mode -> per-edge messages
+  float* grad_in2;
+  float* grad_w;           // per-item weight gradient (item = edge or row)
+  int64_t n_rows;
+  int32_t F1, F2, C;       // in1 / in2 / output features (1 broadcasts)
+  int32_t shared_w, reduced;
+  float alpha;             // fwd output scale
+};
+
+template <int L1, int L2, int LO, bool SYM>
+struct TPConfig {
+  using PL = PathList<L1, L2, LO, SYM>;
+  static constexpr int NP = PL::NP;
+  static constexpr int D1 = ncomp(L1);
+  static constexpr int D2 = ncomp(L2);
+  static constexpr int NOUT = PL::NOUT;
+  static constexpr int NOUT_RED = PL::NOUT_RED;
+};
+
+template <int L1, int L2, int LO, bool SYM, bool CONV>
+__global__ void __launch_bounds__(256) tp_fwd_kernel(TPArgs g) {
+  using CF = TPConfig<L1, L2, LO, SYM>;
+  using PL = typename CF::PL;
+  constexpr int D1 = CF::D1, D2 = CF::D2, NOUT = CF::NOUT, NP = CF::NP;
+  const int64_t row = blockIdx.x;
+  const int f = threadIdx.x;
+  const int C = g.C;
+  if (f >= C) return;
+  const int f1 = g.F1 == 1 ? 0 : f;
+  const int f2 = g.F2 == 1 ? 0 : f;
+  const int64_t s1 = (int64_t)D1 * g.F1, s2 = (int64_t)D2 * g.F2, sw = (int64_t)NP * C;
+
+  float acc[NOUT];
+#pragma unroll
+  for (int k = 0; k < NOUT; ++k) acc[k] = 0.f;
+
+  int64_t e0 = row, e1 = row + 1;
+  if constexpr (CONV) { e0 = g.rowptr[row]; e1 = g.rowptr[row + 1]; }
+  for (int64_t e = e0; e < e1; ++e) {
+    const int64_t j = CONV ? (int64_t)g.idx_j[e] : e;
+    float x[D1], y[D2];
+#pragma unroll
+    for (int u = 0; u < D1; ++u) x[u] = g.in1[j * s1 + u * g.F1 + f1];
+#pragma unroll
+    for (int u = 0; u < D2; ++u) y[u] = g.in2[e * s2 + u * g.F2 + f2];
+    const float* wr = g.shared_w ? g.w : g.w + e * sw;
+    static_for<NP>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      constexpr PathDesc P = PL::at(i);
+      using T = TPPath<P.r1, P.r2, P.lo>;
+      float A[T::NA], t[T::NO];
+      T::amat(y + P.r2 * P.r2, A);
+      T::apply(A, x + P.r1 * P.r1, t);
+      const float wv = wr[i * C + f];
+#pragma unroll
+      for (int a = 0; a < T::NO; ++a) acc[PL::out_index(i, a)] = fmaf(wv, t[a], acc[PL::out_index(i, a)]);
+    });
+  }
+  if (!g.reduced) {
+    float* o = g.out + row * (int64_t)NOUT * C + f;
+#pragma unroll
+    for (int k = 0; k < NOUT; ++k) o[(int64_t)k * C] = g.alpha * acc[k];
+  } else {
+    constexpr int NR = CF::NOUT_RED;
+    float red[NR];
+#pragma unroll
+    for (int k = 0; k < NR; ++k) red[k] = 0.f;
+    static_for<NP>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      constexpr PathDesc P = PL::at(i);
+#pragma unroll
+      for (int a = 0; a < 2 * P.lo + 1; ++a) red[PL::out_index_red(i, a)] += acc[PL::out_index(i, a)];
+    });
+    float* o = g.out + row * (int64_t)NR * C + f;
+#pragma unroll
+    for (int k = 0; k < NR; ++k) o[(int64_t)k * C] = g.alpha * red[k];
+  }
+}
+
+// Backward (vector-Jacobian product) of tp_fwd_kernel.
+//   grad_w[item, p, f]  = sum_a go[a,p,f] t_p[a]            (t = A_p x)
+//   u_p[a]              = w[p,f] go[a,p,f]
+//   gx[b]              += sum_a A_p[a,b] u_p[a]              (conv: per-edge message)
+//   gy[c]              += sum_{a,b} B_p[a,b,c] u_p[a] x[b]
+// Channel-broadcast operands (F == 1) get their gradient summed over channels:
+// wave64 reduction, then a cross-wave sum through LDS in a fixed order, so the
+// result is deterministic.
+constexpr int BWD_CHUNK = 16;
+constexpr int BWD_MAXW = 16;
+
+template <int L1, int L2, int LO, bool SYM, bool CONV>
+__global__ void __launch_bounds__(256) tp_bwd_kernel(TPArgs g) {
+  using CF = TPConfig<L1, L2, LO, SYM>;
+  using PL = typename CF::PL;
+  constexpr int D1 = CF::D1, D2 = CF::D2, NOUT = CF::NOUT, NP = CF::NP;
+  extern __shared__ float red_lds[];  // [BWD_CHUNK][waves][D1 + D2], only when reducing over channels
+
+  const int64_t row = blockIdx.x;
+  const int f = threadIdx.x;
+  const int C = g.C;
+  const bool active = f < C;
+  const int fa = active ? f : 0;
+  const int f1 = g.F1 == 1 ? 0 : fa;
+  const int f2 = g.F2 == 1 ? 0 : fa;
+  const int wave = f >> 6, lane = f & 63, nw = blockDim.x >> 6;
+  const int64_t s1 = (int64_t)D1 * g.F1, s2 = (int64_t)D2 * g.F2, sw = (int64_t)NP * C;
+  const bool need1 = g.grad_in1 != nullptr, need2 = g.grad_in2 != nullptr, needw = g.grad_w != nullptr;
+  const bool red1 = need1 && g.F1 == 1 && C > 1, red2 = need2 && g.F2 == 1 && C > 1;
+
+  float go[NOUT];
+  if (!g.reduced) {
+#pragma unroll
+    for (int k = 0; k < NOUT; ++k) go[k] = active ? g.alpha * g.grad_out[row * (int64_t)NOUT * C + (int64_t)k * C + fa] : 0.f;
+  } else {
+    constexpr int NR = CF::NOUT_RED;
+    float gr[NR];
+#pragma unroll
+    for (int k = 0; k < NR; ++k) gr[k] = active ? g.alpha * g.grad_out[row * (int64_t)NR * C + (int64_t)k * C + fa] : 0.f;
+    static_for<NP>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      constexpr PathDesc P = PL::at(i);
+#pragma unroll
+      for (int a = 0; a < 2 * P.lo + 1; ++a) go[PL::out_index(i, a)] = gr[PL::out_index_red(i, a)];
+    });
+  }
+
+  int64_t e0 = row, e1 = row + 1;
+  if constexpr (CONV) { e0 = g.rowptr[row]; e1 = g.rowptr[row + 1]; }
+  for (int64_t c0 = e0; c0 < e1; c0 += BWD_CHUNK) {
+    const int64_t c1 = c0 + BWD_CHUNK < e1 ? c0 + BWD_CHUNK : e1;
+    for (int64_t e = c0; e < c1; ++e) {
+      const int64_t j = CONV ? (int64_t)g.idx_j[e] : e;
+      float x[D1], y[D2], gx[D1], gy[D2];
+#pragma unroll
+      for (int u = 0; u < D1; ++u) { x[u] = active ? g.in1[j * s1 + u * g.F1 + f1] : 0.f; gx[u] = 0.f; }
+#pragma unroll
+      for (int u = 0; u < D2; ++u) { y[u] = active ? g.in2[e * s2 + u * g.F2 + f2] : 0.f; gy[u] = 0.f; }
+      const float* wr = g.shared_w ? g.w : g.w + e * sw;
+      static_for<NP>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        constexpr PathDesc P = PL::at(i);
+        using T = TPPath<P.r1, P.r2, P.lo>;
+        float A[T::NA], t[T::NO], u[T::NO];
+        T::amat(y + P.r2 * P.r2, A);
+        const float wv = active ? wr[i * C + fa] : 0.f;
+        if (needw) {
+          T::apply(A, x + P.r1 * P.r1, t);
+          float s = 0.f;
+#pragma unroll
+          for (int a = 0; a < T::NO; ++a) s = fmaf(go[PL::out_index(i, a)], t[a], s);
+          if (active) g.grad_w[e * sw + i * C + f] = s;
+        }
+#pragma unroll
+        for (int a = 0; a < T::NO; ++a) u[a] = wv * go[PL::out_index(i, a)];
+        if (need1) T::apply_t(A, u, gx + P.r1 * P.r1);
+        if (need2) T::vjp2(u, x + P.r1 * P.r1, gy + P.r2 * P.r2);
+      });
+      const int slot = (int)(e - c0);
+      if (need1) {
+        if (red1) {
+#pragma unroll
+          for (int u = 0; u < D1; ++u) {
+            const float s = wave_sum(gx[u]);
+            if (lane == 0) red_lds[(slot * nw + wave) * (D1 + D2) + u] = s;
+          }
+        } else if (active) {
+#pragma unroll
+          for (int u = 0; u < D1; ++u) g.grad_in1[e * s1 + u * g.F1 + f] = gx[u];
+        }
+      }
+      if (need2) {
+        if (red2) {
+#pragma unroll
+          for (int u = 0; u < D2; ++u) {
+            const float s = wave_sum(gy[u]);
+            if (lane == 0) red_lds[(slot * nw + wave) * (D1 + D2) + D1 + u] = s;
+          }
+        } else if (active) {
+#pragma unroll
+          for (int u = 0; u < D2; ++u) g.grad_in2[e * s2 + u * g.F2 + f] = gy[u];
+        }
+      }
+    }
+    if (red1 || red2) {
+      __syncthreads();
+      const int n = (int)(c1 - c0);
+      for (int k = f; k < n * (D1 + D2); k += blockDim.x) {
+        const int slot = k / (D1 + D2), u = k % (D1 + D2);
+        float s = 0.f;
+        for (int w = 0; w < nw; ++w) s += red_lds[(slot * nw + w) * (D1 + D2) + u];
+        const int64_t e = c0 + slot;
+        if (u < D1) {
+          if (red1) g.grad_in1[e * D1 + u] = s;
+        } else if (red2) {
+          g.grad_in2[e * D2 + (u - D1)] = s;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Host-side launcher for one configuration.
+template <int L1, int L2, int LO, bool SYM>
+int launch_tp(const TPArgs& g, bool conv, bool bwd, hipStream_t stream) {
+  if (g.n_rows == 0) return FC_OK;
+  const int threads = ((g.C + 63) / 64) * 64;
+  if (threads > 256) return FC_ERR_SHAPE;
+  dim3 grid((unsigned)g.n_rows), block(threads);
+  if (bwd) {
+    const bool reduce = (g.grad_in1 && g.F1 == 1 && g.C > 1) || (g.grad_in2 && g.F2 == 1 && g.C > 1);
+    const size_t lds = reduce ? sizeof(float) * BWD_CHUNK * (threads / 64) * (ncomp(L1) + ncomp(L2)) : 0;
+    if (conv) hipLaunchKernelGGL((tp_bwd_kernel<L1, L2, LO, SYM, true>), grid, block, lds, stream, g);
+    else hipLaunchKernelGGL((tp_bwd_kernel<L1, L2, LO, SYM, false>), grid, block, lds, stream, g);
+  } else {
+    if (conv) hipLaunchKernelGGL((tp_fwd_kernel<L1, L2, LO, SYM, true>), grid, block, 0, stream, g);
+    else hipLaunchKernelGGL((tp_fwd_kernel<L1, L2, LO, SYM, false>), grid, block, 0, stream, g);
+  }
+  FC_LAUNCH_CHECK();
+  return FC_OK;
+}
+
+// Per-L1 dispatchers, defined in fc_tp_l<L1>.hip (split for parallel compilation).
+int dispatch_tp_l0(int l2, int lo, bool sym, const TPArgs& g, bool conv, bool bwd, hipStream_t s);
+int dispatch_tp_l1(int l2, int lo, bool sym, const TPArgs& g, bool conv, bool bwd, hipStream_t s);
+int dispatch_tp_l2(int l2, int lo, bool sym, const TPArgs& g, bool conv, bool bwd, hipStream_t s);
+int dispatch_tp_l3(int l2, int lo, bool sym, const TPArgs& g, bool conv, bool bwd, hipStream_t s);
+
+template <int L1>
+int dispatch_tp_for(int l2, int lo, bool sym, const TPArgs& g, bool conv, bool bwd, hipStream_t s) {
+#define FC_TP_CASE(A, B)                                                        \
+  if (l2 == A && lo == B) {                                                     \
+    if (sym) {                                                                  \
+      if constexpr (L1 == A) return launch_tp<L1, A, B, true>(g, conv, bwd, s); \
+      else return FC_ERR_BAD_DESC;                                              \
+    }                                                                           \
+    return launch_tp<L1, A, B, false>(g, conv, bwd, s);                         \
+  }
+  FC_TP_CASE(0, 0) FC_TP_CASE(0, 1) FC_TP_CASE(0, 2) FC_TP_CASE(0, 3)
+  FC_TP_CASE(1, 0) FC_TP_CASE(1, 1) FC_TP_CASE(1, 2) FC_TP_CASE(1, 3)
+  FC_TP_CASE(2, 0) FC_TP_CASE(2, 1) FC_TP_CASE(2, 2) FC_TP_CASE(2, 3)
+  FC_TP_CASE(3, 0) FC_TP_CASE(3, 1) FC_TP_CASE(3, 2) FC_TP_CASE(3, 3)
+#undef FC_TP_CASE
+  return FC_ERR_UNSUPPORTED_L;
+}
+
+}  // namespace fc

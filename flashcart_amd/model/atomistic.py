@@ -1,0 +1,157 @@
+"""Energy/force driver (reference src/flashcart/model/atomistic.py).
+
+``predict`` sums site energies per structure with the HIP segment sum and obtains
+forces (-dE/dR), stress/virials (symmetric virtual strain) and edge forces (dE/d rij)
+with autograd, whose backward runs through the registered HIP ops.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+from typing import Any, Dict, Optional, Union
+
+import torch
+import torch.nn as nn
+import yaml
+
+from flashcart_amd.o3 import _ops
+from flashcart_amd.utils.geometry import to_voigt6, uses_periodic_shifts
+
+
+def save_inference_metadata(ckpt_dir: Path, model_config: Dict[str, Any], meta: Optional[Dict[str, Any]] = None):
+    ckpt_dir = Path(ckpt_dir)
+    ckpt_dir.mkdir(parents=True, exist_ok=True)
+    with open(ckpt_dir / "model_config.yaml", "w") as fh:
+        yaml.safe_dump(model_config, fh)
+    if meta is not None:
+        with open(ckpt_dir / "meta.yaml", "w") as fh:
+            yaml.safe_dump(meta, fh)
+
+
+def load_model_config(ckpt_dir: Path) -> Dict[str, Any]:
+    path = Path(ckpt_dir) / "model_config.yaml"
+    if not path.exists():
+        raise FileNotFoundError(f"No model_config.yaml in {ckpt_dir}.")
+    with open(path) as fh:
+        return yaml.safe_load(fh)
+
+
+def _graph_dict(graph) -> Dict[str, Any]:
+    if isinstance(graph, dict):
+        return dict(graph)
+    d = graph.to_dict()
+    d["_source"] = graph
+    return d
+
+
+class AtomisticModel(nn.Module):
+    """Base class: site energies -> per-structure energies and their derivatives."""
+
+    def forward(self, graph: Dict[str, torch.Tensor]) -> torch.Tensor:  # pragma: no cover - abstract
+        raise NotImplementedError()
+
+    def predict(self, graph, compute_forces: bool = False, compute_stress: bool = False,
+                compute_edge_forces: bool = False, create_graph: bool = False, use_compile: bool = False,
+                compile_mode: str = "reduce-overhead", fullgraph: bool = True,
+                dynamic: bool = False) -> Dict[str, torch.Tensor]:
+        """Energies and requested derivatives (reference ``model/atomistic.py:75-156``).
+
+        ``create_graph`` (second derivatives, force-loss training) needs the double
+        backward of the kernels, which this build does not provide.
+        """
+        if create_graph:
+            raise NotImplementedError("create_graph=True needs second derivatives of the HIP ops "
+                                      "(training with force losses), which are not built.")
+        gd = self._prepare_predict_graph(graph, compute_forces, compute_stress, compute_edge_forces)
+        return self._predict_impl(gd, compute_forces, compute_stress, compute_edge_forces)
+
+    def _prepare_predict_graph(self, graph, compute_forces, compute_stress, compute_edge_forces):
+        gd = _graph_dict(graph)
+        gd["use_shifts"] = uses_periodic_shifts(gd.get("use_shifts", gd.get("pbc")))
+        if not (compute_forces or compute_stress or compute_edge_forces):
+            gd["positions"] = gd["positions"].detach()
+            return gd
+        positions = gd["positions"].detach()
+        cell = gd["cell"].detach() if torch.is_tensor(gd.get("cell")) else None
+        if compute_stress:
+            if cell is None:
+                raise ValueError("Cannot compute stress without cell information.")
+            disp = torch.zeros_like(cell).requires_grad_(True)
+            sym = 0.5 * (disp + disp.transpose(-1, -2))
+            scaling = torch.eye(3, device=cell.device, dtype=cell.dtype).unsqueeze(0) + sym
+            positions = (positions.unsqueeze(-2) @ scaling[gd["batch"]]).squeeze(-2)
+            cell = cell @ scaling
+            gd["displacement"] = disp
+        if compute_forces:
+            positions.requires_grad_(True)
+        gd["positions"] = positions
+        gd["cell"] = cell
+        if compute_edge_forces:
+            v = gd.get("vectors")
+            if v is None:
+                raise ValueError("Cannot compute edge forces without graph.vectors.")
+            gd["vectors"] = v.detach().requires_grad_(True)
+        return gd
+
+    def _predict_impl(self, gd, compute_forces, compute_stress, compute_edge_forces):
+        node_energies = self(gd)
+        out = {"node_energies": node_energies}
+        n_atoms = gd["n_atoms"]
+        if node_energies.shape[0] == gd["batch"].shape[0]:
+            ptr = gd.get("ptr")
+            if ptr is None:
+                ptr = torch.cat([n_atoms.new_zeros(1), torch.cumsum(n_atoms, 0)])
+            out["energy"] = _ops.segment_sum(node_energies, ptr, gd["batch"])
+        else:
+            out["energy"] = node_energies.sum().reshape(1)
+        inputs, names = [], []
+        if compute_forces:
+            inputs.append(gd["positions"]); names.append("forces")
+        if compute_stress:
+            inputs.append(gd["displacement"]); names.append("stress")
+        if compute_edge_forces:
+            inputs.append(gd["vectors"]); names.append("edge_forces")
+        if inputs:
+            grads = torch.autograd.grad(out["energy"].sum(), inputs, allow_unused=True)
+            for name, g, x in zip(names, grads, inputs):
+                g = torch.zeros_like(x) if g is None else g
+                if name == "forces":
+                    out["forces"] = -g
+                elif name == "stress":
+                    vol = torch.det(gd["cell"])
+                    out["stress"] = to_voigt6(g / vol.view(-1, 1, 1))
+                    out["virials"] = -out["stress"] * vol.unsqueeze(-1)
+                else:
+                    out["edge_forces"] = g
+            out["node_energies"] = out["node_energies"].detach()
+            out["energy"] = out["energy"].detach()
+        return out
+
+    # -- checkpoints (reference model/atomistic.py:441-527) -------------------------------
+    def to_model_config(self) -> Dict[str, Any]:  # pragma: no cover - abstract
+        raise NotImplementedError()
+
+    @classmethod
+    def from_config(cls, cfg: Dict[str, Any]) -> "AtomisticModel":  # pragma: no cover - abstract
+        raise NotImplementedError()
+
+    def save_weights(self, path: Union[str, Path], filename: str = "model.pt") -> None:
+        path = Path(path)
+        path.mkdir(parents=True, exist_ok=True)
+        torch.save(self.state_dict(), path / filename)
+
+    def load_weights(self, path: Union[str, Path], filename: str = "model.pt", map_location="cpu") -> None:
+        self.load_state_dict(torch.load(Path(path) / filename, weights_only=True, map_location=map_location))
+
+    def save_inference_checkpoint(self, path: Union[str, Path], meta: Optional[Dict[str, Any]] = None) -> None:
+        self.save_weights(path)
+        save_inference_metadata(Path(path), self.to_model_config(), meta=meta)
+
+    @classmethod
+    def from_checkpoint(cls, ckpt_dir: Union[str, Path], device=None, map_location="cpu") -> "AtomisticModel":
+        model = cls.from_config(load_model_config(Path(ckpt_dir)))
+        model.load_weights(ckpt_dir, map_location=map_location)
+        if device is not None:
+            model = model.to(device)
+        model.eval()
+        return model

@@ -1,0 +1,619 @@
+"""PyTorch custom operators backed by the HIP C ABI (``torch.ops.flashcart.*``).
+
+Op names follow the reference's registered operators
+(src/flashcart/o3/_tensor_product.py:332,588; src/flashcart/o3/_irreps.py:84,117;
+src/flashcart/o3/_linear.py:328,457) so call sites read the same. Each op has a
+shape-only fake implementation (for torch.compile / meta tracing) and a registered
+autograd formula whose backward is another HIP op. Second derivatives (training
+with force losses) are not provided: the backward ops have no autograd formula.
+
+Every implementation checks that its tensors are float32 on a ROCm device and
+raises otherwise; there is no CPU path.
+"""
+
+from __future__ import annotations
+
+from typing import List, Optional, Tuple
+
+import torch
+
+from flashcart_amd import _lib
+from flashcart_amd.codegen.cartesian import count_output_paths
+
+Tensor = torch.Tensor
+
+
+def _lib_call(name: str, *args) -> None:
+    lib = _lib.load()
+    _lib.check(getattr(lib, name)(*args), name)
+
+
+def _i32(name: str, t: Optional[Tensor]) -> Optional[Tensor]:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise RuntimeError(f"`{name}` must be on a ROCm device, got {t.device}.")
+    if t.dtype != torch.int32:
+        t = t.to(torch.int32)
+    return t.contiguous()
+
+
+def _tp_out_dim(in1_l_max, in2_l_max, out_l_max, in1_features, in2_features, symmetric, reduced) -> int:
+    counts, _ = count_output_paths(in1_l_max, in2_l_max, out_l_max, symmetric)
+    c = max(in1_features, in2_features)
+    return sum((2 * l + 1) * (min(n, 1) if reduced else n) * c for l, n in enumerate(counts))
+
+
+# ---------------------------------------------------------------------------
+# Eq. (1) expansion
+# ---------------------------------------------------------------------------
+
+@torch.library.custom_op("flashcart::irreps_fwd", mutates_args=())
+def irreps_fwd(x: Tensor, l_max: int) -> Tensor:
+    x = _lib.contig("x", x)
+    out = x.new_empty(x.shape[0], (l_max + 1) ** 2)
+    _lib_call("fc_irreps_fwd", x.shape[0], l_max, x.data_ptr(), out.data_ptr(), _lib.stream_of(x))
+    return out
+
+
+@irreps_fwd.register_fake
+def _(x, l_max):
+    return x.new_empty(x.shape[0], (l_max + 1) ** 2)
+
+
+@torch.library.custom_op("flashcart::irreps_bwd", mutates_args=())
+def irreps_bwd(grad_output: Tensor, x: Tensor, l_max: int) -> Tensor:
+    g = _lib.contig("grad_output", grad_output)
+    x = _lib.contig("x", x)
+    gx = torch.empty_like(x)
+    _lib_call("fc_irreps_bwd", x.shape[0], l_max, g.data_ptr(), x.data_ptr(), gx.data_ptr(), _lib.stream_of(x))
+    return gx
+
+
+@irreps_bwd.register_fake
+def _(grad_output, x, l_max):
+    return torch.empty_like(x)
+
+
+def _irreps_setup(ctx, inputs, output):
+    x, l_max = inputs
+    ctx.save_for_backward(x)
+    ctx.l_max = int(l_max)
+
+
+def _irreps_backward(ctx, grad):
+    (x,) = ctx.saved_tensors
+    if not ctx.needs_input_grad[0]:
+        return None, None
+    return irreps_bwd(grad, x, ctx.l_max), None
+
+
+irreps_fwd.register_autograd(_irreps_backward, setup_context=_irreps_setup)
+
+
+# ---------------------------------------------------------------------------
+# Radial basis and cutoff envelope
+# ---------------------------------------------------------------------------
+
+@torch.library.custom_op("flashcart::radial_fwd", mutates_args=())
+def radial_fwd(d: Tensor, basis: int, n_radial: int, r_min: float, r_max: float, poly_order: int) -> Tuple[Tensor, Tensor]:
+    """(feats (n, n_radial) or empty when basis is NONE, env (n,) or empty when poly_order == 0)."""
+    d = _lib.contig("distances", d)
+    n = d.shape[0]
+    feats = d.new_empty(n, n_radial) if basis != _lib.BASIS_NONE else d.new_empty(0)
+    env = d.new_empty(n) if poly_order > 0 else d.new_empty(0)
+    desc = _lib.radial_desc(basis, n_radial, r_min, r_max, poly_order)
+    _lib_call("fc_radial_fwd", desc, n, d.data_ptr(), _lib.ptr(feats) if feats.numel() else None,
+              _lib.ptr(env) if env.numel() else None, _lib.stream_of(d))
+    return feats, env
+
+
+@radial_fwd.register_fake
+def _(d, basis, n_radial, r_min, r_max, poly_order):
+    n = d.shape[0]
+    return (d.new_empty(n, n_radial) if basis != _lib.BASIS_NONE else d.new_empty(0),
+            d.new_empty(n) if poly_order > 0 else d.new_empty(0))
+
+
+@torch.library.custom_op("flashcart::radial_bwd", mutates_args=())
+def radial_bwd(d: Tensor, g_feats: Optional[Tensor], g_env: Optional[Tensor], basis: int, n_radial: int,
+               r_min: float, r_max: float, poly_order: int) -> Tensor:
+    d = _lib.contig("distances", d)
+    gf = _lib.contig("grad_feats", g_feats) if g_feats is not None and basis != _lib.BASIS_NONE else None
+    ge = _lib.contig("grad_env", g_env) if g_env is not None and poly_order > 0 else None
+    gd = torch.empty_like(d)
+    desc = _lib.radial_desc(basis, n_radial, r_min, r_max, poly_order)
+    _lib_call("fc_radial_bwd", desc, d.shape[0], d.data_ptr(), _lib.ptr(gf), _lib.ptr(ge), gd.data_ptr(),
+              _lib.stream_of(d))
+    return gd
+
+
+@radial_bwd.register_fake
+def _(d, g_feats, g_env, basis, n_radial, r_min, r_max, poly_order):
+    return torch.empty_like(d)
+
+
+def _radial_setup(ctx, inputs, output):
+    d, basis, n_radial, r_min, r_max, poly_order = inputs
+    ctx.save_for_backward(d)
+    ctx.cfg = (int(basis), int(n_radial), float(r_min), float(r_max), int(poly_order))
+
+
+def _radial_backward(ctx, g_feats, g_env):
+    (d,) = ctx.saved_tensors
+    if not ctx.needs_input_grad[0]:
+        return (None,) * 6
+    basis, n_radial, r_min, r_max, poly_order = ctx.cfg
+    gf = g_feats if (g_feats is not None and g_feats.numel()) else None
+    ge = g_env if (g_env is not None and g_env.numel()) else None
+    return (radial_bwd(d, gf, ge, basis, n_radial, r_min, r_max, poly_order),) + (None,) * 5
+
+
+radial_fwd.register_autograd(_radial_backward, setup_context=_radial_setup)
+
+
+# ---------------------------------------------------------------------------
+# Fused edge geometry (edge vectors -> expansion, radial basis, envelope)
+# ---------------------------------------------------------------------------
+
+def _edge_desc(l_max, basis, n_radial, r_min, r_max, poly_order):
+    return _lib.EdgeDesc(int(l_max), _lib.radial_desc(basis, n_radial, r_min, r_max, poly_order))
+
+
+@torch.library.custom_op("flashcart::edge_geometry", mutates_args=())
+def edge_geometry(positions: Optional[Tensor], shift_vec: Optional[Tensor], idx_i: Tensor, idx_j: Tensor,
+                  vectors: Optional[Tensor], rowptr: Optional[Tensor], sender_perm: Optional[Tensor],
+                  sender_ptr: Optional[Tensor], l_max: int, basis: int, n_radial: int, r_min: float, r_max: float,
+                  poly_order: int) -> Tuple[Tensor, Tensor, Tensor]:
+    """(edge_attrs (E, (l_max+1)^2), radial feats (E, n_radial), envelope (E,))."""
+    ii = _i32("idx_i", idx_i)
+    jj = _i32("idx_j", idx_j)
+    pos = _lib.contig("positions", positions) if positions is not None else None
+    sv = _lib.contig("shift_vec", shift_vec) if shift_vec is not None else None
+    vec = _lib.contig("vectors", vectors) if vectors is not None else None
+    ref = pos if pos is not None else vec
+    if ref is None:
+        raise ValueError("edge_geometry needs positions or vectors.")
+    E = ii.shape[0]
+    attrs = ref.new_empty(E, (l_max + 1) ** 2)
+    feats = ref.new_empty(E, n_radial) if basis != _lib.BASIS_NONE else ref.new_empty(0)
+    env = ref.new_empty(E) if poly_order > 0 else ref.new_empty(0)
+    desc = _edge_desc(l_max, basis, n_radial, r_min, r_max, poly_order)
+    _lib_call("fc_edge_geometry_fwd", desc, E, _lib.ptr(pos), _lib.ptr(sv), ii.data_ptr(), jj.data_ptr(),
+              _lib.ptr(vec), attrs.data_ptr(), _lib.ptr(feats) if feats.numel() else None,
+              _lib.ptr(env) if env.numel() else None, _lib.stream_of(ref))
+    return attrs, feats, env
+
+
+@edge_geometry.register_fake
+def _(positions, shift_vec, idx_i, idx_j, vectors, rowptr, sender_perm, sender_ptr, l_max, basis, n_radial, r_min,
+      r_max, poly_order):
+    ref = positions if positions is not None else vectors
+    E = idx_i.shape[0]
+    return (ref.new_empty(E, (l_max + 1) ** 2),
+            ref.new_empty(E, n_radial) if basis != _lib.BASIS_NONE else ref.new_empty(0),
+            ref.new_empty(E) if poly_order > 0 else ref.new_empty(0))
+
+
+@torch.library.custom_op("flashcart::edge_geometry_bwd", mutates_args=())
+def edge_geometry_bwd(g_attrs: Optional[Tensor], g_feats: Optional[Tensor], g_env: Optional[Tensor],
+                      positions: Optional[Tensor], shift_vec: Optional[Tensor], idx_i: Tensor, idx_j: Tensor,
+                      vectors: Optional[Tensor], rowptr: Optional[Tensor], sender_perm: Optional[Tensor],
+                      sender_ptr: Optional[Tensor], l_max: int, basis: int, n_radial: int, r_min: float,
+                      r_max: float, poly_order: int, need_positions: bool) -> Tuple[Tensor, Tensor]:
+    """(grad_positions (N, 3) or empty, grad_vec (E, 3))."""
+    ii = _i32("idx_i", idx_i)
+    jj = _i32("idx_j", idx_j)
+    pos = _lib.contig("positions", positions) if positions is not None else None
+    sv = _lib.contig("shift_vec", shift_vec) if shift_vec is not None else None
+    vec = _lib.contig("vectors", vectors) if vectors is not None else None
+    ref = pos if pos is not None else vec
+    ga = _lib.contig("grad_attrs", g_attrs) if g_attrs is not None else None
+    gf = _lib.contig("grad_feats", g_feats) if (g_feats is not None and basis != _lib.BASIS_NONE) else None
+    ge = _lib.contig("grad_env", g_env) if (g_env is not None and poly_order > 0) else None
+    E = ii.shape[0]
+    gvec = ref.new_empty(E, 3)
+    desc = _edge_desc(l_max, basis, n_radial, r_min, r_max, poly_order)
+    stream = _lib.stream_of(ref)
+    _lib_call("fc_edge_geometry_bwd", desc, E, _lib.ptr(pos), _lib.ptr(sv), ii.data_ptr(), jj.data_ptr(),
+              _lib.ptr(vec), _lib.ptr(ga), _lib.ptr(gf), _lib.ptr(ge), gvec.data_ptr(), stream)
+    if not need_positions or pos is None:
+        return ref.new_empty(0), gvec
+    n = pos.shape[0]
+    if rowptr is None or sender_perm is None or sender_ptr is None:
+        from flashcart_amd.o3._graph import build_graph
+        gcsr = build_graph(torch.stack([idx_i, idx_j]), n, check_sorted=False)
+        rowptr, sender_perm, sender_ptr = gcsr.rowptr, gcsr.sender_perm, gcsr.sender_ptr
+    gpos = pos.new_empty(n, 3)
+    csr = _lib.csr_struct(n, E, jj, _i32("rowptr", rowptr), _i32("sender_perm", sender_perm),
+                          _i32("sender_ptr", sender_ptr), n)
+    _lib_call("fc_edge_grad_to_nodes", csr, gvec.data_ptr(), gpos.data_ptr(), stream)
+    return gpos, gvec
+
+
+@edge_geometry_bwd.register_fake
+def _(g_attrs, g_feats, g_env, positions, shift_vec, idx_i, idx_j, vectors, rowptr, sender_perm, sender_ptr,
+      l_max, basis, n_radial, r_min, r_max, poly_order, need_positions):
+    ref = positions if positions is not None else vectors
+    gp = ref.new_empty(positions.shape[0], 3) if (need_positions and positions is not None) else ref.new_empty(0)
+    return gp, ref.new_empty(idx_i.shape[0], 3)
+
+
+def _edge_setup(ctx, inputs, output):
+    positions, shift_vec, idx_i, idx_j, vectors, rowptr, sender_perm, sender_ptr = inputs[:8]
+    ctx.cfg = tuple(inputs[8:])
+    ctx.save_for_backward(positions, shift_vec, idx_i, idx_j, vectors, rowptr, sender_perm, sender_ptr)
+
+
+def _edge_backward(ctx, g_attrs, g_feats, g_env):
+    positions, shift_vec, idx_i, idx_j, vectors, rowptr, sender_perm, sender_ptr = ctx.saved_tensors
+    need_pos = ctx.needs_input_grad[0]
+    need_shift = ctx.needs_input_grad[1]
+    need_vec = ctx.needs_input_grad[4]
+    if not (need_pos or need_shift or need_vec):
+        return (None,) * 14
+    gpos, gvec = edge_geometry_bwd(
+        g_attrs, g_feats if (g_feats is not None and g_feats.numel()) else None,
+        g_env if (g_env is not None and g_env.numel()) else None,
+        positions, shift_vec, idx_i, idx_j, vectors, rowptr, sender_perm, sender_ptr, *ctx.cfg, bool(need_pos))
+    return ((gpos if need_pos else None), (gvec if need_shift else None), None, None,
+            (gvec if need_vec else None)) + (None,) * 9
+
+
+edge_geometry.register_autograd(_edge_backward, setup_context=_edge_setup)
+
+
+# ---------------------------------------------------------------------------
+# Tensor product
+# ---------------------------------------------------------------------------
+
+def _tp_csr(in1: Tensor, idx_i: Tensor, idx_j: Tensor, rowptr: Optional[Tensor], sender_perm: Optional[Tensor],
+            sender_ptr: Optional[Tensor], need_senders: bool):
+    n = in1.shape[0]
+    jj = _i32("idx_j", idx_j)
+    if rowptr is None or (need_senders and (sender_perm is None or sender_ptr is None)):
+        from flashcart_amd.o3._graph import build_graph
+        g = build_graph(torch.stack([idx_i.to(torch.int64), idx_j.to(torch.int64)]), n)
+        rowptr, sender_perm, sender_ptr = g.rowptr, g.sender_perm, g.sender_ptr
+    rp = _i32("rowptr", rowptr)
+    sp = _i32("sender_perm", sender_perm)
+    sq = _i32("sender_ptr", sender_ptr)
+    if rp.shape[0] != n + 1:
+        raise ValueError(f"rowptr must have in1.shape[0] + 1 = {n + 1} entries, got {rp.shape[0]}.")
+    keep = (jj, rp, sp, sq)
+    return _lib.csr_struct(n, jj.shape[0], jj, rp, sp, sq, n), keep
+
+
+def _check_tp_inputs(in1, in2, weights, idx_i, idx_j, in1_l_max, in2_l_max, out_l_max, in1_features,
+                     in2_features, symmetric_product, shared_weights):
+    conv = idx_i is not None and idx_j is not None
+    c = max(in1_features, in2_features)
+    _, n_paths = count_output_paths(in1_l_max, in2_l_max, out_l_max, symmetric_product)
+    if in1.shape[-1] != (in1_l_max + 1) ** 2 * in1_features or in2.shape[-1] != (in2_l_max + 1) ** 2 * in2_features:
+        raise ValueError("tensor-product input widths do not match the configuration.")
+    items = idx_i.shape[0] if conv else in1.shape[0]
+    if conv:
+        if in2.shape[0] != items or idx_j.shape[0] != items:
+            raise ValueError("in2, idx_i and idx_j must have one row per edge.")
+    elif in2.shape[0] != in1.shape[0]:
+        raise ValueError("idx_i and idx_j must be provided when in1 and in2 have different batch sizes. "
+                         f"Got in1_batch={in1.shape[0]}, in2_batch={in2.shape[0]}.")
+    if shared_weights:
+        if weights.dim() != 1 or weights.shape[0] != n_paths * c:
+            raise ValueError(f"Shared weights must be 1D of size {n_paths * c}, got {tuple(weights.shape)}.")
+    elif weights.dim() != 2 or weights.shape[0] != items or weights.shape[1] != n_paths * c:
+        raise ValueError(f"Non-shared weights must have shape ({items}, {n_paths * c}), got {tuple(weights.shape)}.")
+    return conv
+
+
+@torch.library.custom_op("flashcart::tp_fwd", mutates_args=())
+def tp_fwd(in1: Tensor, in2: Tensor, weights: Tensor, idx_i: Optional[Tensor], idx_j: Optional[Tensor],
+           in1_l_max: int, in2_l_max: int, out_l_max: int, in1_features: int, in2_features: int,
+           symmetric_product: bool, shared_weights: bool, reduce_paths: bool, rowptr: Optional[Tensor] = None,
+           sender_perm: Optional[Tensor] = None, sender_ptr: Optional[Tensor] = None, alpha: float = 1.0) -> Tensor:
+    conv = _check_tp_inputs(in1, in2, weights, idx_i, idx_j, in1_l_max, in2_l_max, out_l_max, in1_features,
+                            in2_features, symmetric_product, shared_weights)
+    in1 = _lib.contig("in1", in1)
+    in2 = _lib.contig("in2", in2)
+    w = _lib.contig("weights", weights)
+    desc = _lib.tp_desc(in1_l_max, in2_l_max, out_l_max, in1_features, in2_features, symmetric_product,
+                        shared_weights, reduce_paths)
+    out = in1.new_empty(in1.shape[0], _tp_out_dim(in1_l_max, in2_l_max, out_l_max, in1_features, in2_features,
+                                                  symmetric_product, reduce_paths))
+    csr, keep = (None, None)
+    if conv:
+        csr, keep = _tp_csr(in1, idx_i, idx_j, rowptr, sender_perm, sender_ptr, need_senders=False)
+    _lib_call("fc_tp_fwd", desc, csr, in1.shape[0], in1.data_ptr(), in2.data_ptr(), w.data_ptr(), float(alpha),
+              out.data_ptr(), _lib.stream_of(in1))
+    return out
+
+
+@tp_fwd.register_fake
+def _(in1, in2, weights, idx_i, idx_j, in1_l_max, in2_l_max, out_l_max, in1_features, in2_features,
+      symmetric_product, shared_weights, reduce_paths, rowptr=None, sender_perm=None, sender_ptr=None, alpha=1.0):
+    return in1.new_empty(in1.shape[0], _tp_out_dim(in1_l_max, in2_l_max, out_l_max, in1_features, in2_features,
+                                                   symmetric_product, reduce_paths))
+
+
+@torch.library.custom_op("flashcart::tp_bwd", mutates_args=())
+def tp_bwd(grad_out: Tensor, in1: Tensor, in2: Tensor, weights: Tensor, idx_i: Optional[Tensor],
+           idx_j: Optional[Tensor], in1_l_max: int, in2_l_max: int, out_l_max: int, in1_features: int,
+           in2_features: int, symmetric_product: bool, shared_weights: bool, reduce_paths: bool,
+           need_grad_in1: bool, need_grad_in2: bool, need_grad_weights: bool, rowptr: Optional[Tensor] = None,
+           sender_perm: Optional[Tensor] = None, sender_ptr: Optional[Tensor] = None,
+           alpha: float = 1.0) -> Tuple[Tensor, Tensor, Tensor]:
+    """Gradients wrt (in1, in2, weights); unrequested ones are returned as empty (0,) tensors."""
+    conv = idx_i is not None and idx_j is not None
+    go = _lib.contig("grad_out", grad_out)
+    in1 = _lib.contig("in1", in1)
+    in2 = _lib.contig("in2", in2)
+    w = _lib.contig("weights", weights)
+    desc = _lib.tp_desc(in1_l_max, in2_l_max, out_l_max, in1_features, in2_features, symmetric_product,
+                        shared_weights, reduce_paths)
+    csr, keep = (None, None)
+    if conv:
+        csr, keep = _tp_csr(in1, idx_i, idx_j, rowptr, sender_perm, sender_ptr, need_senders=need_grad_in1)
+    g1 = torch.empty_like(in1) if need_grad_in1 else in1.new_empty(0)
+    g2 = torch.empty_like(in2) if need_grad_in2 else in2.new_empty(0)
+    gw = torch.empty_like(w) if need_grad_weights else w.new_empty(0)
+    lib = _lib.load()
+    n_ws = lib.fc_tp_bwd_workspace(desc, csr, in1.shape[0], int(need_grad_in1), int(need_grad_weights))
+    if n_ws < 0:
+        _lib.check(-n_ws, "fc_tp_bwd_workspace")
+    ws = in1.new_empty(max(int(n_ws), 1))
+    _lib_call("fc_tp_bwd", desc, csr, in1.shape[0], go.data_ptr(), in1.data_ptr(), in2.data_ptr(), w.data_ptr(),
+              float(alpha), g1.data_ptr() if need_grad_in1 else None, g2.data_ptr() if need_grad_in2 else None,
+              gw.data_ptr() if need_grad_weights else None, ws.data_ptr(), int(n_ws), _lib.stream_of(in1))
+    return g1, g2, gw
+
+
+@tp_bwd.register_fake
+def _(grad_out, in1, in2, weights, idx_i, idx_j, in1_l_max, in2_l_max, out_l_max, in1_features, in2_features,
+      symmetric_product, shared_weights, reduce_paths, need_grad_in1, need_grad_in2, need_grad_weights,
+      rowptr=None, sender_perm=None, sender_ptr=None, alpha=1.0):
+    return (torch.empty_like(in1) if need_grad_in1 else in1.new_empty(0),
+            torch.empty_like(in2) if need_grad_in2 else in2.new_empty(0),
+            torch.empty_like(weights) if need_grad_weights else weights.new_empty(0))
+
+
+def _tp_setup(ctx, inputs, output):
+    (in1, in2, weights, idx_i, idx_j, l1, l2, lo, f1, f2, sym, shared, red, rowptr, sperm, sptr, alpha) = inputs
+    ctx.save_for_backward(in1, in2, weights, idx_i, idx_j, rowptr, sperm, sptr)
+    ctx.cfg = (int(l1), int(l2), int(lo), int(f1), int(f2), bool(sym), bool(shared), bool(red))
+    ctx.alpha = float(alpha)
+
+
+def _tp_backward(ctx, grad):
+    in1, in2, weights, idx_i, idx_j, rowptr, sperm, sptr = ctx.saved_tensors
+    n1, n2, nw = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[2]
+    none_tail = (None,) * 14
+    if not (n1 or n2 or nw):
+        return (None, None, None) + none_tail
+    g1, g2, gw = tp_bwd(grad, in1, in2, weights, idx_i, idx_j, *ctx.cfg, bool(n1), bool(n2), bool(nw),
+                        rowptr, sperm, sptr, ctx.alpha)
+    return (g1 if n1 else None, g2 if n2 else None, gw if nw else None) + none_tail
+
+
+tp_fwd.register_autograd(_tp_backward, setup_context=_tp_setup)
+
+
+# ---------------------------------------------------------------------------
+# Equivariant linear map
+# ---------------------------------------------------------------------------
+
+def _linear_dims(in_l_max, out_l_max, in_features, out_features, in_paths):
+    in_dim = sum((2 * l + 1) * in_features * in_paths[l] for l in range(in_l_max + 1))
+    out_dim = sum((2 * l + 1) * out_features for l in range(out_l_max + 1))
+    return in_dim, out_dim
+
+
+def _wlist(w0, w1, w2, w3) -> List[Tensor]:
+    return [w for w in (w0, w1, w2, w3) if w is not None]
+
+
+def _pad4(weights):
+    ws = list(weights) + [None] * (4 - len(weights))
+    if len(ws) != 4:
+        raise ValueError("at most 4 rank blocks (l <= 3) are supported.")
+    return ws
+
+
+@torch.library.custom_op("flashcart::linear_fwd", mutates_args=())
+def linear_fwd_op(x: Tensor, w0: Tensor, w1: Optional[Tensor], w2: Optional[Tensor], w3: Optional[Tensor],
+                  in_l_max: int, out_l_max: int, in_features: int, out_features: int, in_paths: List[int],
+                  scale: List[float], alpha: float = 1.0) -> Tensor:
+    in_dim, out_dim = _linear_dims(in_l_max, out_l_max, in_features, out_features, in_paths)
+    if x.shape[-1] != in_dim:
+        raise RuntimeError(f"Incorrect last dimension for x. Expected {in_dim}, got {x.shape[-1]}.")
+    x = _lib.contig("x", x)
+    ws = [_lib.contig(f"weight[{l}]", w) for l, w in enumerate(_wlist(w0, w1, w2, w3))]
+    out = x.new_empty(x.shape[0], out_dim)
+    desc = _lib.linear_desc(in_l_max, out_l_max, in_features, out_features, in_paths, ws, scale)
+    _lib_call("fc_linear_fwd", desc, x.shape[0], x.data_ptr(), float(alpha), out.data_ptr(), _lib.stream_of(x))
+    return out
+
+
+@linear_fwd_op.register_fake
+def _(x, w0, w1, w2, w3, in_l_max, out_l_max, in_features, out_features, in_paths, scale, alpha=1.0):
+    _, out_dim = _linear_dims(in_l_max, out_l_max, in_features, out_features, in_paths)
+    return x.new_empty(x.shape[0], out_dim)
+
+
+@torch.library.custom_op("flashcart::linear_bwd", mutates_args=())
+def linear_bwd_op(grad_out: Tensor, w0: Tensor, w1: Optional[Tensor], w2: Optional[Tensor], w3: Optional[Tensor],
+                  in_l_max: int, out_l_max: int, in_features: int, out_features: int, in_paths: List[int],
+                  scale: List[float], alpha: float = 1.0) -> Tensor:
+    """Input gradient of linear_fwd (the MFMA dgrad)."""
+    in_dim, _ = _linear_dims(in_l_max, out_l_max, in_features, out_features, in_paths)
+    go = _lib.contig("grad_out", grad_out)
+    ws = [_lib.contig(f"weight[{l}]", w) for l, w in enumerate(_wlist(w0, w1, w2, w3))]
+    gx = go.new_empty(go.shape[0], in_dim)
+    desc = _lib.linear_desc(in_l_max, out_l_max, in_features, out_features, in_paths, ws, scale)
+    _lib_call("fc_linear_dgrad", desc, go.shape[0], go.data_ptr(), float(alpha), gx.data_ptr(), _lib.stream_of(go))
+    return gx
+
+
+@linear_bwd_op.register_fake
+def _(grad_out, w0, w1, w2, w3, in_l_max, out_l_max, in_features, out_features, in_paths, scale, alpha=1.0):
+    in_dim, _ = _linear_dims(in_l_max, out_l_max, in_features, out_features, in_paths)
+    return grad_out.new_empty(grad_out.shape[0], in_dim)
+
+
+def linear_fwd(x: Tensor, weights: List[Tensor], in_l_max: int, out_l_max: int, in_features: int,
+               out_features: int, in_paths: List[int], scale: List[float], alpha: float = 1.0) -> Tensor:
+    """out_l = alpha * scale_l * x_l @ W_l^T for every shared rank (torch.ops.flashcart.linear_fwd)."""
+    return linear_fwd_op(x, *_pad4(weights), in_l_max, out_l_max, in_features, out_features, list(in_paths),
+                         [float(s) for s in scale], float(alpha))
+
+
+def linear_bwd(grad_out: Tensor, weights: List[Tensor], in_l_max: int, out_l_max: int, in_features: int,
+               out_features: int, in_paths: List[int], scale: List[float], alpha: float = 1.0) -> Tensor:
+    return linear_bwd_op(grad_out, *_pad4(weights), in_l_max, out_l_max, in_features, out_features,
+                         list(in_paths), [float(s) for s in scale], float(alpha))
+
+
+def _linear_setup(ctx, inputs, output):
+    x, w0, w1, w2, w3, in_l_max, out_l_max, in_features, out_features, in_paths, scale, alpha = inputs
+    ws = _wlist(w0, w1, w2, w3)
+    ctx.save_for_backward(x, *ws)
+    ctx.cfg = (int(in_l_max), int(out_l_max), int(in_features), int(out_features), list(in_paths), list(scale))
+    ctx.alpha = float(alpha)
+
+
+def _linear_backward(ctx, grad):
+    x, *weights = ctx.saved_tensors
+    in_l_max, out_l_max, fin, fout, in_paths, scale = ctx.cfg
+    need = ctx.needs_input_grad
+    gx = None
+    if need[0]:
+        gx = linear_bwd(grad, weights, in_l_max, out_l_max, fin, fout, in_paths, scale, ctx.alpha)
+    gws = [None, None, None, None]
+    if any(need[1:5]):
+        # Parameter gradients (training only): scale_l * sum_{n,m} go_l^T x_l, on the GPU with torch.
+        n = x.shape[0]
+        in_off = out_off = 0
+        for l in range(min(in_l_max, out_l_max) + 1):
+            k = fin * in_paths[l]
+            m = 2 * l + 1
+            if need[1 + l]:
+                xl = x[:, in_off:in_off + m * k].reshape(n * m, k)
+                gl = grad[:, out_off:out_off + m * fout].reshape(n * m, fout)
+                gws[l] = (gl.t() @ xl) * (scale[l] * ctx.alpha)
+            in_off += m * k
+            out_off += m * fout
+    return (gx, *gws) + (None,) * 7
+
+
+linear_fwd_op.register_autograd(_linear_backward, setup_context=_linear_setup)
+
+
+
+# ---------------------------------------------------------------------------
+# Dense layer with optional rescaled-SiLU epilogue (radial / readout MLPs)
+# ---------------------------------------------------------------------------
+
+@torch.library.custom_op("flashcart::dense_fwd", mutates_args=())
+def dense_fwd(x: Tensor, weight: Tensor, bias: Optional[Tensor], scale: float, act: int) -> Tuple[Tensor, Tensor]:
+    """(activated output, pre-activation (empty when act == 0))."""
+    x = _lib.contig("x", x)
+    w = _lib.contig("weight", weight)
+    b = _lib.contig("bias", bias) if bias is not None else None
+    m, k = w.shape
+    if x.shape[-1] != k:
+        raise RuntimeError(f"Incorrect last dimension for x. Expected {k}, got {x.shape[-1]}.")
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, k)
+    out = x.new_empty(x2.shape[0], m)
+    pre = x.new_empty(x2.shape[0], m) if act else x.new_empty(0)
+    _lib_call("fc_dense_fwd", x2.shape[0], k, m, x2.data_ptr(), w.data_ptr(), float(scale), _lib.ptr(b), int(act),
+              pre.data_ptr() if act else None, out.data_ptr(), _lib.stream_of(x))
+    return out.reshape(*lead, m), (pre.reshape(*lead, m) if act else pre)
+
+
+@dense_fwd.register_fake
+def _(x, weight, bias, scale, act):
+    m = weight.shape[0]
+    return x.new_empty(*x.shape[:-1], m), (x.new_empty(*x.shape[:-1], m) if act else x.new_empty(0))
+
+
+@torch.library.custom_op("flashcart::dense_bwd", mutates_args=())
+def dense_bwd(grad_out: Tensor, pre: Tensor, weight: Tensor, scale: float, act: int) -> Tensor:
+    go = _lib.contig("grad_out", grad_out)
+    w = _lib.contig("weight", weight)
+    m, k = w.shape
+    lead = go.shape[:-1]
+    go2 = go.reshape(-1, m)
+    pr = _lib.contig("pre", pre).reshape(-1, m) if act else None
+    gx = go.new_empty(go2.shape[0], k)
+    _lib_call("fc_dense_dgrad", go2.shape[0], k, m, go2.data_ptr(), _lib.ptr(pr), w.data_ptr(), float(scale),
+              int(act), gx.data_ptr(), _lib.stream_of(go))
+    return gx.reshape(*lead, k)
+
+
+@dense_bwd.register_fake
+def _(grad_out, pre, weight, scale, act):
+    return grad_out.new_empty(*grad_out.shape[:-1], weight.shape[1])
+
+
+def _dense_setup(ctx, inputs, output):
+    x, weight, bias, scale, act = inputs
+    ctx.save_for_backward(x, weight, output[1])
+    ctx.scale = float(scale)
+    ctx.act = int(act)
+    ctx.has_bias = bias is not None
+
+
+def _dense_backward(ctx, grad, grad_pre):
+    x, weight, pre = ctx.saved_tensors
+    gx = gw = gb = None
+    if ctx.needs_input_grad[0]:
+        gx = dense_bwd(grad, pre, weight, ctx.scale, ctx.act)
+    if ctx.needs_input_grad[1] or (ctx.has_bias and ctx.needs_input_grad[2]):
+        # Parameter gradients (training only), with torch on the GPU.
+        g = grad
+        if ctx.act:
+            s = torch.sigmoid(pre)
+            g = grad * 1.6765324703310907 * s * (1 + pre * (1 - s))
+        g2 = g.reshape(-1, g.shape[-1])
+        if ctx.needs_input_grad[1]:
+            gw = (g2.t() @ x.reshape(-1, x.shape[-1])) * ctx.scale
+        if ctx.has_bias and ctx.needs_input_grad[2]:
+            gb = g2.sum(0)
+    return gx, gw, gb, None, None
+
+
+dense_fwd.register_autograd(_dense_backward, setup_context=_dense_setup)
+
+
+# ---------------------------------------------------------------------------
+# Segment sum over contiguous sorted segments (per-graph energies)
+# ---------------------------------------------------------------------------
+
+@torch.library.custom_op("flashcart::segment_sum", mutates_args=())
+def segment_sum(src: Tensor, ptr: Tensor, index: Tensor) -> Tensor:
+    """dst[s] = sum(src[ptr[s]:ptr[s+1]]); ``index`` (row -> segment) is used by the backward."""
+    s = _lib.contig("src", src)
+    p = _i32("ptr", ptr)
+    n_seg = p.shape[0] - 1
+    width = 1 if s.dim() == 1 else int(s[0].numel()) if s.shape[0] else int(torch.Size(s.shape[1:]).numel())
+    dst = s.new_empty((n_seg,) + tuple(s.shape[1:]))
+    _lib_call("fc_segment_sum", n_seg, width, s.data_ptr(), None, p.data_ptr(), dst.data_ptr(), _lib.stream_of(s))
+    return dst
+
+
+@segment_sum.register_fake
+def _(src, ptr, index):
+    return src.new_empty((ptr.shape[0] - 1,) + tuple(src.shape[1:]))
+
+
+def _seg_setup(ctx, inputs, output):
+    src, ptr, index = inputs
+    ctx.save_for_backward(index)
+
+
+def _seg_backward(ctx, grad):
+    (index,) = ctx.saved_tensors
+    return grad.index_select(0, index.to(torch.int64)), None, None
+
+
+segment_sum.register_autograd(_seg_backward, setup_context=_seg_setup)

@@ -1,0 +1,41 @@
+"""Edge-vector helpers (reference src/flashcart/utils/geometry.py)."""
+
+from typing import Union
+
+import numpy as np
+import torch
+
+
+def uses_periodic_shifts(pbc: object) -> bool:
+    """True when any periodic flag is set, or when the flags are unavailable (reference ``geometry.py:7-22``)."""
+    if torch.is_tensor(pbc):
+        return bool(torch.any(pbc).item())
+    if pbc is None:
+        return True
+    return bool(np.any(pbc))
+
+
+def shift_vectors(cell: torch.Tensor, shifts: torch.Tensor, idx_i: torch.Tensor, batch: torch.Tensor) -> torch.Tensor:
+    """Cartesian periodic translation S . cell[batch[i]] of every edge (reference ``geometry.py:52``)."""
+    return (shifts.to(cell.dtype).unsqueeze(-2) @ cell[batch[idx_i]]).squeeze(-2)
+
+
+def get_edge_vectors(positions, cell, shifts, edge_index, batch, use_shifts: bool = True) -> torch.Tensor:
+    """pos[j] - pos[i] (+ S . cell) with plain tensor ops (reference ``geometry.py:25-53``).
+
+    The model itself evaluates edge vectors inside the fused edge-geometry kernel;
+    this helper is kept for callers of the reference utility.
+    """
+    idx_i, idx_j = edge_index[0], edge_index[1]
+    if not use_shifts:
+        return positions[idx_j] - positions[idx_i]
+    return positions[idx_j] - positions[idx_i] + shift_vectors(cell, shifts, idx_i, batch)
+
+
+def to_voigt6(t: Union[np.ndarray, torch.Tensor]):
+    """Symmetrised Voigt order xx, yy, zz, yz, xz, xy (reference ``geometry.py:56-77``)."""
+    comps = [t[..., 0, 0], t[..., 1, 1], t[..., 2, 2], (t[..., 1, 2] + t[..., 2, 1]) / 2,
+             (t[..., 0, 2] + t[..., 2, 0]) / 2, (t[..., 0, 1] + t[..., 1, 0]) / 2]
+    if isinstance(t, torch.Tensor):
+        return torch.stack(comps, dim=-1)
+    return np.stack(comps, axis=-1)

@@ -1,0 +1,221 @@
+/*
+ * flashcart_hip.h -- C ABI of the MI355X (gfx950) FlashCart hot path.
+ *
+ * Every entry point takes plain device pointers, sizes and a HIP stream
+ * (hipStream_t passed as void*; NULL is the default stream). The library never
+ * allocates, frees or retains caller memory: outputs and workspaces are owned by
+ * the caller (in the Python layer, the PyTorch caching allocator). Kernels write
+ * every output element unless stated otherwise. All calls are asynchronous on the
+ * given stream and return an fc_status code; nothing throws across the ABI.
+ *
+ * Feature layout (the reference's layout contract): a tensor of maximal rank L
+ * with F channels is a row of (L+1)^2 * F floats, rank blocks in increasing l,
+ * each block (2l+1, F) component-major. Stored components follow
+ * src/flashcart/o3/_codegen_common.py:37-73 of the reference.
+ */
+#ifndef FLASHCART_HIP_H
+#define FLASHCART_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum fc_status {
+  FC_OK = 0,
+  FC_ERR_BAD_DESC = 1,       /* inconsistent descriptor (feature counts, flags) */
+  FC_ERR_UNSUPPORTED_L = 2,  /* a rank above FC_KERNEL_L_MAX (3) */
+  FC_ERR_LAUNCH = 3,         /* hipGetLastError() reported a launch failure */
+  FC_ERR_SHAPE = 4,          /* sizes the kernels do not support (e.g. > 1024 channels) */
+  FC_ERR_NULL = 5,           /* a required pointer is NULL */
+  FC_ERR_WORKSPACE = 6       /* workspace missing or too small */
+} fc_status;
+
+/* Library version (major*10000 + minor*100 + patch) and the maximal supported rank. */
+int fc_version(void);
+int fc_kernel_l_max(void);
+/* Human-readable message for a status code (static storage). */
+const char* fc_status_string(int status);
+
+/* ------------------------------------------------------------------------- */
+/* Eq. (1) expansion of unit vectors: replaces torch.ops.flashcart.irreps_fwd  */
+/* and irreps_bwd (reference src/flashcart/o3/_irreps.py:84-104, :117-150;    */
+/* generated kernels src/flashcart/o3/_codegen_irreps.py:426-505).             */
+/* x: (n, 3) unit vectors; out: (n, (l_max+1)^2); grad_x: (n, 3).             */
+/* ------------------------------------------------------------------------- */
+int fc_irreps_fwd(int64_t n, int32_t l_max, const float* x, float* out, void* stream);
+int fc_irreps_bwd(int64_t n, int32_t l_max, const float* grad_out, const float* x, float* grad_x,
+                  void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* Radial basis and cutoff envelope: replaces ChebyshevBasis.forward,          */
+/* BesselBasis.forward and PolynomialCutoff.calculate_envelope (reference      */
+/* src/flashcart/nn/radial.py:44-54, :98-121, :181-242) and their autograd.     */
+/* ------------------------------------------------------------------------- */
+typedef enum fc_basis_kind {
+  FC_BASIS_CHEBYSHEV_AFFINE = 0,
+  FC_BASIS_CHEBYSHEV_COSINE = 1,
+  FC_BASIS_BESSEL = 2,
+  FC_BASIS_NONE = 3 /* no radial basis (envelope / expansion only) */
+} fc_basis_kind;
+
+typedef struct fc_radial_desc {
+  int32_t basis;      /* fc_basis_kind */
+  int32_t n_radial;   /* basis functions (1..32) */
+  float r_min;        /* Chebyshev mapping interval [r_min, r_max] */
+  float r_max;        /* basis / cutoff radius */
+  int32_t poly_order; /* cutoff polynomial order p >= 2; 0 disables the envelope */
+} fc_radial_desc;
+
+/* d: (n,) -> feats (n, n_radial) (may be NULL), env (n,) (may be NULL). */
+int fc_radial_fwd(const fc_radial_desc* desc, int64_t n, const float* d, float* feats, float* env,
+                  void* stream);
+/* grad_d (n,) = sum_k g_feats[:,k] dfeat_k/dd + g_env denv/dd (either gradient may be NULL). */
+int fc_radial_bwd(const fc_radial_desc* desc, int64_t n, const float* d, const float* g_feats,
+                  const float* g_env, float* grad_d, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* Fused edge geometry: edge vectors (reference src/flashcart/utils/geometry.py */
+/* :25-53), lengths and directions with the 1e-4 clamp (src/flashcart/model/    */
+/* flashcart.py:22,280-281), the Eq. (1) expansion of the directions, the       */
+/* radial basis and the cutoff envelope (src/flashcart/model/flashcart.py       */
+/* :280-284) in one pass over the edges.                                       */
+/*   positions mode: vec = pos[idx_j] - pos[idx_i] + shift_vec[e]              */
+/*   vectors mode (pos == NULL): vec = vectors[e] (LAMMPS ML-IAP rij)           */
+/* ------------------------------------------------------------------------- */
+typedef struct fc_edge_desc {
+  int32_t l_max;             /* expansion rank (0..3) */
+  fc_radial_desc radial;     /* basis and cutoff */
+} fc_edge_desc;
+
+int fc_edge_geometry_fwd(const fc_edge_desc* desc, int64_t n_edges, const float* pos,
+                         const float* shift_vec, const int32_t* idx_i, const int32_t* idx_j,
+                         const float* vectors, float* attrs, float* feats, float* env,
+                         void* stream);
+/* grad_vec (n_edges, 3) = dL/dvec given dL/dattrs, dL/dfeats, dL/denv (each may be NULL). */
+int fc_edge_geometry_bwd(const fc_edge_desc* desc, int64_t n_edges, const float* pos,
+                         const float* shift_vec, const int32_t* idx_i, const int32_t* idx_j,
+                         const float* vectors, const float* g_attrs, const float* g_feats,
+                         const float* g_env, float* grad_vec, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* Receiver-sorted graph, computed once per neighbour list.                   */
+/* ------------------------------------------------------------------------- */
+typedef struct fc_csr {
+  int64_t n_nodes;             /* receiver rows (output rows of the convolution) */
+  int64_t n_edges;
+  const int32_t* idx_j;        /* sender of each edge */
+  const int32_t* rowptr;       /* receiver CSR over edges sorted by receiver (n_nodes+1) */
+  const int32_t* sender_perm;  /* edge ids ordered by sender (stable), n_edges */
+  const int32_t* sender_ptr;   /* sender CSR into sender_perm (n_sender_rows+1) */
+  int64_t n_sender_rows;       /* rows of in1 (senders may include ghost atoms) */
+} fc_csr;
+
+/* rowptr[n] = first edge with idx_sorted[e] >= n, for n in [0, n_nodes]. */
+int fc_csr_from_sorted(int64_t n_edges, const int32_t* idx_sorted, int64_t n_nodes,
+                       int32_t* rowptr, void* stream);
+
+/* Position gradient from edge-vector gradients, as a segmented reduction
+ * (replaces the autograd index_select -> index_add backward of get_edge_vectors):
+ *   grad_pos[n] = sum_{e: idx_j[e]=n} grad_vec[e] - sum_{e: idx_i[e]=n} grad_vec[e]. */
+int fc_edge_grad_to_nodes(const fc_csr* graph, const float* grad_vec, float* grad_pos,
+                          void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* Irreducible Cartesian tensor product: replaces torch.ops.flashcart.tp_fwd  */
+/* and tp_bwd (reference src/flashcart/o3/_tensor_product.py:332-479,         */
+/* :550-787; kernels src/flashcart/o3/_codegen_tensor_product.py:2062-2140,    */
+/* :2274-2421, :2447-2603, :3245-3311).                                        */
+/* ------------------------------------------------------------------------- */
+typedef struct fc_tp_desc {
+  int32_t in1_l_max, in2_l_max, out_l_max; /* each 0..3 */
+  int32_t in1_features, in2_features;      /* equal, or one of them 1 (broadcast) */
+  int32_t symmetric_product;               /* canonical pairs only (in1 == in2) */
+  int32_t shared_weights;                  /* weights (n_paths*C,) instead of (items, n_paths*C) */
+  int32_t reduce_paths;                    /* sum paths within each output rank */
+} fc_tp_desc;
+
+/* Path count (the weight layout) of a configuration, or a negative fc_status. */
+int fc_tp_num_paths(const fc_tp_desc* desc);
+/* Output width in floats per row, or a negative fc_status. */
+int64_t fc_tp_out_dim(const fc_tp_desc* desc);
+
+/* graph == NULL: independent rows (in1, in2, weights and out all have n_rows rows).
+ * graph != NULL: convolution; in1 has graph->n_sender_rows rows, in2 and weights have
+ * n_edges rows, out has graph->n_nodes rows (receiver-sorted segmented sum).
+ * out = alpha * TP(...). */
+int fc_tp_fwd(const fc_tp_desc* desc, const fc_csr* graph, int64_t n_rows, const float* in1,
+              const float* in2, const float* weights, float alpha, float* out, void* stream);
+
+/* Floats of workspace fc_tp_bwd needs for the requested gradients. */
+int64_t fc_tp_bwd_workspace(const fc_tp_desc* desc, const fc_csr* graph, int64_t n_rows,
+                            int need_in1, int need_weights);
+
+/* Vector-Jacobian product of fc_tp_fwd (with the same alpha). NULL gradient pointers
+ * are not computed. In convolution mode the in1 gradient is gathered to the senders
+ * through graph->sender_perm / sender_ptr (segmented sum, no atomics). */
+int fc_tp_bwd(const fc_tp_desc* desc, const fc_csr* graph, int64_t n_rows, const float* grad_out,
+              const float* in1, const float* in2, const float* weights, float alpha,
+              float* grad_in1, float* grad_in2, float* grad_weights, float* workspace,
+              int64_t workspace_floats, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* Equivariant linear map on MFMA: replaces torch.ops.flashcart.linear_fwd and  */
+/* the input-gradient branch of linear_bwd (reference src/flashcart/o3/         */
+/* _linear.py:64-110, :328-385, :457-538; kernels _codegen_linear.py:161-221).  */
+/*   out_l[n, m, :] = alpha * scale_l * x_l[n, m, :] @ W_l^T   for l <= min(in,out) */
+/* with x_l viewed as (n, 2l+1, in_features*in_paths[l]); output ranks above     */
+/* min(in_l_max, out_l_max) are zero.                                          */
+/* ------------------------------------------------------------------------- */
+typedef struct fc_linear_desc {
+  int32_t in_l_max, out_l_max;
+  int32_t in_features, out_features;
+  int32_t in_paths[4];       /* paths per input rank (1 for plain features) */
+  const float* weight[4];    /* W_l, row-major (out_features, in_features*in_paths[l]) */
+  float scale[4];            /* s_l */
+} fc_linear_desc;
+
+int fc_linear_fwd(const fc_linear_desc* desc, int64_t n_rows, const float* x, float alpha,
+                  float* out, void* stream);
+int fc_linear_dgrad(const fc_linear_desc* desc, int64_t n_rows, const float* grad_out,
+                    float alpha, float* grad_x, void* stream);
+
+/* Plain dense map out = act(x @ W^T * scale + bias), x (n, k), W (m, k) row-major:
+ * the radial and readout MLP layers (reference src/flashcart/nn/layers.py:84-145,
+ * :12-39). act: 0 none, 1 rescaled SiLU (1.6765324703310907 * silu). pre_act (n, m)
+ * receives the value before the activation when non-NULL. */
+int fc_dense_fwd(int64_t n, int32_t k, int32_t m, const float* x, const float* w, float scale,
+                 const float* bias, int32_t act, float* pre_act, float* out, void* stream);
+/* grad_x (n, k) = (grad_out * act'(pre_act)) @ W * scale. */
+int fc_dense_dgrad(int64_t n, int32_t k, int32_t m, const float* grad_out, const float* pre_act,
+                   const float* w, float scale, int32_t act, float* grad_x, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* Segment reductions: replace scatter_sum (reference src/flashcart/utils/     */
+/* scatter.py:33-68) for sorted segments, e.g. per-graph energies              */
+/* (src/flashcart/model/atomistic.py:288).                                     */
+/*   dst[s, :] = sum_{k in [ptr[s], ptr[s+1])} src[perm ? perm[k] : k, :]      */
+/* ------------------------------------------------------------------------- */
+int fc_segment_sum(int64_t n_seg, int64_t width, const float* src, const int32_t* perm,
+                   const int32_t* ptr, float* dst, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* Host neighbour list (cell list over periodic images): replaces            */
+/* NeighborList.build / _matscipy_neighbors (reference src/flashcart/data/      */
+/* neighbors.py:56-77, :120-143). Pairs (i, j, S) with                         */
+/* |pos[j] - pos[i] + S.cell| < cutoff, self pairs with S = 0 removed, sorted   */
+/* lexicographically by (i, j, Sx, Sy, Sz). pos (n,3) and cell (3x3, rows are  */
+/* lattice vectors) in float64; pbc[3] flags. Returns the pair count and fills */
+/* the outputs only when it fits in `capacity`; -1 singular cell, -2 bad args. */
+/* Host memory only; no GPU is touched.                                        */
+/* ------------------------------------------------------------------------- */
+int64_t fc_neighbor_list(int64_t n, const double* pos, const double* cell, const int32_t* pbc,
+                         double cutoff, int64_t capacity, int64_t* out_i, int64_t* out_j,
+                         int32_t* out_shift);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASHCART_HIP_H */

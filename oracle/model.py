@@ -1,0 +1,192 @@
+"""Oracle: functional CPU restatement of the FlashCart potential (energies and forces).
+
+TEST INFRASTRUCTURE ONLY (checker and CPU baseline); never imported by flashcart_amd.
+
+Evaluates the potential from a state dict (the parameter names of the reference's
+module tree) and the model config, following the reference forward:
+  FlashCartPotential.forward      src/flashcart/model/flashcart.py:223-317 (wiring :151-221)
+  InteractionLayer.forward        src/flashcart/nn/layers.py:310-379
+  RMSLayerNorm.forward            src/flashcart/nn/layers.py:494-528
+  EquivariantGatedLayer.forward   src/flashcart/nn/layers.py:609-635
+  ProductLayer.forward            src/flashcart/nn/layers.py:949-995
+  EnergyReadoutLayer / ScaleShift src/flashcart/nn/layers.py:1045-1063, :1097-1108
+  AtomisticModel._predict_impl    src/flashcart/model/atomistic.py:276-340
+Forces are -dE/dpositions through torch autograd on CPU, as the reference's CPU path.
+"""
+
+from __future__ import annotations
+
+from typing import Any, Dict, List, Optional
+
+import torch
+
+from oracle import ops as O
+from oracle.cartesian import enumerate_paths
+
+
+def _paths(l1, l2, lo, sym=False):
+    ps = enumerate_paths(l1, l2, lo, sym)
+    counts = [0] * (lo + 1)
+    for p in ps:
+        counts[p[2]] += 1
+    return counts, len(ps)
+
+
+def _o3_linear(sd, prefix, x, in_l_max, out_l_max, fin, fout, in_paths=None):
+    n = min(in_l_max, out_l_max) + 1
+    ws = [sd[f"{prefix}.weight.{l}"] for l in range(n)]
+    return O.linear(x, ws, in_l_max, out_l_max, fin, fout, in_paths)
+
+
+def _mlp(sd, prefix, x, n_layers):
+    for k in range(n_layers):
+        w = sd[f"{prefix}.{2 * k}.weight"]
+        b = sd.get(f"{prefix}.{2 * k}.bias")
+        x = O.dense(x, w, b)
+        if k < n_layers - 1:
+            x = O.silu(x)
+    return x
+
+
+def rms_norm(sd, prefix, x, l_max, C, eps=1e-6):
+    n = x.shape[0]
+    _, P = _paths(l_max, l_max, 0, True)
+    inv = O.tensor_product(x, x, torch.ones(P * C, dtype=x.dtype), None, None, l_max, l_max, 0, C, C,
+                           symmetric_product=True, shared_weights=True).view(n, l_max + 1, C)
+    lw = torch.tensor([1.0 / ((2 * l + 1) * (l_max + 1)) for l in range(l_max + 1)], dtype=torch.float64)
+    mean_sq = (inv * lw.to(inv.dtype).view(1, -1, 1)).sum(dim=1).mean(dim=-1, keepdim=True)
+    scaled = x * torch.pow(mean_sq + eps, -0.5)
+    g = torch.cat([sd[f"{prefix}.weights.{l}"].repeat(2 * l + 1) for l in range(l_max + 1)]).view(1, -1)
+    return scaled * g
+
+
+def interaction(sd, prefix, cfg, k, node_feats, edge_attrs, edge_feats, envelope, edge_index):
+    C = cfg["n_hidden_feats"]
+    L = cfg["l_max_edge_attrs"]
+    lin = 0 if k == 0 else cfg["l_max_hidden_feats"]
+    lout = L if cfg.get("correlation", 3) > 1 else (cfg["l_max_hidden_feats"] if k < cfg["n_interactions"] - 1 else 0)
+    out_paths, P = _paths(lin, L, lout)
+    residual = node_feats
+    mlp_in = edge_feats * envelope.unsqueeze(-1)
+    h = _o3_linear(sd, f"{prefix}.linear_first", node_feats, lin, lin, C, C)
+    w = _mlp(sd, f"{prefix}.radial_mlp", mlp_in, len(cfg.get("hidden_radial", [64, 64])) + 1)
+    agg = O.tensor_product(h, edge_attrs, w, edge_index[0], edge_index[1], lin, L, lout, C, 1)
+    agg = agg / sd[f"{prefix}.sqrt_avg_neighbors"].to(agg.dtype)
+    out = _o3_linear(sd, f"{prefix}.linear_second", agg, lout, lout, C, C, out_paths)
+    if lin == 0:
+        skip = O.dense(residual, sd[f"{prefix}.skip_projection.weight"])
+        out = torch.cat([out[:, :C] + skip, out[:, C:]], dim=-1)
+    else:
+        out = out + _o3_linear(sd, f"{prefix}.skip_projection", residual, lin, lout, C, C)
+    if cfg.get("layer_norm", False):
+        out = rms_norm(sd, f"{prefix}.layer_norm", out, lout, C)
+    return out
+
+
+def gated(sd, prefix, cfg, x, l_max):
+    C = cfg["n_hidden_feats"]
+    n = x.shape[0]
+    values = _o3_linear(sd, f"{prefix}.value_linear", x, l_max, l_max, C, C)
+    pre = O.dense(x[:, :C], sd[f"{prefix}.gate_linear.weight"], sd.get(f"{prefix}.gate_linear.bias"))
+    if cfg.get("gate_activation", "silu") == "silu":
+        gates = O.silu(pre)
+    else:
+        gates = O.SIGMOID_SCALE * torch.sigmoid(pre)
+    gates = gates.view(n, l_max + 1, C)
+    blocks, off = [], 0
+    for l in range(l_max + 1):
+        b = values[:, off:off + (2 * l + 1) * C].view(n, 2 * l + 1, C)
+        blocks.append((b * gates[:, l].unsqueeze(1)).flatten(1))
+        off += (2 * l + 1) * C
+    return x + _o3_linear(sd, f"{prefix}.output_linear", torch.cat(blocks, dim=-1), l_max, l_max, C, C)
+
+
+def product(sd, prefix, cfg, x, out_l_max):
+    C = cfg["n_hidden_feats"]
+    L = cfg["l_max_edge_attrs"]
+    corr = cfg.get("correlation", 3)
+    reduced = cfg.get("path_reduced_product", True)
+    out_dim = (out_l_max + 1) ** 2 * C
+    output = x.new_zeros(x.shape[0], out_dim)
+    feats = x
+    for k in range(corr):
+        p_out = out_l_max if k == corr - 1 else L
+        l2, f2 = (0, 1) if k == 0 else (L, C)
+        out_paths, P = _paths(L, l2, p_out)
+        delta = sd.get(f"{prefix}.path_weights.{k}.delta")
+        w = 1.0 + (delta if delta is not None else torch.zeros(P * C, dtype=x.dtype))
+        if k == 0:
+            if reduced:
+                idx = torch.cat([torch.arange(l * C, (l + 1) * C).repeat(2 * l + 1) for l in range(L + 1)])
+                feats = x * w[idx]
+            else:
+                feats = x
+        else:
+            feats = O.tensor_product(feats, x, w, None, None, L, L, p_out, C, C, shared_weights=True,
+                                     reduce_paths=reduced)
+        if reduced:
+            norm = torch.cat([torch.full(((2 * l + 1) * C,), out_paths[l] ** -0.5) for l in range(p_out + 1)])
+            if not torch.all(norm == 1.0):
+                feats = feats * norm.to(feats.dtype)
+        else:
+            feats = _o3_linear(sd, f"{prefix}.product_linears.{k}", feats, p_out,
+                               p_out if k < corr - 1 else out_l_max, C, C, out_paths)
+        output = output + feats[:, :out_dim]
+    if reduced:
+        output = _o3_linear(sd, f"{prefix}.final_linear", output, out_l_max, out_l_max, C, C)
+    output = output + _o3_linear(sd, f"{prefix}.skip_projection", x, L, out_l_max, C, C)
+    if cfg.get("layer_norm", False):
+        output = rms_norm(sd, f"{prefix}.layer_norm", output, out_l_max, C)
+    return output
+
+
+def node_energies(sd: Dict[str, torch.Tensor], cfg: Dict[str, Any], graph: Dict[str, Any]) -> torch.Tensor:
+    if not cfg.get("element_agnostic_interaction", True) or not cfg.get("element_agnostic_product", True):
+        raise NotImplementedError("the oracle covers element-agnostic interactions and products")
+    C = cfg["n_hidden_feats"]
+    L = cfg["l_max_edge_attrs"]
+    Lh = cfg["l_max_hidden_feats"]
+    n_int = cfg["n_interactions"]
+    ei = graph["edge_index"]
+    vec = graph.get("vectors")
+    if vec is None:
+        vec = O.edge_vectors(graph["positions"], graph["cell"], graph["shifts"], ei, graph["batch"],
+                             graph.get("use_shifts", True))
+    d = vec.norm(dim=-1)
+    r = vec / d.clamp_min(O.MIN_EDGE_LENGTH).unsqueeze(-1)
+    attrs = O.irreps(r, L)
+    feats = O.chebyshev(d, cfg.get("n_radial", 8), cfg["r_max"], cfg.get("r_min", 0.0),
+                        cfg.get("radial_mapping", "affine"))
+    env = O.cutoff(d, cfg["r_max"], cfg.get("cutoff_poly_order", 6))
+    x = sd["embedding.weight"][graph["atom_types"]]
+    use_products = cfg.get("correlation", 3) > 1
+    outs = []
+    for k in range(n_int):
+        y = interaction(sd, f"interactions.{k}", cfg, k, x, attrs, feats, env, ei)
+        if cfg.get("nonlinearity", False):
+            y = gated(sd, f"nonlinearities.{k}", cfg, y, L if use_products else (Lh if k < n_int - 1 else 0))
+        if use_products:
+            x = product(sd, f"products.{k}", cfg, y, Lh if k < n_int - 1 else 0)
+        else:
+            x = y
+        outs.append(x[:, :C])
+    e = _mlp(sd, "readout.readout_mlp", torch.cat(outs, dim=1), len(cfg.get("hidden_readout", [64, 64])) + 1)
+    return sd["scale_shift.scales"][graph["atom_types"]] * e.squeeze(-1)
+
+
+def predict(sd: Dict[str, torch.Tensor], cfg: Dict[str, Any], graph: Dict[str, Any], compute_forces: bool = True,
+            dtype: torch.dtype = torch.float64) -> Dict[str, torch.Tensor]:
+    """Energies (per structure and per atom) and forces, all on CPU in ``dtype``."""
+    sd = {k: v.detach().to("cpu", dtype) if v.is_floating_point() else v.detach().cpu() for k, v in sd.items()}
+    g = {k: (v.detach().cpu() if torch.is_tensor(v) else v) for k, v in graph.items()}
+    pos = g["positions"].to(dtype).requires_grad_(compute_forces)
+    g["positions"] = pos
+    g["cell"] = g["cell"].to(dtype)
+    e_node = node_energies(sd, cfg, g)
+    n_graphs = int(g["n_atoms"].shape[0])
+    energy = O.scatter_sum(e_node, g["batch"], n_graphs)
+    out = {"node_energies": e_node.detach(), "energy": energy.detach()}
+    if compute_forces:
+        (grad,) = torch.autograd.grad(energy.sum(), pos)
+        out["forces"] = -grad
+    return out

@@ -1,0 +1,218 @@
+"""GPU parity of every HIP op against the CPU oracle (float64 oracle, float32 kernels).
+
+Tolerances: relative 2e-5 plus an absolute floor scaled by the magnitude of the
+quantity (float32 accumulation over up to a few hundred terms).
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import ops as O
+from tests.helpers import assert_close, random_csr_graph, unit_vectors
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _ops():
+    from flashcart_amd.o3 import _ops
+    return _ops
+
+
+@pytest.mark.parametrize("l_max", [0, 1, 2, 3])
+def test_irreps_fwd_bwd(l_max):
+    ops = _ops()
+    x64 = unit_vectors(1000, seed=l_max).float().double().requires_grad_(True)
+    ref = O.irreps(x64, l_max)
+    g = torch.randn_like(ref)
+    if l_max == 0:  # the expansion is the constant 1
+        ref_gx = torch.zeros_like(x64)
+    else:
+        (ref_gx,) = torch.autograd.grad(ref, x64, g)
+    x = x64.detach().float().to(DEV).requires_grad_(True)
+    out = ops.irreps_fwd(x, l_max)
+    (gx,) = torch.autograd.grad(out, x, g.float().to(DEV))
+    assert_close(out, ref, 1e-5, 1e-6, "irreps fwd")
+    assert_close(gx, ref_gx, 1e-5, 1e-5, "irreps bwd")
+
+
+@pytest.mark.parametrize("kind", ["cheb_cos", "cheb_aff", "bessel", "cutoff"])
+def test_radial_fwd_bwd(kind):
+    ops = _ops()
+    from flashcart_amd import _lib
+    torch.manual_seed(1)
+    d64 = torch.empty(4096).uniform_(0.0, 6.0).double().requires_grad_(True)
+    if kind == "cheb_cos":
+        ref, args = O.chebyshev(d64, 8, 5.0, 0.0, "cosine"), (_lib.BASIS_CHEBYSHEV_COSINE, 8, 0.0, 5.0, 0)
+    elif kind == "cheb_aff":
+        ref, args = O.chebyshev(d64, 8, 5.0, 0.5, "affine"), (_lib.BASIS_CHEBYSHEV_AFFINE, 8, 0.5, 5.0, 0)
+    elif kind == "bessel":
+        ref, args = O.bessel(d64, 8, 5.0), (_lib.BASIS_BESSEL, 8, 0.0, 5.0, 0)
+    else:
+        ref, args = O.cutoff(d64, 5.0, 6), (_lib.BASIS_NONE, 1, 0.0, 5.0, 6)
+    g = torch.randn_like(ref)
+    (ref_gd,) = torch.autograd.grad(ref, d64, g)
+    d = d64.detach().float().to(DEV).requires_grad_(True)
+    feats, env = ops.radial_fwd(d, *args)
+    out = env if kind == "cutoff" else feats
+    (gd,) = torch.autograd.grad(out, d, g.float().to(DEV))
+    assert_close(out, ref, 2e-5, 2e-5, f"{kind} fwd")
+    assert_close(gd, ref_gd, 1e-4, 1e-4, f"{kind} bwd")
+
+
+def _tp_case(l1, l2, lo, f1, f2, sym=False, shared=False, reduced=False, conv=True, seed=0,
+             degrees=(0, 1, 5, 26), n=37):
+    ops = _ops()
+    torch.manual_seed(seed)
+    C = max(f1, f2)
+    from oracle.cartesian import enumerate_paths
+    P = len(enumerate_paths(l1, l2, lo, sym))
+    if conv:
+        ei = random_csr_graph(n, degrees, seed=seed)
+        E = ei.shape[1]
+        in1 = torch.randn(n, (l1 + 1) ** 2 * f1, dtype=torch.float64)
+        in2 = torch.randn(E, (l2 + 1) ** 2 * f2, dtype=torch.float64)
+        items = E
+    else:
+        ei = None
+        in1 = torch.randn(n, (l1 + 1) ** 2 * f1, dtype=torch.float64)
+        in2 = in1.clone() if sym else torch.randn(n, (l2 + 1) ** 2 * f2, dtype=torch.float64)
+        items = n
+    w = torch.randn(P * C, dtype=torch.float64) if shared else torch.randn(items, P * C, dtype=torch.float64)
+    leaves64 = [t.clone().requires_grad_(True) for t in (in1, in2, w)]
+    a1, a2, aw = leaves64
+    ref = O.tensor_product(a1, a1 if sym else a2, aw, ei[0] if conv else None, ei[1] if conv else None,
+                           l1, l2, lo, f1, f2, sym, shared, reduced)
+    g = torch.randn_like(ref)
+    ref_grads = torch.autograd.grad(ref, [a1, a2, aw] if not sym else [a1, aw], g)
+    leaves = [t.detach().float().to(DEV).requires_grad_(True) for t in (in1, in2, w)]
+    b1, b2, bw = leaves
+    out = ops.tp_fwd(b1, b1 if sym else b2, bw, ei[0].to(DEV) if conv else None, ei[1].to(DEV) if conv else None,
+                     l1, l2, lo, f1, f2, sym, shared, reduced)
+    grads = torch.autograd.grad(out, [b1, b2, bw] if not sym else [b1, bw], g.float().to(DEV))
+    scale = float(ref.abs().max()) + 1.0
+    assert_close(out, ref, 2e-5, 2e-5 * scale, "tp fwd")
+    for k, (gg, rr) in enumerate(zip(grads, ref_grads)):
+        s = float(rr.abs().max()) + 1.0
+        assert_close(gg, rr, 2e-5, 2e-5 * s, f"tp grad {k}")
+
+
+CONV_CASES = [
+    (0, 3, 3, 16, 1), (2, 3, 3, 16, 1), (1, 2, 2, 8, 1), (2, 2, 2, 8, 1), (3, 3, 3, 4, 1), (0, 2, 2, 64, 1),
+    (2, 3, 3, 128, 1), (1, 1, 2, 8, 8), (2, 1, 1, 1, 8),
+]
+
+
+@pytest.mark.parametrize("case", CONV_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_tp_conv(case):
+    _tp_case(*case, conv=True)
+
+
+def test_tp_conv_reduced_shared():
+    _tp_case(2, 2, 2, 8, 1, shared=True, reduced=True, conv=True, seed=3)
+
+
+ROW_CASES = [
+    dict(l1=3, l2=3, lo=3, f1=8, f2=8, shared=True), dict(l1=3, l2=3, lo=2, f1=8, f2=8, shared=True),
+    dict(l1=3, l2=3, lo=0, f1=8, f2=8, shared=True), dict(l1=3, l2=0, lo=3, f1=8, f2=1, shared=True),
+    dict(l1=3, l2=3, lo=0, f1=8, f2=8, sym=True, shared=True), dict(l1=2, l2=2, lo=0, f1=16, f2=16, sym=True,
+                                                                   shared=True),
+    dict(l1=2, l2=2, lo=2, f1=1, f2=8), dict(l1=2, l2=2, lo=2, f1=8, f2=8, reduced=True),
+    dict(l1=3, l2=3, lo=3, f1=128, f2=128, shared=True),
+]
+
+
+@pytest.mark.parametrize("case", ROW_CASES, ids=lambda c: "-".join(f"{k}{v}" for k, v in c.items()))
+def test_tp_rows(case):
+    _tp_case(conv=False, n=300, **case)
+
+
+@pytest.mark.parametrize("cfg", [(0, 0, 16, 16, None), (2, 2, 32, 16, None), (3, 3, 128, 128, [3, 5, 5, 4]),
+                                 (2, 3, 64, 64, None), (3, 1, 8, 24, [1, 2, 3, 1])])
+def test_linear(cfg):
+    ops = _ops()
+    lin, lout, fin, fout, paths = cfg
+    paths = paths or [1] * (lin + 1)
+    torch.manual_seed(5)
+    n = 333
+    in_dim = sum((2 * l + 1) * fin * paths[l] for l in range(lin + 1))
+    x64 = torch.randn(n, in_dim, dtype=torch.float64, requires_grad=True)
+    ws64 = [torch.randn(fout, fin * paths[l], dtype=torch.float64, requires_grad=True)
+            for l in range(min(lin, lout) + 1)]
+    ref = O.linear(x64, ws64, lin, lout, fin, fout, paths)
+    g = torch.randn_like(ref)
+    ref_g = torch.autograd.grad(ref, [x64] + ws64, g)
+    x = x64.detach().float().to(DEV).requires_grad_(True)
+    ws = [w.detach().float().to(DEV).requires_grad_(True) for w in ws64]
+    scale = [float(fin * paths[l]) ** -0.5 for l in range(min(lin, lout) + 1)]
+    out = ops.linear_fwd(x, ws, lin, lout, fin, fout, paths, scale, 1.0)
+    got_g = torch.autograd.grad(out, [x] + ws, g.float().to(DEV))
+    assert_close(out, ref, 1e-5, 1e-4, "linear fwd")
+    for k, (a, b) in enumerate(zip(got_g, ref_g)):
+        assert_close(a, b, 1e-5, 1e-4 * (float(b.abs().max()) + 1), f"linear grad {k}")
+
+
+@pytest.mark.parametrize("shape", [(1000, 8, 64, 1), (777, 64, 2176, 0), (500, 64, 1, 0), (300, 256, 64, 1)])
+def test_dense(shape):
+    ops = _ops()
+    n, k, m, act = shape
+    torch.manual_seed(7)
+    x64 = torch.randn(n, k, dtype=torch.float64, requires_grad=True)
+    w64 = torch.randn(m, k, dtype=torch.float64, requires_grad=True)
+    b64 = torch.randn(m, dtype=torch.float64, requires_grad=True)
+    ref = O.dense(x64, w64, b64)
+    if act:
+        ref = O.silu(ref)
+    g = torch.randn_like(ref)
+    ref_g = torch.autograd.grad(ref, [x64, w64, b64], g)
+    x, w, b = [t.detach().float().to(DEV).requires_grad_(True) for t in (x64, w64, b64)]
+    out, _ = ops.dense_fwd(x, w, b, float(k) ** -0.5, act)
+    got = torch.autograd.grad(out, [x, w, b], g.float().to(DEV))
+    assert_close(out, ref, 1e-5, 1e-4, "dense fwd")
+    for i, (a, r) in enumerate(zip(got, ref_g)):
+        assert_close(a, r, 1e-5, 1e-4 * (float(r.abs().max()) + 1), f"dense grad {i}")
+
+
+def test_edge_geometry_positions_grad():
+    ops = _ops()
+    from flashcart_amd import _lib
+    from flashcart_amd.o3._graph import build_graph
+    torch.manual_seed(11)
+    n = 64
+    pos64 = (torch.rand(n, 3) * 8.0).double().requires_grad_(True)
+    ei = random_csr_graph(n, (3, 7, 12), seed=2)
+    E = ei.shape[1]
+    shift = torch.randint(-1, 2, (E, 3)).double() * 8.0
+    v = pos64[ei[1]] - pos64[ei[0]] + shift
+    d = v.norm(dim=-1)
+    r = v / d.clamp_min(O.MIN_EDGE_LENGTH).unsqueeze(-1)
+    attrs = O.irreps(r, 3)
+    feats = O.chebyshev(d, 8, 5.0, 0.0, "cosine")
+    env = O.cutoff(d, 5.0, 6)
+    ga, gf, ge = torch.randn_like(attrs), torch.randn_like(feats), torch.randn_like(env)
+    loss = (attrs * ga).sum() + (feats * gf).sum() + (env * ge).sum()
+    (ref_gpos,) = torch.autograd.grad(loss, pos64)
+    pos = pos64.detach().float().to(DEV).requires_grad_(True)
+    g = build_graph(ei.to(DEV), n)
+    a2, f2, e2 = ops.edge_geometry(pos, shift.float().to(DEV), g.idx_i, g.idx_j, None, g.rowptr, g.sender_perm,
+                                   g.sender_ptr, 3, _lib.BASIS_CHEBYSHEV_COSINE, 8, 0.0, 5.0, 6)
+    assert_close(a2, attrs, 1e-5, 1e-5, "edge attrs")
+    assert_close(f2, feats, 1e-5, 5e-5, "edge feats")
+    assert_close(e2, env, 1e-5, 1e-6, "edge env")
+    loss2 = (a2 * ga.float().to(DEV)).sum() + (f2 * gf.float().to(DEV)).sum() + (e2 * ge.float().to(DEV)).sum()
+    (gpos,) = torch.autograd.grad(loss2, pos)
+    assert_close(gpos, ref_gpos, 1e-4, 1e-4 * (float(ref_gpos.abs().max()) + 1), "edge grad positions")
+
+
+def test_segment_sum():
+    ops = _ops()
+    torch.manual_seed(3)
+    counts = torch.tensor([0, 5, 1, 17, 0, 3])
+    ptr = torch.cat([torch.zeros(1, dtype=torch.long), counts.cumsum(0)])
+    index = torch.repeat_interleave(torch.arange(len(counts)), counts)
+    src = torch.randn(int(counts.sum()), dtype=torch.float64)
+    ref = O.scatter_sum(src, index, len(counts))
+    out = ops.segment_sum(src.float().to(DEV), ptr.to(DEV), index.to(DEV))
+    assert_close(out, ref, 1e-6, 1e-6, "segment sum")
