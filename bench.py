@@ -1,0 +1,244 @@
+"""Benchmark: FlashCart energy+forces inference on one MI355X.
+
+Workload (the metric's config): periodic fcc random alloy,
+25x25x10 conventional cells (25,000 atoms, a = 3.6 A, 4 species, jitter 0.05 A),
+FlashCartPotential with the packaged default architecture at 128 channels, L_max = 3,
+2 interactions, r_max = 5 A, random-init weights (seed 1234), float32. Each step is one
+MD-style evaluation (energy + forces via autograd) after a fresh N(0, 0.01^2) A
+perturbation of the positions. Neighbour lists for every step are built before the
+timed region (host cell list at r_max + skin, filtered to r_max per step, rebuilt when an
+atom moved more than skin / 2), as in the reference's timing protocol; the receiver
+CSR of each step's graph is built on the GPU inside the timed region.
+
+Prints one JSON line: atom-steps/s, the roofline of the dominant kernel (measured
+live with HIP events on the stream it is launched on), and the CPU baseline (the
+oracle restatement of the reference PyTorch path on a bounded 256-atom sample).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+# Edge counts change from step to step, so the multi-GB per-edge tensors change size every
+# step; rounding allocations to 1/8 power-of-two steps lets the caching allocator reuse its
+# blocks instead of reserving new ones until it has to flush (set before torch allocates).
+os.environ.setdefault("PYTORCH_HIP_ALLOC_CONF", "roundup_power2_divisions:8")
+
+import torch  # noqa: E402
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+R_MAX = 5.0
+SIGMA_STEP = 0.01
+SKIN = 1.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def make_system(nx=25, ny=25, nz=10, seed=0):
+    from flashcart_amd.data.synthetic import fcc_alloy
+    return fcc_alloy(nx, ny, nz, a=3.6, jitter=0.05, seed=seed)
+
+
+class StepGraphs:
+    """Per-step graphs with exact r_max connectivity from a skin list (host side)."""
+
+    def __init__(self, numbers, pos, cell, pbc, elements, n_steps, seed=1):
+        from flashcart_amd.data.neighbors import neighbor_pairs
+        from flashcart_amd.data.graph import numbers_to_types
+        self.types = torch.as_tensor(numbers_to_types(numbers, elements))
+        self.numbers = numbers
+        self.cell = cell
+        self.pbc = pbc
+        rng = np.random.default_rng(seed)
+        self.graphs = []
+        ref_pos, skin_list = None, None
+        cur = pos.copy()
+        n_rebuild = 0
+        for k in range(n_steps):
+            cur = cur + rng.normal(0.0, SIGMA_STEP, size=cur.shape)
+            if ref_pos is None or np.max(np.linalg.norm(cur - ref_pos, axis=1)) >= SKIN / 2:
+                ref_pos = cur.copy()
+                skin_list = neighbor_pairs(cur, cell, pbc, R_MAX + SKIN)
+                n_rebuild += 1
+            ei, sh = skin_list
+            v = cur[ei[1]] - cur[ei[0]] + sh @ cell
+            keep = np.einsum("ij,ij->i", v, v) < R_MAX * R_MAX
+            self.graphs.append((cur.astype(np.float64), ei[:, keep].copy(), sh[keep].copy()))
+        self.n_rebuild = n_rebuild
+
+    def graph(self, k, device):
+        from flashcart_amd.data.graph import AtomicGraph
+        pos, ei, sh = self.graphs[k]
+        n = pos.shape[0]
+        return AtomicGraph(
+            positions=torch.as_tensor(pos, dtype=torch.float32, device=device),
+            cell=torch.as_tensor(self.cell, dtype=torch.float32, device=device).unsqueeze(0),
+            pbc=torch.as_tensor(self.pbc, device=device).unsqueeze(0),
+            shifts=torch.as_tensor(sh, dtype=torch.long, device=device),
+            edge_index=torch.as_tensor(ei, dtype=torch.long, device=device),
+            atom_types=self.types.to(device), atomic_numbers=torch.as_tensor(self.numbers, device=device),
+            n_atoms=torch.tensor([n], dtype=torch.long, device=device), use_shifts=True)
+
+
+def build_model(avg_neighbors, channels=128, l_max=3):
+    from flashcart_amd.data.synthetic import model_config
+    from flashcart_amd.model import FlashCartPotential
+    cfg = model_config(["Cu", "Ni", "Fe", "Cr"], channels, l_max, r_max=R_MAX, avg_neighbors=avg_neighbors)
+    torch.manual_seed(1234)
+    model = FlashCartPotential.from_config(cfg)
+    for p in model.parameters():
+        p.requires_grad_(False)
+    return model, cfg
+
+
+def tp_conv_bytes(n_nodes, n_send, E, d1, d2, P, C, nout):
+    """Compulsory HBM bytes of one convolution TP forward launch (fp32, int32 indices)."""
+    return 4 * (n_send * d1 * C + E * d2 + E * P * C + n_nodes * nout * C) + 4 * E + 4 * (n_nodes + 1)
+
+
+def measure_dominant(model, graph, dev, reps=10):
+    """Average duration of the layer-1 TP convolution forward (the largest HBM-bound kernel),
+    timed with HIP events on the stream the op launches on (torch's current stream)."""
+    from flashcart_amd.o3 import _ops
+    from flashcart_amd.o3._graph import build_graph
+    inter = model.interactions[1]
+    tp = inter.tp
+    n = graph.num_nodes
+    csr = build_graph(graph.edge_index, n)
+    E = csr.n_edges
+    g = torch.Generator(device=dev).manual_seed(0)
+    in1 = torch.randn(n, tp.in1_dim, device=dev, generator=g)
+    in2 = torch.randn(E, tp.in2_dim, device=dev, generator=g)
+    w = torch.randn(E, tp.n_total_paths * tp.in1_features, device=dev, generator=g)
+    args = (in1, in2, w, csr.idx_i, csr.idx_j, tp.in1_l_max, tp.in2_l_max, tp.out_l_max, tp.in1_features,
+            tp.in2_features, False, False, False, csr.rowptr, csr.sender_perm, csr.sender_ptr, 1.0)
+    for _ in range(2):
+        _ops.tp_fwd(*args)
+    stream = torch.cuda.current_stream(dev)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(dev)
+    ev0.record(stream)
+    for _ in range(reps):
+        _ops.tp_fwd(*args)
+    ev1.record(stream)
+    torch.cuda.synchronize(dev)
+    ms = ev0.elapsed_time(ev1) / reps
+    nout = tp.out_dim // tp.in1_features
+    byts = tp_conv_bytes(n, n, E, (tp.in1_l_max + 1) ** 2, (tp.in2_l_max + 1) ** 2, tp.n_total_paths,
+                         tp.in1_features, nout)
+    return ms, byts
+
+
+def cpu_baseline(model, cfg, avg_neighbors, budget_s=20.0):
+    """Oracle (CPU PyTorch restatement of the reference path), float32, on a 256-atom sample."""
+    from flashcart_amd.data.graph import AtomicGraph
+    from oracle import model as OM
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    numbers, pos, cell, pbc = make_system(4, 4, 4, seed=5)
+    g = AtomicGraph.from_arrays(numbers, pos, cfg["elements"], R_MAX, cell=cell, pbc=pbc)
+    sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+    mcfg = model.to_model_config()
+    gd = g.to_dict()
+    OM.predict(sd, mcfg, gd, dtype=torch.float32)  # warmup
+    t0 = time.perf_counter()
+    calls = 0
+    while calls < 3 or (time.perf_counter() - t0 < budget_s and calls < 50):
+        OM.predict(sd, mcfg, gd, dtype=torch.float32)
+        calls += 1
+    dt = time.perf_counter() - t0
+    n = len(numbers)
+    return {"value": n * calls / dt, "unit": "atom-steps/s", "cores": cores, "kind": "port",
+            "sample": f"oracle (CPU PyTorch restatement of the reference path), float32, fcc 4x4x4 = {n} atoms, "
+                      f"{int(g.edge_index.shape[1])} edges, same model config and weights, {calls} calls after "
+                      f"1 warmup, {dt:.1f} s, torch threads = {cores}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cells", type=int, nargs=3, default=[25, 25, 10])
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; multi-GPU runs are not part of it "
+                                   "(see DESIGN.md for how the path would shard)", "n_gpus": args.gpus}))
+        sys.exit(2)
+    from flashcart_amd import _lib
+    _lib.load()
+    dev = torch.device("cuda", 0)
+    numbers, pos, cell, pbc = make_system(*args.cells)
+    n_steps = args.warmup + args.steps
+    log(f"building {n_steps} step graphs for {len(numbers)} atoms")
+    t0 = time.time()
+    sg = StepGraphs(numbers, pos, cell, pbc, ["Cu", "Ni", "Fe", "Cr"], n_steps)
+    n_edges = [g[1].shape[1] for g in sg.graphs]
+    avg_nbr = float(np.mean(n_edges)) / len(numbers)
+    log(f"graphs ready in {time.time() - t0:.1f}s: mean E = {np.mean(n_edges):.0f} ({avg_nbr:.2f}/atom), "
+        f"{sg.n_rebuild} skin-list builds")
+    model, cfg = build_model(avg_nbr)
+    model = model.to(dev)
+    graphs = [sg.graph(k, dev) for k in range(n_steps)]
+    torch.cuda.synchronize(dev)
+    log("warmup")
+    for k in range(args.warmup):
+        out = model.predict(graphs[k], compute_forces=True)
+    torch.cuda.synchronize(dev)
+    log("timed steps")
+    t0 = time.perf_counter()
+    for k in range(args.warmup, n_steps):
+        out = model.predict(graphs[k], compute_forces=True)
+    torch.cuda.synchronize(dev)
+    dt = time.perf_counter() - t0
+    n_atoms = len(numbers)
+    e = float(out["energy"][0])
+    fmax = float(out["forces"].abs().max())
+    if not (np.isfinite(e) and np.isfinite(fmax)):
+        raise RuntimeError("non-finite energy or forces")
+    log(f"{args.steps} steps in {dt:.3f}s ({1e3 * dt / args.steps:.3f} ms/step); E={e:.6f} |F|max={fmax:.4f}")
+    ms, byts = measure_dominant(model, graphs[-1], dev)
+    gbs = byts / (ms * 1e-3) / 1e9
+    log(f"dominant kernel tp_fwd conv (layer 1): {ms:.3f} ms/launch, {byts / 1e9:.3f} GB algorithmic, {gbs:.1f} GB/s")
+    result = {
+        "metric": "atom-steps/s (energy+forces) at 25k atoms L_max=3",
+        "value": n_atoms * args.steps / dt,
+        "unit": "atom-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": 1e3 * dt / args.steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded fcc random alloy, random-init weights)",
+        "config": {"workload": "fcc_alloy_25k_L3_C128_energy_forces", "n_atoms": n_atoms,
+                   "mean_edges": float(np.mean(n_edges)), "channels": 128, "l_max_edge_attrs": 3,
+                   "l_max_hidden_feats": 2, "n_interactions": 2, "r_max": R_MAX, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": "tp_fwd_kernel<2,3,3> (conv, layer 1)", "achieved": gbs,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": None,
+                     "algorithmic_bytes": byts, "avg_launch_ms": ms},
+        "energy": e,
+    }
+    if not args.no_cpu_baseline:
+        log("cpu baseline")
+        result["cpu_baseline"] = cpu_baseline(model.cpu(), cfg, avg_nbr)
+        result["speedup_vs_cpu"] = result["value"] / result["cpu_baseline"]["value"]
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -16,8 +16,16 @@ def uses_periodic_shifts(pbc: object) -> bool:
 
 
 def shift_vectors(cell: torch.Tensor, shifts: torch.Tensor, idx_i: torch.Tensor, batch: torch.Tensor) -> torch.Tensor:
-    """Cartesian periodic translation S . cell[batch[i]] of every edge (reference ``geometry.py:52``)."""
-    return (shifts.to(cell.dtype).unsqueeze(-2) @ cell[batch[idx_i]]).squeeze(-2)
+    """Cartesian periodic translation S . cell[batch[i]] of every edge (reference ``geometry.py:52``).
+
+    One structure: a single (E,3) x (3,3) product; several: per-edge sums of the three
+    scaled lattice vectors (a per-edge batched 1x3 @ 3x3 product is far slower).
+    """
+    s = shifts.to(cell.dtype)
+    if cell.shape[0] == 1:
+        return s @ cell[0]
+    c = cell[batch[idx_i]]
+    return s[:, 0:1] * c[:, 0] + s[:, 1:2] * c[:, 1] + s[:, 2:3] * c[:, 2]
 
 
 def get_edge_vectors(positions, cell, shifts, edge_index, batch, use_shifts: bool = True) -> torch.Tensor:

@@ -1,0 +1,177 @@
+"""Host-side logic, the C ABI surface and the code generator (no GPU needed)."""
+
+import ctypes
+import itertools
+import re
+from fractions import Fraction
+from pathlib import Path
+
+import numpy as np
+import pytest
+import sympy as sp
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared_symbols():
+    text = (ROOT / "include" / "flashcart_hip.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fc_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from flashcart_amd import _lib
+    lib = _lib.load()
+    declared = _declared_symbols()
+    assert len(declared) >= 20
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in include/flashcart_hip.h but not exported"
+    assert set(declared) == set(_lib.EXPORTED_SYMBOLS)
+    assert lib.fc_kernel_l_max() == 3 and lib.fc_version() >= 100
+
+
+def test_abi_metadata_calls_without_gpu():
+    from flashcart_amd import _lib
+    lib = _lib.load()
+    d = _lib.tp_desc(2, 3, 3, 128, 1, False, False, False)
+    assert lib.fc_tp_num_paths(d) == 17
+    assert lib.fc_tp_out_dim(d) == 71 * 128
+    bad = _lib.tp_desc(4, 3, 3, 128, 1, False, False, False)
+    assert lib.fc_tp_num_paths(bad) == -2  # FC_ERR_UNSUPPORTED_L
+    assert lib.fc_status_string(6) == b"workspace missing or too small"
+
+
+def test_path_order_matches_layout_contract():
+    from flashcart_amd.codegen.cartesian import enumerate_paths
+    got = [f"{a}{b}{c}{'s' if s else 'f'}" for a, b, c, s in enumerate_paths(2, 3, 3, False)]
+    want = ["000f", "110f", "220f", "101f", "211f", "101s", "211s", "321s", "112f", "202f", "222f", "202s",
+            "312s", "213f", "213s", "303s", "323s"]
+    assert got == want
+
+
+def test_path_counts():
+    from flashcart_amd.o3.utils import count_output_paths
+    assert count_output_paths(0, 3, 3) == ([1, 1, 1, 1], 4)
+    assert count_output_paths(3, 3, 3)[1] == 23
+    assert count_output_paths(3, 3, 0, symmetric_product=True) == ([4], 4)
+    assert count_output_paths(2, 2, 2) == ([3, 4, 4], 11)
+
+
+def test_codegen_coefficients_match_oracle():
+    from flashcart_amd.codegen.emit_hip import ordered_triples, triple_coefficients
+    from oracle.cartesian import path_tensor
+    for r1, r2, lo in ordered_triples(3):
+        B = np.zeros((2 * lo + 1, 2 * r1 + 1, 2 * r2 + 1))
+        for (a, b, c), v in triple_coefficients(r1, r2, lo).items():
+            B[a, b, c] = float(v)
+        ref = path_tensor(r1, r2, lo) if r1 >= r2 else np.transpose(path_tensor(r2, r1, lo), (0, 2, 1))
+        assert np.abs(B - ref).max() < 1e-13, (r1, r2, lo)
+
+
+def test_codegen_expansion_matches_oracle():
+    from flashcart_amd.codegen.cartesian import X, Y, Z, expansion_polynomials
+    from oracle.ops import irreps
+    r = torch.randn(7, 3, dtype=torch.float64)
+    o = irreps(r, 3)
+    col = 0
+    for l in range(4):
+        for p in expansion_polynomials(l):
+            f = sp.lambdify((X, Y, Z), p, "numpy")
+            v = np.broadcast_to(f(*[r[:, k].numpy() for k in range(3)]), (7,))
+            assert np.allclose(v, o[:, col].numpy(), atol=1e-13)
+            col += 1
+
+
+def test_generated_header_is_current_and_literals_round_once():
+    from flashcart_amd.codegen.emit_hip import emit_tp_header, flit
+    hdr = (ROOT / "flashcart_amd" / "csrc" / "generated" / "fc_tp_paths.h").read_text()
+    assert hdr == emit_tp_header()
+    for frac in [Fraction(2, 3), Fraction(5, 9), Fraction(-3, 7), Fraction(1, 1)]:
+        lit = flit(frac)
+        assert np.float32(float(lit[:-1])) == np.float32(float(frac))
+
+
+def test_neighbor_list_matches_brute_force():
+    from flashcart_amd.data.neighbors import neighbor_pairs
+    from flashcart_amd.data.synthetic import fcc_alloy
+    from oracle.neighbors import brute_force_pairs
+    rng = np.random.default_rng(0)
+    z, p, cell, pbc = fcc_alloy(2, 2, 2, seed=1)
+    tri = np.array([[7.0, 0.0, 0.0], [2.1, 6.5, 0.0], [-1.3, 0.7, 7.4]])
+    cases = [(p, cell, pbc, 5.0), (rng.uniform(0, 6, (20, 3)) @ np.linalg.inv(np.eye(3) * 6) @ tri, tri,
+                                   np.array([True, True, True]), 4.0),
+             (rng.uniform(0, 5, (15, 3)), np.zeros((3, 3)), np.array([False] * 3), 3.0),
+             (rng.uniform(0, 5, (15, 3)), np.eye(3) * 5.0, np.array([True, False, True]), 3.5)]
+    for pos, c, pb, rc in cases:
+        ei, sh = neighbor_pairs(pos, c, pb, rc)
+        got = [(int(a), int(b)) + tuple(int(s) for s in S) for a, b, S in zip(ei[0], ei[1], sh)]
+        want = brute_force_pairs(pos, c if abs(np.linalg.det(c)) > 1e-7 else np.eye(3), pb, rc)
+        assert got == want
+        assert np.all(np.diff(ei[0]) >= 0)
+
+
+def test_neighbor_count_known_answers():
+    """Average neighbour counts 1, 2 and 2/3 (reference tests/data/test_data.py:96-108)."""
+    from flashcart_amd.data.neighbors import neighbor_pairs
+    h = 1.5 * np.sqrt(3) / 2
+    for pos, want in [([[0, 0, 0], [1.4, 0, 0]], 1.0), ([[0, 0, 0], [1.5, 0, 0], [0.75, h, 0]], 2.0),
+                      ([[0, 0, 0], [1.0, 0, 0], [50.0, 0, 0]], 2.0 / 3.0)]:
+        ei, _ = neighbor_pairs(np.array(pos, float), np.zeros((3, 3)), False, 5.0)
+        assert abs(ei.shape[1] / len(pos) - want) < 1e-12
+
+
+def test_periodic_self_images_exist():
+    from flashcart_amd.data.neighbors import neighbor_pairs
+    ei, sh = neighbor_pairs(np.zeros((1, 3)), np.eye(3) * 3.0, True, 3.5)
+    assert ei.shape[1] == 6 and np.all(ei == 0)  # six face images of a single atom
+
+
+REFERENCE_KEYS = [
+    "embedding.weight", "radial_basis.r_min", "radial_basis.r_max", "cutoff_fn.poly_order", "cutoff_fn.r_max",
+    "cutoff_fn.coeff1", "interactions.0.sqrt_avg_neighbors", "interactions.0.radial_mlp.0.weight",
+    "interactions.0.radial_mlp.2.weight", "interactions.0.radial_mlp.4.weight", "interactions.0.linear_first.weight.0",
+    "interactions.0.linear_second.weight.3", "interactions.0.skip_projection.weight",
+    "interactions.0.layer_norm.weights.3", "interactions.1.skip_projection.weight.2",
+    "products.0.skip_projection.weight.2", "products.0.layer_norm.weights.2", "products.0.product_linears.0.weight.3",
+    "products.0.product_linears.2.weight.2", "products.1.product_linears.2.weight.0",
+    "nonlinearities.0.value_linear.weight.3", "nonlinearities.0.gate_linear.weight",
+    "nonlinearities.0.gate_linear.bias", "nonlinearities.1.output_linear.weight.0", "readout.readout_mlp.0.weight",
+    "readout.readout_mlp.4.weight", "scale_shift.shifts", "scale_shift.scales",
+]
+
+
+def test_state_dict_names_and_shapes():
+    from flashcart_amd.data.synthetic import model_config
+    from flashcart_amd.model import FlashCartPotential
+    m = FlashCartPotential.from_config(model_config(["Cu", "Ni", "Fe", "Cr"], 16, 3, avg_neighbors=40.0))
+    sd = m.state_dict()
+    for k in REFERENCE_KEYS:
+        assert k in sd, k
+    assert tuple(sd["interactions.1.radial_mlp.4.weight"].shape) == (17 * 16, 64)
+    assert tuple(sd["interactions.1.linear_second.weight.3"].shape) == (16, 16 * 4)
+    assert tuple(sd["products.0.product_linears.1.weight.3"].shape) == (16, 16 * 6)
+    assert tuple(sd["readout.readout_mlp.0.weight"].shape) == (64, 32)
+    assert not any("dummy_tp_weights" in k or "l_weights" in k for k in sd)
+    assert abs(float(sd["interactions.0.sqrt_avg_neighbors"]) - 40.0 ** 0.5) < 1e-6
+
+
+def test_ops_reject_cpu_tensors():
+    from flashcart_amd import o3
+    tp = o3.TensorProduct(1, 1, 1, 4, 4)
+    x = torch.randn(3, 16)
+    with pytest.raises(RuntimeError, match="ROCm"):
+        tp(x, x, torch.randn(3, tp.n_total_paths * 4))
+    with pytest.raises(RuntimeError, match="ROCm"):
+        o3.Irreps(2).forward_normalized(torch.tensor([[1.0, 0.0, 0.0]]))
+
+
+def test_checkpoint_round_trip(tmp_path):
+    from flashcart_amd.data.synthetic import model_config
+    from flashcart_amd.model import FlashCartPotential
+    m = FlashCartPotential.from_config(model_config(["H", "O"], 8, 2, avg_neighbors=12.0))
+    m.save_inference_checkpoint(tmp_path)
+    m2 = FlashCartPotential.from_checkpoint(tmp_path)
+    for (k, a), (k2, b) in zip(m.state_dict().items(), m2.state_dict().items()):
+        assert k == k2 and torch.equal(a, b)
+    assert m2.interactions[0]._sqrt_avg == m.interactions[0]._sqrt_avg

@@ -1,0 +1,91 @@
+"""Pin the oracle potential with the reference's model-level invariants (no GPU).
+
+Reference tests/model/test_flashcart.py:43-167: rotation/translation/permutation
+invariance of energies (and equivariance of forces), forces = -dE/dR (checked here by
+central finite differences), batched prediction == per-structure prediction.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from flashcart_amd.data import AtomicGraph, batch_graphs
+from flashcart_amd.data.synthetic import fcc_alloy, model_config, molecules
+from oracle import model as OM
+
+
+def _state(cfg, seed=0):
+    from flashcart_amd.model import FlashCartPotential
+    torch.manual_seed(seed)
+    m = FlashCartPotential.from_config(cfg)
+    g = torch.Generator().manual_seed(seed + 1)
+    with torch.no_grad():
+        for name, p in m.named_parameters():
+            if "output_linear" in name:
+                p.copy_(0.3 * torch.randn(p.shape, generator=g))
+    return m.state_dict(), m.to_model_config()
+
+
+def _mol_graph(z, p, elements):
+    return AtomicGraph.from_arrays(z, p, elements, 5.0, dtype=torch.float64)
+
+
+@pytest.fixture(scope="module")
+def mol_setup():
+    cfg = model_config(["H", "C", "N", "O"], 8, 3, avg_neighbors=8.0)
+    sd, mcfg = _state(cfg, 3)
+    z, p = molecules(1, 9, 9, seed=4)[0]
+    return sd, mcfg, z, p
+
+
+def test_rotation_translation_permutation(mol_setup):
+    sd, cfg, z, p = mol_setup
+    base = OM.predict(sd, cfg, _mol_graph(z, p, cfg["elements"]).to_dict())
+    q, _ = np.linalg.qr(np.random.default_rng(0).normal(size=(3, 3)))
+    rot = OM.predict(sd, cfg, _mol_graph(z, p @ q.T + np.array([1.0, -2.0, 0.5]), cfg["elements"]).to_dict())
+    assert torch.allclose(rot["energy"], base["energy"], rtol=1e-10, atol=1e-10)
+    assert torch.allclose(rot["forces"], base["forces"] @ torch.as_tensor(q.T), atol=1e-9)
+    perm = np.random.default_rng(1).permutation(len(z))
+    pe = OM.predict(sd, cfg, _mol_graph(z[perm], p[perm], cfg["elements"]).to_dict())
+    assert torch.allclose(pe["energy"], base["energy"], rtol=1e-10, atol=1e-10)
+    assert torch.allclose(pe["forces"], base["forces"][perm], atol=1e-9)
+
+
+def test_forces_are_energy_gradient(mol_setup):
+    sd, cfg, z, p = mol_setup
+    f = OM.predict(sd, cfg, _mol_graph(z, p, cfg["elements"]).to_dict())["forces"]
+    h = 1e-5
+    for atom, k in [(0, 0), (3, 1), (7, 2)]:
+        dp = np.zeros_like(p)
+        dp[atom, k] = h
+        ep = OM.predict(sd, cfg, _mol_graph(z, p + dp, cfg["elements"]).to_dict(), compute_forces=False)["energy"]
+        em = OM.predict(sd, cfg, _mol_graph(z, p - dp, cfg["elements"]).to_dict(), compute_forces=False)["energy"]
+        fd = -(ep - em) / (2 * h)
+        assert abs(float(fd) - float(f[atom, k])) < 1e-6 * max(1.0, abs(float(fd)))
+
+
+def test_batched_equals_single():
+    cfg = model_config(["H", "C", "N", "O"], 8, 2, avg_neighbors=8.0)
+    sd, mcfg = _state(cfg, 5)
+    mols = molecules(3, 4, 8, seed=6)
+    gs = [_mol_graph(z, p, cfg["elements"]) for z, p in mols]
+    b = OM.predict(sd, mcfg, batch_graphs(gs).to_dict())
+    off = 0
+    for k, g in enumerate(gs):
+        s = OM.predict(sd, mcfg, g.to_dict())
+        assert torch.allclose(b["energy"][k], s["energy"][0], atol=1e-10)
+        assert torch.allclose(b["forces"][off:off + g.num_nodes], s["forces"], atol=1e-10)
+        off += g.num_nodes
+
+
+def test_periodic_translation_invariance():
+    cfg = model_config(["Cu", "Ni", "Fe", "Cr"], 8, 3, avg_neighbors=42.0)
+    sd, mcfg = _state(cfg, 9)
+    z, p, cell, pbc = fcc_alloy(2, 2, 2, seed=2)
+    g0 = AtomicGraph.from_arrays(z, p, cfg["elements"], 5.0, cell=cell, pbc=pbc, dtype=torch.float64)
+    g1 = AtomicGraph.from_arrays(z, p + np.array([0.37, -1.1, 2.2]), cfg["elements"], 5.0, cell=cell, pbc=pbc,
+                                 dtype=torch.float64)
+    a, b = OM.predict(sd, mcfg, g0.to_dict()), OM.predict(sd, mcfg, g1.to_dict())
+    assert torch.allclose(a["energy"], b["energy"], rtol=1e-10)
+    assert torch.allclose(a["forces"], b["forces"], atol=1e-9)
+    assert abs(float(a["forces"].sum(0).abs().max())) < 1e-9  # periodic: net force vanishes
