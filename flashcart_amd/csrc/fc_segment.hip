@@ -14,19 +14,59 @@ __global__ void csr_from_sorted_kernel(int64_t n_edges, const int32_t* __restric
   for (int64_t n = lo; n <= hi && n <= n_nodes; ++n) rowptr[n] = (int32_t)e;
 }
 
-// dst[s, c] = sum over the segment, one thread per (segment, column).
-__global__ void segment_sum_kernel(int64_t n_seg, int64_t width, const float* __restrict__ src,
-                                   const int32_t* __restrict__ perm, const int32_t* __restrict__ ptr,
-                                   float* __restrict__ dst) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= n_seg * width) return;
-  const int64_t s = t / width, c = t % width;
-  float acc = 0.f;
-  for (int32_t k = ptr[s]; k < ptr[s + 1]; ++k) {
-    const int64_t r = perm ? (int64_t)perm[k] : (int64_t)k;
-    acc += src[r * width + c];
+// Wide rows (width >= 64): one workgroup per segment, threads over columns (float4 when
+// the rows are 16-byte aligned), rows of the segment summed in order.
+__global__ void __launch_bounds__(256) segment_rows_kernel(int64_t width, const float* __restrict__ src,
+                                                           const int32_t* __restrict__ perm,
+                                                           const int32_t* __restrict__ ptr, float* __restrict__ dst,
+                                                           int vec4) {
+  const int64_t s = blockIdx.x;
+  const int32_t k0 = ptr[s], k1 = ptr[s + 1];
+  if (vec4) {
+    const int64_t w4 = width >> 2;
+    for (int64_t c = threadIdx.x + (int64_t)blockIdx.y * blockDim.x; c < w4; c += (int64_t)gridDim.y * blockDim.x) {
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int32_t k = k0; k < k1; ++k) {
+        const int64_t r = perm ? (int64_t)perm[k] : (int64_t)k;
+        const float4 v = reinterpret_cast<const float4*>(src + r * width)[c];
+        acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+      }
+      reinterpret_cast<float4*>(dst + s * width)[c] = acc;
+    }
+  } else {
+    for (int64_t c = threadIdx.x + (int64_t)blockIdx.y * blockDim.x; c < width; c += (int64_t)gridDim.y * blockDim.x) {
+      float acc = 0.f;
+      for (int32_t k = k0; k < k1; ++k) {
+        const int64_t r = perm ? (int64_t)perm[k] : (int64_t)k;
+        acc += src[r * width + c];
+      }
+      dst[s * width + c] = acc;
+    }
   }
-  dst[t] = acc;
+}
+
+// Narrow rows (width < 64, e.g. per-graph energies): one workgroup per segment, threads
+// over rows, then a fixed-shape tree reduction (wave64 butterfly + LDS), per column.
+__global__ void __launch_bounds__(256) segment_narrow_kernel(int64_t width, const float* __restrict__ src,
+                                                             const int32_t* __restrict__ perm,
+                                                             const int32_t* __restrict__ ptr,
+                                                             float* __restrict__ dst) {
+  __shared__ float part[4];
+  const int64_t s = blockIdx.x;
+  const int32_t k0 = ptr[s], k1 = ptr[s + 1];
+  const int t = threadIdx.x;
+  for (int64_t c = 0; c < width; ++c) {
+    float acc = 0.f;
+    for (int32_t k = k0 + t; k < k1; k += blockDim.x) {
+      const int64_t r = perm ? (int64_t)perm[k] : (int64_t)k;
+      acc += src[r * width + c];
+    }
+    acc = wave_sum(acc);
+    if ((t & 63) == 0) part[t >> 6] = acc;
+    __syncthreads();
+    if (t == 0) dst[s * width + c] = (part[0] + part[1]) + (part[2] + part[3]);
+    __syncthreads();
+  }
 }
 
 // grad_pos[n] = sum_{sender segment} g[perm[k]] - sum_{receiver segment} g[k]
@@ -60,11 +100,17 @@ __global__ void fill_kernel(int64_t n, float v, float* __restrict__ dst) {
 
 int segment_sum(int64_t n_seg, int64_t width, const float* src, const int32_t* perm, const int32_t* ptr, float* dst,
                 hipStream_t s) {
-  const int64_t total = n_seg * width;
-  if (total == 0) return FC_OK;
-  const int bs = 256;
-  hipLaunchKernelGGL(segment_sum_kernel, dim3((unsigned)((total + bs - 1) / bs)), dim3(bs), 0, s, n_seg, width, src,
-                     perm, ptr, dst);
+  if (n_seg * width == 0) return FC_OK;
+  if (n_seg > 0x7fffffff) return FC_ERR_SHAPE;
+  if (width < 64) {
+    hipLaunchKernelGGL(segment_narrow_kernel, dim3((unsigned)n_seg), dim3(256), 0, s, width, src, perm, ptr, dst);
+  } else {
+    const int vec4 = (width % 4 == 0) && (((uintptr_t)src & 15) == 0) && (((uintptr_t)dst & 15) == 0);
+    const int64_t cols = vec4 ? width / 4 : width;
+    const unsigned gy = (unsigned)((cols + 255) / 256);
+    hipLaunchKernelGGL(segment_rows_kernel, dim3((unsigned)n_seg, gy), dim3(256), 0, s, width, src, perm, ptr, dst,
+                       vec4);
+  }
   FC_LAUNCH_CHECK();
   return FC_OK;
 }

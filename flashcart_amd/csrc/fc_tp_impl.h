@@ -5,11 +5,14 @@
 //                  over a receiver-sorted CSR (rowptr), as in the reference's
 //                  tp_fwd_csr_kernel (src/flashcart/o3/_codegen_tensor_product.py:3245-3311);
 //   CONV = false : independent rows (reference tp_fwd_kernel, :2062-2140).
-// Work decomposition (gfx950, wave64): one workgroup per output row (node), one
-// lane per feature channel; per-path accumulators live in VGPRs and every output
-// element is stored exactly once, so the aggregation needs no atomics. The
-// per-edge coupling matrix A_p[a][b] = sum_c B_p[a,b,c] y_c depends only on the
-// edge when in2 has one channel; it is formed once per edge per lane.
+// Work decomposition (gfx950, wave64): one workgroup per output row (node), one lane
+// per feature channel; per-path accumulators live in VGPRs and every output element
+// is stored exactly once, so the aggregation needs no atomics. The edge loop is
+// uniform across the workgroup: with a single in2 channel (BC2, the interaction
+// layers) the edge attributes are wave-uniform scalar loads, and the per-edge
+// coupling matrices A_p[a][b] = sum_c B_p[a,b,c] y_c are formed once per edge. The
+// operands of the next edge are prefetched into registers while the current edge
+// is contracted, so the HBM latency of the gathered rows is hidden at 2-3 waves/SIMD.
 #pragma once
 #include "fc_common.h"
 #include "generated/fc_tp_paths.h"
@@ -30,7 +33,7 @@ struct TPArgs {
   int64_t n_rows;
   int32_t F1, F2, C;       // in1 / in2 / output features (1 broadcasts)
   int32_t shared_w, reduced;
-  float alpha;             // fwd output scale
+  float alpha;             // output scale (fwd) / its transpose (bwd)
 };
 
 template <int L1, int L2, int LO, bool SYM>
@@ -43,7 +46,33 @@ struct TPConfig {
   static constexpr int NOUT_RED = PL::NOUT_RED;
 };
 
-template <int L1, int L2, int LO, bool SYM, bool CONV>
+// Operands of one edge (or row) for one lane.
+template <int D1, int D2, int NP>
+struct EdgeOps {
+  float x[D1], y[D2], w[NP];
+};
+
+template <int D1, int D2, int NP, bool CONV, bool BC2>
+__device__ __forceinline__ void load_edge(const TPArgs& g, int64_t e, int f1, int f2, int fw, bool active,
+                                          EdgeOps<D1, D2, NP>& o) {
+  const int64_t j = CONV ? (int64_t)g.idx_j[e] : e;
+  const int64_t s1 = (int64_t)D1 * g.F1;
+#pragma unroll
+  for (int u = 0; u < D1; ++u) o.x[u] = active ? g.in1[j * s1 + u * g.F1 + f1] : 0.f;
+  if constexpr (BC2) {
+#pragma unroll
+    for (int u = 0; u < D2; ++u) o.y[u] = g.in2[e * D2 + u];
+  } else {
+    const int64_t s2 = (int64_t)D2 * g.F2;
+#pragma unroll
+    for (int u = 0; u < D2; ++u) o.y[u] = active ? g.in2[e * s2 + u * g.F2 + f2] : 0.f;
+  }
+  const float* wr = g.shared_w ? g.w : g.w + e * (int64_t)NP * g.C;
+#pragma unroll
+  for (int i = 0; i < NP; ++i) o.w[i] = active ? wr[i * g.C + fw] : 0.f;
+}
+
+template <int L1, int L2, int LO, bool SYM, bool CONV, bool BC2>
 __global__ void __launch_bounds__(256) tp_fwd_kernel(TPArgs g) {
   using CF = TPConfig<L1, L2, LO, SYM>;
   using PL = typename CF::PL;
@@ -54,7 +83,6 @@ __global__ void __launch_bounds__(256) tp_fwd_kernel(TPArgs g) {
   if (f >= C) return;
   const int f1 = g.F1 == 1 ? 0 : f;
   const int f2 = g.F2 == 1 ? 0 : f;
-  const int64_t s1 = (int64_t)D1 * g.F1, s2 = (int64_t)D2 * g.F2, sw = (int64_t)NP * C;
 
   float acc[NOUT];
 #pragma unroll
@@ -62,24 +90,20 @@ __global__ void __launch_bounds__(256) tp_fwd_kernel(TPArgs g) {
 
   int64_t e0 = row, e1 = row + 1;
   if constexpr (CONV) { e0 = g.rowptr[row]; e1 = g.rowptr[row + 1]; }
+  EdgeOps<D1, D2, NP> cur, nxt;
+  if (e0 < e1) load_edge<D1, D2, NP, CONV, BC2>(g, e0, f1, f2, f, true, nxt);
   for (int64_t e = e0; e < e1; ++e) {
-    const int64_t j = CONV ? (int64_t)g.idx_j[e] : e;
-    float x[D1], y[D2];
-#pragma unroll
-    for (int u = 0; u < D1; ++u) x[u] = g.in1[j * s1 + u * g.F1 + f1];
-#pragma unroll
-    for (int u = 0; u < D2; ++u) y[u] = g.in2[e * s2 + u * g.F2 + f2];
-    const float* wr = g.shared_w ? g.w : g.w + e * sw;
+    cur = nxt;
+    if (e + 1 < e1) load_edge<D1, D2, NP, CONV, BC2>(g, e + 1, f1, f2, f, true, nxt);
     static_for<NP>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
       constexpr PathDesc P = PL::at(i);
       using T = TPPath<P.r1, P.r2, P.lo>;
       float A[T::NA], t[T::NO];
-      T::amat(y + P.r2 * P.r2, A);
-      T::apply(A, x + P.r1 * P.r1, t);
-      const float wv = wr[i * C + f];
+      T::amat(cur.y + P.r2 * P.r2, A);
+      T::apply(A, cur.x + P.r1 * P.r1, t);
 #pragma unroll
-      for (int a = 0; a < T::NO; ++a) acc[PL::out_index(i, a)] = fmaf(wv, t[a], acc[PL::out_index(i, a)]);
+      for (int a = 0; a < T::NO; ++a) acc[PL::out_index(i, a)] = fmaf(cur.w[i], t[a], acc[PL::out_index(i, a)]);
     });
   }
   if (!g.reduced) {
@@ -103,22 +127,57 @@ __global__ void __launch_bounds__(256) tp_fwd_kernel(TPArgs g) {
   }
 }
 
+__host__ __device__ constexpr int log2_exact(int n) { return n <= 1 ? 0 : 1 + log2_exact(n >> 1); }
+
+__host__ __device__ constexpr int pow2_at_least(int n) {
+  int p = 1;
+  while (p < n) p <<= 1;
+  return p;
+}
+
+// Sum N per-lane values (N a power of two <= 64) over the 64 lanes of a wave with a
+// halving butterfly: every exchange step keeps half of the values (N-1 + 6-log2 N
+// shuffles instead of 6 N). Afterwards every lane of group lane >> (6 - log2 N) == v
+// holds the total of value v.
+template <int N>
+__device__ __forceinline__ float wave_reduce_halving(float (&v)[N], int lane) {
+  constexpr int LOGN = log2_exact(N);
+  static_assert((1 << LOGN) == N, "N must be a power of two");
+  static_for<LOGN>([&](auto sc) {
+    constexpr int s = decltype(sc)::value;
+    constexpr int half = N >> (s + 1);
+    const int o = 32 >> s;
+    const bool lower = (lane & o) == 0;
+#pragma unroll
+    for (int j = 0; j < half; ++j) {
+      const float mine = lower ? v[j] : v[j + half];
+      const float send = lower ? v[j + half] : v[j];
+      v[j] = mine + __shfl_xor(send, o, 64);
+    }
+  });
+  float r = v[0];
+#pragma unroll
+  for (int o = 32 >> LOGN; o > 0; o >>= 1) r += __shfl_xor(r, o, 64);
+  return r;
+}
+
 // Backward (vector-Jacobian product) of tp_fwd_kernel.
 //   grad_w[item, p, f]  = sum_a go[a,p,f] t_p[a]            (t = A_p x)
 //   u_p[a]              = w[p,f] go[a,p,f]
 //   gx[b]              += sum_a A_p[a,b] u_p[a]              (conv: per-edge message)
 //   gy[c]              += sum_{a,b} B_p[a,b,c] u_p[a] x[b]
-// Channel-broadcast operands (F == 1) get their gradient summed over channels:
-// wave64 reduction, then a cross-wave sum through LDS in a fixed order, so the
-// result is deterministic.
+// Channel-broadcast operands (F == 1) get their gradient summed over channels: a
+// halving butterfly in each wave, then a cross-wave sum through LDS in a fixed
+// order, so the result is deterministic.
 constexpr int BWD_CHUNK = 16;
-constexpr int BWD_MAXW = 16;
 
-template <int L1, int L2, int LO, bool SYM, bool CONV>
+template <int L1, int L2, int LO, bool SYM, bool CONV, bool BC2>
 __global__ void __launch_bounds__(256) tp_bwd_kernel(TPArgs g) {
   using CF = TPConfig<L1, L2, LO, SYM>;
   using PL = typename CF::PL;
   constexpr int D1 = CF::D1, D2 = CF::D2, NOUT = CF::NOUT, NP = CF::NP;
+  constexpr int R1 = pow2_at_least(D1), R2 = pow2_at_least(D2);
+  constexpr int SH1 = 6 - log2_exact(R1), SH2 = 6 - log2_exact(R2);
   extern __shared__ float red_lds[];  // [BWD_CHUNK][waves][D1 + D2], only when reducing over channels
 
   const int64_t row = blockIdx.x;
@@ -129,19 +188,21 @@ __global__ void __launch_bounds__(256) tp_bwd_kernel(TPArgs g) {
   const int f1 = g.F1 == 1 ? 0 : fa;
   const int f2 = g.F2 == 1 ? 0 : fa;
   const int wave = f >> 6, lane = f & 63, nw = blockDim.x >> 6;
-  const int64_t s1 = (int64_t)D1 * g.F1, s2 = (int64_t)D2 * g.F2, sw = (int64_t)NP * C;
+  const int64_t s1 = (int64_t)D1 * g.F1, sw = (int64_t)NP * C;
   const bool need1 = g.grad_in1 != nullptr, need2 = g.grad_in2 != nullptr, needw = g.grad_w != nullptr;
   const bool red1 = need1 && g.F1 == 1 && C > 1, red2 = need2 && g.F2 == 1 && C > 1;
 
   float go[NOUT];
   if (!g.reduced) {
 #pragma unroll
-    for (int k = 0; k < NOUT; ++k) go[k] = active ? g.alpha * g.grad_out[row * (int64_t)NOUT * C + (int64_t)k * C + fa] : 0.f;
+    for (int k = 0; k < NOUT; ++k)
+      go[k] = active ? g.alpha * g.grad_out[row * (int64_t)NOUT * C + (int64_t)k * C + fa] : 0.f;
   } else {
     constexpr int NR = CF::NOUT_RED;
     float gr[NR];
 #pragma unroll
-    for (int k = 0; k < NR; ++k) gr[k] = active ? g.alpha * g.grad_out[row * (int64_t)NR * C + (int64_t)k * C + fa] : 0.f;
+    for (int k = 0; k < NR; ++k)
+      gr[k] = active ? g.alpha * g.grad_out[row * (int64_t)NR * C + (int64_t)k * C + fa] : 0.f;
     static_for<NP>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
       constexpr PathDesc P = PL::at(i);
@@ -152,43 +213,42 @@ __global__ void __launch_bounds__(256) tp_bwd_kernel(TPArgs g) {
 
   int64_t e0 = row, e1 = row + 1;
   if constexpr (CONV) { e0 = g.rowptr[row]; e1 = g.rowptr[row + 1]; }
+  EdgeOps<D1, D2, NP> cur, nxt;
+  if (e0 < e1) load_edge<D1, D2, NP, CONV, BC2>(g, e0, f1, f2, fa, active, nxt);
   for (int64_t c0 = e0; c0 < e1; c0 += BWD_CHUNK) {
     const int64_t c1 = c0 + BWD_CHUNK < e1 ? c0 + BWD_CHUNK : e1;
     for (int64_t e = c0; e < c1; ++e) {
-      const int64_t j = CONV ? (int64_t)g.idx_j[e] : e;
-      float x[D1], y[D2], gx[D1], gy[D2];
+      cur = nxt;
+      if (e + 1 < e1) load_edge<D1, D2, NP, CONV, BC2>(g, e + 1, f1, f2, fa, active, nxt);
+      float gx[R1], gy[R2];
 #pragma unroll
-      for (int u = 0; u < D1; ++u) { x[u] = active ? g.in1[j * s1 + u * g.F1 + f1] : 0.f; gx[u] = 0.f; }
+      for (int u = 0; u < R1; ++u) gx[u] = 0.f;
 #pragma unroll
-      for (int u = 0; u < D2; ++u) { y[u] = active ? g.in2[e * s2 + u * g.F2 + f2] : 0.f; gy[u] = 0.f; }
-      const float* wr = g.shared_w ? g.w : g.w + e * sw;
+      for (int u = 0; u < R2; ++u) gy[u] = 0.f;
       static_for<NP>([&](auto ic) {
         constexpr int i = decltype(ic)::value;
         constexpr PathDesc P = PL::at(i);
         using T = TPPath<P.r1, P.r2, P.lo>;
         float A[T::NA], t[T::NO], u[T::NO];
-        T::amat(y + P.r2 * P.r2, A);
-        const float wv = active ? wr[i * C + fa] : 0.f;
+        T::amat(cur.y + P.r2 * P.r2, A);
         if (needw) {
-          T::apply(A, x + P.r1 * P.r1, t);
+          T::apply(A, cur.x + P.r1 * P.r1, t);
           float s = 0.f;
 #pragma unroll
           for (int a = 0; a < T::NO; ++a) s = fmaf(go[PL::out_index(i, a)], t[a], s);
           if (active) g.grad_w[e * sw + i * C + f] = s;
         }
 #pragma unroll
-        for (int a = 0; a < T::NO; ++a) u[a] = wv * go[PL::out_index(i, a)];
+        for (int a = 0; a < T::NO; ++a) u[a] = cur.w[i] * go[PL::out_index(i, a)];
         if (need1) T::apply_t(A, u, gx + P.r1 * P.r1);
-        if (need2) T::vjp2(u, x + P.r1 * P.r1, gy + P.r2 * P.r2);
+        if (need2) T::vjp2(u, cur.x + P.r1 * P.r1, gy + P.r2 * P.r2);
       });
       const int slot = (int)(e - c0);
       if (need1) {
         if (red1) {
-#pragma unroll
-          for (int u = 0; u < D1; ++u) {
-            const float s = wave_sum(gx[u]);
-            if (lane == 0) red_lds[(slot * nw + wave) * (D1 + D2) + u] = s;
-          }
+          const float s = wave_reduce_halving<R1>(gx, lane);
+          const int v = lane >> SH1;
+          if ((lane & ((1 << SH1) - 1)) == 0 && v < D1) red_lds[(slot * nw + wave) * (D1 + D2) + v] = s;
         } else if (active) {
 #pragma unroll
           for (int u = 0; u < D1; ++u) g.grad_in1[e * s1 + u * g.F1 + f] = gx[u];
@@ -196,12 +256,11 @@ __global__ void __launch_bounds__(256) tp_bwd_kernel(TPArgs g) {
       }
       if (need2) {
         if (red2) {
-#pragma unroll
-          for (int u = 0; u < D2; ++u) {
-            const float s = wave_sum(gy[u]);
-            if (lane == 0) red_lds[(slot * nw + wave) * (D1 + D2) + D1 + u] = s;
-          }
+          const float s = wave_reduce_halving<R2>(gy, lane);
+          const int v = lane >> SH2;
+          if ((lane & ((1 << SH2) - 1)) == 0 && v < D2) red_lds[(slot * nw + wave) * (D1 + D2) + D1 + v] = s;
         } else if (active) {
+          const int64_t s2 = (int64_t)D2 * g.F2;
 #pragma unroll
           for (int u = 0; u < D2; ++u) g.grad_in2[e * s2 + u * g.F2 + f] = gy[u];
         }
@@ -233,14 +292,23 @@ int launch_tp(const TPArgs& g, bool conv, bool bwd, hipStream_t stream) {
   const int threads = ((g.C + 63) / 64) * 64;
   if (threads > 256) return FC_ERR_SHAPE;
   dim3 grid((unsigned)g.n_rows), block(threads);
+  const bool bc2 = conv && g.F2 == 1;
   if (bwd) {
     const bool reduce = (g.grad_in1 && g.F1 == 1 && g.C > 1) || (g.grad_in2 && g.F2 == 1 && g.C > 1);
     const size_t lds = reduce ? sizeof(float) * BWD_CHUNK * (threads / 64) * (ncomp(L1) + ncomp(L2)) : 0;
-    if (conv) hipLaunchKernelGGL((tp_bwd_kernel<L1, L2, LO, SYM, true>), grid, block, lds, stream, g);
-    else hipLaunchKernelGGL((tp_bwd_kernel<L1, L2, LO, SYM, false>), grid, block, lds, stream, g);
+    if (conv) {
+      if (bc2) hipLaunchKernelGGL((tp_bwd_kernel<L1, L2, LO, SYM, true, true>), grid, block, lds, stream, g);
+      else hipLaunchKernelGGL((tp_bwd_kernel<L1, L2, LO, SYM, true, false>), grid, block, lds, stream, g);
+    } else {
+      hipLaunchKernelGGL((tp_bwd_kernel<L1, L2, LO, SYM, false, false>), grid, block, lds, stream, g);
+    }
   } else {
-    if (conv) hipLaunchKernelGGL((tp_fwd_kernel<L1, L2, LO, SYM, true>), grid, block, 0, stream, g);
-    else hipLaunchKernelGGL((tp_fwd_kernel<L1, L2, LO, SYM, false>), grid, block, 0, stream, g);
+    if (conv) {
+      if (bc2) hipLaunchKernelGGL((tp_fwd_kernel<L1, L2, LO, SYM, true, true>), grid, block, 0, stream, g);
+      else hipLaunchKernelGGL((tp_fwd_kernel<L1, L2, LO, SYM, true, false>), grid, block, 0, stream, g);
+    } else {
+      hipLaunchKernelGGL((tp_fwd_kernel<L1, L2, LO, SYM, false, false>), grid, block, 0, stream, g);
+    }
   }
   FC_LAUNCH_CHECK();
   return FC_OK;
