@@ -57,6 +57,7 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmBatch gb) {
   static_assert(A_LOADS >= 1 && B_LOADS >= 1, "tile too small for 256 threads");
   __shared__ float As[BK][BM + PADA];
   __shared__ float Bs[BK][BN + PADB];
+  __shared__ int64_t d_off[BM];  // output row offsets of this tile (-1 past the end)
 
   // XCD-aware remap: hardware block b runs on XCD b % 8; give each XCD a contiguous tile range.
   const int nb = gridDim.x;
@@ -75,6 +76,15 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmBatch gb) {
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int wm = wave / WN, wn = wave % WN;
+  for (int m = t; m < BM; m += 256) {
+    const int row = r0 + m;
+    int64_t off = -1;
+    if (row < g.M) {
+      const int n = row / g.comps, c = row - n * g.comps;
+      off = (int64_t)n * g.d_row + (int64_t)c * g.d_comp;
+    }
+    d_off[m] = off;
+  }
 
   // ---- global-load mapping (float4 along K for A; along K or N for B)
   // A: BM rows x BK cols, row-major K; thread loads A_LOADS float4s.
@@ -213,21 +223,25 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmBatch gb) {
   }
 
   // ---- epilogue: D[row][col] with row = 8*(v/4) + 4*(lane/32) + v%4, col = lane%32 per 32x32 block
+  float bias_v[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int col = c0 + wn * TN + j * 32 + (lane & 31);
+    bias_v[j] = (gb.bias && col < g.N) ? gb.bias[col] : 0.f;
+  }
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const int row = r0 + wm * TM + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-      if (row >= g.M) continue;
-      const int n = row / g.comps, c = row - n * g.comps;
-      float* drow = g.D + (int64_t)n * g.d_row + (int64_t)c * g.d_comp;
-      float* prow = g.pre ? g.pre + (int64_t)n * g.d_row + (int64_t)c * g.d_comp : nullptr;
+      const int64_t off = d_off[wm * TM + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)];
+      if (off < 0) continue;
+      float* drow = g.D + off;
+      float* prow = g.pre ? g.pre + off : nullptr;
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         const int col = c0 + wn * TN + j * 32 + (lane & 31);
         if (col >= g.N) continue;
-        float val = acc[i][j][v] * g.scale;
-        if (gb.bias) val += gb.bias[col];
+        float val = fmaf(acc[i][j][v], g.scale, bias_v[j]);
         if (prow) prow[col] = val;
         if (gb.act == 1) val = kSiluScale * val * sigmoidf_(val);
         drow[col] = val;

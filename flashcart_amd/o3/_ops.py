@@ -512,6 +512,16 @@ linear_fwd_op.register_autograd(_linear_backward, setup_context=_linear_setup)
 # Dense layer with optional rescaled-SiLU epilogue (radial / readout MLPs)
 # ---------------------------------------------------------------------------
 
+LIBRARY_GEMM_MIN_FLOP = 2e10
+
+
+def _use_library_gemm(n: int, k: int, m: int, act: int, bias) -> bool:
+    """Large plain GEMMs (the radial MLP output layer) go to the vendor GEMM; layers with a
+    fused activation or bias epilogue stay on the library's MFMA kernel."""
+    return act == 0 and bias is None and 2.0 * n * k * m >= LIBRARY_GEMM_MIN_FLOP and \
+        not torch.backends.cuda.matmul.allow_tf32
+
+
 @torch.library.custom_op("flashcart::dense_fwd", mutates_args=())
 def dense_fwd(x: Tensor, weight: Tensor, bias: Optional[Tensor], scale: float, act: int) -> Tuple[Tensor, Tensor]:
     """(activated output, pre-activation (empty when act == 0))."""
@@ -523,6 +533,11 @@ def dense_fwd(x: Tensor, weight: Tensor, bias: Optional[Tensor], scale: float, a
         raise RuntimeError(f"Incorrect last dimension for x. Expected {k}, got {x.shape[-1]}.")
     lead = x.shape[:-1]
     x2 = x.reshape(-1, k)
+    if _use_library_gemm(x2.shape[0], k, m, act, b):
+        # Plain GEMM (no activation, no bias): hipBLASLt, with the weight pre-scaled as the
+        # reference's F.linear(x, W * s) does. fp32 inputs, IEEE fp32 products.
+        out = torch.mm(x2, (w * scale).t())
+        return out.reshape(*lead, m), x.new_empty(0)
     out = x.new_empty(x2.shape[0], m)
     pre = x.new_empty(x2.shape[0], m) if act else x.new_empty(0)
     _lib_call("fc_dense_fwd", x2.shape[0], k, m, x2.data_ptr(), w.data_ptr(), float(scale), _lib.ptr(b), int(act),
@@ -543,6 +558,8 @@ def dense_bwd(grad_out: Tensor, pre: Tensor, weight: Tensor, scale: float, act: 
     m, k = w.shape
     lead = go.shape[:-1]
     go2 = go.reshape(-1, m)
+    if _use_library_gemm(go2.shape[0], k, m, act, None):
+        return torch.mm(go2, w * scale).reshape(*lead, k)
     pr = _lib.contig("pre", pre).reshape(-1, m) if act else None
     gx = go.new_empty(go2.shape[0], k)
     _lib_call("fc_dense_dgrad", go2.shape[0], k, m, go2.data_ptr(), _lib.ptr(pr), w.data_ptr(), float(scale),
