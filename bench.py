@@ -36,6 +36,10 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch of the dominant kernel from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of
+# `bench.py --kernel-only` (first step graph, E = 1,080,166), each counter scaled by its reading for
+# a 2 GiB elementwise copy (FETCH x2.000, WRITE x1.000); see profiles/tp_conv_fwd_l1_fcc25k_hbm_traffic.md.
+MEASURED_TRAFFIC_BYTES = 11.77e9
 R_MAX = 5.0
 SIGMA_STEP = 0.01
 SKIN = 1.0
@@ -172,6 +176,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cells", type=int, nargs=3, default=[25, 25, 10])
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="only launch the dominant kernel (5x) and a 2 GiB device copy (5x), for counter runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU runs are not part of it "
@@ -181,6 +187,19 @@ def main():
     _lib.load()
     dev = torch.device("cuda", 0)
     numbers, pos, cell, pbc = make_system(*args.cells)
+    if args.kernel_only:
+        sg = StepGraphs(numbers, pos, cell, pbc, ["Cu", "Ni", "Fe", "Cr"], 1)
+        model, _ = build_model(43.0)
+        g = sg.graph(0, dev)
+        ms, byts = measure_dominant(model.to(dev), g, dev, reps=5)
+        src = torch.ones(2 ** 29, device=dev)  # 2 GiB
+        dst = torch.empty_like(src)
+        for _ in range(5):  # a plain elementwise copy kernel (reads and writes 2 GiB) for counter calibration
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize(dev)
+        print(json.dumps({"kernel_only": True, "avg_launch_ms": ms, "algorithmic_bytes": byts,
+                          "copy_bytes_each_way": src.numel() * 4}), flush=True)
+        return
     n_steps = args.warmup + args.steps
     log(f"building {n_steps} step graphs for {len(numbers)} atoms")
     t0 = time.time()
@@ -229,7 +248,8 @@ def main():
                    "mean_edges": float(np.mean(n_edges)), "channels": 128, "l_max_edge_attrs": 3,
                    "l_max_hidden_feats": 2, "n_interactions": 2, "r_max": R_MAX, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": "tp_fwd_kernel<2,3,3> (conv, layer 1)", "achieved": gbs,
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": None,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
+                     "traffic": MEASURED_TRAFFIC_BYTES, "traffic_launch": "bench.py --kernel-only (E=1080166)",
                      "algorithmic_bytes": byts, "avg_launch_ms": ms},
         "energy": e,
     }

@@ -101,6 +101,18 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 __host__ __device__ constexpr int ncomp(int l_max) { return (l_max + 1) * (l_max + 1); }
 
+// XCD-aware row order: the hardware deals workgroup b to XCD b % 8, so consecutive rows
+// would land in 8 different L2s. Giving each XCD a contiguous row range keeps rows that
+// share gathered operands (neighbouring receivers share senders) in one L2. The grid
+// must be xcd_grid(n) blocks; rows >= n are padding and exit.
+__host__ __device__ inline int64_t xcd_grid(int64_t n) { return n >= 64 ? (n + 7) / 8 * 8 : n; }
+__device__ __forceinline__ int64_t xcd_row(int64_t n) {
+  const int64_t b = blockIdx.x;
+  if (n < 64) return b;
+  const int64_t per = (n + 7) / 8;
+  return (b % 8) * per + b / 8;
+}
+
 // Wave64 sum reduction (result valid in every lane).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

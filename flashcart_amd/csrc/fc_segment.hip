@@ -19,8 +19,9 @@ __global__ void csr_from_sorted_kernel(int64_t n_edges, const int32_t* __restric
 __global__ void __launch_bounds__(256) segment_rows_kernel(int64_t width, const float* __restrict__ src,
                                                            const int32_t* __restrict__ perm,
                                                            const int32_t* __restrict__ ptr, float* __restrict__ dst,
-                                                           int vec4) {
-  const int64_t s = blockIdx.x;
+                                                           int vec4, int64_t n_seg) {
+  const int64_t s = xcd_row(n_seg);
+  if (s >= n_seg) return;
   const int32_t k0 = ptr[s], k1 = ptr[s + 1];
   if (vec4) {
     const int64_t w4 = width >> 2;
@@ -108,8 +109,8 @@ int segment_sum(int64_t n_seg, int64_t width, const float* src, const int32_t* p
     const int vec4 = (width % 4 == 0) && (((uintptr_t)src & 15) == 0) && (((uintptr_t)dst & 15) == 0);
     const int64_t cols = vec4 ? width / 4 : width;
     const unsigned gy = (unsigned)((cols + 255) / 256);
-    hipLaunchKernelGGL(segment_rows_kernel, dim3((unsigned)n_seg, gy), dim3(256), 0, s, width, src, perm, ptr, dst,
-                       vec4);
+    hipLaunchKernelGGL(segment_rows_kernel, dim3((unsigned)xcd_grid(n_seg), gy), dim3(256), 0, s, width, src, perm,
+                       ptr, dst, vec4, n_seg);
   }
   FC_LAUNCH_CHECK();
   return FC_OK;

@@ -77,10 +77,10 @@ __global__ void __launch_bounds__(256) tp_fwd_kernel(TPArgs g) {
   using CF = TPConfig<L1, L2, LO, SYM>;
   using PL = typename CF::PL;
   constexpr int D1 = CF::D1, D2 = CF::D2, NOUT = CF::NOUT, NP = CF::NP;
-  const int64_t row = blockIdx.x;
+  const int64_t row = CONV ? xcd_row(g.n_rows) : (int64_t)blockIdx.x;
   const int f = threadIdx.x;
   const int C = g.C;
-  if (f >= C) return;
+  if (f >= C || row >= g.n_rows) return;
   const int f1 = g.F1 == 1 ? 0 : f;
   const int f2 = g.F2 == 1 ? 0 : f;
 
@@ -180,7 +180,8 @@ __global__ void __launch_bounds__(256) tp_bwd_kernel(TPArgs g) {
   constexpr int SH1 = 6 - log2_exact(R1), SH2 = 6 - log2_exact(R2);
   extern __shared__ float red_lds[];  // [BWD_CHUNK][waves][D1 + D2], only when reducing over channels
 
-  const int64_t row = blockIdx.x;
+  const int64_t row = CONV ? xcd_row(g.n_rows) : (int64_t)blockIdx.x;
+  if (row >= g.n_rows) return;
   const int f = threadIdx.x;
   const int C = g.C;
   const bool active = f < C;
@@ -291,7 +292,7 @@ int launch_tp(const TPArgs& g, bool conv, bool bwd, hipStream_t stream) {
   if (g.n_rows == 0) return FC_OK;
   const int threads = ((g.C + 63) / 64) * 64;
   if (threads > 256) return FC_ERR_SHAPE;
-  dim3 grid((unsigned)g.n_rows), block(threads);
+  dim3 grid((unsigned)(conv ? xcd_grid(g.n_rows) : g.n_rows)), block(threads);
   const bool bc2 = conv && g.F2 == 1;
   if (bwd) {
     const bool reduce = (g.grad_in1 && g.F1 == 1 && g.C > 1) || (g.grad_in2 && g.F2 == 1 && g.C > 1);
