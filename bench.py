@@ -126,7 +126,7 @@ def measure_dominant(model, graph, dev, reps=10):
     in2 = torch.randn(E, tp.in2_dim, device=dev, generator=g)
     w = torch.randn(E, tp.n_total_paths * tp.in1_features, device=dev, generator=g)
     args = (in1, in2, w, csr.idx_i, csr.idx_j, tp.in1_l_max, tp.in2_l_max, tp.out_l_max, tp.in1_features,
-            tp.in2_features, False, False, False, csr.rowptr, csr.sender_perm, csr.sender_ptr, 1.0)
+            tp.in2_features, False, False, *tp.op_meta, False, csr.rowptr, csr.sender_perm, csr.sender_ptr, 1.0)
     for _ in range(2):
         _ops.tp_fwd(*args)
     stream = torch.cuda.current_stream(dev)

@@ -29,6 +29,7 @@ from flashcart_amd.nn.radial import ChebyshevBasis, PolynomialCutoff
 from flashcart_amd.o3 import _ops
 from flashcart_amd.o3._graph import GraphCSR, build_graph
 from flashcart_amd.utils.geometry import shift_vectors, uses_periodic_shifts
+from flashcart_amd.utils.lammps import lammps_exchange_features
 
 MIN_EDGE_LENGTH = 1.0e-4
 
@@ -130,11 +131,9 @@ class FlashCartPotential(AtomisticModel):
         if is_lammps:
             nlocal, ntotal = batch.shape[0], atom_types.shape[0]
             local_types = atom_types[:nlocal]
-            exchange = graph.get("exchange_fn")
         else:
             nlocal = ntotal = None
             local_types = atom_types
-            exchange = None
         csr = self.graph_csr(graph)
         basis = self.radial_basis.basis_kind
         geo = (self.l_max_edge_attrs, basis, self.n_radial, float(self.r_min), self.r_max, self.cutoff_poly_order)
@@ -155,9 +154,8 @@ class FlashCartPotential(AtomisticModel):
         for k, interaction in enumerate(self.interactions):
             msg = node_feats
             if is_lammps and k > 0:
-                if exchange is None:
-                    raise ValueError("LAMMPS graphs need an `exchange_fn` to fill ghost-atom features.")
-                msg = exchange(node_feats, nlocal, ntotal)
+                # owned features (nlocal, C) -> (ntotal, C) with ghost rows from their owners
+                msg = lammps_exchange_features(node_feats, nlocal, ntotal)
             feats = interaction(msg, edge_attrs, edge_feats, edge_index, envelope,
                                 atom_types=atom_types if not self.element_agnostic_interaction else None,
                                 out_nodes=nlocal, graph=csr)

@@ -44,6 +44,43 @@ def _tp_out_dim(in1_l_max, in2_l_max, out_l_max, in1_features, in2_features, sym
     return sum((2 * l + 1) * (min(n, 1) if reduced else n) * c for l, n in enumerate(counts))
 
 
+_META_LEN = 4  # ranks 0..3 compiled into the library
+
+
+def tp_meta(in1_l_max: int, in2_l_max: int, out_l_max: int, in1_features: int, in2_features: int,
+            symmetric_product: bool, reduce_paths: bool):
+    """Layout lists of the reference's ``tp_fwd`` schema for the standard feature layout.
+
+    Returns ``(in1_offs, in2_offs, out_sizes, n_paths_per_l, n_total_paths)``, each list
+    padded with zeros to one entry per compiled rank, as the reference builds them
+    (src/flashcart/o3/_tensor_product.py:51-72,1158-1164).
+    """
+    counts, total = count_output_paths(in1_l_max, in2_l_max, out_l_max, symmetric_product)
+    c = max(in1_features, in2_features)
+
+    def offs(l_max, f):
+        return [l * l * f if l <= l_max else 0 for l in range(_META_LEN)]
+
+    n_paths = [int(counts[l]) if l < len(counts) else 0 for l in range(_META_LEN)]
+    sizes = [((2 * l + 1) * c if n > 0 else 0) if reduce_paths else n * (2 * l + 1) * c
+             for l, n in enumerate(n_paths)]
+    return offs(in1_l_max, in1_features), offs(in2_l_max, in2_features), sizes, n_paths, int(total)
+
+
+def _check_tp_meta(cfg, in1_offs, in2_offs, out_sizes, n_paths_per_l, n_total_paths) -> None:
+    """The kernels implement the standard contiguous layout only; reject any other."""
+    want = tp_meta(*cfg)
+    got = (list(in1_offs), list(in2_offs), list(out_sizes), list(n_paths_per_l), int(n_total_paths))
+    names = ("in1_offs", "in2_offs", "out_sizes", "n_paths_per_l", "n_total_paths")
+    for name, g, w in zip(names, got, want):
+        if isinstance(w, list):
+            g = g + [0] * max(0, len(w) - len(g))
+            if g[:len(w)] != w or any(v != 0 for v in g[len(w):]):
+                raise ValueError(f"{name}={got[names.index(name)]} does not describe the standard layout {w}.")
+        elif g != w:
+            raise ValueError(f"{name}={g} does not match the configuration ({w}).")
+
+
 # ---------------------------------------------------------------------------
 # Eq. (1) expansion
 # ---------------------------------------------------------------------------
@@ -309,8 +346,15 @@ def _check_tp_inputs(in1, in2, weights, idx_i, idx_j, in1_l_max, in2_l_max, out_
 @torch.library.custom_op("flashcart::tp_fwd", mutates_args=())
 def tp_fwd(in1: Tensor, in2: Tensor, weights: Tensor, idx_i: Optional[Tensor], idx_j: Optional[Tensor],
            in1_l_max: int, in2_l_max: int, out_l_max: int, in1_features: int, in2_features: int,
-           symmetric_product: bool, shared_weights: bool, reduce_paths: bool, rowptr: Optional[Tensor] = None,
-           sender_perm: Optional[Tensor] = None, sender_ptr: Optional[Tensor] = None, alpha: float = 1.0) -> Tensor:
+           symmetric_product: bool, shared_weights: bool, in1_offs: List[int], in2_offs: List[int],
+           out_sizes: List[int], n_paths_per_l: List[int], n_total_paths: int, reduce_paths: bool = False,
+           rowptr: Optional[Tensor] = None, sender_perm: Optional[Tensor] = None,
+           sender_ptr: Optional[Tensor] = None, alpha: float = 1.0) -> Tensor:
+    """Reference schema (src/flashcart/o3/_tensor_product.py:332-352) plus optional CSR
+    arrays (``rowptr``, ``sender_perm``, ``sender_ptr``, see ``o3._graph``) and ``alpha``,
+    a scale applied to the output."""
+    _check_tp_meta((in1_l_max, in2_l_max, out_l_max, in1_features, in2_features, symmetric_product, reduce_paths),
+                   in1_offs, in2_offs, out_sizes, n_paths_per_l, n_total_paths)
     conv = _check_tp_inputs(in1, in2, weights, idx_i, idx_j, in1_l_max, in2_l_max, out_l_max, in1_features,
                             in2_features, symmetric_product, shared_weights)
     in1 = _lib.contig("in1", in1)
@@ -330,7 +374,8 @@ def tp_fwd(in1: Tensor, in2: Tensor, weights: Tensor, idx_i: Optional[Tensor], i
 
 @tp_fwd.register_fake
 def _(in1, in2, weights, idx_i, idx_j, in1_l_max, in2_l_max, out_l_max, in1_features, in2_features,
-      symmetric_product, shared_weights, reduce_paths, rowptr=None, sender_perm=None, sender_ptr=None, alpha=1.0):
+      symmetric_product, shared_weights, in1_offs, in2_offs, out_sizes, n_paths_per_l, n_total_paths,
+      reduce_paths=False, rowptr=None, sender_perm=None, sender_ptr=None, alpha=1.0):
     return in1.new_empty(in1.shape[0], _tp_out_dim(in1_l_max, in2_l_max, out_l_max, in1_features, in2_features,
                                                    symmetric_product, reduce_paths))
 
@@ -338,11 +383,17 @@ def _(in1, in2, weights, idx_i, idx_j, in1_l_max, in2_l_max, out_l_max, in1_feat
 @torch.library.custom_op("flashcart::tp_bwd", mutates_args=())
 def tp_bwd(grad_out: Tensor, in1: Tensor, in2: Tensor, weights: Tensor, idx_i: Optional[Tensor],
            idx_j: Optional[Tensor], in1_l_max: int, in2_l_max: int, out_l_max: int, in1_features: int,
-           in2_features: int, symmetric_product: bool, shared_weights: bool, reduce_paths: bool,
-           need_grad_in1: bool, need_grad_in2: bool, need_grad_weights: bool, rowptr: Optional[Tensor] = None,
-           sender_perm: Optional[Tensor] = None, sender_ptr: Optional[Tensor] = None,
-           alpha: float = 1.0) -> Tuple[Tensor, Tensor, Tensor]:
-    """Gradients wrt (in1, in2, weights); unrequested ones are returned as empty (0,) tensors."""
+           in2_features: int, symmetric_product: bool, shared_weights: bool, in1_offs: List[int],
+           in2_offs: List[int], out_sizes: List[int], n_paths_per_l: List[int], n_total_paths: int,
+           reduce_paths: bool, need_grad_in1: bool, need_grad_in2: bool, need_grad_weights: bool,
+           rowptr: Optional[Tensor] = None, sender_perm: Optional[Tensor] = None,
+           sender_ptr: Optional[Tensor] = None, alpha: float = 1.0) -> Tuple[Tensor, Tensor, Tensor]:
+    """Gradients wrt (in1, in2, weights); unrequested ones are returned as empty (0,) tensors.
+
+    Reference schema (src/flashcart/o3/_tensor_product.py:588-611) plus the optional
+    CSR arrays and ``alpha`` of ``tp_fwd``."""
+    _check_tp_meta((in1_l_max, in2_l_max, out_l_max, in1_features, in2_features, symmetric_product, reduce_paths),
+                   in1_offs, in2_offs, out_sizes, n_paths_per_l, n_total_paths)
     conv = idx_i is not None and idx_j is not None
     go = _lib.contig("grad_out", grad_out)
     in1 = _lib.contig("in1", in1)
@@ -369,24 +420,27 @@ def tp_bwd(grad_out: Tensor, in1: Tensor, in2: Tensor, weights: Tensor, idx_i: O
 
 @tp_bwd.register_fake
 def _(grad_out, in1, in2, weights, idx_i, idx_j, in1_l_max, in2_l_max, out_l_max, in1_features, in2_features,
-      symmetric_product, shared_weights, reduce_paths, need_grad_in1, need_grad_in2, need_grad_weights,
-      rowptr=None, sender_perm=None, sender_ptr=None, alpha=1.0):
+      symmetric_product, shared_weights, in1_offs, in2_offs, out_sizes, n_paths_per_l, n_total_paths,
+      reduce_paths, need_grad_in1, need_grad_in2, need_grad_weights, rowptr=None, sender_perm=None,
+      sender_ptr=None, alpha=1.0):
     return (torch.empty_like(in1) if need_grad_in1 else in1.new_empty(0),
             torch.empty_like(in2) if need_grad_in2 else in2.new_empty(0),
             torch.empty_like(weights) if need_grad_weights else weights.new_empty(0))
 
 
 def _tp_setup(ctx, inputs, output):
-    (in1, in2, weights, idx_i, idx_j, l1, l2, lo, f1, f2, sym, shared, red, rowptr, sperm, sptr, alpha) = inputs
+    (in1, in2, weights, idx_i, idx_j, l1, l2, lo, f1, f2, sym, shared, o1, o2, osz, npl, ntot, red,
+     rowptr, sperm, sptr, alpha) = inputs
     ctx.save_for_backward(in1, in2, weights, idx_i, idx_j, rowptr, sperm, sptr)
-    ctx.cfg = (int(l1), int(l2), int(lo), int(f1), int(f2), bool(sym), bool(shared), bool(red))
+    ctx.cfg = (int(l1), int(l2), int(lo), int(f1), int(f2), bool(sym), bool(shared), list(o1), list(o2),
+               list(osz), list(npl), int(ntot), bool(red))
     ctx.alpha = float(alpha)
 
 
 def _tp_backward(ctx, grad):
     in1, in2, weights, idx_i, idx_j, rowptr, sperm, sptr = ctx.saved_tensors
     n1, n2, nw = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[2]
-    none_tail = (None,) * 14
+    none_tail = (None,) * 19
     if not (n1 or n2 or nw):
         return (None, None, None) + none_tail
     g1, g2, gw = tp_bwd(grad, in1, in2, weights, idx_i, idx_j, *ctx.cfg, bool(n1), bool(n2), bool(nw),

@@ -55,6 +55,9 @@ class TensorProduct(nn.Module):
         self.in2_slices = get_irreps_slices(in2_l_max, in2_features)
         self.out_paths, self.n_total_paths = count_output_paths(in1_l_max, in2_l_max, out_l_max,
                                                                 symmetric_product=symmetric_product)
+        # (in1_offs, in2_offs, out_sizes, n_paths_per_l, n_total_paths) of the op schema
+        self.op_meta = _ops.tp_meta(in1_l_max, in2_l_max, out_l_max, in1_features, in2_features,
+                                    symmetric_product, reduce_paths)
 
     @property
     def out_features(self) -> int:
@@ -82,7 +85,7 @@ class TensorProduct(nn.Module):
             raise ValueError("idx_i and idx_j must be given together.")
         return _ops.tp_fwd(in1, in2, weights, idx_i, idx_j, self.in1_l_max, self.in2_l_max, self.out_l_max,
                            self.in1_features, self.in2_features, self.symmetric_product, self.shared_weights,
-                           self.reduce_paths, rowptr, sender_perm, sender_ptr, float(alpha))
+                           *self.op_meta, self.reduce_paths, rowptr, sender_perm, sender_ptr, float(alpha))
 
     def __repr__(self) -> str:
         return (f"{self.__class__.__name__}({self.in1_l_max} x {self.in2_l_max} -> {self.out_l_max}, "

@@ -175,18 +175,37 @@ def node_energies(sd: Dict[str, torch.Tensor], cfg: Dict[str, Any], graph: Dict[
 
 
 def predict(sd: Dict[str, torch.Tensor], cfg: Dict[str, Any], graph: Dict[str, Any], compute_forces: bool = True,
-            dtype: torch.dtype = torch.float64) -> Dict[str, torch.Tensor]:
-    """Energies (per structure and per atom) and forces, all on CPU in ``dtype``."""
+            dtype: torch.dtype = torch.float64, compute_stress: bool = False) -> Dict[str, torch.Tensor]:
+    """Energies (per structure and per atom), forces and optionally stress, on CPU in ``dtype``.
+
+    Stress follows src/flashcart/model/atomistic.py:200-210,290-302: positions and cell
+    are multiplied by (I + sym(D)) for a zero displacement D, and
+    stress = dE/dD / det(cell) in Voigt order xx, yy, zz, yz, xz, xy.
+    """
     sd = {k: v.detach().to("cpu", dtype) if v.is_floating_point() else v.detach().cpu() for k, v in sd.items()}
     g = {k: (v.detach().cpu() if torch.is_tensor(v) else v) for k, v in graph.items()}
     pos = g["positions"].to(dtype).requires_grad_(compute_forces)
-    g["positions"] = pos
-    g["cell"] = g["cell"].to(dtype)
+    cell = g["cell"].to(dtype)
+    inputs = [pos] if compute_forces else []
+    if compute_stress:
+        disp = torch.zeros_like(cell).requires_grad_(True)
+        scaling = torch.eye(3, dtype=dtype) + 0.5 * (disp + disp.transpose(-1, -2))
+        g["positions"] = (pos.unsqueeze(-2) @ scaling[g["batch"]]).squeeze(-2)
+        g["cell"] = cell @ scaling
+        inputs.append(disp)
+    else:
+        g["positions"] = pos
+        g["cell"] = cell
     e_node = node_energies(sd, cfg, g)
     n_graphs = int(g["n_atoms"].shape[0])
     energy = O.scatter_sum(e_node, g["batch"], n_graphs)
     out = {"node_energies": e_node.detach(), "energy": energy.detach()}
-    if compute_forces:
-        (grad,) = torch.autograd.grad(energy.sum(), pos)
-        out["forces"] = -grad
+    if inputs:
+        grads = torch.autograd.grad(energy.sum(), inputs)
+        if compute_forces:
+            out["forces"] = -grads[0]
+        if compute_stress:
+            s = grads[-1] / torch.det(cell).view(-1, 1, 1)
+            out["stress"] = torch.stack([s[:, 0, 0], s[:, 1, 1], s[:, 2, 2], (s[:, 1, 2] + s[:, 2, 1]) / 2,
+                                         (s[:, 0, 2] + s[:, 2, 0]) / 2, (s[:, 0, 1] + s[:, 1, 0]) / 2], dim=-1)
     return out

@@ -89,8 +89,9 @@ def _tp_case(l1, l2, lo, f1, f2, sym=False, shared=False, reduced=False, conv=Tr
     ref_grads = torch.autograd.grad(ref, [a1, a2, aw] if not sym else [a1, aw], g)
     leaves = [t.detach().float().to(DEV).requires_grad_(True) for t in (in1, in2, w)]
     b1, b2, bw = leaves
+    meta = ops.tp_meta(l1, l2, lo, f1, f2, sym, reduced)
     out = ops.tp_fwd(b1, b1 if sym else b2, bw, ei[0].to(DEV) if conv else None, ei[1].to(DEV) if conv else None,
-                     l1, l2, lo, f1, f2, sym, shared, reduced)
+                     l1, l2, lo, f1, f2, sym, shared, *meta, reduced)
     grads = torch.autograd.grad(out, [b1, b2, bw] if not sym else [b1, bw], g.float().to(DEV))
     scale = float(ref.abs().max()) + 1.0
     assert_close(out, ref, 2e-5, 2e-5 * scale, "tp fwd")

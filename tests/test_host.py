@@ -166,6 +166,34 @@ def test_ops_reject_cpu_tensors():
         o3.Irreps(2).forward_normalized(torch.tensor([[1.0, 0.0, 0.0]]))
 
 
+def test_tp_op_schema_follows_reference():
+    """Positional schema of torch.ops.flashcart.tp_fwd/tp_bwd as registered by the reference
+    (src/flashcart/o3/_tensor_product.py:332-352,588-611), extra arguments only at the end."""
+    from flashcart_amd.o3 import _ops
+    ref_fwd = ["in1", "in2", "weights", "idx_i", "idx_j", "in1_l_max", "in2_l_max", "out_l_max", "in1_features",
+               "in2_features", "symmetric_product", "shared_weights", "in1_offs", "in2_offs", "out_sizes",
+               "n_paths_per_l", "n_total_paths", "reduce_paths"]
+    ref_bwd = ["grad_out"] + ref_fwd[:17] + ["reduce_paths", "need_grad_in1", "need_grad_in2", "need_grad_weights"]
+    for op, ref in ((torch.ops.flashcart.tp_fwd.default, ref_fwd), (torch.ops.flashcart.tp_bwd.default, ref_bwd)):
+        names = [a.name for a in op._schema.arguments]
+        assert names[:len(ref)] == ref
+        assert all(a.has_default_value() for a in op._schema.arguments[len(ref):])
+    # Layout lists, as the reference builds them for (2 x 3 -> 3, C=128, in2 single channel):
+    # _slice_offsets pads rank-block starts, _out_block_sizes = paths * (2l+1) * C.
+    in1_offs, in2_offs, sizes, n_paths, total = _ops.tp_meta(2, 3, 3, 128, 1, False, False)
+    assert in1_offs == [0, 128, 512, 0] and in2_offs == [0, 1, 4, 9]
+    assert n_paths == [3, 5, 5, 4] and total == 17
+    assert sizes == [3 * 128, 5 * 3 * 128, 5 * 5 * 128, 4 * 7 * 128]
+    assert _ops.tp_meta(2, 2, 2, 8, 8, True, True)[2] == [8, 24, 40, 0]
+    tp = __import__("flashcart_amd").o3.TensorProduct(1, 1, 1, 4, 4)
+    x = torch.randn(3, 16)
+    bad = list(tp.op_meta)
+    bad[0] = [0, 8, 0, 0]
+    with pytest.raises(ValueError, match="in1_offs"):
+        torch.ops.flashcart.tp_fwd(x, x, torch.randn(3, tp.n_total_paths * 4), None, None, 1, 1, 1, 4, 4, False,
+                                   False, *bad, False)
+
+
 def test_checkpoint_round_trip(tmp_path):
     from flashcart_amd.data.synthetic import model_config
     from flashcart_amd.model import FlashCartPotential

@@ -78,6 +78,29 @@ def test_batched_equals_single():
         off += g.num_nodes
 
 
+def test_stress_is_strain_derivative():
+    """Oracle stress (virtual strain) against central differences of E under a symmetric
+    strain of the positions and cell (reference tests/model/test_flashcart.py stress FD)."""
+    cfg = model_config(["Cu", "Ni", "Fe", "Cr"], 8, 2, avg_neighbors=42.0)
+    sd, mcfg = _state(cfg, 13)
+    z, p, cell, pbc = fcc_alloy(1, 1, 2, seed=8)
+    vol = abs(np.linalg.det(cell))
+
+    def energy(eps):
+        m = np.eye(3) + eps
+        g = AtomicGraph.from_arrays(z, p @ m, cfg["elements"], 5.0, cell=cell @ m, pbc=pbc, dtype=torch.float64)
+        return float(OM.predict(sd, mcfg, g.to_dict(), compute_forces=False)["energy"][0])
+
+    g = AtomicGraph.from_arrays(z, p, cfg["elements"], 5.0, cell=cell, pbc=pbc, dtype=torch.float64)
+    s = OM.predict(sd, mcfg, g.to_dict(), compute_stress=True)["stress"][0]
+    h = 1e-5
+    for k, (a, b) in enumerate([(0, 0), (1, 1), (2, 2), (1, 2), (0, 2), (0, 1)]):
+        e = np.zeros((3, 3))
+        e[a, b] = e[b, a] = h
+        fd = (energy(e) - energy(-e)) / (2 * h) / vol / (1 if a == b else 2)
+        assert abs(fd - float(s[k])) < 1e-7 * max(1.0, abs(fd)), (k, fd, float(s[k]))
+
+
 def test_periodic_translation_invariance():
     cfg = model_config(["Cu", "Ni", "Fe", "Cr"], 8, 3, avg_neighbors=42.0)
     sd, mcfg = _state(cfg, 9)
