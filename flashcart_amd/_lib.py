@@ -83,6 +83,8 @@ _SIGNATURES = {
     "fc_dense_fwd": (c_int, [c_i64, c_i32, c_i32, c_vp, c_vp, c_f32, c_vp, c_i32, c_vp, c_vp, c_vp]),
     "fc_dense_dgrad": (c_int, [c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_f32, c_i32, c_vp, c_vp]),
     "fc_segment_sum": (c_int, [c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "fc_rms_norm_fwd": (c_int, [c_i64, c_int, c_int, c_vp, c_vp, c_f32, c_vp, c_vp, c_vp]),
+    "fc_rms_norm_bwd": (c_int, [c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "fc_neighbor_list": (c_i64, [c_i64, c_vp, c_vp, c_vp, ctypes.c_double, c_i64, c_vp, c_vp, c_vp]),
 }
 

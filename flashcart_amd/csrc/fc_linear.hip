@@ -8,11 +8,21 @@
 //
 // Tiling (gfx950, wave64): 256-thread workgroups, BM x BN output tiles, waves arranged
 // WM x WN, each wave accumulating (BM/WM) x (BN/WN) with v_mfma_f32_32x32x2f32 blocks.
-// The K dimension is staged through LDS k-major (conflict-free operand reads) in BK
-// steps, with the next tile prefetched into registers during the MFMAs. Blocks are
-// ordered N-tile fastest and remapped so that consecutive tiles of one row block land
-// on the same XCD (the hardware deals workgroups round-robin over the 8 XCDs), so the
-// A rows are fetched from HBM once and then hit that XCD's L2.
+// K advances in steps of 32 through LDS (double-buffered for N > 64, one barrier per
+// step): the next step's global loads are in flight while the current step's 16 MFMA
+// k-pairs run. Full K steps load through one branch-free path (row pointers clamped
+// to valid rows and masked afterwards): per-lane divergence between vector and scalar
+// loads made the compiler wait on outstanding loads inside the load sequence.
+// A rows (and B rows when the weight is k-contiguous, the forward) sit in LDS in the
+// order the MFMA consumes them: k-step s takes k = 2s (lanes 0-31) and k = 2s+1
+// (lanes 32-63), so position (k % 2) * 16 + k / 2 puts each half-wave's 16 values of
+// the step sequence next to each other and a lane fetches four k-steps with one
+// 128-bit LDS read; the row pitch of 36 floats makes those reads conflict-free (row
+// stride 9 x 16 B). A column-contiguous weight (the input gradient) is stored k-major
+// with 128-bit writes instead and read one k-step at a time.
+// Blocks are ordered N-tile fastest and remapped so that consecutive tiles of one row
+// block land on the same XCD (the hardware deals workgroups round-robin over the 8
+// XCDs), so the A rows are fetched from HBM once and then hit that XCD's L2.
 // fp32 inputs, fp32 accumulation: no reduced-precision operands.
 #include "fc_common.h"
 
@@ -46,17 +56,24 @@ struct GemmBatch {
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
-template <int BM, int BN, int BK, int WM, int WN>
+constexpr int GEMM_BK = 32;
+constexpr int GEMM_PITCH = GEMM_BK + 4;
+
+// LDS position of k (0..31) inside an operand row.
+__device__ __forceinline__ constexpr int kpos(int k) { return (k & 1) * 16 + (k >> 1); }
+
+template <int BM, int BN, int WM, int WN, int NBUF, bool KB>
 __global__ void __launch_bounds__(256) gemm_kernel(GemmBatch gb) {
   static_assert(WM * WN == 4, "four waves");
+  constexpr int BK = GEMM_BK, LP = GEMM_PITCH;
   constexpr int TM = BM / WM, TN = BN / WN;  // per-wave tile
   constexpr int FM = TM / 32, FN = TN / 32;  // 32x32 MFMA blocks per wave
-  constexpr int PADA = 4, PADB = 4;
-  constexpr int A_LOADS = BM * BK / (256 * 4);  // float4 per thread
-  constexpr int B_LOADS = BN * BK / (256 * 4);
+  constexpr int A_LOADS = BM * BK / 1024;    // float4 per thread and K step
+  constexpr int B_LOADS = BN * BK / 1024;
   static_assert(A_LOADS >= 1 && B_LOADS >= 1, "tile too small for 256 threads");
-  __shared__ float As[BK][BM + PADA];
-  __shared__ float Bs[BK][BN + PADB];
+  __shared__ __attribute__((aligned(16))) float As[NBUF][BM * LP];
+  constexpr int BSZ = KB ? BK * (BN + 4) : BN * LP;
+  __shared__ __attribute__((aligned(16))) float Bs[NBUF][BSZ];
   __shared__ int64_t d_off[BM];  // output row offsets of this tile (-1 past the end)
 
   // XCD-aware remap: hardware block b runs on XCD b % 8; give each XCD a contiguous tile range.
@@ -86,106 +103,135 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmBatch gb) {
     d_off[m] = off;
   }
 
-  // ---- global-load mapping (float4 along K for A; along K or N for B)
-  // A: BM rows x BK cols, row-major K; thread loads A_LOADS float4s.
-  constexpr int A_TPR = BK / 4;  // threads per row
+  // ---- global loads: 8 threads per operand row, one float4 (4 consecutive k) each.
+  // Row pointers are clamped to valid rows and masked afterwards, so that full K steps
+  // take one branch-free path (no per-lane divergence between vector and scalar loads).
+  const int lk4 = (t & 7) * 4;  // k offset of this thread inside a K step
   const float* a_ptr[A_LOADS];
   const float* p_ptr[A_LOADS];
-  int a_k4[A_LOADS], a_m[A_LOADS];
+  bool a_ok[A_LOADS];
+  const bool use_p = gb.act_bwd && g.P;
 #pragma unroll
   for (int i = 0; i < A_LOADS; ++i) {
-    const int idx = t + i * 256;
-    a_m[i] = idx / A_TPR;
-    a_k4[i] = (idx % A_TPR) * 4;
-    const int row = r0 + a_m[i];
-    a_ptr[i] = nullptr;
-    p_ptr[i] = nullptr;
-    if (row < g.M) {
-      const int n = row / g.comps, c = row - n * g.comps;
-      a_ptr[i] = g.A + (int64_t)n * g.a_row + (int64_t)c * g.a_comp;
-      if (g.P) p_ptr[i] = g.P + (int64_t)n * g.a_row + (int64_t)c * g.a_comp;
-    }
+    const int row0 = r0 + (t >> 3) + 32 * i;
+    a_ok[i] = row0 < g.M;
+    const int row = a_ok[i] ? row0 : g.M - 1;
+    const int n = row / g.comps, c = row - n * g.comps;
+    a_ptr[i] = g.A + (int64_t)n * g.a_row + (int64_t)c * g.a_comp;
+    p_ptr[i] = use_p ? g.P + (int64_t)n * g.a_row + (int64_t)c * g.a_comp : nullptr;
   }
   const bool a_vec = ((g.K & 3) == 0) && ((g.a_row & 3) == 0) && ((g.a_comp & 3) == 0) &&
-                     (((uintptr_t)g.A & 15) == 0);
+                     (((uintptr_t)g.A & 15) == 0) && (!use_p || (((uintptr_t)g.P & 15) == 0));
+  const bool b_vec = gb.trans_b ? (((g.K & 3) == 0) && (((uintptr_t)g.B & 15) == 0))
+                                : (((g.N & 3) == 0) && (((uintptr_t)g.B & 15) == 0));
+  // B operand rows: trans_b -> output column c0 + (t>>3) + 32 i (k contiguous);
+  // otherwise k row k0 + t/(BN/4) + (1024/BN) i, 4 consecutive columns from bcol.
+  const float* b_ptr[B_LOADS];
+  bool b_ok[B_LOADS];
+  const int bcol = c0 + (t % (BN / 4)) * 4;
+#pragma unroll
+  for (int i = 0; i < B_LOADS; ++i) {
+    if (gb.trans_b) {
+      const int col0 = c0 + (t >> 3) + 32 * i;
+      b_ok[i] = col0 < g.N;
+      b_ptr[i] = g.B + (int64_t)(b_ok[i] ? col0 : g.N - 1) * g.K;
+    } else {
+      b_ok[i] = bcol + 3 < g.N;
+      b_ptr[i] = g.B + (b_ok[i] ? bcol : 0);
+    }
+  }
+
+  auto slow4 = [&](const float* p, int k, int kmax) -> float4 {
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (k < kmax) v.x = p[k];
+    if (k + 1 < kmax) v.y = p[k + 1];
+    if (k + 2 < kmax) v.z = p[k + 2];
+    if (k + 3 < kmax) v.w = p[k + 3];
+    return v;
+  };
+  const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
 
   float4 ra[A_LOADS], rb[B_LOADS];
-  auto load_a = [&](int k0) {
+  auto load_step = [&](int k0) {
+    const bool full = k0 + BK <= g.K;  // uniform
+    float4 pa[A_LOADS];
+    if (full && a_vec) {
+#pragma unroll
+      for (int i = 0; i < A_LOADS; ++i) ra[i] = *reinterpret_cast<const float4*>(a_ptr[i] + k0 + lk4);
+      if (use_p) {
+#pragma unroll
+        for (int i = 0; i < A_LOADS; ++i) pa[i] = *reinterpret_cast<const float4*>(p_ptr[i] + k0 + lk4);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < A_LOADS; ++i) {
+        ra[i] = slow4(a_ptr[i], k0 + lk4, g.K);
+        if (use_p) pa[i] = slow4(p_ptr[i], k0 + lk4, g.K);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i) {
-      const int k = k0 + a_k4[i];
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (a_ptr[i]) {
-        if (a_vec && k + 3 < g.K) {
-          v = *reinterpret_cast<const float4*>(a_ptr[i] + k);
+      if (use_p) {
+        const float pp[4] = {pa[i].x, pa[i].y, pa[i].z, pa[i].w};
+        float* vv = reinterpret_cast<float*>(&ra[i]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float s = sigmoidf_(pp[j]);
+          vv[j] *= kSiluScale * s * (1.0f + pp[j] * (1.0f - s));
+        }
+      }
+      if (!a_ok[i]) ra[i] = zero4;
+    }
+    if (gb.trans_b) {
+      if (full && b_vec) {
+#pragma unroll
+        for (int i = 0; i < B_LOADS; ++i) rb[i] = *reinterpret_cast<const float4*>(b_ptr[i] + k0 + lk4);
+      } else {
+#pragma unroll
+        for (int i = 0; i < B_LOADS; ++i) rb[i] = slow4(b_ptr[i], k0 + lk4, g.K);
+      }
+#pragma unroll
+      for (int i = 0; i < B_LOADS; ++i)
+        if (!b_ok[i]) rb[i] = zero4;
+    } else {
+#pragma unroll
+      for (int i = 0; i < B_LOADS; ++i) {
+        const int k = k0 + (t / (BN / 4)) + (1024 / BN) * i;
+        if (full && b_vec && b_ok[i]) {
+          rb[i] = *reinterpret_cast<const float4*>(b_ptr[i] + (int64_t)k * g.N);
         } else {
-          if (k < g.K) v.x = a_ptr[i][k];
-          if (k + 1 < g.K) v.y = a_ptr[i][k + 1];
-          if (k + 2 < g.K) v.z = a_ptr[i][k + 2];
-          if (k + 3 < g.K) v.w = a_ptr[i][k + 3];
-        }
-        if (gb.act_bwd && p_ptr[i]) {
-          float pv[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            if (k + j < g.K) pv[j] = p_ptr[i][k + j];
-          float* vv = reinterpret_cast<float*>(&v);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float s = sigmoidf_(pv[j]);
-            vv[j] *= kSiluScale * s * (1.0f + pv[j] * (1.0f - s));
-          }
+          rb[i] = k < g.K ? slow4(g.B + (int64_t)k * g.N, bcol, g.N) : zero4;
         }
       }
-      ra[i] = v;
     }
   };
-  // B: BK x BN tile. trans_b: W[col*K + k] (k contiguous); else W[k*N + col] (col contiguous).
-  auto load_b = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < B_LOADS; ++i) {
-      const int idx = t + i * 256;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      float* vv = reinterpret_cast<float*>(&v);
-      if (gb.trans_b) {
-        const int col = c0 + idx / (BK / 4), k = k0 + (idx % (BK / 4)) * 4;
-        if (col < g.N) {
-          const float* w = g.B + (int64_t)col * g.K;
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            if (k + j < g.K) vv[j] = w[k + j];
-        }
-      } else {
-        const int k = k0 + idx / (BN / 4), col = c0 + (idx % (BN / 4)) * 4;
-        if (k < g.K) {
-          const float* w = g.B + (int64_t)k * g.N;
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            if (col + j < g.N) vv[j] = w[col + j];
-        }
-      }
-      rb[i] = v;
-    }
-  };
-  auto store_tiles = [&]() {
+  auto store_step = [&](int buf) {
+    float* as = As[buf];
+    float* bs = Bs[buf];
+    const int p0 = kpos(lk4);  // lk4 even: (v.x, v.z) at p0, (v.y, v.w) at p0 + 16
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i) {
-      const float* vv = reinterpret_cast<const float*>(&ra[i]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) As[a_k4[i] + j][a_m[i]] = vv[j];
+      float* r = as + ((t >> 3) + 32 * i) * LP;
+      *reinterpret_cast<float2*>(r + p0) = make_float2(ra[i].x, ra[i].z);
+      *reinterpret_cast<float2*>(r + p0 + 16) = make_float2(ra[i].y, ra[i].w);
     }
 #pragma unroll
     for (int i = 0; i < B_LOADS; ++i) {
-      const int idx = t + i * 256;
-      const float* vv = reinterpret_cast<const float*>(&rb[i]);
       if (gb.trans_b) {
-        const int col = idx / (BK / 4), k = (idx % (BK / 4)) * 4;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) Bs[k + j][col] = vv[j];
+        float* r = bs + ((t >> 3) + 32 * i) * LP;
+        *reinterpret_cast<float2*>(r + p0) = make_float2(rb[i].x, rb[i].z);
+        *reinterpret_cast<float2*>(r + p0 + 16) = make_float2(rb[i].y, rb[i].w);
       } else {
-        const int k = idx / (BN / 4), col = (idx % (BN / 4)) * 4;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) Bs[k][col + j] = vv[j];
+        const int kk = (t / (BN / 4)) + (1024 / BN) * i, col = (t % (BN / 4)) * 4;
+        if constexpr (KB) {
+          *reinterpret_cast<float4*>(bs + kk * (BN + 4) + col) = rb[i];
+        } else {
+          const int p = kpos(kk);
+          bs[(col + 0) * LP + p] = rb[i].x;
+          bs[(col + 1) * LP + p] = rb[i].y;
+          bs[(col + 2) * LP + p] = rb[i].z;
+          bs[(col + 3) * LP + p] = rb[i].w;
+        }
       }
     }
   };
@@ -198,28 +244,44 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmBatch gb) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-  load_a(0);
-  load_b(0);
-  for (int k0 = 0; k0 < g.K; k0 += BK) {
-    __syncthreads();
-    store_tiles();
-    __syncthreads();
-    if (k0 + BK < g.K) {
-      load_a(k0 + BK);
-      load_b(k0 + BK);
+  const int half = (lane >> 5) * 16;
+  const int nk = (g.K + BK - 1) / BK;
+  load_step(0);
+  store_step(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = NBUF == 2 ? (kt & 1) : 0;
+    if (kt + 1 < nk) load_step((kt + 1) * BK);
+    const float* as = As[cur] + (wm * TM + (lane & 31)) * LP + half;
+    const float* bs = KB ? Bs[cur] + (lane >> 5) * (BN + 4) + wn * TN + (lane & 31)
+                         : Bs[cur] + (wn * TN + (lane & 31)) * LP + half;
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+      float4 a4[FM], b4[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) a4[i] = *reinterpret_cast<const float4*>(as + i * 32 * LP + s4 * 4);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        if constexpr (KB) {  // k-step s = 4 s4 + q reads row 2 s + lane/32
+          const float* p = bs + j * 32 + (8 * s4) * (BN + 4);
+          b4[j] = make_float4(p[0], p[2 * (BN + 4)], p[4 * (BN + 4)], p[6 * (BN + 4)]);
+        } else {
+          b4[j] = *reinterpret_cast<const float4*>(bs + j * 32 * LP + s4 * 4);
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(reinterpret_cast<const float*>(&a4[i])[q],
+                                                             reinterpret_cast<const float*>(&b4[j])[q], acc[i][j],
+                                                             0, 0, 0);
     }
-#pragma unroll
-    for (int kk = 0; kk < BK; kk += 2) {
-      float a[FM], bv[FN];
-#pragma unroll
-      for (int i = 0; i < FM; ++i) a[i] = As[kk + (lane >> 5)][wm * TM + i * 32 + (lane & 31)];
-#pragma unroll
-      for (int j = 0; j < FN; ++j) bv[j] = Bs[kk + (lane >> 5)][wn * TN + j * 32 + (lane & 31)];
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], bv[j], acc[i][j], 0, 0, 0);
-    }
+    if constexpr (NBUF == 1) __syncthreads();
+    if (kt + 1 < nk) store_step(NBUF == 2 ? cur ^ 1 : 0);
+    __syncthreads();
   }
 
   // ---- epilogue: D[row][col] with row = 8*(v/4) + 4*(lane/32) + v%4, col = lane%32 per 32x32 block
@@ -250,7 +312,7 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmBatch gb) {
   }
 }
 
-template <int BM, int BN, int BK, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int NBUF>
 int launch_gemm_cfg(GemmBatch gb, int n_ranks, hipStream_t s) {
   int64_t total = 0;
   for (int l = 0; l < n_ranks; ++l) {
@@ -265,7 +327,8 @@ int launch_gemm_cfg(GemmBatch gb, int n_ranks, hipStream_t s) {
   gb.n_ranks = n_ranks;
   gb.total_tiles = (int32_t)total;
   const int64_t grid = (total + 7) / 8 * 8;  // a multiple of 8 enables the XCD remap
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, WM, WN>), dim3((unsigned)grid), dim3(256), 0, s, gb);
+  if (gb.trans_b) hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, NBUF, false>), dim3((unsigned)grid), dim3(256), 0, s, gb);
+  else hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, NBUF, true>), dim3((unsigned)grid), dim3(256), 0, s, gb);
   FC_LAUNCH_CHECK();
   return FC_OK;
 }
@@ -279,8 +342,8 @@ int launch_gemm(GemmBatch gb, int n_ranks, hipStream_t s) {
     if (gb.r[l].M < 0) return FC_ERR_SHAPE;
   }
   if (max_m == 0 || max_n == 0 || n_ranks == 0) return FC_OK;
-  if (max_n <= 64) return launch_gemm_cfg<128, 64, 16, 4, 1>(gb, n_ranks, s);
-  return launch_gemm_cfg<128, 128, 16, 2, 2>(gb, n_ranks, s);
+  if (max_n <= 64) return launch_gemm_cfg<128, 64, 4, 1, 1>(gb, n_ranks, s);
+  return launch_gemm_cfg<128, 128, 2, 2, 2>(gb, n_ranks, s);
 }
 
 __global__ void fill_rows_kernel(int64_t rows, int64_t row_stride, int64_t off, int64_t width, float* dst) {

@@ -239,6 +239,10 @@ class RMSLayerNorm(nn.Module):
             raise RuntimeError(f"Incorrect last dimension for node_feats. Expected {self.dim}, "
                                f"got {node_feats.shape[-1]}.")
         n = node_feats.shape[0]
+        if self.affine and not self.centering and self.n_features <= 256:
+            # one fused kernel per direction (same formula as below)
+            out, _ = _ops.rms_norm(node_feats, torch.stack(tuple(self.weights)), self.l_max, float(self.eps))
+            return out
         feats = node_feats
         if self.centering:
             l0 = node_feats[:, : self.n_features]

@@ -688,3 +688,66 @@ def _seg_backward(ctx, grad):
 
 
 segment_sum.register_autograd(_seg_backward, setup_context=_seg_setup)
+
+
+# ---------------------------------------------------------------------------
+# Invariant RMS normalisation
+# ---------------------------------------------------------------------------
+
+@torch.library.custom_op("flashcart::rms_norm", mutates_args=())
+def rms_norm(x: Tensor, weight: Tensor, l_max: int, eps: float) -> Tuple[Tensor, Tensor]:
+    """(out, scale): out_l = x_l * (m + eps)^-1/2 * weight[l] with m the per-node mean of the
+    rank-weighted invariants (reference src/flashcart/nn/layers.py:494-528, no centering)."""
+    x = _lib.contig("x", x)
+    w = _lib.contig("weight", weight)
+    n = x.shape[0]
+    C = w.shape[-1]
+    if w.shape != (l_max + 1, C) or x.shape[-1] != (l_max + 1) ** 2 * C:
+        raise RuntimeError(f"rms_norm: weight {tuple(w.shape)} / x {tuple(x.shape)} do not match l_max={l_max}.")
+    out = torch.empty_like(x)
+    scale = x.new_empty(n)
+    _lib_call("fc_rms_norm_fwd", n, l_max, C, x.data_ptr(), w.data_ptr(), float(eps), out.data_ptr(),
+              scale.data_ptr(), _lib.stream_of(x))
+    return out, scale
+
+
+@rms_norm.register_fake
+def _(x, weight, l_max, eps):
+    return torch.empty_like(x), x.new_empty(x.shape[0])
+
+
+@torch.library.custom_op("flashcart::rms_norm_bwd", mutates_args=())
+def rms_norm_bwd(grad_out: Tensor, x: Tensor, weight: Tensor, scale: Tensor, l_max: int) -> Tensor:
+    go = _lib.contig("grad_out", grad_out)
+    x = _lib.contig("x", x)
+    w = _lib.contig("weight", weight)
+    s = _lib.contig("scale", scale)
+    gx = torch.empty_like(x)
+    _lib_call("fc_rms_norm_bwd", x.shape[0], l_max, w.shape[-1], go.data_ptr(), x.data_ptr(), w.data_ptr(),
+              s.data_ptr(), gx.data_ptr(), _lib.stream_of(x))
+    return gx
+
+
+@rms_norm_bwd.register_fake
+def _(grad_out, x, weight, scale, l_max):
+    return torch.empty_like(x)
+
+
+def _rms_setup(ctx, inputs, output):
+    x, weight, l_max, eps = inputs
+    ctx.save_for_backward(x, weight, output[1])
+    ctx.l_max = int(l_max)
+
+
+def _rms_backward(ctx, grad_out, grad_scale):
+    x, weight, scale = ctx.saved_tensors
+    gx = rms_norm_bwd(grad_out, x, weight, scale, ctx.l_max) if ctx.needs_input_grad[0] else None
+    gw = None
+    if ctx.needs_input_grad[1]:  # d/dg_l[c] = sum_{n,a} grad_out * x * s (parameter training only)
+        n, C = x.shape[0], weight.shape[-1]
+        prod = (grad_out * x * scale.unsqueeze(-1)).view(n, -1, C)
+        gw = torch.stack([prod[:, l * l:(l + 1) ** 2].sum(dim=(0, 1)) for l in range(ctx.l_max + 1)])
+    return gx, gw, None, None
+
+
+rms_norm.register_autograd(_rms_backward, setup_context=_rms_setup)

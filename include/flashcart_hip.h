@@ -192,6 +192,20 @@ int fc_dense_dgrad(int64_t n, int32_t k, int32_t m, const float* grad_out, const
                    const float* w, float scale, int32_t act, float* grad_x, void* stream);
 
 /* ------------------------------------------------------------------------- */
+/* Invariant RMS normalisation: replaces RMSLayerNorm.forward (reference        */
+/* src/flashcart/nn/layers.py:494-528; no centering) and its autograd in one    */
+/* pass each. x, out, grad_x: (n, (l_max+1)^2 * C) feature rows; weight:        */
+/* (l_max+1, C) per-rank gains g_l; scale: (n,) receives (m + eps)^-1/2 in the  */
+/* forward (may be NULL) and is read by the backward, where                     */
+/* m = mean_c sum_l TP_sym(x_l, x_l)_0 / ((2l+1)(l_max+1)).                     */
+/* ------------------------------------------------------------------------- */
+int fc_rms_norm_fwd(int64_t n, int32_t l_max, int32_t C, const float* x, const float* weight, float eps,
+                    float* out, float* scale, void* stream);
+/* grad_x = d<grad_out, out>/dx for fixed weight (the gain gradient is not formed). */
+int fc_rms_norm_bwd(int64_t n, int32_t l_max, int32_t C, const float* grad_out, const float* x,
+                    const float* weight, const float* scale, float* grad_x, void* stream);
+
+/* ------------------------------------------------------------------------- */
 /* Segment reductions: replace scatter_sum (reference src/flashcart/utils/     */
 /* scatter.py:33-68) for sorted segments, e.g. per-graph energies              */
 /* (src/flashcart/model/atomistic.py:288).                                     */

@@ -217,3 +217,27 @@ def test_segment_sum():
     ref = O.scatter_sum(src, index, len(counts))
     out = ops.segment_sum(src.float().to(DEV), ptr.to(DEV), index.to(DEV))
     assert_close(out, ref, 1e-6, 1e-6, "segment sum")
+
+
+@pytest.mark.parametrize("l_max,C", [(0, 128), (1, 16), (2, 128), (3, 128), (3, 40)])
+def test_rms_norm(l_max, C):
+    """Fused RMS norm (forward, input and gain gradients) against the oracle's
+    RMSLayerNorm restatement in float64."""
+    ops = _ops()
+    from oracle.model import rms_norm as ref_norm
+    torch.manual_seed(l_max * 7 + C)
+    n = 300
+    x64 = (torch.randn(n, (l_max + 1) ** 2 * C, dtype=torch.float64) * torch.rand(n, 1, dtype=torch.float64) * 3)
+    x64.requires_grad_(True)
+    g64 = [(1.0 + 0.3 * torch.randn(C, dtype=torch.float64)).requires_grad_(True) for _ in range(l_max + 1)]
+    sd = {f"ln.weights.{l}": g64[l] for l in range(l_max + 1)}
+    ref = ref_norm(sd, "ln", x64, l_max, C)
+    go = torch.randn_like(ref)
+    ref_g = torch.autograd.grad(ref, [x64] + g64, go)
+    x = x64.detach().float().to(DEV).requires_grad_(True)
+    w = torch.stack([g.detach() for g in g64]).float().to(DEV).requires_grad_(True)
+    out, _ = ops.rms_norm(x, w, l_max, 1e-6)
+    gx, gw = torch.autograd.grad(out, [x, w], go.float().to(DEV))
+    assert_close(out, ref, 2e-5, 2e-5 * float(ref.abs().max()), "rms fwd")
+    assert_close(gx, ref_g[0], 1e-4, 1e-4 * float(ref_g[0].abs().max()), "rms grad x")
+    assert_close(gw, torch.stack(ref_g[1:]), 1e-4, 1e-4 * float(torch.stack(ref_g[1:]).abs().max()), "rms grad g")
