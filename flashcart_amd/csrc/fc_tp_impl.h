@@ -286,6 +286,61 @@ __global__ void __launch_bounds__(256) tp_bwd_kernel(TPArgs g) {
   }
 }
 
+// Backward of the node-wise (rows) product with full-width inputs (F1 == F2 == C) and
+// per-path outputs: no channel reduction, so no LDS or barriers. The output gradient
+// of a path is read when the path is processed (the node-wise kernels have no edge
+// loop to amortise a full go row over, and keeping it all in registers halves the
+// occupancy that hides the loads).
+template <int L1, int L2, int LO, bool SYM>
+__global__ void __launch_bounds__(256) tp_bwd_rows_kernel(TPArgs g) {
+  using CF = TPConfig<L1, L2, LO, SYM>;
+  using PL = typename CF::PL;
+  constexpr int D1 = CF::D1, D2 = CF::D2, NOUT = CF::NOUT, NP = CF::NP;
+  const int64_t row = blockIdx.x;
+  const int f = threadIdx.x;
+  const int C = g.C;
+  if (f >= C || row >= g.n_rows) return;
+  const bool need1 = g.grad_in1 != nullptr, need2 = g.grad_in2 != nullptr, needw = g.grad_w != nullptr;
+  const float* gor = g.grad_out + row * (int64_t)NOUT * C + f;
+  const float* wr = (g.shared_w ? g.w : g.w + row * (int64_t)NP * C) + f;
+  float x[D1], y[D2], gx[D1], gy[D2];
+#pragma unroll
+  for (int u = 0; u < D1; ++u) { x[u] = g.in1[(row * D1 + u) * (int64_t)C + f]; gx[u] = 0.f; }
+#pragma unroll
+  for (int u = 0; u < D2; ++u) { y[u] = g.in2[(row * D2 + u) * (int64_t)C + f]; gy[u] = 0.f; }
+  static_for<NP>([&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    constexpr PathDesc P = PL::at(i);
+    using T = TPPath<P.r1, P.r2, P.lo>;
+    float A[T::NA], u[T::NO];
+    float go[T::NO];
+#pragma unroll
+    for (int a = 0; a < T::NO; ++a) go[a] = g.alpha * gor[(int64_t)PL::out_index(i, a) * C];
+    const float w = wr[i * C];
+    T::amat(y + P.r2 * P.r2, A);
+    if (needw) {
+      float t[T::NO];
+      T::apply(A, x + P.r1 * P.r1, t);
+      float s = 0.f;
+#pragma unroll
+      for (int a = 0; a < T::NO; ++a) s = fmaf(go[a], t[a], s);
+      g.grad_w[row * (int64_t)NP * C + i * C + f] = s;
+    }
+#pragma unroll
+    for (int a = 0; a < T::NO; ++a) u[a] = w * go[a];
+    if (need1) T::apply_t(A, u, gx + P.r1 * P.r1);
+    if (need2) T::vjp2(u, x + P.r1 * P.r1, gy + P.r2 * P.r2);
+  });
+  if (need1) {
+#pragma unroll
+    for (int u = 0; u < D1; ++u) g.grad_in1[(row * D1 + u) * (int64_t)C + f] = gx[u];
+  }
+  if (need2) {
+#pragma unroll
+    for (int u = 0; u < D2; ++u) g.grad_in2[(row * D2 + u) * (int64_t)C + f] = gy[u];
+  }
+}
+
 // Host-side launcher for one configuration.
 template <int L1, int L2, int LO, bool SYM>
 int launch_tp(const TPArgs& g, bool conv, bool bwd, hipStream_t stream) {
@@ -300,6 +355,8 @@ int launch_tp(const TPArgs& g, bool conv, bool bwd, hipStream_t stream) {
     if (conv) {
       if (bc2) hipLaunchKernelGGL((tp_bwd_kernel<L1, L2, LO, SYM, true, true>), grid, block, lds, stream, g);
       else hipLaunchKernelGGL((tp_bwd_kernel<L1, L2, LO, SYM, true, false>), grid, block, lds, stream, g);
+    } else if (g.F1 == g.C && g.F2 == g.C && !g.reduced) {
+      hipLaunchKernelGGL((tp_bwd_rows_kernel<L1, L2, LO, SYM>), grid, block, 0, stream, g);
     } else {
       hipLaunchKernelGGL((tp_bwd_kernel<L1, L2, LO, SYM, false, false>), grid, block, lds, stream, g);
     }
