@@ -172,7 +172,7 @@ __device__ __forceinline__ float wave_reduce_halving(float (&v)[N], int lane) {
 constexpr int BWD_CHUNK = 16;
 
 template <int L1, int L2, int LO, bool SYM, bool CONV, bool BC2>
-__global__ void __launch_bounds__(256) tp_bwd_kernel(TPArgs g) {
+__global__ void __launch_bounds__(256, 2) tp_bwd_kernel(TPArgs g) {
   using CF = TPConfig<L1, L2, LO, SYM>;
   using PL = typename CF::PL;
   constexpr int D1 = CF::D1, D2 = CF::D2, NOUT = CF::NOUT, NP = CF::NP;
@@ -191,7 +191,9 @@ __global__ void __launch_bounds__(256) tp_bwd_kernel(TPArgs g) {
   const int wave = f >> 6, lane = f & 63, nw = blockDim.x >> 6;
   const int64_t s1 = (int64_t)D1 * g.F1, sw = (int64_t)NP * C;
   const bool need1 = g.grad_in1 != nullptr, need2 = g.grad_in2 != nullptr, needw = g.grad_w != nullptr;
-  const bool red1 = need1 && g.F1 == 1 && C > 1, red2 = need2 && g.F2 == 1 && C > 1;
+  // BC2 implies F2 == 1, so F1 == C there: in1 is never channel-reduced (compile-time,
+  // which keeps the unused butterfly registers of gx out of the kernel).
+  const bool red1 = !BC2 && need1 && g.F1 == 1 && C > 1, red2 = need2 && g.F2 == 1 && C > 1;
 
   float go[NOUT];
   if (!g.reduced) {
