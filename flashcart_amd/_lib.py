@@ -78,11 +78,13 @@ _SIGNATURES = {
     "fc_tp_bwd_workspace": (c_i64, [ctypes.POINTER(TPDesc), ctypes.POINTER(CSR), c_i64, c_int, c_int]),
     "fc_tp_bwd": (c_int, [ctypes.POINTER(TPDesc), ctypes.POINTER(CSR), c_i64, c_vp, c_vp, c_vp, c_vp, c_f32,
                           c_vp, c_vp, c_vp, c_vp, c_i64, c_vp]),
-    "fc_linear_fwd": (c_int, [ctypes.POINTER(LinearDesc), c_i64, c_vp, c_f32, c_vp, c_vp]),
-    "fc_linear_dgrad": (c_int, [ctypes.POINTER(LinearDesc), c_i64, c_vp, c_f32, c_vp, c_vp]),
+    "fc_linear_fwd": (c_int, [ctypes.POINTER(LinearDesc), c_i64, c_vp, c_f32, c_vp, c_vp, c_vp]),
+    "fc_linear_dgrad": (c_int, [ctypes.POINTER(LinearDesc), c_i64, c_vp, c_f32, c_vp, c_vp, c_vp]),
     "fc_dense_fwd": (c_int, [c_i64, c_i32, c_i32, c_vp, c_vp, c_f32, c_vp, c_i32, c_vp, c_vp, c_vp]),
     "fc_dense_dgrad": (c_int, [c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_f32, c_i32, c_vp, c_vp]),
     "fc_segment_sum": (c_int, [c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "fc_gate_fwd": (c_int, [c_i64, c_int, c_int, c_vp, c_vp, c_int, c_vp, c_vp]),
+    "fc_gate_bwd": (c_int, [c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_int, c_vp, c_vp, c_vp]),
     "fc_rms_norm_fwd": (c_int, [c_i64, c_int, c_int, c_vp, c_vp, c_f32, c_vp, c_vp, c_vp]),
     "fc_rms_norm_bwd": (c_int, [c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "fc_neighbor_list": (c_i64, [c_i64, c_vp, c_vp, c_vp, ctypes.c_double, c_i64, c_vp, c_vp, c_vp]),

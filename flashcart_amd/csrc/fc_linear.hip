@@ -38,6 +38,7 @@ struct GemmRank {
   float* D;         // row r: D + n*d_row + c*d_comp, N contiguous floats
   const float* P;   // dense dgrad: pre-activation (same layout as A), multiplies A by act'(P)
   float* pre;       // dense fwd: pre-activation output (same layout as D)
+  const float* R;   // residual added to the result (same layout as D; may be D itself)
   int64_t a_row, a_comp, d_row, d_comp;
   int32_t M;        // rows = n * comps
   int32_t comps, K, N;
@@ -291,6 +292,23 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmBatch gb) {
     const int col = c0 + wn * TN + j * 32 + (lane & 31);
     bias_v[j] = (gb.bias && col < g.N) ? gb.bias[col] : 0.f;
   }
+  // The residual may alias D (in-place accumulation), so all of this lane's residual
+  // values are read before its first store; loading them inside the store loop would
+  // serialise every load behind the preceding stores.
+  float rv[FM][16][FN];
+  if (g.R) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t off = d_off[wm * TM + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)];
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int col = c0 + wn * TN + j * 32 + (lane & 31);
+          rv[i][v][j] = (off >= 0 && col < g.N) ? g.R[off + col] : 0.f;
+        }
+      }
+  }
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -306,6 +324,7 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmBatch gb) {
         float val = fmaf(acc[i][j][v], g.scale, bias_v[j]);
         if (prow) prow[col] = val;
         if (gb.act == 1) val = kSiluScale * val * sigmoidf_(val);
+        if (g.R) val += rv[i][v][j];
         drow[col] = val;
       }
     }
@@ -346,17 +365,22 @@ int launch_gemm(GemmBatch gb, int n_ranks, hipStream_t s) {
   return launch_gemm_cfg<128, 128, 2, 2, 2>(gb, n_ranks, s);
 }
 
-__global__ void fill_rows_kernel(int64_t rows, int64_t row_stride, int64_t off, int64_t width, float* dst) {
+// dst[r, off:off+width] = src ? src[r, off:off+width] : 0 (same row stride)
+__global__ void fill_rows_kernel(int64_t rows, int64_t row_stride, int64_t off, int64_t width,
+                                 const float* __restrict__ src, float* __restrict__ dst) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= rows * width) return;
-  dst[(t / width) * row_stride + off + (t % width)] = 0.f;
+  const int64_t k = (t / width) * row_stride + off + (t % width);
+  dst[k] = src ? src[k] : 0.f;
 }
 
-int zero_columns(int64_t rows, int64_t row_stride, int64_t off, int64_t width, float* dst, hipStream_t s) {
-  if (rows * width == 0) return FC_OK;
+// Output columns the map does not produce: zero, or the residual's values.
+int fill_columns(int64_t rows, int64_t row_stride, int64_t off, int64_t width, const float* residual, float* dst,
+                 hipStream_t s) {
+  if (rows * width == 0 || residual == dst) return FC_OK;
   const int bs = 256;
   hipLaunchKernelGGL(fill_rows_kernel, dim3((unsigned)((rows * width + bs - 1) / bs)), dim3(bs), 0, s, rows,
-                     row_stride, off, width, dst);
+                     row_stride, off, width, residual, dst);
   FC_LAUNCH_CHECK();
   return FC_OK;
 }
@@ -401,8 +425,8 @@ static LinearLayout linear_layout(const fc_linear_desc* d) {
 
 using namespace fc;
 
-extern "C" int fc_linear_fwd(const fc_linear_desc* d, int64_t n, const float* x, float alpha, float* out,
-                             void* stream) {
+extern "C" int fc_linear_fwd(const fc_linear_desc* d, int64_t n, const float* x, float alpha,
+                             const float* residual, float* out, void* stream) {
   int st = check_linear(d);
   if (st != FC_OK) return st;
   if (n == 0) return FC_OK;
@@ -420,6 +444,7 @@ extern "C" int fc_linear_fwd(const fc_linear_desc* d, int64_t n, const float* x,
     g.a_comp = K;
     g.B = d->weight[l];
     g.D = out + L.out_off[l];
+    g.R = residual ? residual + L.out_off[l] : nullptr;
     g.d_row = L.out_dim;
     g.d_comp = d->out_features;
     g.comps = 2 * l + 1;
@@ -431,12 +456,13 @@ extern "C" int fc_linear_fwd(const fc_linear_desc* d, int64_t n, const float* x,
   st = launch_gemm(gb, L.common + 1, s);
   if (st != FC_OK) return st;
   if (L.common < d->out_l_max)
-    return zero_columns(n, L.out_dim, L.out_off[L.common + 1], L.out_dim - L.out_off[L.common + 1], out, s);
+    return fill_columns(n, L.out_dim, L.out_off[L.common + 1], L.out_dim - L.out_off[L.common + 1], residual, out,
+                        s);
   return FC_OK;
 }
 
-extern "C" int fc_linear_dgrad(const fc_linear_desc* d, int64_t n, const float* go, float alpha, float* gx,
-                               void* stream) {
+extern "C" int fc_linear_dgrad(const fc_linear_desc* d, int64_t n, const float* go, float alpha,
+                               const float* residual, float* gx, void* stream) {
   int st = check_linear(d);
   if (st != FC_OK) return st;
   if (n == 0) return FC_OK;
@@ -454,6 +480,7 @@ extern "C" int fc_linear_dgrad(const fc_linear_desc* d, int64_t n, const float* 
     g.a_comp = d->out_features;
     g.B = d->weight[l];
     g.D = gx + L.in_off[l];
+    g.R = residual ? residual + L.in_off[l] : nullptr;
     g.d_row = L.in_dim;
     g.d_comp = Kin;
     g.comps = 2 * l + 1;
@@ -465,7 +492,7 @@ extern "C" int fc_linear_dgrad(const fc_linear_desc* d, int64_t n, const float* 
   st = launch_gemm(gb, L.common + 1, s);
   if (st != FC_OK) return st;
   if (L.common < d->in_l_max)
-    return zero_columns(n, L.in_dim, L.in_off[L.common + 1], L.in_dim - L.in_off[L.common + 1], gx, s);
+    return fill_columns(n, L.in_dim, L.in_off[L.common + 1], L.in_dim - L.in_off[L.common + 1], residual, gx, s);
   return FC_OK;
 }
 

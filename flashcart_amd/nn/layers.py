@@ -177,13 +177,14 @@ class InteractionLayer(nn.Module):
                              alpha=1.0 / self._sqrt_avg)
         if out_nodes is not None:
             aggregated = aggregated[:out_nodes]
-        out = self.linear_second(aggregated)
-        if self.skip_projection is not None:
-            skip = self.skip_projection(residual_feats)
-            if self.in1_l_max == 0:
+        if self.skip_projection is not None and self.in1_l_max > 0:
+            # the skip projection enters linear_second's GEMM epilogue as its residual
+            out = self.linear_second(aggregated, residual=self.skip_projection(residual_feats))
+        else:
+            out = self.linear_second(aggregated)
+            if self.skip_projection is not None:
+                skip = self.skip_projection(residual_feats)
                 out = torch.cat([out[:, : self.out_features] + skip, out[:, self.out_features:]], dim=-1)
-            else:
-                out = out + skip
         if self.layer_norm is not None:
             out = self.layer_norm(out)
         return out
@@ -290,15 +291,13 @@ class EquivariantGatedLayer(nn.Module):
         if node_feats.shape[-1] != self.in_dim:
             raise RuntimeError(f"Incorrect last dimension for node_feats. Expected {self.in_dim}, "
                                f"got {node_feats.shape[-1]}.")
-        n = node_feats.shape[0]
         values = self.value_linear(node_feats)
-        if self.gate_activation_name == "silu":
-            gates = self.gate_linear(node_feats[:, : self.in_features], act=1)
-        else:
-            gates = self.gate_activation(self.gate_linear(node_feats[:, : self.in_features]))
-        gates = gates.view(n, self.l_max + 1, self.hidden_features).index_select(1, self.comp_rank)
-        gated = (values.view(n, -1, self.hidden_features) * gates).view(n, -1)
-        return node_feats + self.output_linear(gated)
+        if self.gate_activation_name == "silu":  # activation fused into the gate GEMM
+            pre, act = self.gate_linear(node_feats[:, : self.in_features], act=1), 0
+        else:  # rescaled sigmoid applied inside the gating kernel
+            pre, act = self.gate_linear(node_feats[:, : self.in_features]), 1
+        gated = _ops.gate(values, pre, self.l_max, act)
+        return self.output_linear(gated, residual=node_feats)
 
 
 class IrrepsSelector(nn.Module):
@@ -431,6 +430,10 @@ class ProductLayer(nn.Module):
                 name = self.path_norm_names[k]
                 if name is not None:
                     product_feats = product_feats * getattr(self, name)
+            elif k == self.correlation - 1 and output is not None:
+                # last step (output ranks only): the running sum enters the GEMM epilogue
+                product_feats = self.product_linears[k](product_feats, residual=output)
+                output = None
             else:
                 product_feats = self.product_linears[k](product_feats)
             sel = self.irreps_selectors[k](product_feats)
@@ -438,7 +441,7 @@ class ProductLayer(nn.Module):
         if self.path_reduced:
             output = self.final_linear(output)
         if self.skip_projection is not None:
-            output = output + self.skip_projection(node_feats)
+            output = self.skip_projection(node_feats, residual=output)
         if self.layer_norm is not None:
             output = self.layer_norm(output)
         return output

@@ -475,20 +475,24 @@ def _pad4(weights):
 @torch.library.custom_op("flashcart::linear_fwd", mutates_args=())
 def linear_fwd_op(x: Tensor, w0: Tensor, w1: Optional[Tensor], w2: Optional[Tensor], w3: Optional[Tensor],
                   in_l_max: int, out_l_max: int, in_features: int, out_features: int, in_paths: List[int],
-                  scale: List[float], alpha: float = 1.0) -> Tensor:
+                  scale: List[float], alpha: float = 1.0, residual: Optional[Tensor] = None) -> Tensor:
+    """out = linear(x) (+ residual, a tensor of the output's shape added in the GEMM epilogue)."""
     in_dim, out_dim = _linear_dims(in_l_max, out_l_max, in_features, out_features, in_paths)
     if x.shape[-1] != in_dim:
         raise RuntimeError(f"Incorrect last dimension for x. Expected {in_dim}, got {x.shape[-1]}.")
     x = _lib.contig("x", x)
     ws = [_lib.contig(f"weight[{l}]", w) for l, w in enumerate(_wlist(w0, w1, w2, w3))]
     out = x.new_empty(x.shape[0], out_dim)
+    r = _check_residual(residual, out)
     desc = _lib.linear_desc(in_l_max, out_l_max, in_features, out_features, in_paths, ws, scale)
-    _lib_call("fc_linear_fwd", desc, x.shape[0], x.data_ptr(), float(alpha), out.data_ptr(), _lib.stream_of(x))
+    _lib_call("fc_linear_fwd", desc, x.shape[0], x.data_ptr(), float(alpha), _lib.ptr(r), out.data_ptr(),
+              _lib.stream_of(x))
     return out
 
 
 @linear_fwd_op.register_fake
-def _(x, w0, w1, w2, w3, in_l_max, out_l_max, in_features, out_features, in_paths, scale, alpha=1.0):
+def _(x, w0, w1, w2, w3, in_l_max, out_l_max, in_features, out_features, in_paths, scale, alpha=1.0,
+      residual=None):
     _, out_dim = _linear_dims(in_l_max, out_l_max, in_features, out_features, in_paths)
     return x.new_empty(x.shape[0], out_dim)
 
@@ -496,38 +500,52 @@ def _(x, w0, w1, w2, w3, in_l_max, out_l_max, in_features, out_features, in_path
 @torch.library.custom_op("flashcart::linear_bwd", mutates_args=())
 def linear_bwd_op(grad_out: Tensor, w0: Tensor, w1: Optional[Tensor], w2: Optional[Tensor], w3: Optional[Tensor],
                   in_l_max: int, out_l_max: int, in_features: int, out_features: int, in_paths: List[int],
-                  scale: List[float], alpha: float = 1.0) -> Tensor:
-    """Input gradient of linear_fwd (the MFMA dgrad)."""
+                  scale: List[float], alpha: float = 1.0, residual: Optional[Tensor] = None) -> Tensor:
+    """Input gradient of linear_fwd (the MFMA dgrad), plus ``residual`` when given."""
     in_dim, _ = _linear_dims(in_l_max, out_l_max, in_features, out_features, in_paths)
     go = _lib.contig("grad_out", grad_out)
     ws = [_lib.contig(f"weight[{l}]", w) for l, w in enumerate(_wlist(w0, w1, w2, w3))]
     gx = go.new_empty(go.shape[0], in_dim)
+    r = _check_residual(residual, gx)
     desc = _lib.linear_desc(in_l_max, out_l_max, in_features, out_features, in_paths, ws, scale)
-    _lib_call("fc_linear_dgrad", desc, go.shape[0], go.data_ptr(), float(alpha), gx.data_ptr(), _lib.stream_of(go))
+    _lib_call("fc_linear_dgrad", desc, go.shape[0], go.data_ptr(), float(alpha), _lib.ptr(r), gx.data_ptr(),
+              _lib.stream_of(go))
     return gx
 
 
 @linear_bwd_op.register_fake
-def _(grad_out, w0, w1, w2, w3, in_l_max, out_l_max, in_features, out_features, in_paths, scale, alpha=1.0):
+def _(grad_out, w0, w1, w2, w3, in_l_max, out_l_max, in_features, out_features, in_paths, scale, alpha=1.0,
+      residual=None):
     in_dim, _ = _linear_dims(in_l_max, out_l_max, in_features, out_features, in_paths)
     return grad_out.new_empty(grad_out.shape[0], in_dim)
 
 
 def linear_fwd(x: Tensor, weights: List[Tensor], in_l_max: int, out_l_max: int, in_features: int,
-               out_features: int, in_paths: List[int], scale: List[float], alpha: float = 1.0) -> Tensor:
-    """out_l = alpha * scale_l * x_l @ W_l^T for every shared rank (torch.ops.flashcart.linear_fwd)."""
+               out_features: int, in_paths: List[int], scale: List[float], alpha: float = 1.0,
+               residual: Optional[Tensor] = None) -> Tensor:
+    """out_l = alpha * scale_l * x_l @ W_l^T for every shared rank (torch.ops.flashcart.linear_fwd),
+    plus ``residual`` (same shape as the output) when given."""
     return linear_fwd_op(x, *_pad4(weights), in_l_max, out_l_max, in_features, out_features, list(in_paths),
-                         [float(s) for s in scale], float(alpha))
+                         [float(s) for s in scale], float(alpha), residual)
 
 
 def linear_bwd(grad_out: Tensor, weights: List[Tensor], in_l_max: int, out_l_max: int, in_features: int,
-               out_features: int, in_paths: List[int], scale: List[float], alpha: float = 1.0) -> Tensor:
+               out_features: int, in_paths: List[int], scale: List[float], alpha: float = 1.0,
+               residual: Optional[Tensor] = None) -> Tensor:
     return linear_bwd_op(grad_out, *_pad4(weights), in_l_max, out_l_max, in_features, out_features,
-                         list(in_paths), [float(s) for s in scale], float(alpha))
+                         list(in_paths), [float(s) for s in scale], float(alpha), residual)
+
+
+def _check_residual(residual: Optional[Tensor], out: Tensor) -> Optional[Tensor]:
+    if residual is None:
+        return None
+    if residual.shape != out.shape:
+        raise RuntimeError(f"residual shape {tuple(residual.shape)} != output shape {tuple(out.shape)}.")
+    return _lib.contig("residual", residual)
 
 
 def _linear_setup(ctx, inputs, output):
-    x, w0, w1, w2, w3, in_l_max, out_l_max, in_features, out_features, in_paths, scale, alpha = inputs
+    x, w0, w1, w2, w3, in_l_max, out_l_max, in_features, out_features, in_paths, scale, alpha, residual = inputs
     ws = _wlist(w0, w1, w2, w3)
     ctx.save_for_backward(x, *ws)
     ctx.cfg = (int(in_l_max), int(out_l_max), int(in_features), int(out_features), list(in_paths), list(scale))
@@ -555,7 +573,9 @@ def _linear_backward(ctx, grad):
                 gws[l] = (gl.t() @ xl) * (scale[l] * ctx.alpha)
             in_off += m * k
             out_off += m * fout
-    return (gx, *gws) + (None,) * 7
+    # trailing arguments left at their defaults are not part of needs_input_grad
+    g_res = grad if len(need) > 12 and need[12] else None
+    return (gx, *gws) + (None,) * 7 + (g_res,)
 
 
 linear_fwd_op.register_autograd(_linear_backward, setup_context=_linear_setup)
@@ -751,3 +771,65 @@ def _rms_backward(ctx, grad_out, grad_scale):
 
 
 rms_norm.register_autograd(_rms_backward, setup_context=_rms_setup)
+
+
+# ---------------------------------------------------------------------------
+# Rank-wise gating
+# ---------------------------------------------------------------------------
+
+@torch.library.custom_op("flashcart::gate", mutates_args=())
+def gate(values: Tensor, pre: Tensor, l_max: int, act: int) -> Tensor:
+    """values[n, (l, a), c] * act(pre[n, l, c]); act 0 identity, 1 rescaled sigmoid
+    (reference src/flashcart/nn/layers.py:609-635)."""
+    v = _lib.contig("values", values)
+    p = _lib.contig("pre", pre)
+    n = v.shape[0]
+    C = p.shape[-1] // (l_max + 1)
+    if v.shape[-1] != (l_max + 1) ** 2 * C or p.shape[-1] != (l_max + 1) * C or p.shape[0] != n:
+        raise RuntimeError(f"gate: values {tuple(v.shape)} / pre {tuple(p.shape)} do not match l_max={l_max}.")
+    out = torch.empty_like(v)
+    _lib_call("fc_gate_fwd", n, l_max, C, v.data_ptr(), p.data_ptr(), int(act), out.data_ptr(), _lib.stream_of(v))
+    return out
+
+
+@gate.register_fake
+def _(values, pre, l_max, act):
+    return torch.empty_like(values)
+
+
+@torch.library.custom_op("flashcart::gate_bwd", mutates_args=())
+def gate_bwd(grad_out: Tensor, values: Tensor, pre: Tensor, l_max: int, act: int, need_values: bool,
+             need_pre: bool) -> Tuple[Tensor, Tensor]:
+    go = _lib.contig("grad_out", grad_out)
+    v = _lib.contig("values", values)
+    p = _lib.contig("pre", pre)
+    gv = torch.empty_like(v) if need_values else v.new_empty(0)
+    gp = torch.empty_like(p) if need_pre else p.new_empty(0)
+    C = p.shape[-1] // (l_max + 1)
+    _lib_call("fc_gate_bwd", v.shape[0], l_max, C, go.data_ptr(), v.data_ptr(), p.data_ptr(), int(act),
+              gv.data_ptr() if need_values else None, gp.data_ptr() if need_pre else None, _lib.stream_of(v))
+    return gv, gp
+
+
+@gate_bwd.register_fake
+def _(grad_out, values, pre, l_max, act, need_values, need_pre):
+    return (torch.empty_like(values) if need_values else values.new_empty(0),
+            torch.empty_like(pre) if need_pre else pre.new_empty(0))
+
+
+def _gate_setup(ctx, inputs, output):
+    values, pre, l_max, act = inputs
+    ctx.save_for_backward(values, pre)
+    ctx.cfg = (int(l_max), int(act))
+
+
+def _gate_backward(ctx, grad):
+    values, pre = ctx.saved_tensors
+    nv, np_ = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+    if not (nv or np_):
+        return None, None, None, None
+    gv, gp = gate_bwd(grad, values, pre, *ctx.cfg, bool(nv), bool(np_))
+    return (gv if nv else None), (gp if np_ else None), None, None
+
+
+gate.register_autograd(_gate_backward, setup_context=_gate_setup)

@@ -78,11 +78,12 @@ class LinearLayer(nn.Module):
         for l in range(self.common_l_max + 1):
             self.weight.append(nn.Parameter(torch.randn(out_features, in_features * self.in_paths[l])))
 
-    def forward(self, x: torch.Tensor, alpha: float = 1.0) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, alpha: float = 1.0, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """``residual`` (same shape as the output) is added in the GEMM epilogue."""
         if x.shape[-1] != self.in_dim:
             raise RuntimeError(f"Incorrect last dimension for x. Expected {self.in_dim}, got {x.shape[-1]}.")
         return _ops.linear_fwd(x, list(self.weight), self.in_l_max, self.out_l_max, self.in_features,
-                               self.out_features, self.in_paths, self._scale_list, float(alpha))
+                               self.out_features, self.in_paths, self._scale_list, float(alpha), residual)
 
     def extra_repr(self) -> str:
         return (f"in_l_max={self.in_l_max}, out_l_max={self.out_l_max}, in_features={self.in_features}, "

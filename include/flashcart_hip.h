@@ -176,10 +176,12 @@ typedef struct fc_linear_desc {
   float scale[4];            /* s_l */
 } fc_linear_desc;
 
+/* residual (may be NULL, may equal out / grad_x): a tensor of the output's layout added to
+ * the result, e.g. a skip connection or a gradient accumulated by another consumer. */
 int fc_linear_fwd(const fc_linear_desc* desc, int64_t n_rows, const float* x, float alpha,
-                  float* out, void* stream);
+                  const float* residual, float* out, void* stream);
 int fc_linear_dgrad(const fc_linear_desc* desc, int64_t n_rows, const float* grad_out,
-                    float alpha, float* grad_x, void* stream);
+                    float alpha, const float* residual, float* grad_x, void* stream);
 
 /* Plain dense map out = act(x @ W^T * scale + bias), x (n, k), W (m, k) row-major:
  * the radial and readout MLP layers (reference src/flashcart/nn/layers.py:84-145,
@@ -204,6 +206,19 @@ int fc_rms_norm_fwd(int64_t n, int32_t l_max, int32_t C, const float* x, const f
 /* grad_x = d<grad_out, out>/dx for fixed weight (the gain gradient is not formed). */
 int fc_rms_norm_bwd(int64_t n, int32_t l_max, int32_t C, const float* grad_out, const float* x,
                     const float* weight, const float* scale, float* grad_x, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* Rank-wise gating: replaces the gate activation, index_select and product of  */
+/* EquivariantGatedLayer.forward (reference src/flashcart/nn/layers.py:609-635). */
+/* values, out, grad_values: (n, (l_max+1)^2 * C); pre, grad_pre: (n, l_max+1, C) */
+/* gate logits. act: 0 identity (gate already activated), 1 rescaled sigmoid     */
+/* (1.8462285453386054 * sigmoid). out[n,(l,a),c] = values * act(pre[n,l,c]).     */
+/* ------------------------------------------------------------------------- */
+int fc_gate_fwd(int64_t n, int32_t l_max, int32_t C, const float* values, const float* pre, int32_t act,
+                float* out, void* stream);
+/* grad_values = grad_out * act(pre); grad_pre = act'(pre) * sum_a grad_out * values (either may be NULL). */
+int fc_gate_bwd(int64_t n, int32_t l_max, int32_t C, const float* grad_out, const float* values,
+                const float* pre, int32_t act, float* grad_values, float* grad_pre, void* stream);
 
 /* ------------------------------------------------------------------------- */
 /* Segment reductions: replace scatter_sum (reference src/flashcart/utils/     */

@@ -241,3 +241,58 @@ def test_rms_norm(l_max, C):
     assert_close(out, ref, 2e-5, 2e-5 * float(ref.abs().max()), "rms fwd")
     assert_close(gx, ref_g[0], 1e-4, 1e-4 * float(ref_g[0].abs().max()), "rms grad x")
     assert_close(gw, torch.stack(ref_g[1:]), 1e-4, 1e-4 * float(torch.stack(ref_g[1:]).abs().max()), "rms grad g")
+
+
+@pytest.mark.parametrize("lin,lout", [(3, 3), (2, 3), (3, 1)])
+def test_linear_residual(lin, lout):
+    """linear_fwd / linear_bwd with a residual added in the GEMM epilogue (ranks the map
+    does not produce take the residual's values); gradients pass through to the residual."""
+    ops = _ops()
+    torch.manual_seed(9)
+    n, fin, fout = 211, 16, 16
+    in_dim = (lin + 1) ** 2 * fin
+    out_dim = (lout + 1) ** 2 * fout
+    x64 = torch.randn(n, in_dim, dtype=torch.float64, requires_grad=True)
+    r64 = torch.randn(n, out_dim, dtype=torch.float64, requires_grad=True)
+    ws64 = [torch.randn(fout, fin, dtype=torch.float64) for _ in range(min(lin, lout) + 1)]
+    ref = O.linear(x64, ws64, lin, lout, fin, fout) + r64
+    g = torch.randn_like(ref)
+    ref_g = torch.autograd.grad(ref, [x64, r64], g)
+    x = x64.detach().float().to(DEV).requires_grad_(True)
+    r = r64.detach().float().to(DEV).requires_grad_(True)
+    ws = [w.float().to(DEV) for w in ws64]
+    scale = [fin ** -0.5] * len(ws)
+    out = ops.linear_fwd(x, ws, lin, lout, fin, fout, [1] * (lin + 1), scale, 1.0, r)
+    got = torch.autograd.grad(out, [x, r], g.float().to(DEV))
+    assert_close(out, ref, 1e-5, 1e-4, "linear+residual fwd")
+    assert_close(got[0], ref_g[0], 1e-5, 1e-4 * (float(ref_g[0].abs().max()) + 1), "linear+residual grad x")
+    # pass-through: exactly the float32 upstream gradient
+    assert_close(got[1], g.float().double(), 0.0, 0.0, "linear+residual grad residual")
+    # dgrad with an accumulated gradient: gx = go @ W * s + acc
+    acc = torch.randn(n, in_dim, device=DEV)
+    gx = ops.linear_bwd(g.float().to(DEV), ws, lin, lout, fin, fout, [1] * (lin + 1), scale, 1.0, acc)
+    plain = ops.linear_bwd(g.float().to(DEV), ws, lin, lout, fin, fout, [1] * (lin + 1), scale, 1.0)
+    assert_close(gx, plain.double() + acc.double(), 1e-6, 1e-5, "dgrad + residual")
+
+
+@pytest.mark.parametrize("l_max,act", [(3, 1), (2, 0), (0, 1)])
+def test_gate(l_max, act):
+    """Fused rank-wise gate against the reference formula (rescaled sigmoid, index_select,
+    product) in float64, with both gradients."""
+    ops = _ops()
+    torch.manual_seed(l_max + 10 * act)
+    n, C = 257, 64
+    v64 = torch.randn(n, (l_max + 1) ** 2 * C, dtype=torch.float64, requires_grad=True)
+    p64 = torch.randn(n, (l_max + 1) * C, dtype=torch.float64, requires_grad=True)
+    gates = 1.8462285453386054 * torch.sigmoid(p64) if act == 1 else p64
+    rank = torch.cat([torch.full((2 * l + 1,), l) for l in range(l_max + 1)])
+    ref = (v64.view(n, -1, C) * gates.view(n, l_max + 1, C)[:, rank]).view(n, -1)
+    g = torch.randn_like(ref)
+    ref_g = torch.autograd.grad(ref, [v64, p64], g)
+    v = v64.detach().float().to(DEV).requires_grad_(True)
+    p = p64.detach().float().to(DEV).requires_grad_(True)
+    out = ops.gate(v, p, l_max, act)
+    got = torch.autograd.grad(out, [v, p], g.float().to(DEV))
+    assert_close(out, ref, 1e-5, 1e-6, "gate fwd")
+    assert_close(got[0], ref_g[0], 1e-5, 1e-6, "gate grad values")
+    assert_close(got[1], ref_g[1], 1e-5, 1e-5 * float(ref_g[1].abs().max()), "gate grad pre")
