@@ -292,9 +292,41 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmBatch gb) {
     const int col = c0 + wn * TN + j * 32 + (lane & 31);
     bias_v[j] = (gb.bias && col < g.N) ? gb.bias[col] : 0.f;
   }
-  // The residual may alias D (in-place accumulation), so all of this lane's residual
-  // values are read before its first store; loading them inside the store loop would
-  // serialise every load behind the preceding stores.
+  // The residual may alias D (in-place accumulation), so a lane reads its residual values
+  // before storing to them; loading them inside the store loop would serialise every load
+  // behind the preceding stores.
+  if (r0 + BM <= g.M && c0 + BN <= g.N && !g.pre && gb.act == 0) {
+    // interior tile with a plain epilogue (scale, bias, residual): no bound checks, and
+    // residual reads in groups of 4 rows so the values in flight stay in few registers
+    const int cl = c0 + wn * TN + (lane & 31);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+      for (int v4 = 0; v4 < 16; v4 += 4) {  // rows 8 (v4/4) + 4 (lane/32) + q of the 32-row block
+        int64_t offs[4];
+        float rvi[4][FN];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) offs[q] = d_off[wm * TM + i * 32 + 8 * (v4 >> 2) + 4 * (lane >> 5) + q];
+        if (g.R) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) rvi[q][j] = g.R[offs[q] + cl + j * 32];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float* drow = g.D + offs[q] + cl;
+#pragma unroll
+          for (int j = 0; j < FN; ++j) {
+            float val = fmaf(acc[i][j][v4 + q], g.scale, bias_v[j]);
+            if (g.R) val += rvi[q][j];
+            drow[j * 32] = val;
+          }
+        }
+      }
+    }
+    return;
+  }
   float rv[FM][16][FN];
   if (g.R) {
 #pragma unroll
