@@ -78,6 +78,8 @@ _SIGNATURES = {
     "fc_tp_bwd_workspace": (c_i64, [ctypes.POINTER(TPDesc), ctypes.POINTER(CSR), c_i64, c_int, c_int]),
     "fc_tp_bwd": (c_int, [ctypes.POINTER(TPDesc), ctypes.POINTER(CSR), c_i64, c_vp, c_vp, c_vp, c_vp, c_f32,
                           c_vp, c_vp, c_vp, c_vp, c_i64, c_vp]),
+    "fc_tp_bwd_rows_acc": (c_int, [ctypes.POINTER(TPDesc), c_i64, c_vp, c_vp, c_vp, c_vp, c_f32, c_vp, c_i32,
+                                   c_vp, c_i32, c_vp, c_vp, c_vp]),
     "fc_linear_fwd": (c_int, [ctypes.POINTER(LinearDesc), c_i64, c_vp, c_f32, c_vp, c_vp, c_vp]),
     "fc_linear_dgrad": (c_int, [ctypes.POINTER(LinearDesc), c_i64, c_vp, c_f32, c_vp, c_vp, c_vp]),
     "fc_dense_fwd": (c_int, [c_i64, c_i32, c_i32, c_vp, c_vp, c_f32, c_vp, c_i32, c_vp, c_vp, c_vp]),

@@ -179,3 +179,25 @@ extern "C" int fc_tp_bwd(const fc_tp_desc* d, const fc_csr* graph, int64_t n_row
   }
   return FC_OK;
 }
+
+extern "C" int fc_tp_bwd_rows_acc(const fc_tp_desc* d, int64_t n_rows, const float* go, const float* in1,
+                                  const float* in2, const float* w, float alpha, const float* res1,
+                                  int32_t res1_comps, const float* res2, int32_t res2_comps, float* gin1,
+                                  float* gin2, void* stream) {
+  int st = check_tp(d);
+  if (st != FC_OK) return st;
+  if (d->in1_features != d->in2_features || d->reduce_paths) return FC_ERR_BAD_DESC;
+  if (n_rows < 0) return FC_ERR_SHAPE;
+  if ((res1 && (res1_comps < 0 || res1_comps > ncomp(d->in1_l_max))) ||
+      (res2 && (res2_comps < 0 || res2_comps > ncomp(d->in2_l_max))))
+    return FC_ERR_SHAPE;
+  if (n_rows == 0 || (!gin1 && !gin2)) return FC_OK;
+  if (!go || !in1 || !in2 || !w) return FC_ERR_NULL;
+  TPArgs g = make_args(d, n_rows);
+  g.in1 = in1; g.in2 = in2; g.w = w; g.grad_out = go; g.alpha = alpha;
+  g.grad_in1 = gin1;
+  g.grad_in2 = gin2;
+  g.res1 = res1; g.res1_comps = res1 ? res1_comps : 0;
+  g.res2 = res2; g.res2_comps = res2 ? res2_comps : 0;
+  return dispatch(d, g, false, true, (hipStream_t)stream);
+}

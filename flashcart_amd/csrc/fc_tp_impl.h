@@ -34,6 +34,11 @@ struct TPArgs {
   int32_t F1, F2, C;       // in1 / in2 / output features (1 broadcasts)
   int32_t shared_w, reduced;
   float alpha;             // output scale (fwd) / its transpose (bwd)
+  // rows backward only: gradients added to grad_in1 / grad_in2 (leading res*_comps
+  // components of each row, row width res*_comps * C; may alias the gradient)
+  const float* res1;
+  const float* res2;
+  int32_t res1_comps, res2_comps;
 };
 
 template <int L1, int L2, int LO, bool SYM>
@@ -333,11 +338,22 @@ __global__ void __launch_bounds__(256) tp_bwd_rows_kernel(TPArgs g) {
     if (need1) T::apply_t(A, u, gx + P.r1 * P.r1);
     if (need2) T::vjp2(u, x + P.r1 * P.r1, gy + P.r2 * P.r2);
   });
+  // residual gradients: each element is read and then written by this thread only
   if (need1) {
+    if (g.res1) {
+#pragma unroll
+      for (int u = 0; u < D1; ++u)
+        if (u < g.res1_comps) gx[u] += g.res1[(row * g.res1_comps + u) * (int64_t)C + f];
+    }
 #pragma unroll
     for (int u = 0; u < D1; ++u) g.grad_in1[(row * D1 + u) * (int64_t)C + f] = gx[u];
   }
   if (need2) {
+    if (g.res2) {
+#pragma unroll
+      for (int u = 0; u < D2; ++u)
+        if (u < g.res2_comps) gy[u] += g.res2[(row * g.res2_comps + u) * (int64_t)C + f];
+    }
 #pragma unroll
     for (int u = 0; u < D2; ++u) g.grad_in2[(row * D2 + u) * (int64_t)C + f] = gy[u];
   }

@@ -1,0 +1,144 @@
+"""Fused inference backward of the product and gating blocks.
+
+With frozen parameters (energy + forces evaluation), the input gradient is all that the
+backward of a block has to produce. Autograd over the per-module ops then spends a large
+share of its time on glue: the block input feeds every product step, the skip projection
+and the gate, so its gradient is summed by separate elementwise kernels, and the rank
+selections (``x[:, :stop]``) come back as zero-padded copies. The Functions below run the
+same forward ops and a backward written out by hand in which every such sum happens inside
+a kernel: the linear input gradients take the running gradient as their GEMM-epilogue
+residual, and the node-wise product backward adds into its operands' gradients
+(``fc_tp_bwd_rows_acc``).
+
+They are used only when the block input needs a gradient, no parameter of the block does,
+and no graph is being traced; otherwise the modules run op by op with autograd (training,
+parameter gradients, torch.compile). Reference behaviour: ``nn/layers.py:538-652`` (gated
+update) and ``nn/layers.py:769-1016`` (product layer) — the outputs are those of the
+op-by-op path; only the order of floating-point additions in the backward differs.
+"""
+
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from flashcart_amd.o3 import _ops
+
+
+def applies(module: torch.nn.Module, x: Tensor) -> bool:
+    """True when ``module`` may run as one fused Function on input ``x``."""
+    if not (torch.is_grad_enabled() and x.requires_grad and x.is_cuda):
+        return False
+    if torch.compiler.is_compiling():
+        return False
+    return not any(p.requires_grad for p in module.parameters())
+
+
+class _ProductBlock(torch.autograd.Function):
+    """ProductLayer without path reduction and with shared path weights, up to and
+    including the skip projection (the RMS norm stays a separate op).
+
+    Forward, with t_0 = x and sel() the leading rank blocks up to out_l_max:
+        p_k = L_k(t_k),  t_{k+1} = TP_k(p_k, x, w_{k+1}),  out = sum_{k<K-1} sel(p_k) + L_{K-1}(t_{K-1})
+        out += Skip(x)
+    Backward, given g = dL/d out:
+        gx  = Skip^T g
+        gt  = L_{K-1}^T g
+        for k = K-1 .. 1:  (gp, gx) = TP_{k-1}^T gt + (sel^T g, gx)      one kernel
+                           gt = L_{k-1}^T gp                               (k > 1)
+        gx  = L_0^T gp + gx                                                residual epilogue
+    """
+
+    @staticmethod
+    def forward(ctx, x: Tensor, layer) -> Tensor:
+        K = layer.correlation
+        out: Optional[Tensor] = None
+        p = x
+        saved = []
+        for k in range(K):
+            if k == 0:
+                t = x
+            else:
+                w = layer.path_weights[k](None)
+                saved += [p, w]
+                t = layer.tensor_products[k - 1](p, x, w)
+            if k == K - 1 and out is not None:
+                p = layer.product_linears[k](t, residual=out)
+                out = None
+            else:
+                p = layer.product_linears[k](t)
+            sel = layer.irreps_selectors[k](p)
+            out = sel if out is None else out + sel
+        if layer.skip_projection is not None:
+            out = layer.skip_projection(x, residual=out)
+        ctx.layer = layer
+        ctx.save_for_backward(x, *saved)
+        return out
+
+    @staticmethod
+    def backward(ctx, g: Tensor):
+        layer = ctx.layer
+        x, *saved = ctx.saved_tensors
+        g = g.contiguous()
+        K = layer.correlation
+        gx = layer.skip_projection.input_grad(g) if layer.skip_projection is not None else None
+        gt = layer.product_linears[K - 1].input_grad(g)
+        for k in range(K - 1, 0, -1):
+            p, w = saved[2 * (k - 1)], saved[2 * (k - 1) + 1]
+            tp = layer.tensor_products[k - 1]
+            gp, gx = _ops.tp_bwd_rows_acc(gt, p, x, w, tp.in1_l_max, tp.in2_l_max, tp.out_l_max, tp.in1_features,
+                                          tp.shared_weights, res1=g, res2=gx, inplace2=True)
+            if k > 1:
+                gt = layer.product_linears[k - 1].input_grad(gp)
+            else:
+                gx = layer.product_linears[0].input_grad(gp, residual=gx)
+        return gx, None
+
+
+def product_applies(layer, x: Tensor, atom_types: Optional[Tensor]) -> bool:
+    return (not layer.path_reduced and layer.step0_weight_index is None and
+            all(tp.shared_weights and tp.in1_features == tp.in2_features and not tp.symmetric_product
+                for tp in layer.tensor_products) and applies(layer, x))
+
+
+def product_block(layer, x: Tensor) -> Tensor:
+    return _ProductBlock.apply(x, layer)
+
+
+class _GatedBlock(torch.autograd.Function):
+    """EquivariantGatedLayer: out = L_out(gate(L_val(x), act(L_gate(x_0)))) + x.
+
+    Backward, given g: g_gated = L_out^T g; (g_val, g_pre) = gate^T; gx = L_val^T g_val + g
+    (residual epilogue); gx_0 += L_gate^T g_pre (the scalar block only).
+    """
+
+    @staticmethod
+    def forward(ctx, x: Tensor, layer) -> Tensor:
+        values = layer.value_linear(x)
+        gl = layer.gate_linear
+        act_gemm = 1 if layer.gate_activation_name == "silu" else 0
+        pre, pre_act = _ops.dense_fwd(x[:, : layer.in_features], gl.weight, gl.bias, gl._scale, act_gemm)
+        act = 0 if act_gemm else 1
+        gated = _ops.gate(values, pre, layer.l_max, act)
+        out = layer.output_linear(gated, residual=x)
+        ctx.layer = layer
+        ctx.acts = (act, act_gemm)
+        ctx.save_for_backward(values, pre, pre_act)
+        return out
+
+    @staticmethod
+    def backward(ctx, g: Tensor):
+        layer = ctx.layer
+        values, pre, pre_act = ctx.saved_tensors
+        act, act_gemm = ctx.acts
+        g = g.contiguous()
+        g_gated = layer.output_linear.input_grad(g)
+        g_values, g_pre = _ops.gate_bwd(g_gated, values, pre, layer.l_max, act, True, True)
+        gx = layer.value_linear.input_grad(g_values, residual=g)
+        gl = layer.gate_linear
+        gx[:, : layer.in_features] += _ops.dense_bwd(g_pre, pre_act, gl.weight, gl._scale, act_gemm)
+        return gx, None
+
+
+def gated_block(layer, x: Tensor) -> Tensor:
+    return _GatedBlock.apply(x, layer)

@@ -17,6 +17,7 @@ import torch.nn.functional as F
 from flashcart_amd import o3
 from flashcart_amd.o3 import _ops
 from flashcart_amd.o3._graph import GraphCSR
+from flashcart_amd.nn import fused
 
 SILU_SCALE = 1.6765324703310907      # reference nn/layers.py:23
 SIGMOID_SCALE = 1.8462285453386054   # reference nn/layers.py:59
@@ -291,6 +292,9 @@ class EquivariantGatedLayer(nn.Module):
         if node_feats.shape[-1] != self.in_dim:
             raise RuntimeError(f"Incorrect last dimension for node_feats. Expected {self.in_dim}, "
                                f"got {node_feats.shape[-1]}.")
+        if fused.applies(self, node_feats):
+            # frozen parameters: one Function whose backward sums gradients inside kernels
+            return fused.gated_block(self, node_feats)
         values = self.value_linear(node_feats)
         if self.gate_activation_name == "silu":  # activation fused into the gate GEMM
             pre, act = self.gate_linear(node_feats[:, : self.in_features], act=1), 0
@@ -414,6 +418,10 @@ class ProductLayer(nn.Module):
             self.step0_weight_index = None
 
     def forward(self, node_feats: torch.Tensor, atom_types: Optional[torch.Tensor] = None) -> torch.Tensor:
+        if fused.product_applies(self, node_feats, atom_types):
+            # frozen parameters: one Function whose backward sums gradients inside kernels
+            output = fused.product_block(self, node_feats)
+            return self.layer_norm(output) if self.layer_norm is not None else output
         output = None
         product_feats = node_feats
         for k in range(self.correlation):

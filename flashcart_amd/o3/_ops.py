@@ -451,6 +451,42 @@ def _tp_backward(ctx, grad):
 tp_fwd.register_autograd(_tp_backward, setup_context=_tp_setup)
 
 
+def tp_bwd_rows_acc(grad_out: Tensor, in1: Tensor, in2: Tensor, weights: Tensor, in1_l_max: int, in2_l_max: int,
+                    out_l_max: int, features: int, shared_weights: bool, res1: Optional[Tensor] = None,
+                    res2: Optional[Tensor] = None, alpha: float = 1.0, inplace1: bool = False,
+                    inplace2: bool = False) -> Tuple[Tensor, Tensor]:
+    """(pad(res1) + dL/d in1, pad(res2) + dL/d in2) of a node-wise product with per-path
+    outputs and in1_features == in2_features (``fc_tp_bwd_rows_acc``; outside autograd).
+
+    ``res1`` / ``res2`` hold gradients of the leading rank blocks of in1 / in2 from other
+    consumers (any whole number of components per row, zero above). With ``inplace1`` /
+    ``inplace2``, a residual as wide as its operand is accumulated into and returned."""
+    go = _lib.contig("grad_out", grad_out)
+    in1 = _lib.contig("in1", in1)
+    in2 = _lib.contig("in2", in2)
+    w = _lib.contig("weights", weights)
+    C = int(features)
+
+    def prep(name, res, like, l_max, inplace):
+        full = (l_max + 1) ** 2
+        if res is None:
+            return None, 0, torch.empty_like(like)
+        res = _lib.contig(name, res)
+        comps = res.shape[-1] // C
+        if res.dim() != 2 or res.shape[0] != like.shape[0] or comps * C != res.shape[-1] or comps > full:
+            raise RuntimeError(f"{name} of shape {tuple(res.shape)} does not match an operand of shape "
+                               f"{tuple(like.shape)} with {C} channels.")
+        return res, comps, (res if inplace and comps == full else torch.empty_like(like))
+
+    r1, c1, g1 = prep("res1", res1, in1, in1_l_max, inplace1)
+    r2, c2, g2 = prep("res2", res2, in2, in2_l_max, inplace2)
+    desc = _lib.tp_desc(in1_l_max, in2_l_max, out_l_max, C, C, False, shared_weights, False)
+    _lib_call("fc_tp_bwd_rows_acc", desc, in1.shape[0], go.data_ptr(), in1.data_ptr(), in2.data_ptr(), w.data_ptr(),
+              float(alpha), _lib.ptr(r1), int(c1), _lib.ptr(r2), int(c2), g1.data_ptr(), g2.data_ptr(),
+              _lib.stream_of(in1))
+    return g1, g2
+
+
 # ---------------------------------------------------------------------------
 # Equivariant linear map
 # ---------------------------------------------------------------------------

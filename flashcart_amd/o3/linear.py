@@ -85,6 +85,13 @@ class LinearLayer(nn.Module):
         return _ops.linear_fwd(x, list(self.weight), self.in_l_max, self.out_l_max, self.in_features,
                                self.out_features, self.in_paths, self._scale_list, float(alpha), residual)
 
+    def input_grad(self, grad_out: torch.Tensor, alpha: float = 1.0,
+                   residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Gradient of ``forward`` wrt its input (the MFMA dgrad, outside autograd), plus
+        ``residual`` (a tensor of the input's shape) added in the GEMM epilogue."""
+        return _ops.linear_bwd(grad_out, list(self.weight), self.in_l_max, self.out_l_max, self.in_features,
+                               self.out_features, self.in_paths, self._scale_list, float(alpha), residual)
+
     def extra_repr(self) -> str:
         return (f"in_l_max={self.in_l_max}, out_l_max={self.out_l_max}, in_features={self.in_features}, "
                 f"out_features={self.out_features}, in_paths={self.in_paths}, out_dim={self.out_dim}, "

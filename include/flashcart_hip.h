@@ -160,6 +160,21 @@ int fc_tp_bwd(const fc_tp_desc* desc, const fc_csr* graph, int64_t n_rows, const
               float* grad_in1, float* grad_in2, float* grad_weights, float* workspace,
               int64_t workspace_floats, void* stream);
 
+/* Input gradients of a node-wise product (graph == NULL mode of fc_tp_bwd) added to
+ * gradients that other consumers of the operands already produced:
+ *   grad_in1 = pad(res1) + dL/d in1,   grad_in2 = pad(res2) + dL/d in2
+ * res1 / res2 hold the first res1_comps / res2_comps rank components of each row (row
+ * width comps * C, the leading rank blocks of the operand's layout), zero above; NULL
+ * adds nothing, and a residual may be the very gradient buffer it is added to. Needs
+ * in1_features == in2_features and per-path outputs (reduce_paths == 0); NULL gradient
+ * pointers are not computed. No counterpart in the reference, where autograd adds the
+ * gradients of an operand used by several products; its caller is the fused backward
+ * of the product block (inference with frozen parameters). */
+int fc_tp_bwd_rows_acc(const fc_tp_desc* desc, int64_t n_rows, const float* grad_out, const float* in1,
+                       const float* in2, const float* weights, float alpha, const float* res1,
+                       int32_t res1_comps, const float* res2, int32_t res2_comps, float* grad_in1,
+                       float* grad_in2, void* stream);
+
 /* ------------------------------------------------------------------------- */
 /* Equivariant linear map on MFMA: replaces torch.ops.flashcart.linear_fwd and  */
 /* the input-gradient branch of linear_bwd (reference src/flashcart/o3/         */

@@ -33,10 +33,13 @@ def _model(cfg, seed=1234):
     return m
 
 
-def _check(model, graph, cfg):
+def _check(model, graph, cfg, frozen=False):
+    """``frozen``: parameters without gradients, which routes the gated and product blocks
+    through their fused inference backward (flashcart_amd/nn/fused.py)."""
     sd = model.state_dict()
     ref = OM.predict(sd, model.to_model_config(), graph.to_dict(), compute_forces=True)
     m = model.to(DEV)
+    m.requires_grad_(not frozen)
     out = m.predict(graph.to(DEV), compute_forces=True)
     e_ref = ref["energy"]
     assert_close(out["energy"], e_ref, E_REL, 1e-6, "energy")
@@ -46,30 +49,59 @@ def _check(model, graph, cfg):
     return out, ref
 
 
-def test_fcc_alloy_L3():
+@pytest.mark.parametrize("frozen", [False, True])
+def test_fcc_alloy_L3(frozen):
     numbers, pos, cell, pbc = fcc_alloy(2, 2, 2, seed=3)
     cfg = model_config(["Cu", "Ni", "Fe", "Cr"], 16, 3, avg_neighbors=42.0)
     g = AtomicGraph.from_arrays(numbers, pos, cfg["elements"], 5.0, cell=cell, pbc=pbc)
-    _check(_model(cfg), g, cfg)
+    _check(_model(cfg), g, cfg, frozen)
 
 
-def test_water_L2():
+@pytest.mark.parametrize("frozen", [False, True])
+def test_water_L2(frozen):
     numbers, pos, cell, pbc = water_box(16, seed=1)
     cfg = model_config(["H", "O"], 16, 2, avg_neighbors=20.0)
     g = AtomicGraph.from_arrays(numbers, pos, cfg["elements"], 5.0, cell=cell, pbc=pbc)
-    _check(_model(cfg, seed=7), g, cfg)
+    _check(_model(cfg, seed=7), g, cfg, frozen)
 
 
-def test_molecule_batch_L2():
+@pytest.mark.parametrize("frozen", [False, True])
+def test_molecule_batch_L2(frozen):
     mols = molecules(4, 5, 12, seed=2)
     cfg = model_config(["H", "C", "N", "O"], 8, 2, avg_neighbors=6.0)
     gs = [AtomicGraph.from_arrays(z, p, cfg["elements"], 5.0) for z, p in mols]
-    out, ref = _check(_model(cfg, seed=5), batch_graphs(gs), cfg)
+    out, ref = _check(_model(cfg, seed=5), batch_graphs(gs), cfg, frozen)
     assert out["energy"].shape[0] == 4
 
 
-def test_channels_128_L3():
+@pytest.mark.parametrize("frozen", [False, True])
+def test_channels_128_L3(frozen):
     numbers, pos, cell, pbc = fcc_alloy(2, 2, 2, seed=4)
     cfg = model_config(["Cu", "Ni", "Fe", "Cr"], 128, 3, avg_neighbors=42.0)
     g = AtomicGraph.from_arrays(numbers, pos, cfg["elements"], 5.0, cell=cell, pbc=pbc)
-    _check(_model(cfg, seed=11), g, cfg)
+    _check(_model(cfg, seed=11), g, cfg, frozen)
+
+
+@pytest.mark.parametrize("frozen", [False, True])
+def test_silu_gate_correlation2(frozen, monkeypatch):
+    """SiLU gate (activation fused into the gate GEMM) and a two-step product; with frozen
+    parameters both blocks must take the fused backward."""
+    from flashcart_amd.nn import fused
+    calls = {"product": 0, "gated": 0}
+    real_p, real_g = fused.product_block, fused.gated_block
+
+    def count(name, fn):
+        def wrapped(*a):
+            calls[name] += 1
+            return fn(*a)
+        return wrapped
+
+    monkeypatch.setattr(fused, "product_block", count("product", real_p))
+    monkeypatch.setattr(fused, "gated_block", count("gated", real_g))
+    numbers, pos, cell, pbc = fcc_alloy(2, 2, 2, seed=6)
+    cfg = model_config(["Cu", "Ni", "Fe", "Cr"], 16, 3, avg_neighbors=42.0)
+    cfg.update(gate_activation="silu", correlation=2)
+    g = AtomicGraph.from_arrays(numbers, pos, cfg["elements"], 5.0, cell=cell, pbc=pbc)
+    _check(_model(cfg, seed=13), g, cfg, frozen)
+    n_layers = cfg["n_interactions"]
+    assert calls == ({"product": n_layers, "gated": n_layers} if frozen else {"product": 0, "gated": 0})

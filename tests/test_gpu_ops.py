@@ -130,6 +130,43 @@ def test_tp_rows(case):
     _tp_case(conv=False, n=300, **case)
 
 
+@pytest.mark.parametrize("l1,l2,lo,comps1,shared", [(3, 3, 3, 9, True), (3, 3, 2, 16, True), (2, 2, 2, 4, False),
+                                                    (3, 3, 0, 1, True)])
+def test_tp_rows_accumulate(l1, l2, lo, comps1, shared):
+    """fc_tp_bwd_rows_acc: input gradients of the node-wise product plus residual gradients
+    (res1 over the leading comps1 components of in1, res2 over all of in2, accumulated in
+    place), against the float64 oracle's vector-Jacobian product plus the residuals."""
+    ops = _ops()
+    torch.manual_seed(l1 + 3 * lo + comps1)
+    n, C = 300, 32
+    from oracle.cartesian import enumerate_paths
+    P = len(enumerate_paths(l1, l2, lo, False))
+    in1 = torch.randn(n, (l1 + 1) ** 2 * C, dtype=torch.float64, requires_grad=True)
+    in2 = torch.randn(n, (l2 + 1) ** 2 * C, dtype=torch.float64, requires_grad=True)
+    w = torch.randn(P * C, dtype=torch.float64) if shared else torch.randn(n, P * C, dtype=torch.float64)
+    ref = O.tensor_product(in1, in2, w, None, None, l1, l2, lo, C, C, False, shared, False)
+    g = torch.randn_like(ref)
+    q1, q2 = torch.autograd.grad(ref, [in1, in2], g)
+    r1, r2 = q1, q2
+    res1 = torch.randn(n, comps1 * C, dtype=torch.float64)
+    res2 = torch.randn(n, (l2 + 1) ** 2 * C, dtype=torch.float64)
+    r1 = r1.clone()
+    r1[:, : comps1 * C] += res1
+    r2 = r2 + res2
+    d = [t.detach().float().to(DEV) for t in (in1, in2, w, g, res1, res2)]
+    res1_dev = d[4].clone()
+    g1, g2 = ops.tp_bwd_rows_acc(d[3], d[0], d[1], d[2], l1, l2, lo, C, shared, res1=d[4], res2=d[5],
+                                 inplace2=True)
+    assert g2.data_ptr() == d[5].data_ptr(), "full-width residual must be accumulated in place"
+    assert torch.equal(d[4], res1_dev), "res1 must not be modified"
+    assert_close(g1, r1, 2e-5, 2e-5 * (float(r1.abs().max()) + 1.0), "rows acc grad in1")
+    assert_close(g2, r2, 2e-5, 2e-5 * (float(r2.abs().max()) + 1.0), "rows acc grad in2")
+    # no residuals: plain input gradients
+    h1, h2 = ops.tp_bwd_rows_acc(d[3], d[0], d[1], d[2], l1, l2, lo, C, shared)
+    assert_close(h1, q1, 2e-5, 2e-5 * (float(q1.abs().max()) + 1.0), "rows grad in1")
+    assert_close(h2, q2, 2e-5, 2e-5 * (float(q2.abs().max()) + 1.0), "rows grad in2")
+
+
 @pytest.mark.parametrize("cfg", [(0, 0, 16, 16, None), (2, 2, 32, 16, None), (3, 3, 128, 128, [3, 5, 5, 4]),
                                  (2, 3, 64, 64, None), (3, 1, 8, 24, [1, 2, 3, 1])])
 def test_linear(cfg):
