@@ -108,6 +108,9 @@ class FlashCartCalculator(_CalculatorBase):
             if checkpoint is None:
                 raise ValueError("Provide either checkpoint or model.")
             model = FlashCartPotential.from_checkpoint(checkpoint, device=device)
+            # the calculator's own copy only evaluates: frozen parameters select the fused
+            # inference backward of the gated and product blocks
+            model.requires_grad_(False)
         elif device is not None:
             model = model.to(device)
         if compile_mode is not None or pad_n_atoms > 0 or pad_n_edges > 0:

@@ -57,14 +57,15 @@ struct EdgeOps {
   float x[D1], y[D2], w[NP];
 };
 
-template <int D1, int D2, int NP, bool CONV, bool BC2>
+template <int D1, int D2, int NP, bool CONV, bool BC2, bool LOADY = true>
 __device__ __forceinline__ void load_edge(const TPArgs& g, int64_t e, int f1, int f2, int fw, bool active,
                                           EdgeOps<D1, D2, NP>& o) {
   const int64_t j = CONV ? (int64_t)g.idx_j[e] : e;
   const int64_t s1 = (int64_t)D1 * g.F1;
 #pragma unroll
   for (int u = 0; u < D1; ++u) o.x[u] = active ? g.in1[j * s1 + u * g.F1 + f1] : 0.f;
-  if constexpr (BC2) {
+  if constexpr (!LOADY) {
+  } else if constexpr (BC2) {
 #pragma unroll
     for (int u = 0; u < D2; ++u) o.y[u] = g.in2[e * D2 + u];
   } else {
@@ -77,8 +78,58 @@ __device__ __forceinline__ void load_edge(const TPArgs& g, int64_t e, int f1, in
   for (int i = 0; i < NP; ++i) o.w[i] = active ? wr[i * g.C + fw] : 0.f;
 }
 
+// Per-edge coupling matrices in LDS. With a single in2 channel (BC2) the matrices
+// A_p(y_e) are the same for every channel of an edge, so forming them in each lane
+// repeats the work 64 times per wave. Instead, lanes 0..n-1 of each wave form them for
+// a chunk of n edges (each wave a contiguous share of the paths) into LDS, and the
+// edge loop reads them back as broadcast LDS loads. Each path's block is padded to a
+// multiple of 4 floats (16-byte aligned).
+template <int L1, int L2, int LO, bool SYM>
+struct AmatLayout {
+  using PL = PathList<L1, L2, LO, SYM>;
+  template <int I>
+  static constexpr int size() {
+    constexpr PathDesc P = PL::at(I);
+    return (TPPath<P.r1, P.r2, P.lo>::NA + 3) & ~3;
+  }
+  template <int I>
+  static constexpr int off() {
+    if constexpr (I == 0) return 0;
+    else return off<I - 1>() + size<I - 1>();
+  }
+  static constexpr int total = off<PL::NP>();
+  // edges per chunk: two chunk buffers within 32 KiB
+  static constexpr int chunk = total * 16 * 2 * 4 <= 32768 ? 16 : (32768 / (total * 2 * 4) > 0 ? 32768 / (total * 2 * 4) : 1);
+};
+
+// Lanes 0..n-1 of each wave form the coupling matrices of edge c0 + lane for this
+// wave's share of the paths.
+template <int L1, int L2, int LO, bool SYM>
+__device__ __forceinline__ void fill_amat(const float* __restrict__ in2, int64_t c0, int n, float* a, int lane,
+                                          int wave, int nw) {
+  using PL = PathList<L1, L2, LO, SYM>;
+  using AL = AmatLayout<L1, L2, LO, SYM>;
+  constexpr int D2 = ncomp(L2);
+  if (lane >= n) return;
+  float y[D2];
+#pragma unroll
+  for (int u = 0; u < D2; ++u) y[u] = in2[(c0 + lane) * D2 + u];
+  float* ae = a + lane * AL::total;
+  const int p0 = wave * PL::NP / nw, p1 = (wave + 1) * PL::NP / nw;
+  static_for<PL::NP>([&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    if (i >= p0 && i < p1) {
+      constexpr PathDesc P = PL::at(i);
+      TPPath<P.r1, P.r2, P.lo>::amat(y + P.r2 * P.r2, ae + AL::template off<i>());
+    }
+  });
+}
+
 template <int L1, int L2, int LO, bool SYM, bool CONV, bool BC2>
 __global__ void __launch_bounds__(256) tp_fwd_kernel(TPArgs g) {
+  // The forward keeps the per-lane coupling matrices: it is bound by the gathered
+  // operand stream, and staging the matrices in LDS (as the backward does) measured
+  // slower here (chunk barriers and broadcast LDS reads on the critical path).
   using CF = TPConfig<L1, L2, LO, SYM>;
   using PL = typename CF::PL;
   constexpr int D1 = CF::D1, D2 = CF::D2, NOUT = CF::NOUT, NP = CF::NP;
@@ -166,24 +217,32 @@ __device__ __forceinline__ float wave_reduce_halving(float (&v)[N], int lane) {
   return r;
 }
 
-// Backward (vector-Jacobian product) of tp_fwd_kernel.
-//   grad_w[item, p, f]  = sum_a go[a,p,f] t_p[a]            (t = A_p x)
-//   u_p[a]              = w[p,f] go[a,p,f]
-//   gx[b]              += sum_a A_p[a,b] u_p[a]              (conv: per-edge message)
-//   gy[c]              += sum_{a,b} B_p[a,b,c] u_p[a] x[b]
+// Backward (vector-Jacobian product) of tp_fwd_kernel. With v_p = A_p^T go_p (one
+// transposed product shared by the weight and in1 gradients):
+//   grad_w[item, p, f]  = sum_a go[a,p,f] (A_p x)[a] = sum_b v_p[b] x[b]
+//   gx[b]              += w[p,f] v_p[b]                      (conv: per-edge message)
+//   gy[c]              += sum_{a,b} B_p[a,b,c] go[a,p,f] (w[p,f] x[b])
 // Channel-broadcast operands (F == 1) get their gradient summed over channels: a
 // halving butterfly in each wave, then a cross-wave sum through LDS in a fixed
-// order, so the result is deterministic.
-constexpr int BWD_CHUNK = 16;
+// order, so the result is deterministic. Edges are processed in chunks of
+// bwd_chunk<...>() edges (the LDS coupling-matrix chunk in BC2 convolutions).
+template <int L1, int L2, int LO, bool SYM, bool CONV, bool BC2>
+__host__ __device__ constexpr int bwd_chunk() {
+  return (CONV && BC2) ? AmatLayout<L1, L2, LO, SYM>::chunk : 16;
+}
 
 template <int L1, int L2, int LO, bool SYM, bool CONV, bool BC2>
 __global__ void __launch_bounds__(256, 2) tp_bwd_kernel(TPArgs g) {
   using CF = TPConfig<L1, L2, LO, SYM>;
   using PL = typename CF::PL;
+  using AL = AmatLayout<L1, L2, LO, SYM>;
   constexpr int D1 = CF::D1, D2 = CF::D2, NOUT = CF::NOUT, NP = CF::NP;
   constexpr int R1 = pow2_at_least(D1), R2 = pow2_at_least(D2);
   constexpr int SH1 = 6 - log2_exact(R1), SH2 = 6 - log2_exact(R2);
-  extern __shared__ float red_lds[];  // [BWD_CHUNK][waves][D1 + D2], only when reducing over channels
+  constexpr bool LDSA = CONV && BC2;
+  constexpr int CH = bwd_chunk<L1, L2, LO, SYM, CONV, BC2>();
+  extern __shared__ float red_lds[];  // [CH][waves][D1 + D2], only when reducing over channels
+  __shared__ __align__(16) float a_lds[LDSA ? 2 * CH * AL::total : 1];
 
   const int64_t row = CONV ? xcd_row(g.n_rows) : (int64_t)blockIdx.x;
   if (row >= g.n_rows) return;
@@ -222,12 +281,22 @@ __global__ void __launch_bounds__(256, 2) tp_bwd_kernel(TPArgs g) {
   int64_t e0 = row, e1 = row + 1;
   if constexpr (CONV) { e0 = g.rowptr[row]; e1 = g.rowptr[row + 1]; }
   EdgeOps<D1, D2, NP> cur, nxt;
-  if (e0 < e1) load_edge<D1, D2, NP, CONV, BC2>(g, e0, f1, f2, fa, active, nxt);
-  for (int64_t c0 = e0; c0 < e1; c0 += BWD_CHUNK) {
-    const int64_t c1 = c0 + BWD_CHUNK < e1 ? c0 + BWD_CHUNK : e1;
+  if (e0 < e1) {
+    load_edge<D1, D2, NP, CONV, BC2, !LDSA>(g, e0, f1, f2, fa, active, nxt);
+    if constexpr (LDSA) {
+      fill_amat<L1, L2, LO, SYM>(g.in2, e0, e1 - e0 < CH ? (int)(e1 - e0) : CH, a_lds, lane, wave, nw);
+      __syncthreads();
+    }
+  }
+  int buf = 0;
+  for (int64_t c0 = e0; c0 < e1; c0 += CH) {
+    const int64_t c1 = c0 + CH < e1 ? c0 + CH : e1;
+    const int n_next = e1 - c1 < CH ? (int)(e1 - c1) : CH;
+    const float* ab = a_lds + buf * CH * AL::total;
     for (int64_t e = c0; e < c1; ++e) {
       cur = nxt;
-      if (e + 1 < e1) load_edge<D1, D2, NP, CONV, BC2>(g, e + 1, f1, f2, fa, active, nxt);
+      if (e + 1 < e1) load_edge<D1, D2, NP, CONV, BC2, !LDSA>(g, e + 1, f1, f2, fa, active, nxt);
+      const float* ae = ab + (int)(e - c0) * AL::total;
       float gx[R1], gy[R2];
 #pragma unroll
       for (int u = 0; u < R1; ++u) gx[u] = 0.f;
@@ -237,19 +306,39 @@ __global__ void __launch_bounds__(256, 2) tp_bwd_kernel(TPArgs g) {
         constexpr int i = decltype(ic)::value;
         constexpr PathDesc P = PL::at(i);
         using T = TPPath<P.r1, P.r2, P.lo>;
-        float A[T::NA], t[T::NO], u[T::NO];
-        T::amat(cur.y + P.r2 * P.r2, A);
-        if (needw) {
-          T::apply(A, cur.x + P.r1 * P.r1, t);
-          float s = 0.f;
+        const float* xp = cur.x + P.r1 * P.r1;
+        float gop[T::NO];
 #pragma unroll
-          for (int a = 0; a < T::NO; ++a) s = fmaf(go[PL::out_index(i, a)], t[a], s);
-          if (active) g.grad_w[e * sw + i * C + f] = s;
+        for (int a = 0; a < T::NO; ++a) gop[a] = go[PL::out_index(i, a)];
+        if (needw || need1) {
+          // v = A_p^T go_p serves both: grad_w = <go_p, A_p x> = <v, x>, gx += w_p v
+          float v[T::N1];
+#pragma unroll
+          for (int b = 0; b < T::N1; ++b) v[b] = 0.f;
+          if constexpr (LDSA) {
+            T::apply_t(ae + AL::template off<i>(), gop, v);
+          } else {
+            float A[T::NA];
+            T::amat(cur.y + P.r2 * P.r2, A);
+            T::apply_t(A, gop, v);
+          }
+          if (needw) {
+            float s = 0.f;
+#pragma unroll
+            for (int b = 0; b < T::N1; ++b) s = fmaf(v[b], xp[b], s);
+            if (active) g.grad_w[e * sw + i * C + f] = s;
+          }
+          if (need1) {
+#pragma unroll
+            for (int b = 0; b < T::N1; ++b) gx[P.r1 * P.r1 + b] = fmaf(cur.w[i], v[b], gx[P.r1 * P.r1 + b]);
+          }
         }
+        if (need2) {  // gy += B_p(go_p, w_p x)
+          float xw[T::N1];
 #pragma unroll
-        for (int a = 0; a < T::NO; ++a) u[a] = cur.w[i] * go[PL::out_index(i, a)];
-        if (need1) T::apply_t(A, u, gx + P.r1 * P.r1);
-        if (need2) T::vjp2(u, cur.x + P.r1 * P.r1, gy + P.r2 * P.r2);
+          for (int b = 0; b < T::N1; ++b) xw[b] = cur.w[i] * xp[b];
+          T::vjp2(gop, xw, gy + P.r2 * P.r2);
+        }
       });
       const int slot = (int)(e - c0);
       if (need1) {
@@ -274,6 +363,11 @@ __global__ void __launch_bounds__(256, 2) tp_bwd_kernel(TPArgs g) {
         }
       }
     }
+    if (LDSA && n_next > 0) {
+      // the other buffer was last read in the previous chunk, before this chunk's barrier;
+      // the barrier below (or the reduction's first one) publishes it
+      fill_amat<L1, L2, LO, SYM>(g.in2, c1, n_next, a_lds + (buf ^ 1) * CH * AL::total, lane, wave, nw);
+    }
     if (red1 || red2) {
       __syncthreads();
       const int n = (int)(c1 - c0);
@@ -289,7 +383,10 @@ __global__ void __launch_bounds__(256, 2) tp_bwd_kernel(TPArgs g) {
         }
       }
       __syncthreads();
+    } else if (LDSA && n_next > 0) {
+      __syncthreads();
     }
+    buf ^= 1;
   }
 }
 
@@ -319,24 +416,34 @@ __global__ void __launch_bounds__(256) tp_bwd_rows_kernel(TPArgs g) {
     constexpr int i = decltype(ic)::value;
     constexpr PathDesc P = PL::at(i);
     using T = TPPath<P.r1, P.r2, P.lo>;
-    float A[T::NA], u[T::NO];
+    const float* xp = x + P.r1 * P.r1;
     float go[T::NO];
 #pragma unroll
     for (int a = 0; a < T::NO; ++a) go[a] = g.alpha * gor[(int64_t)PL::out_index(i, a) * C];
     const float w = wr[i * C];
-    T::amat(y + P.r2 * P.r2, A);
-    if (needw) {
-      float t[T::NO];
-      T::apply(A, x + P.r1 * P.r1, t);
-      float s = 0.f;
+    if (needw || need1) {  // v = A_p^T go_p: grad_w = <v, x>, gx += w v
+      float A[T::NA], v[T::N1];
+      T::amat(y + P.r2 * P.r2, A);
 #pragma unroll
-      for (int a = 0; a < T::NO; ++a) s = fmaf(go[a], t[a], s);
-      g.grad_w[row * (int64_t)NP * C + i * C + f] = s;
+      for (int b = 0; b < T::N1; ++b) v[b] = 0.f;
+      T::apply_t(A, go, v);
+      if (needw) {
+        float s = 0.f;
+#pragma unroll
+        for (int b = 0; b < T::N1; ++b) s = fmaf(v[b], xp[b], s);
+        g.grad_w[row * (int64_t)NP * C + i * C + f] = s;
+      }
+      if (need1) {
+#pragma unroll
+        for (int b = 0; b < T::N1; ++b) gx[P.r1 * P.r1 + b] = fmaf(w, v[b], gx[P.r1 * P.r1 + b]);
+      }
     }
+    if (need2) {  // gy += B_p(go_p, w x)
+      float xw[T::N1];
 #pragma unroll
-    for (int a = 0; a < T::NO; ++a) u[a] = w * go[a];
-    if (need1) T::apply_t(A, u, gx + P.r1 * P.r1);
-    if (need2) T::vjp2(u, x + P.r1 * P.r1, gy + P.r2 * P.r2);
+      for (int b = 0; b < T::N1; ++b) xw[b] = w * xp[b];
+      T::vjp2(go, xw, gy + P.r2 * P.r2);
+    }
   });
   // residual gradients: each element is read and then written by this thread only
   if (need1) {
@@ -369,14 +476,19 @@ int launch_tp(const TPArgs& g, bool conv, bool bwd, hipStream_t stream) {
   const bool bc2 = conv && g.F2 == 1;
   if (bwd) {
     const bool reduce = (g.grad_in1 && g.F1 == 1 && g.C > 1) || (g.grad_in2 && g.F2 == 1 && g.C > 1);
-    const size_t lds = reduce ? sizeof(float) * BWD_CHUNK * (threads / 64) * (ncomp(L1) + ncomp(L2)) : 0;
+    const size_t per_edge = reduce ? sizeof(float) * (threads / 64) * (ncomp(L1) + ncomp(L2)) : 0;
     if (conv) {
-      if (bc2) hipLaunchKernelGGL((tp_bwd_kernel<L1, L2, LO, SYM, true, true>), grid, block, lds, stream, g);
-      else hipLaunchKernelGGL((tp_bwd_kernel<L1, L2, LO, SYM, true, false>), grid, block, lds, stream, g);
+      if (bc2)
+        hipLaunchKernelGGL((tp_bwd_kernel<L1, L2, LO, SYM, true, true>), grid, block,
+                           (per_edge * bwd_chunk<L1, L2, LO, SYM, true, true>()), stream, g);
+      else
+        hipLaunchKernelGGL((tp_bwd_kernel<L1, L2, LO, SYM, true, false>), grid, block,
+                           (per_edge * bwd_chunk<L1, L2, LO, SYM, true, false>()), stream, g);
     } else if (g.F1 == g.C && g.F2 == g.C && !g.reduced) {
       hipLaunchKernelGGL((tp_bwd_rows_kernel<L1, L2, LO, SYM>), grid, block, 0, stream, g);
     } else {
-      hipLaunchKernelGGL((tp_bwd_kernel<L1, L2, LO, SYM, false, false>), grid, block, lds, stream, g);
+      hipLaunchKernelGGL((tp_bwd_kernel<L1, L2, LO, SYM, false, false>), grid, block,
+                         (per_edge * bwd_chunk<L1, L2, LO, SYM, false, false>()), stream, g);
     }
   } else {
     if (conv) {
