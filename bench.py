@@ -276,9 +276,14 @@ def run_other_workload(name, args, dev):
             q.requires_grad_(False)
         model = model.to(dev)
         gdev = graph.to(dev)
-        dt, out = _timed(lambda: model.predict(gdev, compute_forces=True), args.steps, args.warmup, dev)
+        dt_eager, _ = _timed(lambda: model.predict(gdev, compute_forces=True), args.steps, args.warmup, dev)
+        # fixed topology: the whole prediction replayed as one HIP graph (predict(use_compile=True))
+        dt, out = _timed(lambda: model.predict(gdev, compute_forces=True, use_compile=True), args.steps,
+                         args.warmup, dev)
         res.update({"metric": "atom-steps/s (energy+forces)", "value": n_atoms * args.steps / dt,
                     "unit": "atom-steps/s", "ms_per_step": 1e3 * dt / args.steps,
+                    "mode": "HIP graph replay of predict (use_compile=True)",
+                    "eager": {"value": n_atoms * args.steps / dt_eager, "ms_per_step": 1e3 * dt_eager / args.steps},
                     "config": {"n_atoms": n_atoms, "n_graphs": graph.num_graphs,
                                "n_edges": int(graph.edge_index.shape[1]), "channels": C, "l_max_edge_attrs": L}})
         if not args.no_cpu_baseline:

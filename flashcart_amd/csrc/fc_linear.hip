@@ -8,9 +8,10 @@
 //
 // Tiling (gfx950, wave64): 256-thread workgroups, BM x BN output tiles, waves arranged
 // WM x WN, each wave accumulating (BM/WM) x (BN/WN) with v_mfma_f32_32x32x2f32 blocks.
-// K advances in steps of 32 through LDS (double-buffered for N > 64, one barrier per
-// step): the next step's global loads are in flight while the current step's 16 MFMA
-// k-pairs run. Full K steps load through one branch-free path (row pointers clamped
+// K advances in steps of 32 through LDS (a single buffer with two barriers per step in
+// the tile shapes launched, which leaves room for four workgroups per CU): the next
+// step's global loads are in flight while the current step's 16 MFMA k-pairs run.
+// Full K steps load through one branch-free path (row pointers clamped
 // to valid rows and masked afterwards): per-lane divergence between vector and scalar
 // loads made the compiler wait on outstanding loads inside the load sequence.
 // A rows (and B rows when the weight is k-contiguous, the forward) sit in LDS in the
@@ -393,8 +394,12 @@ int launch_gemm(GemmBatch gb, int n_ranks, hipStream_t s) {
     if (gb.r[l].M < 0) return FC_ERR_SHAPE;
   }
   if (max_m == 0 || max_n == 0 || n_ranks == 0) return FC_OK;
-  if (max_n <= 64) return launch_gemm_cfg<128, 64, 4, 1, 1>(gb, n_ranks, s);
-  return launch_gemm_cfg<128, 128, 2, 2, 2>(gb, n_ranks, s);
+  // Measured on the model's shapes (M = n (2l+1) rows, K and N of 128 or paths x 128):
+  // 128 x 64 tiles (waves stacked along M) for the input gradient and narrow maps, 64 x 128
+  // (waves side by side along N) for the forward. Both hold four workgroups per CU, whose
+  // prologues and epilogues overlap each other's MFMA work better than two 128 x 128 tiles.
+  if (max_n <= 64 || !gb.trans_b) return launch_gemm_cfg<128, 64, 4, 1, 1>(gb, n_ranks, s);
+  return launch_gemm_cfg<64, 128, 1, 4, 1>(gb, n_ranks, s);
 }
 
 // dst[r, off:off+width] = src ? src[r, off:off+width] : 0 (same row stride)

@@ -72,8 +72,9 @@ class AtomicGraph:
 
     def to_dict(self) -> Dict[str, object]:
         d = {k: v for k, v in self.__dict__.items() if v is not None}
-        d.setdefault("use_shifts", bool(torch.any(self.pbc).item()) if torch.is_tensor(getattr(self, "pbc", None))
-                     else True)
+        if "use_shifts" not in d:  # (a device pbc tensor costs a synchronisation)
+            d["use_shifts"] = bool(torch.any(self.pbc).item()) if torch.is_tensor(getattr(self, "pbc", None)) \
+                else True
         return d
 
     @classmethod

@@ -105,3 +105,31 @@ def test_silu_gate_correlation2(frozen, monkeypatch):
     _check(_model(cfg, seed=13), g, cfg, frozen)
     n_layers = cfg["n_interactions"]
     assert calls == ({"product": n_layers, "gated": n_layers} if frozen else {"product": 0, "gated": 0})
+
+
+@pytest.mark.parametrize("frozen", [False, True])
+def test_predict_replay(frozen):
+    """predict(use_compile=True) captures the whole prediction as a HIP graph: replays with
+    new positions (and eager work and synchronisations in between) must match eager
+    predictions on the same inputs, energies, forces and stress alike."""
+    numbers, pos, cell, pbc = water_box(12, seed=4)
+    cfg = model_config(["H", "O"], 16, 2, avg_neighbors=20.0)
+    g = AtomicGraph.from_arrays(numbers, pos, cfg["elements"], 5.0, cell=cell, pbc=pbc).to(DEV)
+    m = _model(cfg, seed=17).to(DEV)
+    m.requires_grad_(not frozen)
+    gen = torch.Generator(device="cpu").manual_seed(0)
+    base = g.positions.clone()
+    for it in range(5):
+        g.positions = base + 0.02 * torch.randn(base.shape, generator=gen).to(DEV)
+        if it == 2:  # a new edge-list tensor: the CSR graph replays
+            g.edge_index = g.edge_index.clone()
+        if it == 3:  # modified in place (same contents): replays as well
+            g.edge_index.add_(0)
+        got = m.predict(g, compute_forces=True, compute_stress=True, use_compile=True)
+        junk = torch.randn(1000, 1000, device=DEV) @ torch.randn(1000, 1000, device=DEV)  # eager work between
+        torch.cuda.synchronize()
+        ref = m.predict(g, compute_forces=True, compute_stress=True)
+        del junk
+        for k in ("energy", "forces", "stress", "node_energies"):
+            assert_close(got[k], ref[k].double(), 1e-6, 1e-6 * (float(ref[k].abs().max()) + 1.0), f"replay {it} {k}")
+    assert len(m._replay_cache) == 1
