@@ -395,10 +395,13 @@ int launch_gemm(GemmBatch gb, int n_ranks, hipStream_t s) {
   }
   if (max_m == 0 || max_n == 0 || n_ranks == 0) return FC_OK;
   // Measured on the model's shapes (M = n (2l+1) rows, K and N of 128 or paths x 128):
-  // 128 x 64 tiles (waves stacked along M) for the input gradient and narrow maps, 64 x 128
+  // 128 x 64 tiles (waves stacked along M) for the wider input gradients, 64 x 128
   // (waves side by side along N) for the forward. Both hold four workgroups per CU, whose
   // prologues and epilogues overlap each other's MFMA work better than two 128 x 128 tiles.
-  if (max_n <= 64 || !gb.trans_b) return launch_gemm_cfg<128, 64, 4, 1, 1>(gb, n_ranks, s);
+  // Maps at most 64 wide (the 64-channel models, radial hidden layers) take 64 x 64
+  // tiles: twice the workgroups, so short-K launches fill the chip.
+  if (max_n <= 64) return launch_gemm_cfg<64, 64, 2, 2, 1>(gb, n_ranks, s);
+  if (!gb.trans_b) return launch_gemm_cfg<128, 64, 4, 1, 1>(gb, n_ranks, s);
   return launch_gemm_cfg<64, 128, 1, 4, 1>(gb, n_ranks, s);
 }
 
