@@ -311,6 +311,9 @@ def main():
                     help="cfg4_fcc25k (the metric's configuration) or one of the other BASELINE configurations")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only launch the dominant kernel (5x) and a 2 GiB device copy (5x), for counter runs")
+    ap.add_argument("--profile-step", action="store_true",
+                    help="two energy+forces steps on the first step graph, then a 2 GiB device copy (2x) "
+                         "for counter calibration, for per-kernel counter runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU runs are not part of it "
@@ -323,6 +326,21 @@ def main():
         run_other_workload(args.workload, args, dev)
         return
     numbers, pos, cell, pbc = make_system(*args.cells)
+    if args.profile_step:
+        sg = StepGraphs(numbers, pos, cell, pbc, ["Cu", "Ni", "Fe", "Cr"], 1)
+        g = sg.graph(0, dev)
+        model, _ = build_model(g.edge_index.shape[1] / len(numbers))
+        model = model.to(dev)
+        for _ in range(2):
+            model.predict(g, compute_forces=True)
+        src = torch.ones(2 ** 29, device=dev)  # 2 GiB
+        dst = torch.empty_like(src)
+        for _ in range(2):  # plain elementwise copy (reads and writes 2 GiB) for counter calibration
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize(dev)
+        print(json.dumps({"profile_step": True, "n_atoms": len(numbers), "n_edges": int(g.edge_index.shape[1]),
+                          "copy_bytes_each_way": src.numel() * 4}), flush=True)
+        return
     if args.kernel_only:
         sg = StepGraphs(numbers, pos, cell, pbc, ["Cu", "Ni", "Fe", "Cr"], 1)
         model, _ = build_model(43.0)
