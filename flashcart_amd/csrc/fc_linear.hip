@@ -536,12 +536,142 @@ extern "C" int fc_linear_dgrad(const fc_linear_desc* d, int64_t n, const float* 
   return FC_OK;
 }
 
+namespace fc {
+
+// ---- Wide output, K = 64: out (n x m) = scale * x (n x 64) @ W^T, W (m x 64), m >> 64 (the
+// radial MLP's output layer, m = paths x channels). Writing the output is as costly as the
+// MFMA work here, so each workgroup keeps its 128 x 64 block of x in LDS and walks the
+// output columns in chunks of 64: the next weight chunk is loaded while the current one
+// is multiplied, and the previous chunk's results are stored in between the MFMAs.
+// MFMA step s (of 32) contracts k = s in lanes 0-31 and k = 32 + s in lanes 32-63, so
+// rows sit in LDS in natural k order (a float4 from global memory is written as is, no
+// register shuffle) and a lane reads four steps with one 128-bit load; the pitch of 68
+// floats (17 x 16 B) keeps those reads conflict-free. Four waves stacked along the rows,
+// 32 x 64 outputs each per chunk.
+constexpr int WIDE_BM = 128, WIDE_BN = 64, WIDE_K = 64, WIDE_P = 68;
+
+// GUARD = false: every row and column of the block is in range (m a multiple of 64), so
+// the stores are unconditional and the compiler can count them as outstanding rather
+// than wait for them before the next weight chunk is written to LDS. The last, partial
+// row block runs as a separate GUARD = true launch.
+template <bool GUARD>
+__global__ void __launch_bounds__(256, 2) gemm_wide_kernel(int64_t n, int m, const float* __restrict__ x,
+                                                            const float* __restrict__ w, float scale,
+                                                            float* __restrict__ out, int64_t first_block) {
+  __shared__ __attribute__((aligned(16))) float As[WIDE_BM * WIDE_P];
+  __shared__ __attribute__((aligned(16))) float Bs[2][WIDE_BN * WIDE_P];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int64_t r0 = (first_block + blockIdx.x) * WIDE_BM;
+  // row (or weight column) q, k = 4 kk .. 4 kk + 3 of one float4 -> LDS positions
+  auto put4 = [&](float* base, int q, int k4, float4 v) {
+    *reinterpret_cast<float4*>(base + q * WIDE_P + k4) = v;
+  };
+  // x block: 128 rows x 16 float4, 8 per thread; rows past n read row n-1 (never stored)
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int e = t + 256 * i, q = e >> 4, k4 = (e & 15) * 4;
+    int64_t row = r0 + q;
+    row = row < n ? row : n - 1;
+    put4(As, q, k4, *reinterpret_cast<const float4*>(x + row * WIDE_K + k4));
+  }
+  float4 rb[4];
+  auto load_b = [&](int c0) {  // 64 weight rows x 16 float4, 4 per thread
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = t + 256 * i, q = e >> 4, k4 = (e & 15) * 4;
+      const int col = c0 + q < m ? c0 + q : m - 1;
+      rb[i] = *reinterpret_cast<const float4*>(w + (int64_t)col * WIDE_K + k4);
+    }
+  };
+  auto store_b = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = t + 256 * i;
+      put4(Bs[buf], e >> 4, (e & 15) * 4, rb[i]);
+    }
+  };
+  load_b(0);
+  store_b(0);
+  __syncthreads();
+
+  const int half = (lane >> 5) * (WIDE_K / 2);  // k offset of this half-wave
+  const float* as = As + (wave * 32 + (lane & 31)) * WIDE_P + half;
+  const int nch = (m + WIDE_BN - 1) / WIDE_BN;
+  // output rows of this lane: r0 + 32 wave + 8 (v/4) + 4 (lane/32) + v%4
+  const int64_t rl = r0 + wave * 32 + 4 * (lane >> 5);
+  // results of output row v (of this lane's 16) and column block j of a chunk at column c0
+  auto store_one = [&](const floatx16 (&res)[2], int c0, int v, int j) {
+    const int64_t row = rl + 8 * (v >> 2) + (v & 3);
+    const int col = c0 + j * 32 + (lane & 31);
+    if (!GUARD || (row < n && col < m)) out[row * m + col] = res[j][v] * scale;
+  };
+  // One chunk into `cur`; the previous chunk's results (`prv`, complete by now) are
+  // stored in between this chunk's MFMAs, so the wave keeps the matrix core fed while
+  // its stores issue (two accumulator sets used alternately).
+  auto chunk = [&](int ch, floatx16 (&cur)[2], const floatx16 (&prv)[2], bool have_prev) {
+    const int c0 = ch * WIDE_BN, buf = ch & 1;
+    if (ch + 1 < nch) load_b(c0 + WIDE_BN);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) cur[j][v] = 0.f;
+    const float* bs = Bs[buf] + (lane & 31) * WIDE_P + half;
+#pragma unroll
+    for (int s4 = 0; s4 < 8; ++s4) {  // 32 MFMA steps, four per 128-bit read
+      const int o = 4 * s4;
+      const float4 a4 = *reinterpret_cast<const float4*>(as + o);
+      float4 b4[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) b4[j] = *reinterpret_cast<const float4*>(bs + j * 32 * WIDE_P + o);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          cur[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(reinterpret_cast<const float*>(&a4)[q],
+                                                        reinterpret_cast<const float*>(&b4[j])[q], cur[j], 0, 0, 0);
+          if (have_prev && (q & 1) == 0) store_one(prv, c0 - WIDE_BN, 2 * s4 + (q >> 1), j);
+        }
+    }
+    if (ch + 1 < nch) {
+      store_b(buf ^ 1);  // the other buffer was last read in the previous chunk
+      __syncthreads();
+    }
+  };
+  floatx16 r0acc[2], r1acc[2];
+  for (int ch = 0; ch < nch; ch += 2) {
+    chunk(ch, r0acc, r1acc, ch > 0);
+    if (ch + 1 < nch) chunk(ch + 1, r1acc, r0acc, true);
+  }
+  const int last = nch - 1;
+#pragma unroll
+  for (int v = 0; v < 16; ++v)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) store_one((last & 1) ? r1acc : r0acc, last * WIDE_BN, v, j);
+}
+
+}  // namespace fc
+
 extern "C" int fc_dense_fwd(int64_t n, int32_t k, int32_t m, const float* x, const float* w, float scale,
                             const float* bias, int32_t act, float* pre_act, float* out, void* stream) {
   if (n < 0 || k < 1 || m < 1 || act < 0 || act > 1) return FC_ERR_BAD_DESC;
   if (n == 0) return FC_OK;
   if (!x || !w || !out) return FC_ERR_NULL;
   if (n > 0x7fffffff) return FC_ERR_SHAPE;
+  if (k == WIDE_K && m >= 4 * WIDE_BN && !bias && act == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0) {
+    const int64_t blocks = (n + WIDE_BM - 1) / WIDE_BM;
+    const int64_t full = m % WIDE_BN == 0 ? n / WIDE_BM : 0;
+    if (full > 0) {
+      hipLaunchKernelGGL(gemm_wide_kernel<false>, dim3((unsigned)full), dim3(256), 0, (hipStream_t)stream, n, m, x,
+                         w, scale, out, (int64_t)0);
+      FC_LAUNCH_CHECK();
+    }
+    if (blocks > full) {
+      hipLaunchKernelGGL(gemm_wide_kernel<true>, dim3((unsigned)(blocks - full)), dim3(256), 0, (hipStream_t)stream,
+                         n, m, x, w, scale, out, full);
+      FC_LAUNCH_CHECK();
+    }
+    return FC_OK;
+  }
   GemmBatch gb{};
   gb.trans_b = 1;
   gb.bias = bias;

@@ -643,7 +643,9 @@ def dense_fwd(x: Tensor, weight: Tensor, bias: Optional[Tensor], scale: float, a
         raise RuntimeError(f"Incorrect last dimension for x. Expected {k}, got {x.shape[-1]}.")
     lead = x.shape[:-1]
     x2 = x.reshape(-1, k)
-    if _use_library_gemm(x2.shape[0], k, m, act, b):
+    # K = 64 (the radial output layer) runs on the library's wide-output kernel, which
+    # overlaps its output stores with the MFMA work; other large plain GEMMs on hipBLASLt
+    if k != 64 and _use_library_gemm(x2.shape[0], k, m, act, b):
         # Plain GEMM (no activation, no bias): hipBLASLt, with the weight pre-scaled as the
         # reference's F.linear(x, W * s) does. fp32 inputs, IEEE fp32 products.
         out = torch.mm(x2, (w * scale).t())

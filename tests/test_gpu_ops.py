@@ -192,22 +192,27 @@ def test_linear(cfg):
         assert_close(a, b, 1e-5, 1e-4 * (float(b.abs().max()) + 1), f"linear grad {k}")
 
 
-@pytest.mark.parametrize("shape", [(1000, 8, 64, 1), (777, 64, 2176, 0), (500, 64, 1, 0), (300, 256, 64, 1)])
+@pytest.mark.parametrize("shape", [(1000, 8, 64, 1, True), (777, 64, 2176, 0, True), (500, 64, 1, 0, True),
+                                   (300, 256, 64, 1, True),
+                                   # no bias, K = 64: the wide-output kernel (full and partial row blocks,
+                                   # and a width that is not a multiple of 64)
+                                   (1000, 64, 512, 0, False), (777, 64, 2176, 0, False), (129, 64, 300, 0, False)])
 def test_dense(shape):
     ops = _ops()
-    n, k, m, act = shape
+    n, k, m, act, with_bias = shape
     torch.manual_seed(7)
     x64 = torch.randn(n, k, dtype=torch.float64, requires_grad=True)
     w64 = torch.randn(m, k, dtype=torch.float64, requires_grad=True)
-    b64 = torch.randn(m, dtype=torch.float64, requires_grad=True)
+    b64 = torch.randn(m, dtype=torch.float64, requires_grad=True) if with_bias else None
     ref = O.dense(x64, w64, b64)
     if act:
         ref = O.silu(ref)
     g = torch.randn_like(ref)
-    ref_g = torch.autograd.grad(ref, [x64, w64, b64], g)
-    x, w, b = [t.detach().float().to(DEV).requires_grad_(True) for t in (x64, w64, b64)]
-    out, _ = ops.dense_fwd(x, w, b, float(k) ** -0.5, act)
-    got = torch.autograd.grad(out, [x, w, b], g.float().to(DEV))
+    leaves64 = [x64, w64] + ([b64] if with_bias else [])
+    ref_g = torch.autograd.grad(ref, leaves64, g)
+    leaves = [t.detach().float().to(DEV).requires_grad_(True) for t in leaves64]
+    out, _ = ops.dense_fwd(leaves[0], leaves[1], leaves[2] if with_bias else None, float(k) ** -0.5, act)
+    got = torch.autograd.grad(out, leaves, g.float().to(DEV))
     assert_close(out, ref, 1e-5, 1e-4, "dense fwd")
     for i, (a, r) in enumerate(zip(got, ref_g)):
         assert_close(a, r, 1e-5, 1e-4 * (float(r.abs().max()) + 1), f"dense grad {i}")
