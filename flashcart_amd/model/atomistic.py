@@ -116,8 +116,10 @@ class AtomisticModel(nn.Module):
                 dynamic: bool = False) -> Dict[str, torch.Tensor]:
         """Energies and requested derivatives (reference ``model/atomistic.py:75-156``).
 
-        ``create_graph`` (second derivatives, force-loss training) needs the double
-        backward of the kernels, which this build does not provide.
+        ``create_graph`` keeps the derivatives differentiable (force-loss training): the
+        returned energies and forces carry autograd graphs whose backward runs the second
+        derivatives of the ops. Every block then runs op by op (no fused first-order
+        backward) and ``use_compile`` is ignored (graph replay serves inference only).
 
         ``use_compile`` takes the place of the reference's ``torch.compile`` (default mode
         "reduce-overhead", i.e. graph replay): the whole prediction, forward and backward,
@@ -128,8 +130,10 @@ class AtomisticModel(nn.Module):
         compatibility; shapes are always static.
         """
         if create_graph:
-            raise NotImplementedError("create_graph=True needs second derivatives of the HIP ops "
-                                      "(training with force losses), which are not built.")
+            from flashcart_amd.nn import fused
+            with fused.disabled():
+                gd = self._prepare_predict_graph(graph, compute_forces, compute_stress, compute_edge_forces)
+                return self._predict_impl(gd, compute_forces, compute_stress, compute_edge_forces, True)
         if use_compile:
             return self._replay_predict(_graph_dict(graph), compute_forces, compute_stress, compute_edge_forces)
         gd = self._prepare_predict_graph(graph, compute_forces, compute_stress, compute_edge_forces)
@@ -181,7 +185,7 @@ class AtomisticModel(nn.Module):
             gd["vectors"] = v.detach().requires_grad_(True)
         return gd
 
-    def _predict_impl(self, gd, compute_forces, compute_stress, compute_edge_forces):
+    def _predict_impl(self, gd, compute_forces, compute_stress, compute_edge_forces, create_graph=False):
         node_energies = self(gd)
         out = {"node_energies": node_energies}
         n_atoms = gd["n_atoms"]
@@ -200,7 +204,7 @@ class AtomisticModel(nn.Module):
         if compute_edge_forces:
             inputs.append(gd["vectors"]); names.append("edge_forces")
         if inputs:
-            grads = torch.autograd.grad(out["energy"].sum(), inputs, allow_unused=True)
+            grads = torch.autograd.grad(out["energy"].sum(), inputs, allow_unused=True, create_graph=create_graph)
             for name, g, x in zip(names, grads, inputs):
                 g = torch.zeros_like(x) if g is None else g
                 if name == "forces":
@@ -211,8 +215,9 @@ class AtomisticModel(nn.Module):
                     out["virials"] = -out["stress"] * vol.unsqueeze(-1)
                 else:
                     out["edge_forces"] = g
-            out["node_energies"] = out["node_energies"].detach()
-            out["energy"] = out["energy"].detach()
+            if not create_graph:
+                out["node_energies"] = out["node_energies"].detach()
+                out["energy"] = out["energy"].detach()
         return out
 
     # -- checkpoints (reference model/atomistic.py:441-527) -------------------------------

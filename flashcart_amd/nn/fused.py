@@ -11,22 +11,43 @@ residual, and the node-wise product backward adds into its operands' gradients
 (``fc_tp_bwd_rows_acc``).
 
 They are used only when the block input needs a gradient, no parameter of the block does,
-and no graph is being traced; otherwise the modules run op by op with autograd (training,
-parameter gradients, torch.compile). Reference behaviour: ``nn/layers.py:538-652`` (gated
-update) and ``nn/layers.py:769-1016`` (product layer) — the outputs are those of the
-op-by-op path; only the order of floating-point additions in the backward differs.
+no second derivative is wanted and no graph is being traced; otherwise the modules run op
+by op with autograd (training, parameter gradients, create_graph, torch.compile). The
+hand-written backward is first-order only (``once_differentiable``: differentiating it
+again raises). Reference behaviour: ``nn/layers.py:538-652`` (gated update) and
+``nn/layers.py:769-1016`` (product layer) — the outputs are those of the op-by-op path;
+only the order of floating-point additions in the backward differs.
 """
 
+import contextlib
+import threading
 from typing import Optional
 
 import torch
 from torch import Tensor
+from torch.autograd.function import once_differentiable
 
 from flashcart_amd.o3 import _ops
+
+_state = threading.local()
+
+
+@contextlib.contextmanager
+def disabled():
+    """Run every block op by op inside the context (used when the backward will be
+    differentiated again, e.g. ``predict(create_graph=True)``)."""
+    prev = getattr(_state, "off", False)
+    _state.off = True
+    try:
+        yield
+    finally:
+        _state.off = prev
 
 
 def applies(module: torch.nn.Module, x: Tensor) -> bool:
     """True when ``module`` may run as one fused Function on input ``x``."""
+    if getattr(_state, "off", False):
+        return False
     if not (torch.is_grad_enabled() and x.requires_grad and x.is_cuda):
         return False
     if torch.compiler.is_compiling():
@@ -76,6 +97,7 @@ class _ProductBlock(torch.autograd.Function):
         return out
 
     @staticmethod
+    @once_differentiable
     def backward(ctx, g: Tensor):
         layer = ctx.layer
         x, *saved = ctx.saved_tensors
@@ -127,6 +149,7 @@ class _GatedBlock(torch.autograd.Function):
         return out
 
     @staticmethod
+    @once_differentiable
     def backward(ctx, g: Tensor):
         layer = ctx.layer
         values, pre, pre_act = ctx.saved_tensors

@@ -4,8 +4,9 @@ Op names follow the reference's registered operators
 (src/flashcart/o3/_tensor_product.py:332,588; src/flashcart/o3/_irreps.py:84,117;
 src/flashcart/o3/_linear.py:328,457) so call sites read the same. Each op has a
 shape-only fake implementation (for torch.compile / meta tracing) and a registered
-autograd formula whose backward is another HIP op. Second derivatives (training
-with force losses) are not provided: the backward ops have no autograd formula.
+autograd formula whose backward is another HIP op. The backward ops' own autograd
+formulas (second derivatives, for training with force losses) are registered by
+``flashcart_amd.o3._second_order``, imported at the end of this module.
 
 Every implementation checks that its tensors are float32 on a ROCm device and
 raises otherwise; there is no CPU path.
@@ -690,20 +691,35 @@ def _dense_setup(ctx, inputs, output):
     ctx.scale = float(scale)
     ctx.act = int(act)
     ctx.has_bias = bias is not None
+    # an unused output's gradient arrives as None rather than a zero tensor
+    ctx.set_materialize_grads(False)
 
 
 def _dense_backward(ctx, grad, grad_pre):
+    """Gradients from the activated output and, when a second derivative has been taken
+    through a ``dense_bwd`` that read it, from the pre-activation output."""
     x, weight, pre = ctx.saved_tensors
+    if not ctx.act or (grad_pre is not None and grad_pre.numel() == 0):
+        grad_pre = None
+    if grad is None and grad_pre is None:
+        return None, None, None, None, None
+    m = weight.shape[0]
     gx = gw = gb = None
     if ctx.needs_input_grad[0]:
-        gx = dense_bwd(grad, pre, weight, ctx.scale, ctx.act)
+        if grad is not None:
+            gx = dense_bwd(grad, pre, weight, ctx.scale, ctx.act)
+        if grad_pre is not None:
+            gp = dense_bwd(grad_pre, pre, weight, ctx.scale, 0)
+            gx = gp if gx is None else gx + gp
     if ctx.needs_input_grad[1] or (ctx.has_bias and ctx.needs_input_grad[2]):
         # Parameter gradients (training only), with torch on the GPU.
-        g = grad
-        if ctx.act:
+        g = grad if grad is not None else torch.zeros_like(grad_pre)
+        if ctx.act and grad is not None:
             s = torch.sigmoid(pre)
             g = grad * 1.6765324703310907 * s * (1 + pre * (1 - s))
-        g2 = g.reshape(-1, g.shape[-1])
+        if grad_pre is not None:
+            g = g + grad_pre
+        g2 = g.reshape(-1, m)
         if ctx.needs_input_grad[1]:
             gw = (g2.t() @ x.reshape(-1, x.shape[-1])) * ctx.scale
         if ctx.has_bias and ctx.needs_input_grad[2]:
@@ -795,11 +811,25 @@ def _rms_setup(ctx, inputs, output):
     x, weight, l_max, eps = inputs
     ctx.save_for_backward(x, weight, output[1])
     ctx.l_max = int(l_max)
+    ctx.set_materialize_grads(False)
 
 
 def _rms_backward(ctx, grad_out, grad_scale):
+    """Gradients from the normalised output and, when a second derivative has been taken
+    through an expression that read the saved scale, from the scale output."""
     x, weight, scale = ctx.saved_tensors
+    if grad_out is None:
+        grad_out = torch.zeros_like(x)
     gx = rms_norm_bwd(grad_out, x, weight, scale, ctx.l_max) if ctx.needs_input_grad[0] else None
+    if gx is not None and grad_scale is not None:
+        # s = (m(x) + eps)^-1/2: ds/dx = -s^3/2 dm/dx, differentiated through the torch statement
+        from flashcart_amd.o3 import _torch_math as M
+        with torch.enable_grad():
+            xx = x if x.requires_grad else x.detach().requires_grad_(True)
+            m = M.rms_mean(xx, ctx.l_max, weight.shape[-1])
+            (gm,) = torch.autograd.grad(m, xx, grad_scale * (-0.5) * scale.pow(3),
+                                        create_graph=torch.is_grad_enabled())
+        gx = gx + gm
     gw = None
     if ctx.needs_input_grad[1]:  # d/dg_l[c] = sum_{n,a} grad_out * x * s (parameter training only)
         n, C = x.shape[0], weight.shape[-1]
@@ -871,3 +901,7 @@ def _gate_backward(ctx, grad):
 
 
 gate.register_autograd(_gate_backward, setup_context=_gate_setup)
+
+
+# second derivatives: autograd formulas of the backward ops above
+from flashcart_amd.o3 import _second_order  # noqa: E402,F401

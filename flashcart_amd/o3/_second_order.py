@@ -1,0 +1,326 @@
+"""Second derivatives: autograd formulas for the first-order backward ops.
+
+Training with a force loss differentiates F = -dE/dR once more, i.e. differentiates
+every backward op of the energy graph (the reference's ``*_dbwd`` ops,
+src/flashcart/o3/_tensor_product.py:1095-1096, src/flashcart/o3/_linear.py:777-778,
+src/flashcart/o3/_irreps.py:201-202).
+
+* ``tp_bwd``: the product is linear in each of (grad_out, in1, in2, weights), so the
+  derivative of <c1, g1> + <c2, g2> + <cw, gw> is again a set of products of the same
+  configuration with one operand replaced by a cotangent: three ``tp_fwd`` (for
+  grad_out) and up to three ``tp_bwd`` calls, each a HIP kernel launch.
+* ``linear_bwd`` (the dgrad GEMM) is linear in grad_out and the weights: its derivative
+  is ``linear_fwd`` of the cotangent and a weight-gradient GEMM.
+* ``dense_bwd``: explicit formulas with the rescaled SiLU's first and second derivative.
+* elementwise layers (edge geometry, Eq. 1, radial basis, envelope, RMS norm, gate):
+  differentiate their torch restatements twice (``_torch_math.vjp_of_vjp``).
+
+Importing this module registers the formulas on the ``flashcart::*`` ops.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from flashcart_amd.o3 import _ops
+from flashcart_amd.o3 import _torch_math as M
+
+Tensor = torch.Tensor
+
+
+def _live(t):
+    """A cotangent that carries information (not None, not the empty stand-in tensor)."""
+    return t if (t is not None and t.numel() > 0) else None
+
+
+def _acc(*terms):
+    out = None
+    for t in terms:
+        if t is None or t.numel() == 0:
+            continue
+        out = t if out is None else out + t
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Tensor product
+# ---------------------------------------------------------------------------
+
+def _tp_bwd_setup(ctx, inputs, output):
+    (go, in1, in2, w, idx_i, idx_j, l1, l2, lo, f1, f2, sym, shared, o1, o2, osz, npl, ntot, red,
+     n1, n2, nw, rowptr, sperm, sptr, alpha) = inputs
+    ctx.save_for_backward(go, in1, in2, w, idx_i, idx_j, rowptr, sperm, sptr)
+    ctx.cfg = (int(l1), int(l2), int(lo), int(f1), int(f2), bool(sym), bool(shared), list(o1), list(o2),
+               list(osz), list(npl), int(ntot), bool(red))
+    ctx.alpha = float(alpha)
+    ctx.computed = (bool(n1), bool(n2), bool(nw))
+
+
+def _tp_dbwd(ctx, c1, c2, cw):
+    """Backward of tp_bwd (reference tp_dbwd, src/flashcart/o3/_tensor_product.py:789-1093)."""
+    go, in1, in2, w, ii, jj, rp, sp, sq = ctx.saved_tensors
+    need = ctx.needs_input_grad
+    c1 = _live(c1) if ctx.computed[0] else None
+    c2 = _live(c2) if ctx.computed[1] else None
+    cw = _live(cw) if ctx.computed[2] else None
+    cfg, alpha = ctx.cfg, ctx.alpha
+    tail = (None,) * 22
+
+    def fwd(a, b, ww):
+        return _ops.tp_fwd(a, b, ww, ii, jj, *cfg, rp, sp, sq, alpha)
+
+    def bwd(a, b, ww, n1, n2, nw):
+        if not (n1 or n2 or nw):
+            return None, None, None
+        g1, g2, gw = _ops.tp_bwd(go, a, b, ww, ii, jj, *cfg, bool(n1), bool(n2), bool(nw), rp, sp, sq, alpha)
+        return (g1 if n1 else None), (g2 if n2 else None), (gw if nw else None)
+
+    d_go = None
+    if need[0]:
+        d_go = _acc(fwd(c1, in2, w) if c1 is not None else None,
+                    fwd(in1, c2, w) if c2 is not None else None,
+                    fwd(in1, in2, cw) if cw is not None else None)
+    a = bwd(c1, in2, w, False, need[2], need[3]) if c1 is not None else (None,) * 3
+    b = bwd(in1, c2, w, need[1], False, need[3]) if c2 is not None else (None,) * 3
+    c = bwd(in1, in2, cw, need[1], need[2], False) if cw is not None else (None,) * 3
+    d_in1 = _acc(b[0], c[0]) if need[1] else None
+    d_in2 = _acc(a[1], c[1]) if need[2] else None
+    d_w = _acc(a[2], b[2]) if need[3] else None
+    return (d_go, d_in1, d_in2, d_w) + tail
+
+
+_ops.tp_bwd.register_autograd(_tp_dbwd, setup_context=_tp_bwd_setup)
+
+
+# ---------------------------------------------------------------------------
+# Equivariant linear map
+# ---------------------------------------------------------------------------
+
+def _linear_bwd_setup(ctx, inputs, output):
+    go, w0, w1, w2, w3, in_l_max, out_l_max, fin, fout, in_paths, scale, alpha, residual = inputs
+    ws = _ops._wlist(w0, w1, w2, w3)
+    ctx.save_for_backward(go, *ws)
+    ctx.cfg = (int(in_l_max), int(out_l_max), int(fin), int(fout), list(in_paths), list(scale))
+    ctx.alpha = float(alpha)
+
+
+def _linear_dbwd(ctx, c):
+    """Backward of linear_bwd (reference linear_dbwd, src/flashcart/o3/_linear.py:540-760):
+    gx_l = a s_l go_l W_l, so d/d go = linear_fwd(c) and d/dW_l = a s_l go_l^T c_l."""
+    go, *weights = ctx.saved_tensors
+    in_l_max, out_l_max, fin, fout, in_paths, scale = ctx.cfg
+    need = ctx.needs_input_grad
+    d_go = None
+    if need[0]:
+        d_go = _ops.linear_fwd(c, weights, in_l_max, out_l_max, fin, fout, in_paths, scale, ctx.alpha)
+    d_ws = [None, None, None, None]
+    if any(need[1:5]):
+        n = go.shape[0]
+        in_off = out_off = 0
+        for l in range(min(in_l_max, out_l_max) + 1):
+            k = fin * in_paths[l]
+            m = 2 * l + 1
+            if need[1 + l]:
+                cl = c[:, in_off:in_off + m * k].reshape(n * m, k)
+                gl = go[:, out_off:out_off + m * fout].reshape(n * m, fout)
+                d_ws[l] = (gl.t() @ cl) * (scale[l] * ctx.alpha)
+            in_off += m * k
+            out_off += m * fout
+    d_res = c if len(need) > 12 and need[12] else None
+    return (d_go, *d_ws) + (None,) * 7 + (d_res,)
+
+
+_ops.linear_bwd_op.register_autograd(_linear_dbwd, setup_context=_linear_bwd_setup)
+
+
+# ---------------------------------------------------------------------------
+# Dense layer
+# ---------------------------------------------------------------------------
+
+def _dense_bwd_setup(ctx, inputs, output):
+    go, pre, weight, scale, act = inputs
+    ctx.save_for_backward(go, pre, weight)
+    ctx.scale = float(scale)
+    ctx.act = int(act)
+
+
+def _dense_dbwd(ctx, c):
+    """gx = s * h @ W with h = go * f'(pre) (h = go without activation):
+    dh = s * c @ W^T, d go = dh * f'(pre), d pre = dh * go * f''(pre), dW = s * h^T @ c."""
+    go, pre, w = ctx.saved_tensors
+    need = ctx.needs_input_grad
+    m, k = w.shape
+    c2 = c.reshape(-1, k)
+    go2 = go.reshape(-1, m)
+    d_go = d_pre = d_w = None
+    dh = None
+    if need[0] or (ctx.act and need[1]):
+        dh, _ = _ops.dense_fwd(c2, w, None, ctx.scale, 0)
+    if ctx.act:
+        p2 = pre.reshape(-1, m)
+        if need[0]:
+            d_go = (dh * M.silu_grad(p2)).reshape(go.shape)
+        if need[1]:
+            d_pre = (dh * go2 * M.silu_grad2(p2)).reshape(pre.shape)
+        h = go2 * M.silu_grad(p2) if need[2] else None
+    else:
+        if need[0]:
+            d_go = dh.reshape(go.shape)
+        h = go2
+    if need[2]:
+        d_w = (h.t() @ c2) * ctx.scale
+    return d_go, d_pre, d_w, None, None
+
+
+_ops.dense_bwd.register_autograd(_dense_dbwd, setup_context=_dense_bwd_setup)
+
+
+# ---------------------------------------------------------------------------
+# Eq. (1) expansion and radial basis
+# ---------------------------------------------------------------------------
+
+def _irreps_bwd_setup(ctx, inputs, output):
+    g, x, l_max = inputs
+    ctx.save_for_backward(g, x)
+    ctx.l_max = int(l_max)
+
+
+def _irreps_dbwd(ctx, c):
+    """Backward of irreps_bwd (reference irreps_dbwd, src/flashcart/o3/_irreps.py:146-199)."""
+    g, x = ctx.saved_tensors
+    need = ctx.needs_input_grad
+    gp, gg = M.vjp_of_vjp(lambda xx: M.expansion(xx, ctx.l_max), [x], [0], [g], [c], [need[1]], [need[0]])
+    return gg[0], gp[0], None
+
+
+_ops.irreps_bwd.register_autograd(_irreps_dbwd, setup_context=_irreps_bwd_setup)
+
+
+def _radial_bwd_setup(ctx, inputs, output):
+    d, g_feats, g_env, basis, n_radial, r_min, r_max, poly_order = inputs
+    ctx.save_for_backward(d, g_feats, g_env)
+    ctx.cfg = (int(basis), int(n_radial), float(r_min), float(r_max), int(poly_order))
+
+
+def _radial_dbwd(ctx, c):
+    d, gf, ge = ctx.saved_tensors
+    basis, n_radial, r_min, r_max, poly_order = ctx.cfg
+    need = ctx.needs_input_grad
+    gf = _live(gf) if basis != _ops._lib.BASIS_NONE else None
+    ge = _live(ge) if poly_order > 0 else None
+
+    def fn(dd):
+        return (M.radial_basis(dd, basis, n_radial, r_min, r_max) if gf is not None else None,
+                M.envelope(dd, r_max, poly_order) if ge is not None else None)
+
+    gp, gg = M.vjp_of_vjp(fn, [d], [0], [gf, ge], [c], [need[0]], [need[1], need[2]])
+    return (gp[0], gg[0], gg[1]) + (None,) * 5
+
+
+_ops.radial_bwd.register_autograd(_radial_dbwd, setup_context=_radial_bwd_setup)
+
+
+# ---------------------------------------------------------------------------
+# Fused edge geometry
+# ---------------------------------------------------------------------------
+
+def _edge_bwd_setup(ctx, inputs, output):
+    (g_attrs, g_feats, g_env, positions, shift_vec, idx_i, idx_j, vectors, rowptr, sperm, sptr) = inputs[:11]
+    ctx.save_for_backward(g_attrs, g_feats, g_env, positions, shift_vec, idx_i, idx_j, vectors)
+    ctx.cfg = tuple(inputs[11:17])
+    ctx.computed_pos = bool(inputs[17]) and positions is not None
+
+
+def _edge_dbwd(ctx, c_pos, c_vec):
+    """gvec = d<g, geometry(v)>/dv and gpos = its scatter onto the atoms (v = R_j - R_i + shift),
+    so <c_pos, gpos> + <c_vec, gvec> = <c_vec + c_pos[j] - c_pos[i], gvec>."""
+    g_attrs, g_feats, g_env, positions, shift_vec, idx_i, idx_j, vectors = ctx.saved_tensors
+    l_max, basis, n_radial, r_min, r_max, poly_order = ctx.cfg
+    need = ctx.needs_input_grad
+    ii = idx_i.to(torch.int64)
+    jj = idx_j.to(torch.int64)
+    cv = _live(c_vec)
+    cp = _live(c_pos) if ctx.computed_pos else None
+    if cp is not None:
+        cv = _acc(cv, cp.index_select(0, jj) - cp.index_select(0, ii))
+    none = (None,) * 18
+    if cv is None:
+        return none
+    v = M.edge_vectors(positions, shift_vec, idx_i, idx_j, vectors)
+    gs = [_live(g_attrs), _live(g_feats) if basis != _ops._lib.BASIS_NONE else None,
+          _live(g_env) if poly_order > 0 else None]
+    need_v = need[3] or need[4] or need[7]
+
+    def fn(vv):
+        return M.edge_geometry(vv, l_max, basis, n_radial, r_min, r_max, poly_order)
+
+    gp, gg = M.vjp_of_vjp(fn, [v], [0], gs, [cv], [need_v], [need[0], need[1], need[2]])
+    hv = gp[0]
+    d_pos = d_shift = d_vec = None
+    if hv is not None:
+        if need[3] and positions is not None:
+            d_pos = torch.zeros_like(positions).index_add(0, jj, hv).index_add(0, ii, -hv)
+        if need[4] and shift_vec is not None:
+            d_shift = hv
+        if need[7] and vectors is not None:
+            d_vec = hv
+    return (gg[0], gg[1], gg[2], d_pos, d_shift, None, None, d_vec) + (None,) * 10
+
+
+_ops.edge_geometry_bwd.register_autograd(_edge_dbwd, setup_context=_edge_bwd_setup)
+
+
+# ---------------------------------------------------------------------------
+# RMS norm and gate
+# ---------------------------------------------------------------------------
+
+def _rms_bwd_setup(ctx, inputs, output):
+    go, x, weight, scale, l_max = inputs
+    ctx.save_for_backward(go, x, weight, scale)
+    ctx.l_max = int(l_max)
+
+
+def _rms_fn_from_scale(x0: Tensor, s0: Tensor, l_max: int, channels: int):
+    """The norm as a function of (x, weight) with the constant fixed by the saved scale:
+    s(x) = (m(x) - m(x0) + s0^-2)^-1/2 equals (m(x) + eps)^-1/2 for every x."""
+    with torch.no_grad():
+        k = s0.double().pow(-2) - M.rms_mean(x0.double(), l_max, channels)
+
+    def fn(x, w):
+        s = torch.rsqrt(M.rms_mean(x, l_max, channels) + k.to(x.dtype))
+        gain = torch.cat([w[l].unsqueeze(0).expand(2 * l + 1, channels) for l in range(l_max + 1)]).reshape(1, -1)
+        return x * s.unsqueeze(-1) * gain
+
+    return fn
+
+
+def _rms_dbwd(ctx, c):
+    go, x, weight, scale = ctx.saved_tensors
+    need = ctx.needs_input_grad
+    fn = _rms_fn_from_scale(x, scale, ctx.l_max, weight.shape[-1])
+    gp, gg = M.vjp_of_vjp(fn, [x, weight], [0], [go], [c], [need[1], need[2]], [need[0]])
+    return gg[0], gp[0], gp[1], None, None
+
+
+_ops.rms_norm_bwd.register_autograd(_rms_dbwd, setup_context=_rms_bwd_setup)
+
+
+def _gate_bwd_setup(ctx, inputs, output):
+    go, values, pre, l_max, act, need_values, need_pre = inputs
+    ctx.save_for_backward(go, values, pre)
+    ctx.cfg = (int(l_max), int(act))
+    ctx.computed = (bool(need_values), bool(need_pre))
+
+
+def _gate_dbwd(ctx, c_values, c_pre):
+    go, values, pre = ctx.saved_tensors
+    l_max, act = ctx.cfg
+    need = ctx.needs_input_grad
+    wrt = [k for k in (0, 1) if ctx.computed[k]]
+    cots = [_live(c) for k, c in zip((0, 1), (c_values, c_pre)) if ctx.computed[k]]
+    gp, gg = M.vjp_of_vjp(lambda v, p: M.gate(v, p, l_max, act), [values, pre], wrt, [go], cots,
+                          [need[1], need[2]], [need[0]])
+    return gg[0], gp[0], gp[1], None, None, None, None
+
+
+_ops.gate_bwd.register_autograd(_gate_dbwd, setup_context=_gate_bwd_setup)

@@ -209,3 +209,35 @@ def predict(sd: Dict[str, torch.Tensor], cfg: Dict[str, Any], graph: Dict[str, A
             out["stress"] = torch.stack([s[:, 0, 0], s[:, 1, 1], s[:, 2, 2], (s[:, 1, 2] + s[:, 2, 1]) / 2,
                                          (s[:, 0, 2] + s[:, 2, 0]) / 2, (s[:, 0, 1] + s[:, 1, 0]) / 2], dim=-1)
     return out
+
+
+def force_loss_grads(sd: Dict[str, torch.Tensor], cfg: Dict[str, Any], graph: Dict[str, Any],
+                     energy_ref: torch.Tensor, forces_ref: torch.Tensor, names: List[str],
+                     w_energy: float = 1.0, w_forces: float = 1.0,
+                     dtype: torch.dtype = torch.float64) -> Dict[str, torch.Tensor]:
+    """Gradients of the force-matching loss
+        w_e * mean((E - E_ref)^2) + w_f * mean((F - F_ref)^2),  F = -dE/dR (create_graph=True)
+    with respect to the parameters ``names`` of the state dict, in ``dtype`` on CPU.
+
+    The second derivatives come from torch autograd over the oracle's forward, as in the
+    reference's training step (src/flashcart/model/atomistic.py:276-340 with
+    create_graph=True; src/flashcart/training/loss.py:127-305). Returns the loss under
+    "loss" and one gradient per name.
+    """
+    params = {k: v.detach().to("cpu", dtype) if v.is_floating_point() else v.detach().cpu() for k, v in sd.items()}
+    for k in names:
+        params[k].requires_grad_(True)
+    g = {k: (v.detach().cpu() if torch.is_tensor(v) else v) for k, v in graph.items()}
+    pos = g["positions"].to(dtype).requires_grad_(True)
+    g["positions"] = pos
+    g["cell"] = g["cell"].to(dtype)
+    e_node = node_energies(params, cfg, g)
+    energy = O.scatter_sum(e_node, g["batch"], int(g["n_atoms"].shape[0]))
+    (de,) = torch.autograd.grad(energy.sum(), pos, create_graph=True)
+    forces = -de
+    loss = w_energy * ((energy - energy_ref.to(dtype)) ** 2).mean() + \
+        w_forces * ((forces - forces_ref.to(dtype)) ** 2).mean()
+    grads = torch.autograd.grad(loss, [params[k] for k in names], allow_unused=True)
+    out = {k: (gr if gr is not None else torch.zeros_like(params[k])) for k, gr in zip(names, grads)}
+    out["loss"] = loss.detach()
+    return out
