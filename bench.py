@@ -253,6 +253,8 @@ def run_other_workload(name, args, dev):
                     "value": E * args.steps / dt, "unit": "edges/s", "ms_per_step": ms,
                     "roofline": {"bound": "hbm (launch-bound at this size)", "algorithmic_bytes": 112 * E,
                                  "achieved": 112 * E / (ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s"}})
+    elif name.startswith("train_"):
+        run_training(name, args, dev, res)
     else:
         if name == "cfg3_water_1536":
             z, p, cell, pbc = water_box(512, seed=0)
@@ -297,7 +299,82 @@ def run_other_workload(name, args, dev):
     print(json.dumps(res), flush=True)
 
 
-WORKLOADS = ("cfg4_fcc25k", "cfg1_tp_standalone", "cfg2_expansion_radial", "cfg3_water_1536", "cfg5_molecules_512")
+def run_training(name, args, dev, res):
+    """Force-loss training step: energies and forces with create_graph=True, the reference's
+    default loss (Huber on per-atom energies, delta 0.005, weight 1; Huber on force components,
+    delta 0.05, weight 0.01; src/flashcart/configs/default.yaml:95-106), its backward through
+    the second derivatives, and an AdamW update of every parameter."""
+    from flashcart_amd.data import AtomicGraph, batch_graphs
+    from flashcart_amd.data.synthetic import fcc_alloy, model_config, molecules
+    from flashcart_amd.model import FlashCartPotential
+    if name == "train_molecules_192":
+        mols = molecules(192, seed=0)
+        elements = ["H", "C", "N", "O"]
+        gs = [AtomicGraph.from_arrays(zz, pp, elements, R_MAX) for zz, pp in mols]
+        graph, oracle_graph = batch_graphs(gs), batch_graphs(gs[:4])
+    elif name == "train_fcc_2048":
+        z, p, cell, pbc = fcc_alloy(8, 8, 8, a=3.6, jitter=0.05, seed=0)
+        elements = ["Cu", "Ni", "Fe", "Cr"]
+        graph = AtomicGraph.from_arrays(z, p, elements, R_MAX, cell=cell, pbc=pbc)
+        zo, po, co, pbo = fcc_alloy(2, 2, 2, a=3.6, jitter=0.05, seed=0)
+        oracle_graph = AtomicGraph.from_arrays(zo, po, elements, R_MAX, cell=co, pbc=pbo)
+    else:
+        raise SystemExit(f"unknown workload {name}")
+    n_atoms, n_graphs = graph.num_nodes, graph.num_graphs
+    avg = graph.edge_index.shape[1] / n_atoms
+    torch.manual_seed(1234)
+    model = FlashCartPotential.from_config(model_config(elements, 128, 3, r_max=R_MAX, avg_neighbors=avg)).to(dev)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4)
+    gdev = graph.to(dev)
+    gen = torch.Generator().manual_seed(0)
+    e_ref = torch.randn(n_graphs, generator=gen).to(dev)
+    f_ref = (0.1 * torch.randn(gdev.positions.shape, generator=gen)).to(dev)
+    per_atom = gdev.n_atoms.to(torch.float32)
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        out = model.predict(gdev, compute_forces=True, create_graph=True)
+        loss = torch.nn.functional.huber_loss(out["energy"] / per_atom, e_ref, reduction="sum", delta=0.005) + \
+            0.01 * torch.nn.functional.huber_loss(out["forces"], f_ref, reduction="sum", delta=0.05)
+        loss.backward()
+        opt.step()
+        return loss
+
+    torch.cuda.reset_peak_memory_stats(dev)
+    dt, loss = _timed(step, args.steps, args.warmup, dev)
+    if not torch.isfinite(loss):
+        raise RuntimeError("non-finite training loss")
+    ms = 1e3 * dt / args.steps
+    res.update({"metric": "training atom-steps/s (energy+force loss, create_graph, AdamW)",
+                "value": n_atoms * args.steps / dt, "unit": "atom-steps/s", "ms_per_step": ms,
+                "structures_per_s": n_graphs * args.steps / dt,
+                "peak_memory_gb": torch.cuda.max_memory_allocated(dev) / 1e9,
+                "config": {"n_atoms": n_atoms, "n_graphs": n_graphs, "n_edges": int(graph.edge_index.shape[1]),
+                           "channels": 128, "l_max_edge_attrs": 3, "l_max_hidden_feats": 2}})
+    if not args.no_cpu_baseline:
+        from oracle import model as OM
+        cores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(cores)
+        sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+        names = [k for k, _ in model.named_parameters()]
+        gd = oracle_graph.to_dict()
+        eo = torch.zeros(oracle_graph.num_graphs)
+        fo = torch.zeros(oracle_graph.num_nodes, 3)
+        OM.force_loss_grads(sd, model.to_model_config(), gd, eo, fo, names, dtype=torch.float32)  # warmup
+        calls, t0 = 0, time.perf_counter()
+        while calls < 1 or (calls < 3 and time.perf_counter() - t0 < 20.0):
+            OM.force_loss_grads(sd, model.to_model_config(), gd, eo, fo, names, dtype=torch.float32)
+            calls += 1
+        cdt = time.perf_counter() - t0
+        rate = oracle_graph.num_nodes * calls / cdt
+        res["cpu_baseline"] = {"value": rate, "unit": "atom-steps/s", "cores": cores, "kind": "port",
+                               "sample": f"oracle float32 force-loss gradients on {oracle_graph.num_nodes} atoms "
+                                         f"({oracle_graph.num_graphs} graphs), {calls} calls, {cdt:.1f} s"}
+        res["speedup_vs_cpu"] = res["value"] / rate
+
+
+WORKLOADS = ("cfg4_fcc25k", "cfg1_tp_standalone", "cfg2_expansion_radial", "cfg3_water_1536", "cfg5_molecules_512",
+             "train_molecules_192", "train_fcc_2048")
 
 
 def main():

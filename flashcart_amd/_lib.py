@@ -84,6 +84,11 @@ _SIGNATURES = {
     "fc_linear_dgrad": (c_int, [ctypes.POINTER(LinearDesc), c_i64, c_vp, c_f32, c_vp, c_vp, c_vp]),
     "fc_dense_fwd": (c_int, [c_i64, c_i32, c_i32, c_vp, c_vp, c_f32, c_vp, c_i32, c_vp, c_vp, c_vp]),
     "fc_dense_dgrad": (c_int, [c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_f32, c_i32, c_vp, c_vp]),
+    "fc_linear_wgrad_workspace": (c_i64, [ctypes.POINTER(LinearDesc), c_i64, ctypes.POINTER(c_vp)]),
+    "fc_linear_wgrad": (c_int, [ctypes.POINTER(LinearDesc), c_i64, c_vp, c_vp, c_f32, ctypes.POINTER(c_vp), c_vp,
+                                c_i64, c_vp]),
+    "fc_dense_wgrad_workspace": (c_i64, [c_i64, c_i32, c_i32, c_i32]),
+    "fc_dense_wgrad": (c_int, [c_i64, c_i32, c_i32, c_vp, c_vp, c_i32, c_vp, c_f32, c_vp, c_vp, c_vp, c_i64, c_vp]),
     "fc_segment_sum": (c_int, [c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "fc_gate_fwd": (c_int, [c_i64, c_int, c_int, c_vp, c_vp, c_int, c_vp, c_vp]),
     "fc_gate_bwd": (c_int, [c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_int, c_vp, c_vp, c_vp]),

@@ -702,3 +702,402 @@ extern "C" int fc_dense_dgrad(int64_t n, int32_t k, int32_t m, const float* go, 
   g.comps = 1; g.M = (int32_t)n; g.K = m; g.N = k; g.scale = scale;
   return launch_gemm(gb, 1, (hipStream_t)stream);
 }
+
+namespace fc {
+
+// ---- Weight gradients (training): dW[o, j] = scale * sum_r A'[r, o] * B[r, j] over every row
+// r = (node, component) of a rank, with A = grad_out (A' = A * act'(pre) for a dense layer
+// with the fused SiLU) and B = the layer input; optionally db[o] = sum_r A'[r, o].
+// The contraction runs over rows, so the MFMA operands are row slices: step s contracts
+// rows 2s (lanes 0-31) and 2s+1 (lanes 32-63), lane % 32 indexing o in the A operand and j
+// in the B operand. Both stage tiles therefore sit in LDS row-major exactly as loaded
+// (32 rows per stage, float4 global loads, no transposition), and the rows of a rank block
+// are read in place from the packed feature rows (no gather copy).
+// The row range is split over workgroups for parallelism (rows_per_split each); with more
+// than one split every workgroup writes its unscaled partial block to a workspace and a
+// second kernel sums the partials in split order, so results do not depend on scheduling.
+struct WgradProblem {
+  const float* A;  // row r = (n, c): A + n*a_row + c*a_comp, O floats
+  const float* P;  // pre-activation in A's layout (SiLU derivative prologue) or null
+  const float* B;  // row r: B + n*b_row + c*b_comp, J floats
+  float* D;        // (O, J) row-major
+  float* Db;       // (O) bias gradient or null
+  int64_t a_row, a_comp, b_row, b_comp;
+  int64_t R, rows_per_split;
+  int32_t comps, O, J;
+  float scale;
+  int32_t tiles_o, tiles_j, splits, wg_base;
+  int64_t part_off, partb_off;  // workspace offsets (floats) of the partial blocks
+};
+
+// One block of partial sums to reduce: dst[k] = scale * sum_s src[s * stride + k], k < count.
+struct WgradSection {
+  const float* src;
+  float* dst;
+  int64_t count, stride, base;  // base: first element in the reduce grid (multiple of 256)
+  int32_t splits;
+  float scale;
+};
+
+struct WgradBatch {
+  WgradProblem p[4];
+  WgradSection sec[8];
+  int32_t n, total_wg, n_sec;
+  int64_t total_elems;
+  float* part;
+};
+
+__device__ __forceinline__ float silu_grad_(float p) {
+  const float s = sigmoidf_(p);
+  return kSiluScale * s * (1.0f + p * (1.0f - s));
+}
+
+// Four consecutive floats of row r starting at column col (zero outside the row range and
+// past the last column), times act'(pre) when P is given.
+__device__ __forceinline__ float4 wgrad_fetch4(const float* p, int col, int ncol, bool vec) {
+  if (vec) return *reinterpret_cast<const float4*>(p);
+  return make_float4(p[0], col + 1 < ncol ? p[1] : 0.f, col + 2 < ncol ? p[2] : 0.f, col + 3 < ncol ? p[3] : 0.f);
+}
+
+// Row indices fit in 32 bits (the entry points check), so the (node, component) split of a
+// row is a 32-bit division.
+__device__ __forceinline__ float4 wgrad_load4(const float* base, const float* pbase, int64_t row_stride,
+                                              int64_t comp_stride, int comps, int r, int r_end, int col,
+                                              int ncol, bool vec) {
+  if (r >= r_end || col >= ncol) return make_float4(0.f, 0.f, 0.f, 0.f);
+  const int n = r / comps, c = r - n * comps;
+  const int64_t off = (int64_t)n * row_stride + (int64_t)c * comp_stride + col;
+  float4 v = wgrad_fetch4(base + off, col, ncol, vec);
+  if (pbase) {
+    const float4 p = wgrad_fetch4(pbase + off, col, ncol, vec);
+    v.x *= silu_grad_(p.x); v.y *= silu_grad_(p.y); v.z *= silu_grad_(p.z); v.w *= silu_grad_(p.w);
+  }
+  return v;
+}
+
+template <int TO, int TJ>
+__global__ void __launch_bounds__(256) wgrad_kernel(WgradBatch wb) {
+  constexpr int RK = 32;                                  // rows per stage
+  constexpr int WO = TO / 2, WJ = TJ / 2;                 // per-wave tile (waves 2 x 2)
+  constexpr int FO = WO / 32, FJ = WJ / 32;               // 32 x 32 MFMA blocks per wave
+  constexpr int A_TPR = TO / 4, B_TPR = TJ / 4;           // threads per stage row (one float4 each)
+  constexpr int AL = RK * A_TPR / 256, BL = RK * B_TPR / 256;  // float4 per thread and stage
+  __shared__ __attribute__((aligned(16))) float As[RK * TO];
+  __shared__ __attribute__((aligned(16))) float Bs[RK * TJ];
+  const int b = blockIdx.x;
+  if (b >= wb.total_wg) return;
+  int pi = 0;
+#pragma unroll
+  for (int q = 1; q < 4; ++q)
+    if (q < wb.n && b >= wb.p[q].wg_base) pi = q;
+  const WgradProblem& g = wb.p[pi];
+  const int local = b - g.wg_base;
+  const int tiles = g.tiles_o * g.tiles_j;
+  const int split = local / tiles, tile = local - split * tiles;
+  const int to = tile / g.tiles_j, tj = tile - to * g.tiles_j;
+  const int o0 = to * TO, j0 = tj * TJ;
+  const int r_begin = (int)(split * g.rows_per_split);
+  const int r_end = (int)(r_begin + g.rows_per_split < g.R ? r_begin + g.rows_per_split : g.R);
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wo = wave >> 1, wj = wave & 1;
+  const bool a_vec = ((g.O & 3) == 0) && ((g.a_row & 3) == 0) && ((g.a_comp & 3) == 0) &&
+                     (((uintptr_t)g.A & 15) == 0) && (!g.P || (((uintptr_t)g.P & 15) == 0));
+  const bool b_vec = ((g.J & 3) == 0) && ((g.b_row & 3) == 0) && ((g.b_comp & 3) == 0) &&
+                     (((uintptr_t)g.B & 15) == 0);
+  const bool do_bias = g.Db && tj == 0 && wj == 0;
+
+  float4 ra[AL], rb[BL];
+  auto load = [&](int r0) {
+#pragma unroll
+    for (int i = 0; i < AL; ++i)
+      ra[i] = wgrad_load4(g.A, g.P, g.a_row, g.a_comp, g.comps, r0 + t / A_TPR + i * (256 / A_TPR), r_end,
+                          o0 + (t % A_TPR) * 4, g.O, a_vec);
+#pragma unroll
+    for (int i = 0; i < BL; ++i)
+      rb[i] = wgrad_load4(g.B, nullptr, g.b_row, g.b_comp, g.comps, r0 + t / B_TPR + i * (256 / B_TPR), r_end,
+                          j0 + (t % B_TPR) * 4, g.J, b_vec);
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int i = 0; i < AL; ++i)
+      *reinterpret_cast<float4*>(As + (t / A_TPR + i * (256 / A_TPR)) * TO + (t % A_TPR) * 4) = ra[i];
+#pragma unroll
+    for (int i = 0; i < BL; ++i)
+      *reinterpret_cast<float4*>(Bs + (t / B_TPR + i * (256 / B_TPR)) * TJ + (t % B_TPR) * 4) = rb[i];
+  };
+
+  floatx16 acc[FO][FJ];
+#pragma unroll
+  for (int i = 0; i < FO; ++i)
+#pragma unroll
+    for (int j = 0; j < FJ; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+  float bsum[FO];
+#pragma unroll
+  for (int i = 0; i < FO; ++i) bsum[i] = 0.f;
+
+  load(r_begin);
+  for (int r0 = r_begin; r0 < r_end; r0 += RK) {
+    __syncthreads();  // the previous stage's reads are done
+    store();
+    __syncthreads();
+    if (r0 + RK < r_end) load(r0 + RK);  // next stage in flight during this stage's MFMAs
+    const float* as = As + wo * WO + (lane & 31);
+    const float* bs = Bs + wj * WJ + (lane & 31);
+#pragma unroll
+    for (int s = 0; s < RK / 2; ++s) {
+      const int rr = 2 * s + (lane >> 5);
+      float av[FO], bv[FJ];
+#pragma unroll
+      for (int i = 0; i < FO; ++i) av[i] = as[rr * TO + i * 32];
+#pragma unroll
+      for (int j = 0; j < FJ; ++j) bv[j] = bs[rr * TJ + j * 32];
+#pragma unroll
+      for (int i = 0; i < FO; ++i)
+#pragma unroll
+        for (int j = 0; j < FJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+      if (do_bias) {
+#pragma unroll
+        for (int i = 0; i < FO; ++i) bsum[i] += av[i];
+      }
+    }
+  }
+
+  // ---- epilogue: D[o][j] with o = 8*(v/4) + 4*(lane/32) + v%4, j = lane%32 per 32x32 block
+  const bool direct = g.splits == 1;
+  float* dst = direct ? g.D : wb.part + g.part_off + (int64_t)split * g.O * g.J;
+  const float sc = direct ? g.scale : 1.0f;
+#pragma unroll
+  for (int i = 0; i < FO; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int o = o0 + wo * WO + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+      if (o >= g.O) continue;
+#pragma unroll
+      for (int j = 0; j < FJ; ++j) {
+        const int jj = j0 + wj * WJ + j * 32 + (lane & 31);
+        if (jj < g.J) dst[(int64_t)o * g.J + jj] = acc[i][j][v] * sc;
+      }
+    }
+  if (do_bias) {
+    float* bdst = direct ? g.Db : wb.part + g.partb_off + (int64_t)split * g.O;
+#pragma unroll
+    for (int i = 0; i < FO; ++i) {
+      const float tot = bsum[i] + __shfl_xor(bsum[i], 32, 64);  // rows of both lane halves
+      const int o = o0 + wo * WO + i * 32 + lane;
+      if (lane < 32 && o < g.O) bdst[o] = tot;
+    }
+  }
+}
+
+// D = scale * sum over splits of the partial blocks (and Db = sum of the partial bias sums).
+// Every workgroup covers 256 consecutive elements of one section (a weight or bias block;
+// section starts are padded to multiples of 256): 64 threads x 4 elements per split lane,
+// four split lanes (splits q, q+4, q+8, ...) whose sums are combined in a fixed order, so
+// each thread keeps four independent loads in flight and the result is deterministic.
+__global__ void __launch_bounds__(256) wgrad_reduce_kernel(WgradBatch wb) {
+  __shared__ float red[4][256];
+  const int64_t e0 = (int64_t)blockIdx.x * 256;
+  int si = 0;
+  for (int q = 1; q < wb.n_sec; ++q)
+    if (e0 >= wb.sec[q].base) si = q;
+  const WgradSection& sc = wb.sec[si];
+  const int t = threadIdx.x, c = t & 63, lane_split = t >> 6;
+  const int64_t k = e0 - sc.base + 4 * c;  // first of this thread's four elements
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int sp = lane_split; sp < sc.splits; sp += 4) {
+    const float* src = sc.src + (int64_t)sp * sc.stride;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (k + q < sc.count) acc[q] += src[k + q];
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) red[lane_split][4 * c + q] = acc[q];
+  __syncthreads();
+  if (lane_split == 0) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int i = 4 * c + q;
+      if (k + q < sc.count) sc.dst[k + q] = ((red[0][i] + red[1][i]) + (red[2][i] + red[3][i])) * sc.scale;
+    }
+  }
+}
+
+// Tile shape, splits and workspace layout; returns the workspace size in floats.
+static int64_t plan_wgrad(WgradBatch& wb, int* TO, int* TJ) {
+  int max_o = 0, max_j = 0;
+  for (int q = 0; q < wb.n; ++q) {
+    if (wb.p[q].O > max_o) max_o = wb.p[q].O;
+    if (wb.p[q].J > max_j) max_j = wb.p[q].J;
+  }
+  *TO = max_o >= 128 ? 128 : 64;
+  *TJ = max_j >= 128 ? 128 : 64;
+  int64_t work = 0;
+  for (int q = 0; q < wb.n; ++q) {
+    WgradProblem& g = wb.p[q];
+    g.tiles_o = (g.O + *TO - 1) / *TO;
+    g.tiles_j = (g.J + *TJ - 1) / *TJ;
+    work += (int64_t)g.tiles_o * g.tiles_j * g.R;
+  }
+  // about 1024 workgroups, at least 256 rows each (a partial block costs as much as
+  // reading 128 rows of both operands)
+  int64_t rps = (work + 1023) / 1024;
+  if (rps < 256) rps = 256;
+  rps = (rps + 31) / 32 * 32;
+  int64_t wg = 0, ws = 0;
+  for (int q = 0; q < wb.n; ++q) {
+    WgradProblem& g = wb.p[q];
+    g.rows_per_split = rps;
+    g.splits = (int32_t)(g.R > 0 ? (g.R + rps - 1) / rps : 1);
+    g.wg_base = (int32_t)wg;
+    wg += (int64_t)g.splits * g.tiles_o * g.tiles_j;
+    if (g.splits > 1) {
+      g.part_off = ws;
+      ws += (int64_t)g.splits * g.O * g.J;
+      g.partb_off = ws;
+      if (g.Db) ws += (int64_t)g.splits * g.O;
+    }
+  }
+  wb.total_wg = (int32_t)wg;
+  return ws;
+}
+
+// The reduce grid: one section per weight (and bias) block that was split.
+static void wgrad_sections(WgradBatch& wb) {
+  wb.n_sec = 0;
+  int64_t base = 0;
+  auto add = [&](const float* src, float* dst, int64_t count, int64_t stride, int32_t splits, float scale) {
+    WgradSection& sc = wb.sec[wb.n_sec++];
+    sc.src = src; sc.dst = dst; sc.count = count; sc.stride = stride; sc.splits = splits; sc.scale = scale;
+    sc.base = base;
+    base += (count + 255) / 256 * 256;
+  };
+  for (int q = 0; q < wb.n; ++q) {
+    const WgradProblem& g = wb.p[q];
+    if (g.splits == 1) continue;
+    const int64_t nw = (int64_t)g.O * g.J;
+    add(wb.part + g.part_off, g.D, nw, nw, g.splits, g.scale);
+    if (g.Db) add(wb.part + g.partb_off, g.Db, g.O, g.O, g.splits, 1.0f);
+  }
+  wb.total_elems = base;
+}
+
+static int launch_wgrad(WgradBatch wb, float* workspace, int64_t workspace_floats, hipStream_t s) {
+  int TO, TJ;
+  const int64_t need = plan_wgrad(wb, &TO, &TJ);
+  if (wb.total_wg == 0) return FC_OK;
+  if (need > 0 && (!workspace || workspace_floats < need)) return FC_ERR_WORKSPACE;
+  wb.part = workspace;
+  wgrad_sections(wb);
+  const dim3 grid((unsigned)wb.total_wg), block(256);
+  if (TO == 128 && TJ == 128) hipLaunchKernelGGL((wgrad_kernel<128, 128>), grid, block, 0, s, wb);
+  else if (TO == 128) hipLaunchKernelGGL((wgrad_kernel<128, 64>), grid, block, 0, s, wb);
+  else if (TJ == 128) hipLaunchKernelGGL((wgrad_kernel<64, 128>), grid, block, 0, s, wb);
+  else hipLaunchKernelGGL((wgrad_kernel<64, 64>), grid, block, 0, s, wb);
+  FC_LAUNCH_CHECK();
+  if (need > 0) {
+    hipLaunchKernelGGL(wgrad_reduce_kernel, dim3((unsigned)((wb.total_elems + 255) / 256)), dim3(256), 0, s, wb);
+    FC_LAUNCH_CHECK();
+  }
+  return FC_OK;
+}
+
+static void linear_wgrad_batch(const fc_linear_desc* d, int64_t n, const float* go, const float* x, float alpha,
+                               float* const* gw, WgradBatch& wb) {
+  const LinearLayout L = linear_layout(d);
+  wb = WgradBatch{};
+  for (int l = 0; l <= L.common; ++l) {
+    if (!gw || !gw[l]) continue;
+    WgradProblem& g = wb.p[wb.n++];
+    g.A = go + L.out_off[l];
+    g.a_row = L.out_dim;
+    g.a_comp = d->out_features;
+    g.B = x + L.in_off[l];
+    g.b_row = L.in_dim;
+    g.b_comp = (int64_t)d->in_features * d->in_paths[l];
+    g.D = gw[l];
+    g.comps = 2 * l + 1;
+    g.R = n * g.comps;
+    g.O = d->out_features;
+    g.J = d->in_features * d->in_paths[l];
+    g.scale = alpha * d->scale[l];
+  }
+}
+
+static void dense_wgrad_batch(int64_t n, int32_t k, int32_t m, const float* go, const float* pre_act, int32_t act,
+                              const float* x, float scale, float* gw, float* gb, WgradBatch& wb) {
+  wb = WgradBatch{};
+  wb.n = 1;
+  WgradProblem& g = wb.p[0];
+  g.A = go; g.a_row = m; g.a_comp = 0;
+  g.P = act ? pre_act : nullptr;
+  g.B = x; g.b_row = k; g.b_comp = 0;
+  g.D = gw; g.Db = gb;
+  g.comps = 1; g.R = n; g.O = m; g.J = k; g.scale = scale;
+}
+
+}  // namespace fc
+
+extern "C" int64_t fc_linear_wgrad_workspace(const fc_linear_desc* d, int64_t n, float* const* grad_w) {
+  const int st = check_linear(d);
+  if (st != FC_OK) return -st;
+  if (n < 0) return -FC_ERR_SHAPE;
+  // only which entries are non-NULL matters here (NULL array: every rank)
+  float* all[4] = {reinterpret_cast<float*>(16), reinterpret_cast<float*>(16), reinterpret_cast<float*>(16),
+                   reinterpret_cast<float*>(16)};
+  WgradBatch wb;
+  linear_wgrad_batch(d, n, nullptr, nullptr, 1.f, grad_w ? grad_w : all, wb);
+  int TO, TJ;
+  return plan_wgrad(wb, &TO, &TJ);
+}
+
+extern "C" int fc_linear_wgrad(const fc_linear_desc* d, int64_t n, const float* go, const float* x, float alpha,
+                               float* const* grad_w, float* workspace, int64_t workspace_floats, void* stream) {
+  int st = check_linear(d);
+  if (st != FC_OK) return st;
+  if (n < 0) return FC_ERR_SHAPE;
+  if (!grad_w) return FC_ERR_NULL;
+  if (n * 7 > 0x7fffffff) return FC_ERR_SHAPE;
+  const int common = d->in_l_max < d->out_l_max ? d->in_l_max : d->out_l_max;
+  if (n == 0) {  // no rows: zero gradients (a fill kernel, so the call can be graph-captured)
+    for (int l = 0; l <= common; ++l)
+      if (grad_w[l]) {
+        const int64_t sz = (int64_t)d->out_features * d->in_features * d->in_paths[l];
+        st = fill_columns(1, sz, 0, sz, nullptr, grad_w[l], (hipStream_t)stream);
+        if (st != FC_OK) return st;
+      }
+    return FC_OK;
+  }
+  if (!go || !x) return FC_ERR_NULL;
+  WgradBatch wb;
+  linear_wgrad_batch(d, n, go, x, alpha, grad_w, wb);
+  if (wb.n == 0) return FC_OK;
+  return launch_wgrad(wb, workspace, workspace_floats, (hipStream_t)stream);
+}
+
+extern "C" int64_t fc_dense_wgrad_workspace(int64_t n, int32_t k, int32_t m, int32_t with_bias) {
+  if (n < 0 || k < 1 || m < 1) return -FC_ERR_BAD_DESC;
+  WgradBatch wb;
+  dense_wgrad_batch(n, k, m, nullptr, nullptr, 0, nullptr, 1.f, reinterpret_cast<float*>(16),
+                    with_bias ? reinterpret_cast<float*>(16) : nullptr, wb);
+  int TO, TJ;
+  return plan_wgrad(wb, &TO, &TJ);
+}
+
+extern "C" int fc_dense_wgrad(int64_t n, int32_t k, int32_t m, const float* go, const float* pre_act, int32_t act,
+                              const float* x, float scale, float* gw, float* gb, float* workspace,
+                              int64_t workspace_floats, void* stream) {
+  if (n < 0 || k < 1 || m < 1 || act < 0 || act > 1) return FC_ERR_BAD_DESC;
+  if (!gw) return FC_ERR_NULL;
+  if (n == 0) {  // no rows: zero gradients (a fill kernel, so the call can be graph-captured)
+    const int st = fill_columns(1, (int64_t)k * m, 0, (int64_t)k * m, nullptr, gw, (hipStream_t)stream);
+    if (st != FC_OK || !gb) return st;
+    return fill_columns(1, m, 0, m, nullptr, gb, (hipStream_t)stream);
+  }
+  if (!go || !x || (act == 1 && !pre_act)) return FC_ERR_NULL;
+  if (n > 0x7fffffff - 256) return FC_ERR_SHAPE;  // row indices are 32-bit in the kernel
+  WgradBatch wb;
+  dense_wgrad_batch(n, k, m, go, pre_act, act, x, scale, gw, gb, wb);
+  return launch_wgrad(wb, workspace, workspace_floats, (hipStream_t)stream);
+}

@@ -67,7 +67,7 @@ class LinearLayer(nn.Module):
 
     def forward(self, x: torch.Tensor, act: int = 0) -> torch.Tensor:
         """``act=1`` fuses the following RescaledSiLULayer into the GEMM epilogue."""
-        out, _ = _ops.dense_fwd(x, self.weight, self.bias, self._scale, act)
+        out, _ = _ops.dense_fwd(x, _ops.param_alias(self.weight), _ops.param_alias(self.bias), self._scale, act)
         return out
 
     def __repr__(self) -> str:

@@ -20,6 +20,7 @@ import torch
 
 from flashcart_amd import _lib
 from flashcart_amd.codegen.cartesian import count_output_paths
+from flashcart_amd.o3 import _torch_math
 
 Tensor = torch.Tensor
 
@@ -66,6 +67,56 @@ def tp_meta(in1_l_max: int, in2_l_max: int, out_l_max: int, in1_features: int, i
     sizes = [((2 * l + 1) * c if n > 0 else 0) if reduce_paths else n * (2 * l + 1) * c
              for l, n in enumerate(n_paths)]
     return offs(in1_l_max, in1_features), offs(in2_l_max, in2_features), sizes, n_paths, int(total)
+
+
+def param_alias(t: Optional[Tensor]) -> Optional[Tensor]:
+    """A parameter as an op input: a view of it while autograd records, so that the backward
+    can ask the engine whether the current pass needs the parameter's gradient (it cannot
+    for the leaf itself inside ``autograd.grad``). No copy; the kernels read the same memory."""
+    if t is not None and t.is_leaf and t.requires_grad and torch.is_grad_enabled():
+        return t.view_as(t)
+    return t
+
+
+def _register_autograd(op, backward, setup_context) -> None:
+    """``op.register_autograd`` with ``ctx.needs_input_grad`` narrowed, while the backward
+    runs, to the inputs the running backward pass will actually use.
+
+    The static flags say which inputs require grad; a pass such as
+    ``autograd.grad(E, positions)`` (forces) needs none of the parameter gradients, so the
+    weight-gradient GEMMs are skipped there. A gradient the pass does not use is dropped by
+    the engine anyway, so returning None for it changes no result. The engine cannot answer
+    for a leaf inside ``autograd.grad``; such an input keeps its static flag, which is why
+    parameters are handed to the ops through ``param_alias``."""
+    def setup(ctx, inputs, output):
+        ctx.tensor_inputs = tuple(torch.is_tensor(a) for a in inputs)
+        setup_context(ctx, inputs, output)
+
+    def used(node) -> bool:
+        if node is None:
+            return False
+        try:
+            return bool(torch._C._will_engine_execute_node(node))
+        except RuntimeError:  # a leaf's accumulator during autograd.grad: unknown
+            return True
+
+    def bwd(ctx, *grads):
+        static = ctx.needs_input_grad
+        node = torch._C._current_autograd_node()
+        mask = ctx.tensor_inputs
+        if node is not None and len(node.next_functions) == sum(mask):
+            edges = iter(node.next_functions)
+            need = []
+            for k, is_tensor in enumerate(mask):
+                nxt = next(edges)[0] if is_tensor else None
+                need.append(bool(k < len(static) and static[k] and used(nxt)))
+            ctx.needs_input_grad = tuple(need[:len(static)])
+        try:
+            return backward(ctx, *grads)
+        finally:
+            ctx.needs_input_grad = static
+
+    op.register_autograd(bwd, setup_context=setup)
 
 
 def _check_tp_meta(cfg, in1_offs, in2_offs, out_sizes, n_paths_per_l, n_total_paths) -> None:
@@ -126,7 +177,7 @@ def _irreps_backward(ctx, grad):
     return irreps_bwd(grad, x, ctx.l_max), None
 
 
-irreps_fwd.register_autograd(_irreps_backward, setup_context=_irreps_setup)
+_register_autograd(irreps_fwd, _irreps_backward, _irreps_setup)
 
 
 # ---------------------------------------------------------------------------
@@ -187,7 +238,7 @@ def _radial_backward(ctx, g_feats, g_env):
     return (radial_bwd(d, gf, ge, basis, n_radial, r_min, r_max, poly_order),) + (None,) * 5
 
 
-radial_fwd.register_autograd(_radial_backward, setup_context=_radial_setup)
+_register_autograd(radial_fwd, _radial_backward, _radial_setup)
 
 
 # ---------------------------------------------------------------------------
@@ -298,7 +349,7 @@ def _edge_backward(ctx, g_attrs, g_feats, g_env):
             (gvec if need_vec else None)) + (None,) * 9
 
 
-edge_geometry.register_autograd(_edge_backward, setup_context=_edge_setup)
+_register_autograd(edge_geometry, _edge_backward, _edge_setup)
 
 
 # ---------------------------------------------------------------------------
@@ -449,7 +500,7 @@ def _tp_backward(ctx, grad):
     return (g1 if n1 else None, g2 if n2 else None, gw if nw else None) + none_tail
 
 
-tp_fwd.register_autograd(_tp_backward, setup_context=_tp_setup)
+_register_autograd(tp_fwd, _tp_backward, _tp_setup)
 
 
 def tp_bwd_rows_acc(grad_out: Tensor, in1: Tensor, in2: Tensor, weights: Tensor, in1_l_max: int, in2_l_max: int,
@@ -597,25 +648,58 @@ def _linear_backward(ctx, grad):
     if need[0]:
         gx = linear_bwd(grad, weights, in_l_max, out_l_max, fin, fout, in_paths, scale, ctx.alpha)
     gws = [None, None, None, None]
-    if any(need[1:5]):
-        # Parameter gradients (training only): scale_l * sum_{n,m} go_l^T x_l, on the GPU with torch.
-        n = x.shape[0]
-        in_off = out_off = 0
-        for l in range(min(in_l_max, out_l_max) + 1):
-            k = fin * in_paths[l]
-            m = 2 * l + 1
-            if need[1 + l]:
-                xl = x[:, in_off:in_off + m * k].reshape(n * m, k)
-                gl = grad[:, out_off:out_off + m * fout].reshape(n * m, fout)
-                gws[l] = (gl.t() @ xl) * (scale[l] * ctx.alpha)
-            in_off += m * k
-            out_off += m * fout
+    if any(need[1:5]):  # parameter gradients (training)
+        gws = linear_wgrad(grad, x, weights, in_l_max, out_l_max, fin, fout, in_paths, scale, ctx.alpha,
+                           [bool(need[1 + l]) for l in range(len(weights))])
+        gws = gws + [None] * (4 - len(gws))
     # trailing arguments left at their defaults are not part of needs_input_grad
     g_res = grad if len(need) > 12 and need[12] else None
     return (gx, *gws) + (None,) * 7 + (g_res,)
 
 
-linear_fwd_op.register_autograd(_linear_backward, setup_context=_linear_setup)
+_register_autograd(linear_fwd_op, _linear_backward, _linear_setup)
+
+
+def linear_wgrad(grad_out: Tensor, x: Tensor, weights: List[Tensor], in_l_max: int, out_l_max: int,
+                 in_features: int, out_features: int, in_paths: List[int], scale: List[float], alpha: float,
+                 need: List[bool]) -> List[Optional[Tensor]]:
+    """dW_l = alpha * scale_l * sum over (node, component) rows of grad_out_l^T x_l for every rank
+    with ``need[l]`` (``fc_linear_wgrad``: split-K MFMA over the rows read in place).
+
+    Under grad mode (a backward with create_graph) the same sums are formed with torch
+    matmuls instead, so that they stay differentiable."""
+    common = min(in_l_max, out_l_max)
+    if torch.is_grad_enabled():
+        n = x.shape[0]
+        outs: List[Optional[Tensor]] = []
+        in_off = out_off = 0
+        for l in range(common + 1):
+            k = in_features * in_paths[l]
+            m = 2 * l + 1
+            if need[l]:
+                xl = x[:, in_off:in_off + m * k].reshape(n * m, k)
+                gl = grad_out[:, out_off:out_off + m * out_features].reshape(n * m, out_features)
+                outs.append((gl.t() @ xl) * (scale[l] * alpha))
+            else:
+                outs.append(None)
+            in_off += m * k
+            out_off += m * out_features
+        return outs
+    go = _lib.contig("grad_out", grad_out)
+    xx = _lib.contig("x", x)
+    ws = [_lib.contig(f"weight[{l}]", w) for l, w in enumerate(weights)]
+    outs = [torch.empty_like(ws[l]) if (l <= common and need[l]) else None for l in range(len(ws))]
+    desc = _lib.linear_desc(in_l_max, out_l_max, in_features, out_features, in_paths, ws, scale)
+    lib = _lib.load()
+    n = go.shape[0]
+    ptrs = (_lib.c_vp * 4)(*([o.data_ptr() if o is not None else None for o in outs] + [None] * (4 - len(outs))))
+    n_ws = lib.fc_linear_wgrad_workspace(desc, n, ptrs)
+    if n_ws < 0:
+        _lib.check(-n_ws, "fc_linear_wgrad_workspace")
+    buf = go.new_empty(max(int(n_ws), 1))
+    _lib_call("fc_linear_wgrad", desc, n, go.data_ptr(), xx.data_ptr(), float(alpha), ptrs, buf.data_ptr(),
+              int(n_ws), _lib.stream_of(go))
+    return outs
 
 
 
@@ -711,23 +795,45 @@ def _dense_backward(ctx, grad, grad_pre):
         if grad_pre is not None:
             gp = dense_bwd(grad_pre, pre, weight, ctx.scale, 0)
             gx = gp if gx is None else gx + gp
-    if ctx.needs_input_grad[1] or (ctx.has_bias and ctx.needs_input_grad[2]):
-        # Parameter gradients (training only), with torch on the GPU.
-        g = grad if grad is not None else torch.zeros_like(grad_pre)
-        if ctx.act and grad is not None:
-            s = torch.sigmoid(pre)
-            g = grad * 1.6765324703310907 * s * (1 + pre * (1 - s))
-        if grad_pre is not None:
-            g = g + grad_pre
-        g2 = g.reshape(-1, m)
-        if ctx.needs_input_grad[1]:
-            gw = (g2.t() @ x.reshape(-1, x.shape[-1])) * ctx.scale
-        if ctx.has_bias and ctx.needs_input_grad[2]:
-            gb = g2.sum(0)
+    if ctx.needs_input_grad[1] or (ctx.has_bias and ctx.needs_input_grad[2]):  # parameter gradients (training)
+        if grad_pre is None:  # act'(pre) is applied inside the weight-gradient kernel
+            g, act = grad, ctx.act
+        else:
+            g = grad * _torch_math.silu_grad(pre) + grad_pre if grad is not None else grad_pre
+            act = 0
+        gw, gb = dense_wgrad(g, pre, act, x, ctx.scale, bool(ctx.needs_input_grad[1]),
+                             bool(ctx.has_bias and ctx.needs_input_grad[2]))
     return gx, gw, gb, None, None
 
 
-dense_fwd.register_autograd(_dense_backward, setup_context=_dense_setup)
+_register_autograd(dense_fwd, _dense_backward, _dense_setup)
+
+
+def dense_wgrad(grad_out: Tensor, pre: Optional[Tensor], act: int, x: Tensor, scale: float, need_weight: bool,
+                need_bias: bool) -> Tuple[Optional[Tensor], Optional[Tensor]]:
+    """(scale * g^T x, column sums of g) with g = grad_out * act'(pre) (act 1) or grad_out
+    (``fc_dense_wgrad``); torch matmuls under grad mode, so that the result stays differentiable."""
+    if not (need_weight or need_bias):
+        return None, None
+    m, k = grad_out.shape[-1], x.shape[-1]
+    if torch.is_grad_enabled():
+        g2 = (grad_out * _torch_math.silu_grad(pre) if act else grad_out).reshape(-1, m)
+        gw = (g2.t() @ x.reshape(-1, k)) * scale if need_weight else None
+        return gw, (g2.sum(0) if need_bias else None)
+    go = _lib.contig("grad_out", grad_out).reshape(-1, m)
+    xx = _lib.contig("x", x).reshape(-1, k)
+    pr = _lib.contig("pre", pre).reshape(-1, m) if act else None
+    n = go.shape[0]
+    gw = go.new_empty(m, k)
+    gb = go.new_empty(m) if need_bias else None
+    lib = _lib.load()
+    n_ws = lib.fc_dense_wgrad_workspace(n, k, m, int(need_bias))
+    if n_ws < 0:
+        _lib.check(-n_ws, "fc_dense_wgrad_workspace")
+    buf = go.new_empty(max(int(n_ws), 1))
+    _lib_call("fc_dense_wgrad", n, k, m, go.data_ptr(), _lib.ptr(pr), int(act), xx.data_ptr(), float(scale),
+              gw.data_ptr(), _lib.ptr(gb), buf.data_ptr(), int(n_ws), _lib.stream_of(go))
+    return (gw if need_weight else None), gb
 
 
 # ---------------------------------------------------------------------------
@@ -761,7 +867,7 @@ def _seg_backward(ctx, grad):
     return grad.index_select(0, index.to(torch.int64)), None, None
 
 
-segment_sum.register_autograd(_seg_backward, setup_context=_seg_setup)
+_register_autograd(segment_sum, _seg_backward, _seg_setup)
 
 
 # ---------------------------------------------------------------------------
@@ -838,7 +944,7 @@ def _rms_backward(ctx, grad_out, grad_scale):
     return gx, gw, None, None
 
 
-rms_norm.register_autograd(_rms_backward, setup_context=_rms_setup)
+_register_autograd(rms_norm, _rms_backward, _rms_setup)
 
 
 # ---------------------------------------------------------------------------
@@ -900,7 +1006,7 @@ def _gate_backward(ctx, grad):
     return (gv if nv else None), (gp if np_ else None), None, None
 
 
-gate.register_autograd(_gate_backward, setup_context=_gate_setup)
+_register_autograd(gate, _gate_backward, _gate_setup)
 
 
 # second derivatives: autograd formulas of the backward ops above

@@ -89,7 +89,7 @@ def _tp_dbwd(ctx, c1, c2, cw):
     return (d_go, d_in1, d_in2, d_w) + tail
 
 
-_ops.tp_bwd.register_autograd(_tp_dbwd, setup_context=_tp_bwd_setup)
+_ops._register_autograd(_ops.tp_bwd, _tp_dbwd, _tp_bwd_setup)
 
 
 # ---------------------------------------------------------------------------
@@ -115,22 +115,14 @@ def _linear_dbwd(ctx, c):
         d_go = _ops.linear_fwd(c, weights, in_l_max, out_l_max, fin, fout, in_paths, scale, ctx.alpha)
     d_ws = [None, None, None, None]
     if any(need[1:5]):
-        n = go.shape[0]
-        in_off = out_off = 0
-        for l in range(min(in_l_max, out_l_max) + 1):
-            k = fin * in_paths[l]
-            m = 2 * l + 1
-            if need[1 + l]:
-                cl = c[:, in_off:in_off + m * k].reshape(n * m, k)
-                gl = go[:, out_off:out_off + m * fout].reshape(n * m, fout)
-                d_ws[l] = (gl.t() @ cl) * (scale[l] * ctx.alpha)
-            in_off += m * k
-            out_off += m * fout
+        d_ws = _ops.linear_wgrad(go, c, weights, in_l_max, out_l_max, fin, fout, in_paths, scale, ctx.alpha,
+                                 [bool(need[1 + l]) for l in range(len(weights))])
+        d_ws = d_ws + [None] * (4 - len(d_ws))
     d_res = c if len(need) > 12 and need[12] else None
     return (d_go, *d_ws) + (None,) * 7 + (d_res,)
 
 
-_ops.linear_bwd_op.register_autograd(_linear_dbwd, setup_context=_linear_bwd_setup)
+_ops._register_autograd(_ops.linear_bwd_op, _linear_dbwd, _linear_bwd_setup)
 
 
 # ---------------------------------------------------------------------------
@@ -162,17 +154,15 @@ def _dense_dbwd(ctx, c):
             d_go = (dh * M.silu_grad(p2)).reshape(go.shape)
         if need[1]:
             d_pre = (dh * go2 * M.silu_grad2(p2)).reshape(pre.shape)
-        h = go2 * M.silu_grad(p2) if need[2] else None
-    else:
-        if need[0]:
-            d_go = dh.reshape(go.shape)
-        h = go2
-    if need[2]:
-        d_w = (h.t() @ c2) * ctx.scale
+    elif need[0]:
+        d_go = dh.reshape(go.shape)
+    if need[2]:  # s * h^T c with h = go * act'(pre)
+        d_w, _ = _ops.dense_wgrad(go2, pre.reshape(-1, m) if ctx.act else None, ctx.act, c2, ctx.scale, True,
+                                  False)
     return d_go, d_pre, d_w, None, None
 
 
-_ops.dense_bwd.register_autograd(_dense_dbwd, setup_context=_dense_bwd_setup)
+_ops._register_autograd(_ops.dense_bwd, _dense_dbwd, _dense_bwd_setup)
 
 
 # ---------------------------------------------------------------------------
@@ -193,7 +183,7 @@ def _irreps_dbwd(ctx, c):
     return gg[0], gp[0], None
 
 
-_ops.irreps_bwd.register_autograd(_irreps_dbwd, setup_context=_irreps_bwd_setup)
+_ops._register_autograd(_ops.irreps_bwd, _irreps_dbwd, _irreps_bwd_setup)
 
 
 def _radial_bwd_setup(ctx, inputs, output):
@@ -217,7 +207,7 @@ def _radial_dbwd(ctx, c):
     return (gp[0], gg[0], gg[1]) + (None,) * 5
 
 
-_ops.radial_bwd.register_autograd(_radial_dbwd, setup_context=_radial_bwd_setup)
+_ops._register_autograd(_ops.radial_bwd, _radial_dbwd, _radial_bwd_setup)
 
 
 # ---------------------------------------------------------------------------
@@ -267,7 +257,7 @@ def _edge_dbwd(ctx, c_pos, c_vec):
     return (gg[0], gg[1], gg[2], d_pos, d_shift, None, None, d_vec) + (None,) * 10
 
 
-_ops.edge_geometry_bwd.register_autograd(_edge_dbwd, setup_context=_edge_bwd_setup)
+_ops._register_autograd(_ops.edge_geometry_bwd, _edge_dbwd, _edge_bwd_setup)
 
 
 # ---------------------------------------------------------------------------
@@ -302,7 +292,7 @@ def _rms_dbwd(ctx, c):
     return gg[0], gp[0], gp[1], None, None
 
 
-_ops.rms_norm_bwd.register_autograd(_rms_dbwd, setup_context=_rms_bwd_setup)
+_ops._register_autograd(_ops.rms_norm_bwd, _rms_dbwd, _rms_bwd_setup)
 
 
 def _gate_bwd_setup(ctx, inputs, output):
@@ -323,4 +313,4 @@ def _gate_dbwd(ctx, c_values, c_pre):
     return gg[0], gp[0], gp[1], None, None, None, None
 
 
-_ops.gate_bwd.register_autograd(_gate_dbwd, setup_context=_gate_bwd_setup)
+_ops._register_autograd(_ops.gate_bwd, _gate_dbwd, _gate_bwd_setup)

@@ -82,8 +82,9 @@ class LinearLayer(nn.Module):
         """``residual`` (same shape as the output) is added in the GEMM epilogue."""
         if x.shape[-1] != self.in_dim:
             raise RuntimeError(f"Incorrect last dimension for x. Expected {self.in_dim}, got {x.shape[-1]}.")
-        return _ops.linear_fwd(x, list(self.weight), self.in_l_max, self.out_l_max, self.in_features,
-                               self.out_features, self.in_paths, self._scale_list, float(alpha), residual)
+        return _ops.linear_fwd(x, [_ops.param_alias(w) for w in self.weight], self.in_l_max, self.out_l_max,
+                               self.in_features, self.out_features, self.in_paths, self._scale_list, float(alpha),
+                               residual)
 
     def input_grad(self, grad_out: torch.Tensor, alpha: float = 1.0,
                    residual: Optional[torch.Tensor] = None) -> torch.Tensor:

@@ -83,7 +83,8 @@ class TensorProduct(nn.Module):
             rowptr, sender_perm, sender_ptr = graph.rowptr, graph.sender_perm, graph.sender_ptr
         elif (idx_i is None) != (idx_j is None):
             raise ValueError("idx_i and idx_j must be given together.")
-        return _ops.tp_fwd(in1, in2, weights, idx_i, idx_j, self.in1_l_max, self.in2_l_max, self.out_l_max,
+        return _ops.tp_fwd(in1, in2, _ops.param_alias(weights), idx_i, idx_j, self.in1_l_max, self.in2_l_max,
+                           self.out_l_max,
                            self.in1_features, self.in2_features, self.symmetric_product, self.shared_weights,
                            *self.op_meta, self.reduce_paths, rowptr, sender_perm, sender_ptr, float(alpha))
 

@@ -208,6 +208,26 @@ int fc_dense_fwd(int64_t n, int32_t k, int32_t m, const float* x, const float* w
 int fc_dense_dgrad(int64_t n, int32_t k, int32_t m, const float* grad_out, const float* pre_act,
                    const float* w, float scale, int32_t act, float* grad_x, void* stream);
 
+/* Weight gradients (training). Replaces the weight-gradient part of the reference's
+ * linear_bwd and its linear_wgrad kernel (src/flashcart/o3/_linear.py:457-570), and the
+ * autograd weight gradient of the torch dense layers (src/flashcart/nn/layers.py:84-145).
+ * grad_w[l] (out_features, in_features*in_paths[l]) = alpha * scale_l *
+ * sum over rows (node, component) of grad_out_l^T x_l, for every rank l <= min(in_l_max,
+ * out_l_max) whose pointer is non-NULL. The row reduction is split over workgroups; the
+ * partial sums need fc_linear_wgrad_workspace() floats of workspace (0: none; pass the
+ * same grad_w array, whose non-NULL entries select the ranks, or NULL for all ranks) and
+ * are added in a fixed order, so results are deterministic. */
+int64_t fc_linear_wgrad_workspace(const fc_linear_desc* desc, int64_t n_rows, float* const* grad_w);
+int fc_linear_wgrad(const fc_linear_desc* desc, int64_t n_rows, const float* grad_out, const float* x,
+                    float alpha, float* const* grad_w, float* workspace, int64_t workspace_floats,
+                    void* stream);
+/* grad_w (m, k) = scale * g^T x and grad_b (m, may be NULL) = column sums of g, with
+ * g = grad_out * act'(pre_act) (act 1) or grad_out (act 0). */
+int64_t fc_dense_wgrad_workspace(int64_t n, int32_t k, int32_t m, int32_t with_bias);
+int fc_dense_wgrad(int64_t n, int32_t k, int32_t m, const float* grad_out, const float* pre_act, int32_t act,
+                   const float* x, float scale, float* grad_w, float* grad_b, float* workspace,
+                   int64_t workspace_floats, void* stream);
+
 /* ------------------------------------------------------------------------- */
 /* Invariant RMS normalisation: replaces RMSLayerNorm.forward (reference        */
 /* src/flashcart/nn/layers.py:494-528; no centering) and its autograd in one    */

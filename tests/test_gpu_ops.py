@@ -338,3 +338,65 @@ def test_gate(l_max, act):
     assert_close(out, ref, 1e-5, 1e-6, "gate fwd")
     assert_close(got[0], ref_g[0], 1e-5, 1e-6, "gate grad values")
     assert_close(got[1], ref_g[1], 1e-5, 1e-5 * float(ref_g[1].abs().max()), "gate grad pre")
+
+
+@pytest.mark.parametrize("lin,lout,fin,fout,paths,n", [
+    (3, 3, 128, 128, [1, 1, 1, 1], 3000),   # several row splits per rank, 128 x 128 tiles
+    (2, 2, 16, 8, [1, 3, 2], 77),           # one split, 64 x 64 tiles, partial tiles
+    (3, 1, 6, 10, [1, 1, 1, 1], 150),       # widths not multiples of 4: scalar loads
+    (1, 2, 64, 200, [2, 1], 1200),
+])
+def test_linear_wgrad(lin, lout, fin, fout, paths, n):
+    """Split-K MFMA weight gradients of the equivariant map against float64 sums of
+    grad_out_l^T x_l, one rank per block of (2l+1) rows per node."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(n + fin)
+    common = min(lin, lout)
+    in_dim = sum((2 * l + 1) * fin * paths[l] for l in range(lin + 1))
+    out_dim = sum((2 * l + 1) * fout for l in range(lout + 1))
+    x = torch.randn(n, in_dim, generator=g, dtype=torch.float64)
+    go = torch.randn(n, out_dim, generator=g, dtype=torch.float64)
+    ws = [torch.randn(fout, fin * paths[l], generator=g).to(DEV) for l in range(common + 1)]
+    scale = [0.5 + l for l in range(common + 1)]
+    with torch.no_grad():
+        got = ops.linear_wgrad(go.float().to(DEV), x.float().to(DEV), ws, lin, lout, fin, fout, paths, scale, 0.75,
+                               [True] * (common + 1))
+    io = oo = 0
+    for l in range(common + 1):
+        k, m = fin * paths[l], 2 * l + 1
+        xl = x[:, io:io + m * k].reshape(n * m, k)
+        gl = go[:, oo:oo + m * fout].reshape(n * m, fout)
+        want = gl.t() @ xl * (0.75 * scale[l])
+        assert_close(got[l], want, 0.0, 2e-5 * float(want.abs().max()), f"wgrad rank {l}")
+        io += m * k
+        oo += m * fout
+    with torch.no_grad():  # a subset of ranks
+        part = ops.linear_wgrad(go.float().to(DEV), x.float().to(DEV), ws, lin, lout, fin, fout, paths, scale, 0.75,
+                                [l == common for l in range(common + 1)])
+    assert all(p is None for p in part[:common])
+    assert_close(part[common], got[common].double(), 0.0, 0.0, "subset of ranks")
+
+
+@pytest.mark.parametrize("n,k,m,act,bias", [(20000, 64, 2176, 0, False), (5000, 64, 64, 1, True),
+                                            (333, 8, 64, 1, True), (90, 30, 17, 0, True)])
+def test_dense_wgrad(n, k, m, act, bias):
+    """Dense weight (and bias) gradients with the SiLU derivative applied to grad_out
+    inside the kernel, against float64."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(n + m)
+    x = torch.randn(n, k, generator=g, dtype=torch.float64)
+    go = torch.randn(n, m, generator=g, dtype=torch.float64)
+    pre = torch.randn(n, m, generator=g, dtype=torch.float64)
+    with torch.no_grad():
+        gw, gb = ops.dense_wgrad(go.float().to(DEV), pre.float().to(DEV), act, x.float().to(DEV), 0.125, True, bias)
+    h = go
+    if act:
+        s = torch.sigmoid(pre)
+        h = go * 1.6765324703310907 * s * (1 + pre * (1 - s))
+    want = h.t() @ x * 0.125
+    assert_close(gw, want, 0.0, 2e-5 * float(want.abs().max()), "dense wgrad")
+    if bias:
+        wb = h.sum(0)
+        assert_close(gb, wb, 0.0, 2e-5 * float(wb.abs().max()), "dense bias grad")
+    else:
+        assert gb is None
