@@ -94,6 +94,8 @@ _SIGNATURES = {
     "fc_gate_bwd": (c_int, [c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_int, c_vp, c_vp, c_vp]),
     "fc_rms_norm_fwd": (c_int, [c_i64, c_int, c_int, c_vp, c_vp, c_f32, c_vp, c_vp, c_vp]),
     "fc_rms_norm_bwd": (c_int, [c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "fc_rms_norm_dbwd": (c_int, [c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "fc_gate_dbwd": (c_int, [c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "fc_neighbor_list": (c_i64, [c_i64, c_vp, c_vp, c_vp, ctypes.c_double, c_i64, c_vp, c_vp, c_vp]),
 }
 

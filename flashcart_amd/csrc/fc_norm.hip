@@ -110,6 +110,91 @@ __global__ void __launch_bounds__(256) rms_norm_bwd_kernel(int64_t n, int C, con
   });
 }
 
+// Second derivative (force-loss training): the backward of rms_norm_bwd. With
+// G = g_l[c] broadcast over components, u = d m / dx = (1/C) w_l (vjp1 + vjp2)(x_l) and
+// gx = s go G - s^3/2 t u, t = sum go G x, the cotangent cc of gx gives, per node,
+//   p = sum cc go G,  q = sum cc u,  v = (1/C) w_l (vjp1 + vjp2)(cc_l)  (M_l symmetric):
+//   d go = s cc G - s^3/2 q G x
+//   d x  = u (-s^3/2 p + 3/4 s^5 t q) - s^3/2 q go G - s^3/2 t v
+//   d g_l[c] (this node's share) = sum_a (s cc go - s^3/2 q go x)
+template <int L>
+__global__ void __launch_bounds__(256) rms_norm_dbwd_kernel(int64_t n, int C, const float* __restrict__ go,
+                                                            const float* __restrict__ x,
+                                                            const float* __restrict__ g,
+                                                            const float* __restrict__ scale,
+                                                            const float* __restrict__ cc, float* __restrict__ d_go,
+                                                            float* __restrict__ d_x, float* __restrict__ d_g_part) {
+  constexpr int D = ncomp(L);
+  __shared__ float part[4];
+  const int64_t node = blockIdx.x;
+  const int f = threadIdx.x;
+  const bool active = f < C;
+  const int fa = active ? f : 0;
+  const int64_t base = node * (int64_t)D * C;
+  float xv[D], gv[D], cv[D], ux[D], vc[D], G[L + 1];
+  float t = 0.f, p = 0.f, q = 0.f;
+  static_for<L + 1>([&](auto lc) {
+    constexpr int l = decltype(lc)::value;
+    constexpr int N = 2 * l + 1;
+    G[l] = active ? g[l * C + fa] : 0.f;
+#pragma unroll
+    for (int a = 0; a < N; ++a) {
+      const int k = l * l + a;
+      xv[k] = active ? x[base + (int64_t)k * C + fa] : 0.f;
+      gv[k] = active ? go[base + (int64_t)k * C + fa] : 0.f;
+      cv[k] = active ? cc[base + (int64_t)k * C + fa] : 0.f;
+    }
+    float dx[N], dc[N];
+#pragma unroll
+    for (int a = 0; a < N; ++a) dx[a] = dc[a] = 0.f;
+    const float one[1] = {1.0f};
+    TPPath<l, l, 0>::vjp1(one, xv + l * l, dx);
+    TPPath<l, l, 0>::vjp2(one, xv + l * l, dx);
+    TPPath<l, l, 0>::vjp1(one, cv + l * l, dc);
+    TPPath<l, l, 0>::vjp2(one, cv + l * l, dc);
+    const float wl = rank_weight<L>(l) / (float)C;
+#pragma unroll
+    for (int a = 0; a < N; ++a) {
+      const int k = l * l + a;
+      ux[k] = wl * dx[a];
+      vc[k] = wl * dc[a];
+      t = fmaf(gv[k] * G[l], xv[k], t);
+      p = fmaf(cv[k] * gv[k], G[l], p);
+      q = fmaf(cv[k], ux[k], q);
+    }
+  });
+  t = block_channel_sum(active ? t : 0.f, part);
+  p = block_channel_sum(active ? p : 0.f, part);
+  q = block_channel_sum(active ? q : 0.f, part);
+  if (!active) return;
+  const float s = scale[node];
+  const float h3 = 0.5f * s * s * s;  // s^3 / 2
+  const float cu = -h3 * p + 1.5f * h3 * s * s * t * q;  // -s^3/2 p + 3/4 s^5 t q
+  static_for<L + 1>([&](auto lc) {
+    constexpr int l = decltype(lc)::value;
+    float dg = 0.f;
+#pragma unroll
+    for (int a = 0; a < 2 * l + 1; ++a) {
+      const int k = l * l + a;
+      const int64_t o = base + (int64_t)k * C + f;
+      if (d_go) d_go[o] = G[l] * (s * cv[k] - h3 * q * xv[k]);
+      if (d_x) d_x[o] = cu * ux[k] - h3 * q * gv[k] * G[l] - h3 * t * vc[k];
+      dg += gv[k] * (s * cv[k] - h3 * q * xv[k]);
+    }
+    if (d_g_part) d_g_part[(node * (L + 1) + l) * C + f] = dg;
+  });
+}
+
+template <int L>
+int launch_rms_dbwd(int64_t n, int C, const float* go, const float* x, const float* g, const float* scale,
+                    const float* cc, float* d_go, float* d_x, float* d_g_part, hipStream_t s) {
+  const int threads = ((C + 63) / 64) * 64;
+  hipLaunchKernelGGL(rms_norm_dbwd_kernel<L>, dim3((unsigned)n), dim3(threads), 0, s, n, C, go, x, g, scale, cc,
+                     d_go, d_x, d_g_part);
+  FC_LAUNCH_CHECK();
+  return FC_OK;
+}
+
 template <int L>
 int launch_rms(bool bwd, int64_t n, int C, const float* go, const float* x, const float* g, float eps, float* out,
                float* scale, hipStream_t s) {
@@ -153,4 +238,23 @@ extern "C" int fc_rms_norm_bwd(int64_t n, int32_t l_max, int32_t C, const float*
   if (n > 0 && (!grad_out || !x || !weight || !scale || !grad_x)) return FC_ERR_NULL;
   return rms_dispatch(true, n, l_max, C, grad_out, x, weight, 0.f, grad_x, const_cast<float*>(scale),
                       (hipStream_t)stream);
+}
+
+extern "C" int fc_rms_norm_dbwd(int64_t n, int32_t l_max, int32_t C, const float* grad_out, const float* x,
+                                const float* weight, const float* scale, const float* cot, float* d_grad_out,
+                                float* d_x, float* d_weight_part, void* stream) {
+  if (n < 0 || C < 1) return FC_ERR_SHAPE;
+  if (l_max < 0) return FC_ERR_BAD_DESC;
+  if (l_max > FC_KERNEL_L_MAX) return FC_ERR_UNSUPPORTED_L;
+  if (C > 256 || n > 0x7fffffff) return FC_ERR_SHAPE;
+  if (n == 0) return FC_OK;
+  if (!grad_out || !x || !weight || !scale || !cot) return FC_ERR_NULL;
+  hipStream_t s = (hipStream_t)stream;
+  switch (l_max) {
+    case 0: return launch_rms_dbwd<0>(n, C, grad_out, x, weight, scale, cot, d_grad_out, d_x, d_weight_part, s);
+    case 1: return launch_rms_dbwd<1>(n, C, grad_out, x, weight, scale, cot, d_grad_out, d_x, d_weight_part, s);
+    case 2: return launch_rms_dbwd<2>(n, C, grad_out, x, weight, scale, cot, d_grad_out, d_x, d_weight_part, s);
+    case 3: return launch_rms_dbwd<3>(n, C, grad_out, x, weight, scale, cot, d_grad_out, d_x, d_weight_part, s);
+  }
+  return FC_ERR_UNSUPPORTED_L;
 }

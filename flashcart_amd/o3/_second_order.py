@@ -12,8 +12,10 @@ src/flashcart/o3/_irreps.py:201-202).
 * ``linear_bwd`` (the dgrad GEMM) is linear in grad_out and the weights: its derivative
   is ``linear_fwd`` of the cotangent and a weight-gradient GEMM.
 * ``dense_bwd``: explicit formulas with the rescaled SiLU's first and second derivative.
-* elementwise layers (edge geometry, Eq. 1, radial basis, envelope, RMS norm, gate):
-  differentiate their torch restatements twice (``_torch_math.vjp_of_vjp``).
+* ``rms_norm_bwd`` and ``gate_bwd``: closed-form second derivatives in one node-wise
+  kernel each (``fc_rms_norm_dbwd``, ``fc_gate_dbwd``).
+* per-edge layers (edge geometry, Eq. 1, radial basis, envelope): differentiate their
+  torch restatements twice (``_torch_math.vjp_of_vjp``).
 
 Importing this module registers the formulas on the ``flashcart::*`` ops.
 """
@@ -270,26 +272,32 @@ def _rms_bwd_setup(ctx, inputs, output):
     ctx.l_max = int(l_max)
 
 
-def _rms_fn_from_scale(x0: Tensor, s0: Tensor, l_max: int, channels: int):
-    """The norm as a function of (x, weight) with the constant fixed by the saved scale:
-    s(x) = (m(x) - m(x0) + s0^-2)^-1/2 equals (m(x) + eps)^-1/2 for every x."""
-    with torch.no_grad():
-        k = s0.double().pow(-2) - M.rms_mean(x0.double(), l_max, channels)
-
-    def fn(x, w):
-        s = torch.rsqrt(M.rms_mean(x, l_max, channels) + k.to(x.dtype))
-        gain = torch.cat([w[l].unsqueeze(0).expand(2 * l + 1, channels) for l in range(l_max + 1)]).reshape(1, -1)
-        return x * s.unsqueeze(-1) * gain
-
-    return fn
+def _no_third(name: str) -> None:
+    if torch.is_grad_enabled():
+        raise NotImplementedError(f"third derivatives of {name} are not provided "
+                                  "(a second-order backward was run with create_graph=True).")
 
 
 def _rms_dbwd(ctx, c):
+    """Backward of rms_norm_bwd: one node-wise kernel (``fc_rms_norm_dbwd``) for the
+    gradients with respect to grad_out and x and each node's share of the gain gradient."""
+    _no_third("the RMS norm")
     go, x, weight, scale = ctx.saved_tensors
     need = ctx.needs_input_grad
-    fn = _rms_fn_from_scale(x, scale, ctx.l_max, weight.shape[-1])
-    gp, gg = M.vjp_of_vjp(fn, [x, weight], [0], [go], [c], [need[1], need[2]], [need[0]])
-    return gg[0], gp[0], gp[1], None, None
+    if c is None or not any(need[:3]):
+        return None, None, None, None, None
+    n, C, l_max = x.shape[0], weight.shape[-1], ctx.l_max
+    g = _ops._lib.contig("grad_out", go)
+    xx = _ops._lib.contig("x", x)
+    cc = _ops._lib.contig("cotangent", c)
+    d_go = torch.empty_like(xx) if need[0] else None
+    d_x = torch.empty_like(xx) if need[1] else None
+    part = xx.new_empty(n, l_max + 1, C) if need[2] else None
+    _ops._lib_call("fc_rms_norm_dbwd", n, l_max, C, g.data_ptr(), xx.data_ptr(),
+                   _ops._lib.contig("weight", weight).data_ptr(), _ops._lib.contig("scale", scale).data_ptr(),
+                   cc.data_ptr(), _ops._lib.ptr(d_go), _ops._lib.ptr(d_x), _ops._lib.ptr(part),
+                   _ops._lib.stream_of(xx))
+    return d_go, d_x, (part.sum(0) if part is not None else None), None, None
 
 
 _ops._register_autograd(_ops.rms_norm_bwd, _rms_dbwd, _rms_bwd_setup)
@@ -303,14 +311,28 @@ def _gate_bwd_setup(ctx, inputs, output):
 
 
 def _gate_dbwd(ctx, c_values, c_pre):
+    """Backward of gate_bwd: one elementwise kernel (``fc_gate_dbwd``)."""
+    _no_third("the gate")
     go, values, pre = ctx.saved_tensors
     l_max, act = ctx.cfg
     need = ctx.needs_input_grad
-    wrt = [k for k in (0, 1) if ctx.computed[k]]
-    cots = [_live(c) for k, c in zip((0, 1), (c_values, c_pre)) if ctx.computed[k]]
-    gp, gg = M.vjp_of_vjp(lambda v, p: M.gate(v, p, l_max, act), [values, pre], wrt, [go], cots,
-                          [need[1], need[2]], [need[0]])
-    return gg[0], gp[0], gp[1], None, None, None, None
+    cv = _live(c_values) if ctx.computed[0] else None
+    cp = _live(c_pre) if ctx.computed[1] else None
+    if (cv is None and cp is None) or not any(need[:3]):
+        return None, None, None, None, None, None, None
+    L = _ops._lib
+    g = L.contig("grad_out", go)
+    v = L.contig("values", values)
+    p = L.contig("pre", pre)
+    cv = L.contig("cot_values", cv) if cv is not None else None
+    cp = L.contig("cot_pre", cp) if cp is not None else None
+    d_go = torch.empty_like(g) if need[0] else None
+    d_v = torch.empty_like(v) if need[1] else None
+    d_p = torch.empty_like(p) if need[2] else None
+    C = p.shape[-1] // (l_max + 1)
+    _ops._lib_call("fc_gate_dbwd", v.shape[0], l_max, C, g.data_ptr(), v.data_ptr(), p.data_ptr(), int(act),
+                   L.ptr(cv), L.ptr(cp), L.ptr(d_go), L.ptr(d_v), L.ptr(d_p), L.stream_of(v))
+    return d_go, d_v, d_p, None, None, None, None
 
 
 _ops._register_autograd(_ops.gate_bwd, _gate_dbwd, _gate_bwd_setup)

@@ -1,14 +1,14 @@
-"""Differentiable PyTorch statements of the per-edge and per-node elementwise layers.
+"""Differentiable PyTorch statements of the per-edge layers, for second derivatives.
 
 The forward and first backward of every op run as HIP kernels. Training with a force
-loss differentiates the first backward once more: for the tensor product and the
-equivariant linear map that second derivative is again a composition of the HIP
-kernels, while the elementwise layers (edge geometry with Eq. 1, radial basis,
-envelope, RMS norm, gate, rescaled SiLU) are restated here so that autograd can
-differentiate their first backward. They run with torch on the tensors' own device,
-only inside a backward that builds a graph; like the reference, which implements the
-same layers with torch (src/flashcart/nn/radial.py; src/flashcart/nn/layers.py:12-75,
-494-528,609-635; src/flashcart/model/flashcart.py:22).
+loss differentiates the first backward once more. For the tensor product, the linear
+maps, the RMS norm and the gate that second derivative is again HIP kernels; the edge
+geometry (edge vector, Eq. 1 expansion, radial basis, envelope) is restated here so
+that autograd can differentiate its first backward twice. The statements run with torch
+on the tensors' own device, only inside a second-order backward; like the reference,
+which implements these layers with torch (src/flashcart/nn/radial.py;
+src/flashcart/model/flashcart.py:22). ``rms_mean`` (the RMS norm's mean invariant) and
+the rescaled-SiLU derivatives serve the first-order formulas of auxiliary outputs.
 
 Each function evaluates exactly what the matching kernel evaluates (same expressions,
 clamps and masks), so first derivatives taken here agree with the kernels' to rounding.
@@ -28,7 +28,6 @@ Tensor = torch.Tensor
 
 MIN_EDGE_LENGTH = 1.0e-4  # src/flashcart/model/flashcart.py:22
 SILU_SCALE = 1.6765324703310907  # RescaledSiLULayer, src/flashcart/nn/layers.py:12-45
-SIGMOID_SCALE = 1.8462285453386054  # RescaledSigmoidLayer, src/flashcart/nn/layers.py:48-75
 
 
 # ---------------------------------------------------------------------------
@@ -142,30 +141,6 @@ def rms_mean(x: Tensor, l_max: int, channels: int) -> Tensor:
         M = torch.tensor(_rank0_metric(l), dtype=x.dtype, device=x.device)
         m = m + (xl * torch.einsum("bc,ncf->nbf", M, xl)).sum(1) / ((2 * l + 1) * (l_max + 1))
     return m.mean(-1)
-
-
-def rms_scale(x: Tensor, l_max: int, channels: int, eps: float) -> Tensor:
-    """s[n] = (m + eps)^-1/2."""
-    return torch.rsqrt(rms_mean(x, l_max, channels) + eps)
-
-
-def rms_norm(x: Tensor, weight: Tensor, l_max: int, eps: float) -> Tensor:
-    C = weight.shape[-1]
-    s = rms_scale(x, l_max, C, eps)
-    gain = torch.cat([weight[l].unsqueeze(0).expand(2 * l + 1, C) for l in range(l_max + 1)]).reshape(1, -1)
-    return x * s.unsqueeze(-1) * gain
-
-
-def gate_activation(pre: Tensor, act: int) -> Tensor:
-    return SIGMOID_SCALE * torch.sigmoid(pre) if act else pre
-
-
-def gate(values: Tensor, pre: Tensor, l_max: int, act: int) -> Tensor:
-    n = values.shape[0]
-    C = pre.shape[-1] // (l_max + 1)
-    g = gate_activation(pre, act).reshape(n, l_max + 1, C)
-    g = torch.cat([g[:, l:l + 1].expand(n, 2 * l + 1, C) for l in range(l_max + 1)], dim=1)
-    return values * g.reshape(n, -1)
 
 
 def silu_grad(pre: Tensor) -> Tensor:

@@ -241,6 +241,13 @@ int fc_rms_norm_fwd(int64_t n, int32_t l_max, int32_t C, const float* x, const f
 /* grad_x = d<grad_out, out>/dx for fixed weight (the gain gradient is not formed). */
 int fc_rms_norm_bwd(int64_t n, int32_t l_max, int32_t C, const float* grad_out, const float* x,
                     const float* weight, const float* scale, float* grad_x, void* stream);
+/* Second derivative (no counterpart in the reference, which differentiates its torch norm
+ * with autograd): the gradients of <cot, grad_x> with respect to grad_out, x and the gain.
+ * d_weight_part (n, l_max+1, C) receives each node's share of the gain gradient (sum it
+ * over nodes). Any output may be NULL. */
+int fc_rms_norm_dbwd(int64_t n, int32_t l_max, int32_t C, const float* grad_out, const float* x,
+                     const float* weight, const float* scale, const float* cot, float* d_grad_out,
+                     float* d_x, float* d_weight_part, void* stream);
 
 /* ------------------------------------------------------------------------- */
 /* Rank-wise gating: replaces the gate activation, index_select and product of  */
@@ -254,6 +261,12 @@ int fc_gate_fwd(int64_t n, int32_t l_max, int32_t C, const float* values, const 
 /* grad_values = grad_out * act(pre); grad_pre = act'(pre) * sum_a grad_out * values (either may be NULL). */
 int fc_gate_bwd(int64_t n, int32_t l_max, int32_t C, const float* grad_out, const float* values,
                 const float* pre, int32_t act, float* grad_values, float* grad_pre, void* stream);
+/* Second derivative (no counterpart in the reference, which differentiates its torch gate
+ * with autograd): gradients of <cot_values, grad_values> + <cot_pre, grad_pre> with respect
+ * to grad_out, values and pre. Cotangents and outputs may be NULL. */
+int fc_gate_dbwd(int64_t n, int32_t l_max, int32_t C, const float* grad_out, const float* values,
+                 const float* pre, int32_t act, const float* cot_values, const float* cot_pre,
+                 float* d_grad_out, float* d_values, float* d_pre, void* stream);
 
 /* ------------------------------------------------------------------------- */
 /* Segment reductions: replace scatter_sum (reference src/flashcart/utils/     */
