@@ -255,6 +255,38 @@ def run_other_workload(name, args, dev):
                                  "achieved": 112 * E / (ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s"}})
     elif name.startswith("train_"):
         run_training(name, args, dev, res)
+    elif name == "nl_fcc25k":
+        # Neighbour list of the cfg 4 system at r_max + skin, built on the GPU from positions in
+        # HBM (fc_neighbor_list_device), a fresh N(0, 0.01^2) perturbation per build; the CPU
+        # baseline is the host cell list of this library (identical pairs) on the same system.
+        from flashcart_amd.data.neighbors import neighbor_pairs, neighbor_pairs_device
+        numbers, pos, cell, pbc = make_system()
+        rng = np.random.default_rng(1)
+        steps = [torch.as_tensor(pos + rng.normal(scale=SIGMA_STEP, size=pos.shape), device=dev)
+                 for _ in range(args.warmup + args.steps)]
+        for k in range(args.warmup):
+            neighbor_pairs_device(steps[k], cell, pbc, R_MAX + SKIN)
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        for k in range(args.warmup, args.warmup + args.steps):
+            ei, _ = neighbor_pairs_device(steps[k], cell, pbc, R_MAX + SKIN)
+        torch.cuda.synchronize(dev)
+        dt = time.perf_counter() - t0
+        ms = 1e3 * dt / args.steps
+        res.update({"metric": "neighbour-list builds per second (25,000-atom fcc, cutoff 6 A, on the GPU)",
+                    "value": args.steps / dt, "unit": "builds/s", "ms_per_step": ms,
+                    "pairs": int(ei.shape[1]), "dtype": "f64",
+                    "config": {"n_atoms": len(numbers), "cutoff": R_MAX + SKIN, "pbc": [True, True, True]}})
+        if not args.no_cpu_baseline:
+            t0 = time.perf_counter()
+            calls = 0
+            while calls < 3 or time.perf_counter() - t0 < 2.0:
+                neighbor_pairs(pos, cell, pbc, R_MAX + SKIN)
+                calls += 1
+            rate = calls / (time.perf_counter() - t0)
+            res["cpu_baseline"] = {"value": rate, "unit": "builds/s", "cores": 1, "kind": "port",
+                                   "sample": f"host cell list (fc_neighbor_list), same system, {calls} builds"}
+            res["speedup_vs_cpu"] = res["value"] / rate
     else:
         if name == "cfg3_water_1536":
             z, p, cell, pbc = water_box(512, seed=0)
@@ -374,7 +406,7 @@ def run_training(name, args, dev, res):
 
 
 WORKLOADS = ("cfg4_fcc25k", "cfg1_tp_standalone", "cfg2_expansion_radial", "cfg3_water_1536", "cfg5_molecules_512",
-             "train_molecules_192", "train_fcc_2048")
+             "train_molecules_192", "train_fcc_2048", "nl_fcc25k")
 
 
 def main():

@@ -97,6 +97,9 @@ _SIGNATURES = {
     "fc_rms_norm_dbwd": (c_int, [c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "fc_gate_dbwd": (c_int, [c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "fc_neighbor_list": (c_i64, [c_i64, c_vp, c_vp, c_vp, ctypes.c_double, c_i64, c_vp, c_vp, c_vp]),
+    "fc_neighbor_list_device_workspace": (c_i64, [c_i64]),
+    "fc_neighbor_list_device": (c_i64, [c_i64, c_vp, c_vp, c_vp, ctypes.c_double, c_i64, c_vp, c_vp, c_vp, c_vp,
+                                        c_i64, c_vp]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

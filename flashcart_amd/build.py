@@ -36,6 +36,12 @@ CFLAGS = [
 ]
 
 
+# The device neighbour list must reproduce the host list's float64 distance tests bit for
+# bit, so its products and sums stay separate roundings (no fused multiply-add), like the
+# host build's.
+NO_CONTRACT = {"fc_neighbors_dev.hip": ["-ffp-contract=off"]}
+
+
 def _sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith((".hip", ".cpp")))
 
@@ -47,7 +53,7 @@ def _deps_digest() -> str:
             if f.endswith((".h", ".hip", ".cpp")):
                 with open(os.path.join(d, f), "rb") as fh:
                     h.update(f.encode() + fh.read())
-    h.update(" ".join(CFLAGS).encode())
+    h.update(" ".join(CFLAGS).encode() + repr(sorted(NO_CONTRACT.items())).encode())
     return h.hexdigest()
 
 
@@ -56,7 +62,7 @@ def _compile(src: str) -> str:
     if src.endswith(".cpp"):  # host-only code
         cmd = ["g++", "-O3", "-fPIC", "-std=c++17", "-c", src, "-o", obj]
     else:
-        cmd = [HIPCC, *CFLAGS, "-c", src, "-o", obj]
+        cmd = [HIPCC, *CFLAGS, *NO_CONTRACT.get(os.path.basename(src), []), "-c", src, "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{res.stderr[-6000:]}")

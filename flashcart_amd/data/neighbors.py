@@ -3,9 +3,10 @@
 ``NeighborList`` keeps the reference's interface (``r_max``, ``skin``, ``build``,
 ``from_arrays``, ``edge_index`` / ``unit_shifts`` arrays). The pairs come from the
 host cell list of libflashcart_hip.so (``fc_neighbor_list``) in the canonical order
-(i, j, Sx, Sy, Sz); the reference delegates to matscipy, whose order inside a
-receiver block is not documented, so only the edge set and the receiver sort are
-shared with it.
+(i, j, Sx, Sy, Sz), or from its GPU twin (``fc_neighbor_list_device``, same pairs and
+order) for positions already in HBM; the reference delegates to matscipy, whose order
+inside a receiver block is not documented, so only the edge set and the receiver sort
+are shared with it.
 """
 
 from __future__ import annotations
@@ -14,6 +15,7 @@ import ctypes
 from typing import Optional, Union
 
 import numpy as np
+import torch
 
 from flashcart_amd import _lib
 
@@ -48,8 +50,52 @@ def neighbor_pairs(positions: np.ndarray, cell: np.ndarray, pbc, cutoff: float, 
         cap = int(cnt)
 
 
+_last_device_count = {}  # atom count -> pairs of the last device build (output size hint)
+
+
+def neighbor_pairs_device(positions: torch.Tensor, cell, pbc, cutoff: float, eps: float = 1e-7):
+    """The pairs of ``neighbor_pairs`` built on the GPU from positions in HBM
+    (``fc_neighbor_list_device``): (edge_index (2, E) int64, unit_shifts (E, 3) int32) on
+    the positions' device, identical to the host list (same float64 tests, same order)."""
+    if not positions.is_cuda:
+        raise RuntimeError(f"neighbor_pairs_device needs positions on a ROCm device, got {positions.device}.")
+    pos = positions.detach().to(torch.float64).reshape(-1, 3).contiguous()
+    cell_np = np.ascontiguousarray(
+        cell.detach().cpu().numpy() if torch.is_tensor(cell) else np.asarray(cell), dtype=np.float64).reshape(3, 3)
+    pbc = np.broadcast_to(np.asarray(pbc.cpu() if torch.is_tensor(pbc) else pbc, dtype=bool).reshape(-1), (3,))
+    n = pos.shape[0]
+    if abs(np.linalg.det(cell_np)) < eps:  # open boundaries: a padded bounding box, as the host list
+        span = (pos.amax(0) - pos.amin(0)).cpu().numpy() if n else np.zeros(3)
+        cell_np = np.diag(np.maximum(span, 1e-3) + 2.0 * cutoff)
+        pbc = np.zeros(3, dtype=bool)
+    flags = np.ascontiguousarray(pbc.astype(np.int32))
+    lib = _lib.load()
+    ws_bytes = int(lib.fc_neighbor_list_device_workspace(n))
+    if ws_bytes < 0:
+        _lib.check(-ws_bytes, "fc_neighbor_list_device_workspace")
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=pos.device)
+    # an undersized output costs a second search: start from the last count for this size
+    cap = max(64, int(n * 64), _last_device_count.get(n, 0) * 9 // 8)
+    while True:
+        ei = torch.empty(2, cap, dtype=torch.int64, device=pos.device)
+        sh = torch.empty(cap, 3, dtype=torch.int32, device=pos.device)
+        cnt = lib.fc_neighbor_list_device(n, pos.data_ptr(), cell_np.ctypes.data, flags.ctypes.data, float(cutoff),
+                                          cap, ei[0].data_ptr(), ei[1].data_ptr(), sh.data_ptr(), ws.data_ptr(),
+                                          ws_bytes, _lib.stream_of(pos))
+        if cnt < 0:
+            _lib.check(-cnt, "fc_neighbor_list_device")
+        _last_device_count[n] = int(cnt)
+        if cnt <= cap:
+            return ei[:, :cnt].contiguous(), sh[:cnt]
+        cap = int(cnt) * 9 // 8
+
+
 class NeighborList:
-    """Pairs within ``r_max + skin`` (reference ``neighbors.py:10-117``)."""
+    """Pairs within ``r_max + skin`` (reference ``neighbors.py:10-117``).
+
+    ``backend="device"`` builds the list on the GPU (``neighbor_pairs_device``) from
+    positions given as a ROCm tensor and keeps ``edge_index`` / ``unit_shifts`` as device
+    tensors; the pairs are those of the host backend."""
 
     def __init__(self, r_max: float, skin: float = 0.0, backend: str = "native"):
         self.r_max = r_max
@@ -64,11 +110,15 @@ class NeighborList:
 
     def copy(self) -> "NeighborList":
         nl = NeighborList(self.r_max, self.skin, self.backend)
-        nl.edge_index = None if self.edge_index is None else self.edge_index.copy()
-        nl.unit_shifts = None if self.unit_shifts is None else self.unit_shifts.copy()
+        for name in ("edge_index", "unit_shifts"):
+            v = getattr(self, name)
+            setattr(nl, name, None if v is None else (v.clone() if torch.is_tensor(v) else v.copy()))
         return nl
 
     def build(self, positions: np.ndarray, cell: np.ndarray, pbc: Union[bool, list]) -> "NeighborList":
+        if self.backend == "device":
+            self.edge_index, self.unit_shifts = neighbor_pairs_device(positions, cell, pbc, self.r_max + self.skin)
+            return self
         ei, sh = neighbor_pairs(positions, cell, pbc, self.r_max + self.skin)
         self.edge_index = np.asarray(ei, dtype=np.int64)
         self.unit_shifts = np.asarray(sh, dtype=np.int32)

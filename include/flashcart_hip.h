@@ -291,6 +291,20 @@ int64_t fc_neighbor_list(int64_t n, const double* pos, const double* cell, const
                          double cutoff, int64_t capacity, int64_t* out_i, int64_t* out_j,
                          int32_t* out_shift);
 
+/* The same list built on the GPU from device positions (also replaces NeighborList.build,
+ * reference src/flashcart/data/neighbors.py:56-77,120-143): identical pairs in identical
+ * order (float64 arithmetic of the host list, no fused multiply-adds). pos (n,3) float64
+ * and the outputs are device memory; cell[9] and pbc[3] host memory. workspace: device
+ * memory of fc_neighbor_list_device_workspace(n) bytes. Synchronises `stream` (the pair
+ * count is read back). Returns the pair count (outputs written only when it fits in
+ * `capacity`), or -fc_status: FC_ERR_BAD_DESC (singular cell, bad cutoff),
+ * FC_ERR_SHAPE (more than 1024 pairs for one atom, or a shift component >= 512). */
+int64_t fc_neighbor_list_device_workspace(int64_t n);
+int64_t fc_neighbor_list_device(int64_t n, const double* pos, const double* cell, const int32_t* pbc,
+                                double cutoff, int64_t capacity, int64_t* out_i, int64_t* out_j,
+                                int32_t* out_shift, void* workspace, int64_t workspace_bytes,
+                                void* stream);
+
 #ifdef __cplusplus
 }
 #endif
