@@ -40,6 +40,9 @@ HBM_PEAK_GBS = 8000.0
 # `bench.py --kernel-only` (first step graph, E = 1,080,166), each counter scaled by its reading for
 # a 2 GiB elementwise copy (FETCH x2.000, WRITE x1.000); see profiles/tp_conv_fwd_l1_fcc25k_hbm_traffic.md.
 MEASURED_TRAFFIC_BYTES = 11.77e9
+# The same for the layer-1 backward op (tp_bwd_kernel 27.085 GB + segment_rows_kernel 5.116 GB) from
+# the `bench.py --profile-step` counter runs; see profiles/fcc25k_L3_C128_kernel_hbm_mfma.md.
+MEASURED_TRAFFIC_BWD_BYTES = 32.20e9
 R_MAX = 5.0
 SIGMA_STEP = 0.01
 SKIN = 1.0
@@ -111,9 +114,10 @@ def tp_conv_bytes(n_nodes, n_send, E, d1, d2, P, C, nout):
     return 4 * (n_send * d1 * C + E * d2 + E * P * C + n_nodes * nout * C) + 4 * E + 4 * (n_nodes + 1)
 
 
-def measure_dominant(model, graph, dev, reps=10):
-    """Average duration of the layer-1 TP convolution forward (the largest HBM-bound kernel),
-    timed with HIP events on the stream the op launches on (torch's current stream)."""
+def measure_dominant(model, graph, dev, reps=10, with_backward=False):
+    """Average duration of the layer-1 TP convolution forward (the north star's TP kernel),
+    timed with HIP events on the stream the op launches on (torch's current stream), and
+    with ``with_backward`` also of its backward op (the largest kernel of the step by time)."""
     from flashcart_amd.o3 import _ops
     from flashcart_amd.o3._graph import build_graph
     inter = model.interactions[1]
@@ -139,9 +143,28 @@ def measure_dominant(model, graph, dev, reps=10):
     torch.cuda.synchronize(dev)
     ms = ev0.elapsed_time(ev1) / reps
     nout = tp.out_dim // tp.in1_features
-    byts = tp_conv_bytes(n, n, E, (tp.in1_l_max + 1) ** 2, (tp.in2_l_max + 1) ** 2, tp.n_total_paths,
-                         tp.in1_features, nout)
-    return ms, byts
+    d1, d2, P, C = (tp.in1_l_max + 1) ** 2, (tp.in2_l_max + 1) ** 2, tp.n_total_paths, tp.in1_features
+    byts = tp_conv_bytes(n, n, E, d1, d2, P, C, nout)
+    if not with_backward:
+        return ms, byts
+    # The backward op as the energy+forces step runs it (gradients for in1, in2 and the
+    # weights): tp_bwd_kernel, then the sender-ordered segmented sum of the per-edge messages.
+    go = torch.randn(n, tp.out_dim, device=dev, generator=g)
+    bargs = (go,) + args[:17] + (False, True, True, True) + args[18:]
+    for _ in range(2):
+        _ops.tp_bwd(*bargs)
+    torch.cuda.synchronize(dev)
+    ev0.record(stream)
+    for _ in range(reps):
+        _ops.tp_bwd(*bargs)
+    ev1.record(stream)
+    torch.cuda.synchronize(dev)
+    ms_b = ev0.elapsed_time(ev1) / reps
+    # tp_bwd_kernel: the forward's reads plus the weight gradient, the per-edge sender messages
+    # and the edge-attribute gradient written; segment_rows_kernel: messages read, in1 gradient written
+    kern = byts + 4 * (E * P * C + E * d1 * C + E * d2)
+    seg = 4 * (E * d1 * C + n * d1 * C) + 4 * E + 4 * (n + 1)
+    return ms, byts, ms_b, kern + seg
 
 
 def cpu_baseline(model, cfg, avg_neighbors, budget_s=20.0):
@@ -491,9 +514,11 @@ def main():
     if not (np.isfinite(e) and np.isfinite(fmax)):
         raise RuntimeError("non-finite energy or forces")
     log(f"{args.steps} steps in {dt:.3f}s ({1e3 * dt / args.steps:.3f} ms/step); E={e:.6f} |F|max={fmax:.4f}")
-    ms, byts = measure_dominant(model, graphs[-1], dev)
+    ms, byts, ms_b, byts_b = measure_dominant(model, graphs[-1], dev, with_backward=True)
     gbs = byts / (ms * 1e-3) / 1e9
-    log(f"dominant kernel tp_fwd conv (layer 1): {ms:.3f} ms/launch, {byts / 1e9:.3f} GB algorithmic, {gbs:.1f} GB/s")
+    gbs_b = byts_b / (ms_b * 1e-3) / 1e9
+    log(f"tp_fwd conv (layer 1): {ms:.3f} ms/launch, {byts / 1e9:.3f} GB algorithmic, {gbs:.1f} GB/s; "
+        f"backward op: {ms_b:.3f} ms, {byts_b / 1e9:.3f} GB, {gbs_b:.1f} GB/s")
     result = {
         "metric": "atom-steps/s (energy+forces) at 25k atoms L_max=3",
         "value": n_atoms * args.steps / dt,
@@ -513,7 +538,16 @@ def main():
         "roofline": {"bound": "hbm", "kernel": "tp_fwd_kernel<2,3,3> (conv, layer 1)", "achieved": gbs,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
                      "traffic": MEASURED_TRAFFIC_BYTES, "traffic_launch": "bench.py --kernel-only (E=1080166)",
-                     "algorithmic_bytes": byts, "avg_launch_ms": ms},
+                     "algorithmic_bytes": byts, "avg_launch_ms": ms,
+                     "note": "the north star's TP kernel; by time the layer-1 backward dominates the step "
+                             "(roofline_tp_bwd)"},
+        # the step's largest kernel by time: the layer-1 TP backward op = tp_bwd_kernel<2,3,3> (VALU-bound)
+        # + segment_rows_kernel (sender gather); achieved = both kernels' algorithmic bytes / op time
+        "roofline_tp_bwd": {"bound": "hbm", "kernel": "tp_bwd_kernel<2,3,3> + segment_rows_kernel (layer 1)",
+                            "achieved": gbs_b, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs_b / HBM_PEAK_GBS,
+                            "traffic": MEASURED_TRAFFIC_BWD_BYTES,
+                            "traffic_launch": "bench.py --profile-step (E=1080166)",
+                            "algorithmic_bytes": byts_b, "avg_launch_ms": ms_b},
         "energy": e,
     }
     if not args.no_cpu_baseline:
