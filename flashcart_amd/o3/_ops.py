@@ -69,6 +69,13 @@ def tp_meta(in1_l_max: int, in2_l_max: int, out_l_max: int, in1_features: int, i
     return offs(in1_l_max, in1_features), offs(in2_l_max, in2_features), sizes, n_paths, int(total)
 
 
+# Engine queries used to narrow needs_input_grad; without them (another torch build) every
+# statically required gradient is computed, which is correct, only slower.
+_current_node = getattr(torch._C, "_current_autograd_node", None)
+if not hasattr(torch._C, "_will_engine_execute_node"):
+    _current_node = None
+
+
 def param_alias(t: Optional[Tensor]) -> Optional[Tensor]:
     """A parameter as an op input: a view of it while autograd records, so that the backward
     can ask the engine whether the current pass needs the parameter's gradient (it cannot
@@ -102,7 +109,7 @@ def _register_autograd(op, backward, setup_context) -> None:
 
     def bwd(ctx, *grads):
         static = ctx.needs_input_grad
-        node = torch._C._current_autograd_node()
+        node = _current_node() if _current_node is not None else None
         mask = ctx.tensor_inputs
         if node is not None and len(node.next_functions) == sum(mask):
             edges = iter(node.next_functions)
