@@ -278,6 +278,28 @@ def run_other_workload(name, args, dev):
                                  "achieved": 112 * E / (ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s"}})
     elif name.startswith("train_"):
         run_training(name, args, dev, res)
+    elif name == "lammps_fcc25k":
+        # The LAMMPS ML-IAP path on the cfg 4 system as a single rank hands it over: owned atoms,
+        # ghost images, pair indices and device pair vectors (SingleRankMLIAPData); one step =
+        # FlashCartLAMMPSUnified.compute_forces (site energies + pair forces, ghost exchange hooks).
+        from flashcart_amd.calculators import FlashCartLAMMPSUnified, SingleRankMLIAPData
+        numbers, pos, cell, pbc = make_system()
+        graph = AtomicGraph.from_arrays(numbers, pos, ["Cu", "Ni", "Fe", "Cr"], R_MAX, cell=cell, pbc=pbc)
+        avg = graph.edge_index.shape[1] / graph.num_nodes
+        model, cfg = build_model(avg)
+        unified = FlashCartLAMMPSUnified(model.to(dev))
+        data = SingleRankMLIAPData(graph, device=dev)
+        dt, _ = _timed(lambda: unified.compute_forces(data), args.steps, args.warmup, dev)
+        if not np.isfinite(data.energy):
+            raise RuntimeError("non-finite energy")
+        res.update({"metric": "atom-steps/s (LAMMPS ML-IAP compute_forces, 25k-atom fcc, L_max=3)",
+                    "value": data.nlocal * args.steps / dt, "unit": "atom-steps/s",
+                    "ms_per_step": 1e3 * dt / args.steps,
+                    "config": {"n_local": data.nlocal, "n_ghost": data.ntotal - data.nlocal, "n_pairs": data.npairs,
+                               "channels": 128, "l_max_edge_attrs": 3}})
+        if not args.no_cpu_baseline:
+            res["cpu_baseline"] = cpu_baseline(model.cpu(), cfg, avg)
+            res["speedup_vs_cpu"] = res["value"] / res["cpu_baseline"]["value"]
     elif name == "nl_fcc25k":
         # Neighbour list of the cfg 4 system at r_max + skin, built on the GPU from positions in
         # HBM (fc_neighbor_list_device), a fresh N(0, 0.01^2) perturbation per build; the CPU
@@ -429,7 +451,7 @@ def run_training(name, args, dev, res):
 
 
 WORKLOADS = ("cfg4_fcc25k", "cfg1_tp_standalone", "cfg2_expansion_radial", "cfg3_water_1536", "cfg5_molecules_512",
-             "train_molecules_192", "train_fcc_2048", "nl_fcc25k")
+             "train_molecules_192", "train_fcc_2048", "nl_fcc25k", "lammps_fcc25k")
 
 
 def main():

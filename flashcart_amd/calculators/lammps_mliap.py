@@ -226,6 +226,67 @@ def build_lammps_unified(checkpoint: Union[str, Path], compile_mode: Optional[st
     return FlashCartLAMMPSUnified(model, compile_mode=compile_mode)
 
 
+class SingleRankMLIAPData:
+    """A periodic structure in the layout a single-rank LAMMPS run hands to ML-IAP: owned
+    atoms, one ghost atom per periodic image that a pair reaches, pair indices into
+    owned + ghost atoms and the pair vectors r_ij = x_j - x_i on the device. The exchange
+    hooks copy owner features to their ghosts and add ghost gradients back to the owners,
+    as LAMMPS's forward / reverse communication does on one rank.
+
+    Drives ``FlashCartLAMMPSUnified.compute_forces`` without LAMMPS (tests, benchmarks);
+    pair forces are kept as a device tensor (``pair_forces``) through
+    ``update_pair_forces``, and ``atom_forces()`` folds them onto the owned atoms."""
+
+    def __init__(self, graph, device=None):
+        ei = graph.edge_index.cpu().numpy()
+        shifts = graph.shifts.cpu().numpy().astype(np.int64)
+        n_local = int(graph.positions.shape[0])
+        ghost = np.any(shifts != 0, axis=1)
+        keys, inv = np.unique(np.concatenate([ei[1][ghost, None], shifts[ghost]], axis=1), axis=0,
+                              return_inverse=True)
+        pair_j = ei[1].copy()
+        pair_j[ghost] = n_local + inv.reshape(-1)
+        device = torch.device(device) if device is not None else graph.positions.device
+        self.nlocal = n_local
+        self.ntotal = n_local + keys.shape[0]
+        self.npairs = ei.shape[1]
+        self.owner = torch.as_tensor(keys[:, 0], device=device)
+        pos = graph.positions.double().cpu().numpy()
+        cell = graph.cell[0].double().cpu().numpy()
+        self.pair_i = torch.as_tensor(ei[0].astype(np.int32), device=device)
+        self.pair_j = torch.as_tensor(pair_j.astype(np.int32), device=device)
+        self.rij = torch.as_tensor(pos[ei[1]] + shifts @ cell - pos[ei[0]], dtype=torch.float32, device=device)
+        types = graph.atom_types.cpu().numpy()
+        self.elems = torch.as_tensor(np.concatenate([types, types[keys[:, 0]]]).astype(np.int32), device=device)
+        self.eflag = True
+        self.eatoms = None
+        self.energy = None
+        self.pair_forces = None
+
+    def forward_exchange(self, src, dst, width) -> None:
+        dst[: self.nlocal] = src[: self.nlocal]
+        dst[self.nlocal:] = src[self.owner]
+
+    def reverse_exchange(self, src, dst, width) -> None:
+        dst.copy_(src)
+        dst[self.nlocal:] = 0
+        dst.index_add_(0, self.owner, src[self.nlocal:])
+
+    def update_pair_forces(self, pair_forces) -> None:
+        self.pair_forces = pair_forces
+
+    def atom_forces(self) -> torch.Tensor:
+        """Forces on the owned atoms: -dE/dx from the pair forces dE/dr_ij, ghost forces folded
+        onto their owners."""
+        pf = torch.as_tensor(self.pair_forces)
+        f = torch.zeros(self.ntotal, 3, dtype=pf.dtype, device=pf.device)
+        f.index_add_(0, self.pair_i.to(pf.device, torch.long), pf)
+        f.index_add_(0, self.pair_j.to(pf.device, torch.long), -pf)
+        out = f[: self.nlocal].clone()
+        out.index_add_(0, self.owner.to(pf.device), f[self.nlocal:])
+        return out
+
+
 def save_lammps_unified(unified: FlashCartLAMMPSUnified, path: Union[str, Path]) -> Path:
     """Write the interface for the LAMMPS ``pair_style mliap unified <file>`` command
     (``torch.save`` of the object, as the reference does)."""

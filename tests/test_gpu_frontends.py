@@ -209,3 +209,20 @@ def test_lammps_mliap_matches_periodic_prediction(use_f):
                  1e-5, 1e-6, "eatoms")
     forces = data.fold_ghosts(data.f) if use_f else _pair_forces_to_atoms(data, data.pair_forces)
     assert_close(torch.as_tensor(forces), ref["forces"], 0.0, 1e-4, "LAMMPS forces")
+
+
+def test_single_rank_mliap_data_matches_prediction():
+    """The packaged single-rank ML-IAP layout (``SingleRankMLIAPData``: ghosts per periodic
+    image, device arrays, pair forces kept on the device) reproduces the periodic prediction."""
+    from flashcart_amd.calculators import FlashCartLAMMPSUnified, SingleRankMLIAPData
+    z, p, cell, pbc = fcc_alloy(3, 2, 2, seed=11)
+    cfg = model_config(["Cu", "Ni", "Fe", "Cr"], 16, 3, avg_neighbors=42.0)
+    model = _model(cfg, 31)
+    g = AtomicGraph.from_arrays(z, p, cfg["elements"], 5.0, cell=cell, pbc=pbc)
+    ref = model.to(DEV).predict(g.to(DEV), compute_forces=True)
+    data = SingleRankMLIAPData(g, device=DEV)
+    FlashCartLAMMPSUnified(model).compute_forces(data)
+    assert data.ntotal > data.nlocal and data.pair_forces.is_cuda
+    e_ref = float(ref["energy"][0])
+    assert abs(data.energy - e_ref) <= 1e-5 * abs(e_ref) + 1e-6
+    assert_close(data.atom_forces(), ref["forces"], 0.0, 1e-4, "LAMMPS forces (single-rank data)")
