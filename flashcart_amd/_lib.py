@@ -70,6 +70,7 @@ _SIGNATURES = {
     "fc_radial_bwd": (c_int, [ctypes.POINTER(RadialDesc), c_i64, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "fc_edge_geometry_fwd": (c_int, [ctypes.POINTER(EdgeDesc), c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "fc_edge_geometry_bwd": (c_int, [ctypes.POINTER(EdgeDesc), c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "fc_edge_geometry_dbwd": (c_int, [ctypes.POINTER(EdgeDesc), c_i64] + [c_vp] * 14),
     "fc_csr_from_sorted": (c_int, [c_i64, c_vp, c_i64, c_vp, c_vp]),
     "fc_edge_grad_to_nodes": (c_int, [ctypes.POINTER(CSR), c_vp, c_vp, c_vp]),
     "fc_tp_num_paths": (c_int, [ctypes.POINTER(TPDesc)]),

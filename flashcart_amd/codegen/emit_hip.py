@@ -217,6 +217,27 @@ def emit_expand_header(l_max: int = KERNEL_L_MAX) -> str:
             if terms:
                 L.append(f"    g[{k}] += " + " + ".join(terms) + ";")
         L.append("  }")
+        # second-order helpers (training): directional derivative and Hessian-vector product
+        L.append("  // dt[a] = sum_j dT_a/du_j du_j")
+        L.append("  __device__ static __forceinline__ void jvp(float x, float y, float z, const float* __restrict__ du, "
+                 "float* __restrict__ dt) {")
+        for a, p in enumerate(polys):
+            terms = [f"du[{j}] * ({_c_expr(sp.diff(p, s))})" for j, s in enumerate((X, Y, Z)) if sp.diff(p, s) != 0]
+            L.append(f"    dt[{a}] = " + (" + ".join(terms) if terms else "0.0f") + ";")
+        L.append("  }")
+        L.append("  // h[i] += sum_a gt[a] sum_j d2T_a/(du_i du_j) du[j]")
+        L.append("  __device__ static __forceinline__ void hvp(float x, float y, float z, const float* __restrict__ gt, "
+                 "const float* __restrict__ du, float* __restrict__ h) {")
+        for i, si in enumerate((X, Y, Z)):
+            terms = []
+            for a, p in enumerate(polys):
+                for j, sj in enumerate((X, Y, Z)):
+                    d2 = sp.diff(p, si, sj)
+                    if d2 != 0:
+                        terms.append(f"gt[{a}] * du[{j}] * ({_c_expr(d2)})")
+            if terms:
+                L.append(f"    h[{i}] += " + " + ".join(terms) + ";")
+        L.append("  }")
         L.append("};")
     L.append("}  // namespace fc")
     return "\n".join(L) + "\n"

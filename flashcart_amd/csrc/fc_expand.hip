@@ -262,6 +262,184 @@ __global__ void edge_bwd_kernel(RadialParams p, int64_t n, const float* __restri
   for (int k = 0; k < 3; ++k) gvec[3 * e + k] = gr[k] * inv + nd * v[k];
 }
 
+// ---------------------------------------------------------------------------
+// Second derivatives (force-loss training): the backward of the edge-geometry backward.
+// ---------------------------------------------------------------------------
+template <int L>
+__device__ __forceinline__ void expand_all_jvp(float x, float y, float z, const float* du, float* dt) {
+  static_for<L + 1>([&](auto ic) {
+    constexpr int l = decltype(ic)::value;
+    Expand<l>::jvp(x, y, z, du, dt + l * l);
+  });
+}
+
+template <int L>
+__device__ __forceinline__ void expand_all_hvp(float x, float y, float z, const float* g, const float* du, float* h) {
+  static_for<L + 1>([&](auto ic) {
+    constexpr int l = decltype(ic)::value;
+    if constexpr (l > 1) Expand<l>::hvp(x, y, z, g + l * l, du, h);
+  });
+}
+
+// First and second derivatives of the radial basis with respect to d.
+__device__ __forceinline__ void radial_d12(const RadialParams& p, float d, float* df, float* d2f) {
+  const int n = p.n_radial;
+  if (p.basis == FC_BASIS_BESSEL) {
+    // f = sqrt(2/r_max) sin(w d) / d = pre w sinc(t), t = w d: f' = pre w^2 sinc'(t), f'' = pre w^3 sinc''(t)
+    const float pre = sqrtf(2.0f / p.r_max);
+    for (int k = 0; k < n; ++k) {
+      const float w = (float)M_PI / p.r_max * (float)(k + 1);
+      const float t = w * d;
+      float s1, s2;
+      if (fabsf(t) < 0.05f) {  // Taylor series (the closed forms cancel for small t)
+        const float t2 = t * t;
+        s1 = t * (-1.0f / 3.0f + t2 * (1.0f / 30.0f));
+        s2 = -1.0f / 3.0f + t2 * (1.0f / 10.0f);
+      } else {
+        const float sn = sinf(t), cs = cosf(t), it = 1.0f / t;
+        s1 = (cs - sn * it) * it;
+        s2 = ((2.0f * it * it - 1.0f) * sn - 2.0f * cs * it) * it;
+      }
+      df[k] = pre * w * w * s1;
+      d2f[k] = pre * w * w * w * s2;
+    }
+    return;
+  }
+  // Chebyshev T_k(x(t)), t = (d - r_min) / span: F' = T_k' x', F'' = T_k'' x'^2 + T_k' x''
+  const float span = p.r_max - p.r_min;
+  const float t = (d - p.r_min) / span;
+  float x, x1, x2;
+  if (p.basis == FC_BASIS_CHEBYSHEV_COSINE) {
+    const float a = t * (float)M_PI;
+    x = cosf(a);
+    x1 = -sinf(a) * (float)M_PI / span;
+    x2 = -x * (float)(M_PI * M_PI) / (span * span);
+  } else {
+    x = 2.0f * t - 1.0f;
+    x1 = 2.0f / span;
+    x2 = 0.0f;
+  }
+  float tm2 = 1.0f, tm1 = x, dm2 = 0.0f, dm1 = 1.0f, sm2 = 0.0f, sm1 = 0.0f;  // T, T', T'' of k-2, k-1
+  df[0] = 0.0f;
+  d2f[0] = 0.0f;
+  if (n > 1) {
+    df[1] = x1;
+    d2f[1] = x2;
+  }
+  for (int k = 2; k < n; ++k) {
+    const float tk = 2.0f * x * tm1 - tm2;
+    const float dk = 2.0f * tm1 + 2.0f * x * dm1 - dm2;
+    const float sk = 4.0f * dm1 + 2.0f * x * sm1 - sm2;
+    df[k] = dk * x1;
+    d2f[k] = sk * x1 * x1 + dk * x2;
+    tm2 = tm1; tm1 = tk; dm2 = dm1; dm1 = dk; sm2 = sm1; sm1 = sk;
+  }
+}
+
+// First and second derivatives of the envelope with respect to d (zero where the clamps or
+// the cutoff mask hold it constant, as the first derivative of envelope_eval).
+__device__ __forceinline__ void envelope_d12(const RadialParams& p, float d, float* de, float* d2e) {
+  const int po = p.poly_order;
+  const float dc = fmaxf(d, 0.0f);
+  const float t = dc / p.r_max;
+  float g = 0.0f, dg = 0.0f, d2g = 0.0f;  // Horner for g, g', g''
+  for (int k = po - 1; k >= 0; --k) {
+    d2g = fmaf(d2g, t, 2.0f * dg);
+    dg = fmaf(dg, t, g);
+    g = fmaf(g, t, 0.5f * (float)((k + 1) * (k + 2)));
+  }
+  const float s = 1.0f - t;
+  const float mask = dc < p.r_max ? 1.0f : 0.0f;
+  const float v = s * s * s * g * mask;
+  const bool pass = (v >= 0.0f && v <= 1.0f) && (d >= 0.0f);
+  const float h = s * dg - 3.0f * g;  // P = s^3 g: dP/dt = s^2 h, d2P/dt2 = -2 s h + s^2 (s g'' - 4 g')
+  *de = pass ? mask * s * s * h / p.r_max : 0.0f;
+  *d2e = pass ? mask * (-2.0f * s * h + s * s * (s * d2g - 4.0f * dg)) / (p.r_max * p.r_max) : 0.0f;
+}
+
+// With the edge vector v, d = |v|, u = v / max(d, eps), a = dA/du^T g_attrs and
+// s = g_feats . F'(d) + g_env P'(d), the first-order backward is
+//   gvec = (a - (u.a) u) / d + s u   (d >= eps),   a / eps + s v / d   (0 < d < eps).
+// Its derivative along the cotangent c of gvec gives d_vec (the Hessian-vector product of
+// g . geometry), and the derivative of the geometry along c gives the gradients of the
+// upstream gradients: d_g_attrs = dA/du du, d_g_feats = F'(d) dd, d_g_env = P'(d) dd.
+template <int L>
+__global__ void edge_dbwd_kernel(RadialParams p, int64_t n, const float* __restrict__ pos,
+                                 const float* __restrict__ shift, const int32_t* __restrict__ ii,
+                                 const int32_t* __restrict__ jj, const float* __restrict__ vectors,
+                                 const float* __restrict__ ga, const float* __restrict__ gf,
+                                 const float* __restrict__ ge, const float* __restrict__ cvec,
+                                 float* __restrict__ d_ga, float* __restrict__ d_gf, float* __restrict__ d_ge,
+                                 float* __restrict__ d_vec) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n) return;
+  float v[3];
+  edge_vector(e, pos, shift, ii, jj, vectors, v);
+  const float d = sqrtf(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
+  const bool big = d >= kMinEdgeLength;
+  const float inv = 1.0f / fmaxf(d, kMinEdgeLength);
+  const float u[3] = {v[0] * inv, v[1] * inv, v[2] * inv};
+  const float c[3] = {cvec[3 * e], cvec[3 * e + 1], cvec[3 * e + 2]};
+  const float dd = d > 0.f ? (v[0] * c[0] + v[1] * c[1] + v[2] * c[2]) / d : 0.f;  // tangent of d
+  float du[3];  // tangent of u
+#pragma unroll
+  for (int k = 0; k < 3; ++k) du[k] = big ? (c[k] - dd * u[k]) * inv : c[k] * inv;
+  float a[3] = {0.f, 0.f, 0.f}, da[3] = {0.f, 0.f, 0.f};
+  if (ga) {
+    float g[ncomp(L)];
+#pragma unroll
+    for (int k = 0; k < ncomp(L); ++k) g[k] = ga[e * ncomp(L) + k];
+    expand_all_bwd<L>(u[0], u[1], u[2], g, a);
+    expand_all_hvp<L>(u[0], u[1], u[2], g, du, da);
+  }
+  if (d_ga) {
+    float dt[ncomp(L)];
+    expand_all_jvp<L>(u[0], u[1], u[2], du, dt);
+#pragma unroll
+    for (int k = 0; k < ncomp(L); ++k) d_ga[e * ncomp(L) + k] = dt[k];
+  }
+  float s = 0.f, s2 = 0.f;
+  if (p.basis != FC_BASIS_NONE && (gf || d_gf)) {
+    float df[kMaxRadial], d2f[kMaxRadial];
+    radial_d12(p, d, df, d2f);
+    for (int k = 0; k < p.n_radial; ++k) {
+      if (gf) {
+        s = fmaf(gf[e * p.n_radial + k], df[k], s);
+        s2 = fmaf(gf[e * p.n_radial + k], d2f[k], s2);
+      }
+      if (d_gf) d_gf[e * p.n_radial + k] = df[k] * dd;
+    }
+  }
+  if (p.poly_order > 0 && (ge || d_ge)) {
+    float de, d2e;
+    envelope_d12(p, d, &de, &d2e);
+    if (ge) {
+      s = fmaf(ge[e], de, s);
+      s2 = fmaf(ge[e], d2e, s2);
+    }
+    if (d_ge) d_ge[e] = de * dd;
+  }
+  if (!d_vec) return;
+  float out[3];
+  if (big) {
+    const float ua = u[0] * a[0] + u[1] * a[1] + u[2] * a[2];
+    const float dua = du[0] * a[0] + du[1] * a[1] + du[2] * a[2] + u[0] * da[0] + u[1] * da[1] + u[2] * da[2];
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+      out[k] = (da[k] - dua * u[k] - ua * du[k]) * inv - (a[k] - ua * u[k]) * inv * inv * dd + s2 * dd * u[k] +
+               s * du[k];
+  } else if (d > 0.f) {
+    const float id = 1.0f / d;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) out[k] = da[k] * inv + (s2 * dd - s * dd * id) * id * v[k] + s * id * c[k];
+  } else {
+#pragma unroll
+    for (int k = 0; k < 3; ++k) out[k] = da[k] * inv;
+  }
+#pragma unroll
+  for (int k = 0; k < 3; ++k) d_vec[3 * e + k] = out[k];
+}
+
 template <template <int> class K, class... Args>
 int launch_by_l(int l, int64_t n, hipStream_t s, Args... args) {
   if (n == 0) return FC_OK;
@@ -392,4 +570,31 @@ extern "C" int fc_edge_geometry_bwd(const fc_edge_desc* desc, int64_t n, const f
     case 3: return launch_edge_bwd<3>(p, n, pos, shift, ii, jj, vectors, ga, gf, ge, gvec, s);
   }
   return FC_ERR_UNSUPPORTED_L;
+}
+
+extern "C" int fc_edge_geometry_dbwd(const fc_edge_desc* desc, int64_t n, const float* pos, const float* shift,
+                                     const int32_t* ii, const int32_t* jj, const float* vectors,
+                                     const float* ga, const float* gf, const float* ge, const float* cot_vec,
+                                     float* d_ga, float* d_gf, float* d_ge, float* d_vec, void* stream) {
+  if (!desc) return FC_ERR_NULL;
+  int st = check_radial(&desc->radial);
+  if (st != FC_OK) return st;
+  if (desc->l_max < 0 || desc->l_max > 3) return FC_ERR_UNSUPPORTED_L;
+  if (n == 0) return FC_OK;
+  if (!cot_vec || (pos ? (!ii || !jj) : !vectors)) return FC_ERR_NULL;
+  const RadialParams p = radial_params(desc->radial);
+  const dim3 grid((unsigned)((n + 255) / 256)), block(256);
+  hipStream_t s = (hipStream_t)stream;
+#define FC_EDGE_DBWD(LL)                                                                                   \
+  hipLaunchKernelGGL(edge_dbwd_kernel<LL>, grid, block, 0, s, p, n, pos, shift, ii, jj, vectors, ga, gf, ge, \
+                     cot_vec, d_ga, d_gf, d_ge, d_vec)
+  switch (desc->l_max) {
+    case 0: FC_EDGE_DBWD(0); break;
+    case 1: FC_EDGE_DBWD(1); break;
+    case 2: FC_EDGE_DBWD(2); break;
+    case 3: FC_EDGE_DBWD(3); break;
+  }
+#undef FC_EDGE_DBWD
+  FC_LAUNCH_CHECK();
+  return FC_OK;
 }

@@ -315,16 +315,25 @@ def edge_geometry_bwd(g_attrs: Optional[Tensor], g_feats: Optional[Tensor], g_en
               _lib.ptr(vec), _lib.ptr(ga), _lib.ptr(gf), _lib.ptr(ge), gvec.data_ptr(), stream)
     if not need_positions or pos is None:
         return ref.new_empty(0), gvec
-    n = pos.shape[0]
+    return edge_grad_to_nodes(gvec, pos.shape[0], idx_i, idx_j, rowptr, sender_perm, sender_ptr), gvec
+
+
+def edge_grad_to_nodes(gvec: Tensor, n_nodes: int, idx_i: Tensor, idx_j: Tensor, rowptr: Optional[Tensor],
+                       sender_perm: Optional[Tensor], sender_ptr: Optional[Tensor]) -> Tensor:
+    """Gradient of the positions from that of the edge vectors v = R_j - R_i (+ shift):
+    sender sums minus receiver sums, as segmented sums in a fixed order (``fc_edge_grad_to_nodes``)."""
     if rowptr is None or sender_perm is None or sender_ptr is None:
         from flashcart_amd.o3._graph import build_graph
-        gcsr = build_graph(torch.stack([idx_i, idx_j]), n, check_sorted=False)
+        gcsr = build_graph(torch.stack([idx_i, idx_j]), n_nodes, check_sorted=False)
         rowptr, sender_perm, sender_ptr = gcsr.rowptr, gcsr.sender_perm, gcsr.sender_ptr
-    gpos = pos.new_empty(n, 3)
-    csr = _lib.csr_struct(n, E, jj, _i32("rowptr", rowptr), _i32("sender_perm", sender_perm),
-                          _i32("sender_ptr", sender_ptr), n)
-    _lib_call("fc_edge_grad_to_nodes", csr, gvec.data_ptr(), gpos.data_ptr(), stream)
-    return gpos, gvec
+    gv = _lib.contig("grad_vec", gvec)
+    # int32 copies stay referenced until the launch has read their addresses
+    jj, rp, sp, sq = (_i32("idx_j", idx_j), _i32("rowptr", rowptr), _i32("sender_perm", sender_perm),
+                      _i32("sender_ptr", sender_ptr))
+    gpos = gv.new_empty(n_nodes, 3)
+    csr = _lib.csr_struct(n_nodes, jj.shape[0], jj, rp, sp, sq, n_nodes)
+    _lib_call("fc_edge_grad_to_nodes", csr, gv.data_ptr(), gpos.data_ptr(), _lib.stream_of(gv))
+    return gpos
 
 
 @edge_geometry_bwd.register_fake

@@ -12,10 +12,11 @@ src/flashcart/o3/_irreps.py:201-202).
 * ``linear_bwd`` (the dgrad GEMM) is linear in grad_out and the weights: its derivative
   is ``linear_fwd`` of the cotangent and a weight-gradient GEMM.
 * ``dense_bwd``: explicit formulas with the rescaled SiLU's first and second derivative.
-* ``rms_norm_bwd`` and ``gate_bwd``: closed-form second derivatives in one node-wise
-  kernel each (``fc_rms_norm_dbwd``, ``fc_gate_dbwd``).
-* per-edge layers (edge geometry, Eq. 1, radial basis, envelope): differentiate their
-  torch restatements twice (``_torch_math.vjp_of_vjp``).
+* ``rms_norm_bwd``, ``gate_bwd`` and ``edge_geometry_bwd``: closed-form second
+  derivatives in one kernel each (``fc_rms_norm_dbwd``, ``fc_gate_dbwd`` per node,
+  ``fc_edge_geometry_dbwd`` per edge).
+* the standalone ``irreps_bwd`` and ``radial_bwd``: differentiate their torch
+  restatements twice (``_torch_math.vjp_of_vjp``).
 
 Importing this module registers the formulas on the ``flashcart::*`` ops.
 """
@@ -218,45 +219,56 @@ _ops._register_autograd(_ops.radial_bwd, _radial_dbwd, _radial_bwd_setup)
 
 def _edge_bwd_setup(ctx, inputs, output):
     (g_attrs, g_feats, g_env, positions, shift_vec, idx_i, idx_j, vectors, rowptr, sperm, sptr) = inputs[:11]
-    ctx.save_for_backward(g_attrs, g_feats, g_env, positions, shift_vec, idx_i, idx_j, vectors)
+    ctx.save_for_backward(g_attrs, g_feats, g_env, positions, shift_vec, idx_i, idx_j, vectors, rowptr, sperm, sptr)
     ctx.cfg = tuple(inputs[11:17])
     ctx.computed_pos = bool(inputs[17]) and positions is not None
 
 
 def _edge_dbwd(ctx, c_pos, c_vec):
     """gvec = d<g, geometry(v)>/dv and gpos = its scatter onto the atoms (v = R_j - R_i + shift),
-    so <c_pos, gpos> + <c_vec, gvec> = <c_vec + c_pos[j] - c_pos[i], gvec>."""
-    g_attrs, g_feats, g_env, positions, shift_vec, idx_i, idx_j, vectors = ctx.saved_tensors
+    so <c_pos, gpos> + <c_vec, gvec> = <c_vec + c_pos[j] - c_pos[i], gvec>: one per-edge
+    kernel (``fc_edge_geometry_dbwd``) for the Hessian-vector product and the gradients of
+    the upstream gradients, and the node scatter of the first-order backward for positions."""
+    _no_third("the edge geometry")
+    g_attrs, g_feats, g_env, positions, shift_vec, idx_i, idx_j, vectors, rowptr, sperm, sptr = ctx.saved_tensors
     l_max, basis, n_radial, r_min, r_max, poly_order = ctx.cfg
     need = ctx.needs_input_grad
-    ii = idx_i.to(torch.int64)
-    jj = idx_j.to(torch.int64)
+    L = _ops._lib
     cv = _live(c_vec)
     cp = _live(c_pos) if ctx.computed_pos else None
     if cp is not None:
+        ii, jj = idx_i.to(torch.int64), idx_j.to(torch.int64)
         cv = _acc(cv, cp.index_select(0, jj) - cp.index_select(0, ii))
-    none = (None,) * 18
     if cv is None:
-        return none
-    v = M.edge_vectors(positions, shift_vec, idx_i, idx_j, vectors)
-    gs = [_live(g_attrs), _live(g_feats) if basis != _ops._lib.BASIS_NONE else None,
+        return (None,) * 18
+    gs = [_live(g_attrs), _live(g_feats) if basis != L.BASIS_NONE else None,
           _live(g_env) if poly_order > 0 else None]
+    gs = [L.contig(name, t) if t is not None else None for name, t in zip(("g_attrs", "g_feats", "g_env"), gs)]
+    E = idx_i.shape[0]
+    ref = cv
+    d_ga = ref.new_empty(E, (l_max + 1) ** 2) if need[0] else None
+    d_gf = ref.new_empty(E, n_radial) if (need[1] and basis != L.BASIS_NONE) else None
+    d_ge = ref.new_empty(E) if (need[2] and poly_order > 0) else None
     need_v = need[3] or need[4] or need[7]
-
-    def fn(vv):
-        return M.edge_geometry(vv, l_max, basis, n_radial, r_min, r_max, poly_order)
-
-    gp, gg = M.vjp_of_vjp(fn, [v], [0], gs, [cv], [need_v], [need[0], need[1], need[2]])
-    hv = gp[0]
+    hv = ref.new_empty(E, 3) if need_v else None
+    pos = L.contig("positions", positions) if positions is not None else None
+    sv = L.contig("shift_vec", shift_vec) if shift_vec is not None else None
+    vec = L.contig("vectors", vectors) if vectors is not None else None
+    desc = _ops._edge_desc(l_max, basis, n_radial, r_min, r_max, poly_order)
+    # converted copies stay referenced until the launch has read their addresses
+    ii32, jj32, cvc = _ops._i32("idx_i", idx_i), _ops._i32("idx_j", idx_j), L.contig("cotangent", cv)
+    _ops._lib_call("fc_edge_geometry_dbwd", desc, E, L.ptr(pos), L.ptr(sv), ii32.data_ptr(), jj32.data_ptr(),
+                   L.ptr(vec), *(L.ptr(t) for t in gs), cvc.data_ptr(), L.ptr(d_ga), L.ptr(d_gf), L.ptr(d_ge),
+                   L.ptr(hv), L.stream_of(cvc))
     d_pos = d_shift = d_vec = None
     if hv is not None:
         if need[3] and positions is not None:
-            d_pos = torch.zeros_like(positions).index_add(0, jj, hv).index_add(0, ii, -hv)
+            d_pos = _ops.edge_grad_to_nodes(hv, positions.shape[0], idx_i, idx_j, rowptr, sperm, sptr)
         if need[4] and shift_vec is not None:
             d_shift = hv
         if need[7] and vectors is not None:
             d_vec = hv
-    return (gg[0], gg[1], gg[2], d_pos, d_shift, None, None, d_vec) + (None,) * 10
+    return (d_ga, d_gf, d_ge, d_pos, d_shift, None, None, d_vec) + (None,) * 10
 
 
 _ops._register_autograd(_ops.edge_geometry_bwd, _edge_dbwd, _edge_bwd_setup)
@@ -290,11 +302,12 @@ def _rms_dbwd(ctx, c):
     g = _ops._lib.contig("grad_out", go)
     xx = _ops._lib.contig("x", x)
     cc = _ops._lib.contig("cotangent", c)
+    w = _ops._lib.contig("weight", weight)
+    sc = _ops._lib.contig("scale", scale)
     d_go = torch.empty_like(xx) if need[0] else None
     d_x = torch.empty_like(xx) if need[1] else None
     part = xx.new_empty(n, l_max + 1, C) if need[2] else None
-    _ops._lib_call("fc_rms_norm_dbwd", n, l_max, C, g.data_ptr(), xx.data_ptr(),
-                   _ops._lib.contig("weight", weight).data_ptr(), _ops._lib.contig("scale", scale).data_ptr(),
+    _ops._lib_call("fc_rms_norm_dbwd", n, l_max, C, g.data_ptr(), xx.data_ptr(), w.data_ptr(), sc.data_ptr(),
                    cc.data_ptr(), _ops._lib.ptr(d_go), _ops._lib.ptr(d_x), _ops._lib.ptr(part),
                    _ops._lib.stream_of(xx))
     return d_go, d_x, (part.sum(0) if part is not None else None), None, None

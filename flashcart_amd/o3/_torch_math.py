@@ -1,14 +1,12 @@
-"""Differentiable PyTorch statements of the per-edge layers, for second derivatives.
+"""Differentiable PyTorch statements for second derivatives of the standalone ops.
 
-The forward and first backward of every op run as HIP kernels. Training with a force
-loss differentiates the first backward once more. For the tensor product, the linear
-maps, the RMS norm and the gate that second derivative is again HIP kernels; the edge
-geometry (edge vector, Eq. 1 expansion, radial basis, envelope) is restated here so
-that autograd can differentiate its first backward twice. The statements run with torch
-on the tensors' own device, only inside a second-order backward; like the reference,
-which implements these layers with torch (src/flashcart/nn/radial.py;
-src/flashcart/model/flashcart.py:22). ``rms_mean`` (the RMS norm's mean invariant) and
-the rescaled-SiLU derivatives serve the first-order formulas of auxiliary outputs.
+The forward and first backward of every op run as HIP kernels, and so do the second
+derivatives of everything on the model's path. The standalone ``irreps`` (Eq. 1) and
+``radial`` (radial basis, envelope) ops differentiate their first backward through the
+statements here instead; they run with torch on the tensors' own device, only inside a
+second-order backward, like the reference's torch layers (src/flashcart/nn/radial.py).
+``rms_mean`` (the RMS norm's mean invariant) and the rescaled-SiLU derivatives serve the
+first- and second-order formulas of auxiliary outputs.
 
 Each function evaluates exactly what the matching kernel evaluates (same expressions,
 clamps and masks), so first derivatives taken here agree with the kernels' to rounding.
@@ -18,7 +16,6 @@ from __future__ import annotations
 
 import math
 from functools import lru_cache
-from typing import Optional, Tuple
 
 import torch
 
@@ -26,7 +23,6 @@ from flashcart_amd import _lib
 
 Tensor = torch.Tensor
 
-MIN_EDGE_LENGTH = 1.0e-4  # src/flashcart/model/flashcart.py:22
 SILU_SCALE = 1.6765324703310907  # RescaledSiLULayer, src/flashcart/nn/layers.py:12-45
 
 
@@ -93,27 +89,6 @@ def envelope(d: Tensor, r_max: float, poly_order: int) -> Tensor:
     s = 1.0 - t
     env = s * s * s * g * (dc < r_max).to(d.dtype)
     return torch.clamp(env, min=0.0, max=1.0)
-
-
-def edge_vectors(positions: Optional[Tensor], shift_vec: Optional[Tensor], idx_i: Tensor, idx_j: Tensor,
-                 vectors: Optional[Tensor]) -> Tensor:
-    if vectors is not None:
-        return vectors
-    ii = idx_i.to(torch.int64)
-    jj = idx_j.to(torch.int64)
-    v = positions.index_select(0, jj) - positions.index_select(0, ii)
-    return v + shift_vec if shift_vec is not None else v
-
-
-def edge_geometry(v: Tensor, l_max: int, basis: int, n_radial: int, r_min: float, r_max: float,
-                  poly_order: int) -> Tuple[Tensor, Optional[Tensor], Optional[Tensor]]:
-    """(attrs, radial feats or None, envelope or None) of edge vectors ``v`` (E, 3)."""
-    d = torch.sqrt((v * v).sum(-1))
-    u = v / torch.clamp(d, min=MIN_EDGE_LENGTH).unsqueeze(-1)
-    attrs = expansion(u, l_max)
-    feats = radial_basis(d, basis, n_radial, r_min, r_max) if basis != _lib.BASIS_NONE else None
-    env = envelope(d, r_max, poly_order) if poly_order > 0 else None
-    return attrs, feats, env
 
 
 # ---------------------------------------------------------------------------

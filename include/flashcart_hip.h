@@ -98,6 +98,17 @@ int fc_edge_geometry_bwd(const fc_edge_desc* desc, int64_t n_edges, const float*
                          const float* shift_vec, const int32_t* idx_i, const int32_t* idx_j,
                          const float* vectors, const float* g_attrs, const float* g_feats,
                          const float* g_env, float* grad_vec, void* stream);
+/* Second derivative (force-loss training; the reference differentiates its torch edge
+ * geometry and irreps_dbwd, src/flashcart/o3/_irreps.py:146-199): for the cotangent cot_vec
+ * (n_edges, 3) of grad_vec, d_vec = the derivative of grad_vec along cot_vec (Hessian-vector
+ * product of g . geometry) and d_g_* = the derivative of the geometry along cot_vec (the
+ * gradients with respect to g_attrs / g_feats / g_env). Any input gradient and any output
+ * may be NULL. */
+int fc_edge_geometry_dbwd(const fc_edge_desc* desc, int64_t n_edges, const float* pos,
+                          const float* shift_vec, const int32_t* idx_i, const int32_t* idx_j,
+                          const float* vectors, const float* g_attrs, const float* g_feats,
+                          const float* g_env, const float* cot_vec, float* d_g_attrs, float* d_g_feats,
+                          float* d_g_env, float* d_vec, void* stream);
 
 /* ------------------------------------------------------------------------- */
 /* Receiver-sorted graph, computed once per neighbour list.                   */

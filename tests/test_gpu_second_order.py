@@ -189,21 +189,25 @@ def test_radial_second_order(basis):
     _compare(gpu, ref, [d], seed=4)
 
 
-@pytest.mark.parametrize("l_max,use_shift", [(2, True), (3, False)])
-def test_edge_geometry_second_order(l_max, use_shift):
+@pytest.mark.parametrize("l_max,use_shift,basis", [(2, True, "affine"), (3, False, "affine"), (3, True, "cosine"),
+                                                   (1, False, "bessel"), (0, True, "cosine")])
+def test_edge_geometry_second_order(l_max, use_shift, basis):
+    """Some edges reach beyond r_max (envelope masked) — both sides of the cutoff."""
     from flashcart_amd import _lib
     from flashcart_amd.o3 import _ops
-    g = torch.Generator().manual_seed(l_max)
+    code = {"affine": _lib.BASIS_CHEBYSHEV_AFFINE, "cosine": _lib.BASIS_CHEBYSHEV_COSINE,
+            "bessel": _lib.BASIS_BESSEL}[basis]
+    g = torch.Generator().manual_seed(l_max + 10 * code)
     n, e = 14, 80
     pos = 3.0 * torch.rand(n, 3, generator=g, dtype=torch.float64)
     idx_i = torch.sort(torch.randint(0, n, (e,), generator=g)).values
     idx_j = (idx_i + 1 + torch.randint(0, n - 1, (e,), generator=g)) % n
     shift = (torch.randint(-1, 2, (e, 3), generator=g) * 1.5).to(torch.float64) if use_shift else None
-    r_max = 7.0
+    r_max = 4.5 if use_shift else 7.0
 
     def gpu(p, *sv):
         return _ops.edge_geometry(p, sv[0] if sv else None, idx_i.to(DEV), idx_j.to(DEV), None, None, None, None,
-                                  l_max, _lib.BASIS_CHEBYSHEV_AFFINE, 8, 0.0, r_max, 6)
+                                  l_max, code, 8, 0.0, r_max, 6)
 
     def ref(p, *sv):
         v = p[idx_j] - p[idx_i]
@@ -211,7 +215,8 @@ def test_edge_geometry_second_order(l_max, use_shift):
             v = v + sv[0]
         d = v.norm(dim=-1)
         u = v / d.clamp_min(1e-4).unsqueeze(-1)
-        return O.irreps(u, l_max), O.chebyshev(d, 8, r_max, 0.0, "affine"), O.cutoff(d, r_max, 6)
+        f = O.bessel(d, 8, r_max) if basis == "bessel" else O.chebyshev(d, 8, r_max, 0.0, basis)
+        return O.irreps(u, l_max), f, O.cutoff(d, r_max, 6)
 
     _compare(gpu, ref, [pos] + ([shift] if use_shift else []), seed=9)
 

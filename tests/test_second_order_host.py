@@ -1,9 +1,10 @@
-"""CPU checks of the torch statements that carry the elementwise layers' second derivatives.
+"""CPU checks of the torch statements used for second derivatives of the standalone ops.
 
-``flashcart_amd.o3._torch_math`` restates the per-edge and per-node layers so autograd can
-differentiate their first backward. Here each statement is compared in float64 with the
-oracle's (values, first and second derivatives), and the double-vjp helper with plain
-nested autograd. The statements use the kernels' forms (the factored envelope, the
+``flashcart_amd.o3._torch_math`` restates Eq. (1), the radial bases, the envelope and the RMS
+norm's mean invariant so autograd can differentiate the first backward of the standalone
+ops (and route gradients of auxiliary outputs). Here each statement is compared in float64
+with the oracle's (values, first and second derivatives), and the double-vjp helper with
+plain nested autograd. The statements use the kernels' forms (the factored envelope, the
 rank-0 metric of the RMS norm), so agreement with the oracle's textbook forms pins them.
 """
 
@@ -66,25 +67,6 @@ def test_envelope_matches_oracle(p):
     for k, (x, y) in enumerate(zip(a, b)):
         # the expanded form cancels near the cutoff: compare with an absolute bar
         assert float((x - y).abs().max()) <= 1e-9 * (1 + float(y.abs().max())), f"envelope[{k}]"
-
-
-def test_edge_geometry_matches_oracle():
-    g = torch.Generator().manual_seed(5)
-    v = 2.0 * torch.randn(40, 3, dtype=torch.float64, generator=g)
-
-    def mine(t):
-        a, f, e = M.edge_geometry(t, 3, _lib.BASIS_CHEBYSHEV_AFFINE, 8, 0.0, 6.0, 6)
-        return torch.cat([a, f, e.unsqueeze(-1)], dim=-1)
-
-    def ref(t):
-        d = t.norm(dim=-1)
-        u = t / d.clamp_min(1e-4).unsqueeze(-1)
-        return torch.cat([O.irreps(u, 3), O.chebyshev(d, 8, 6.0, 0.0, "affine"), O.cutoff(d, 6.0, 6).unsqueeze(-1)],
-                         dim=-1)
-
-    a, b = _hvp(mine, v, 6), _hvp(ref, v, 6)
-    for k, (x, y) in enumerate(zip(a, b)):
-        assert float((x - y).abs().max()) <= 1e-9 * (1 + float(y.abs().max())), f"edge geometry[{k}]"
 
 
 @pytest.mark.parametrize("l_max,C", [(1, 4), (2, 8), (3, 4)])
