@@ -390,6 +390,131 @@ __global__ void __launch_bounds__(256, 2) tp_bwd_kernel(TPArgs g) {
   }
 }
 
+// Backward of the interaction-layer convolution (one in2 channel, unreduced outputs),
+// specialised at compile time: C channels = the block size (every lane active, operand
+// offsets are immediates), the weight and edge-attribute gradients always formed, the
+// per-edge in1 messages when NEED1. Same arithmetic, in the same order, as
+// tp_bwd_kernel<..., CONV, BC2>; without the run-time flags the path contractions are one
+// basic block, so loads, stores and LDS reads of neighbouring paths interleave with
+// their FMAs. The edge loop is unrolled by two with two operand sets (no register
+// copies between iterations): the operands of edge e+1 load while edge e is contracted.
+template <int L1, int L2, int LO, bool SYM>
+__host__ __device__ constexpr int bwd_conv_chunk() {
+  return AmatLayout<L1, L2, LO, SYM>::chunk >= 2 ? (AmatLayout<L1, L2, LO, SYM>::chunk & ~1) : 2;
+}
+
+template <int L1, int L2, int LO, bool SYM, int C, bool NEED1>
+__global__ void __launch_bounds__(C, 2) tp_bwd_conv_kernel(TPArgs g) {
+  using CF = TPConfig<L1, L2, LO, SYM>;
+  using PL = typename CF::PL;
+  using AL = AmatLayout<L1, L2, LO, SYM>;
+  constexpr int D1 = CF::D1, D2 = CF::D2, NOUT = CF::NOUT, NP = CF::NP;
+  constexpr int R2 = pow2_at_least(D2), SH2 = 6 - log2_exact(R2);
+  constexpr int CH = bwd_conv_chunk<L1, L2, LO, SYM>();
+  constexpr int NW = C / 64;
+  static_assert(C % 64 == 0 && C <= 256, "one lane per channel, whole waves");
+  static_assert(2 * CH * AL::total * 4 <= 65536, "coupling-matrix chunks exceed the LDS budget");
+  constexpr int64_t SW = (int64_t)NP * C, S1 = (int64_t)D1 * C;
+  __shared__ __align__(16) float a_lds[2 * CH * AL::total];
+  __shared__ float red_lds[CH * NW * D2];
+
+  const int64_t row = xcd_row(g.n_rows);
+  if (row >= g.n_rows) return;
+  const int f = threadIdx.x, wave = f >> 6, lane = f & 63;
+  const int64_t e0 = g.rowptr[row], e1 = g.rowptr[row + 1];
+  if (e0 >= e1) return;  // uniform over the workgroup: no barrier is skipped by a part of it
+
+  float go[NOUT];
+#pragma unroll
+  for (int k = 0; k < NOUT; ++k) go[k] = g.alpha * g.grad_out[row * (int64_t)NOUT * C + (int64_t)k * C + f];
+
+  auto load = [&](int64_t e, EdgeOps<D1, D2, NP>& o) {
+    const int64_t j = (int64_t)g.idx_j[e];
+    const float* xr = g.in1 + j * S1 + f;
+    const float* wr = g.w + e * SW + f;
+#pragma unroll
+    for (int u = 0; u < D1; ++u) o.x[u] = xr[u * C];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) o.w[i] = wr[i * C];
+  };
+
+  auto step = [&](int64_t e, const EdgeOps<D1, D2, NP>& cur, const float* ae, int slot) {
+    float gx[D1], gy[R2];
+#pragma unroll
+    for (int u = 0; u < D1; ++u) gx[u] = 0.f;
+#pragma unroll
+    for (int u = 0; u < R2; ++u) gy[u] = 0.f;
+    float* gwr = g.grad_w + e * SW + f;
+    static_for<NP>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      constexpr PathDesc P = PL::at(i);
+      using T = TPPath<P.r1, P.r2, P.lo>;
+      const float* xp = cur.x + P.r1 * P.r1;
+      float gop[T::NO];
+#pragma unroll
+      for (int a = 0; a < T::NO; ++a) gop[a] = go[PL::out_index(i, a)];
+      float v[T::N1];
+#pragma unroll
+      for (int b = 0; b < T::N1; ++b) v[b] = 0.f;
+      T::apply_t(ae + AL::template off<i>(), gop, v);
+      float s = 0.f;
+#pragma unroll
+      for (int b = 0; b < T::N1; ++b) s = fmaf(v[b], xp[b], s);
+      gwr[i * C] = s;
+      if constexpr (NEED1) {
+#pragma unroll
+        for (int b = 0; b < T::N1; ++b) gx[P.r1 * P.r1 + b] = fmaf(cur.w[i], v[b], gx[P.r1 * P.r1 + b]);
+      }
+      float xw[T::N1];
+#pragma unroll
+      for (int b = 0; b < T::N1; ++b) xw[b] = cur.w[i] * xp[b];
+      T::vjp2(gop, xw, gy + P.r2 * P.r2);
+    });
+    const float s = wave_reduce_halving<R2>(gy, lane);
+    const int v = lane >> SH2;
+    if ((lane & ((1 << SH2) - 1)) == 0 && v < D2) red_lds[(slot * NW + wave) * D2 + v] = s;
+    if constexpr (NEED1) {
+      float* mr = g.grad_in1 + e * S1 + f;
+#pragma unroll
+      for (int u = 0; u < D1; ++u) mr[u * C] = gx[u];
+    }
+  };
+
+  EdgeOps<D1, D2, NP> opa, opb;
+  load(e0, opa);
+  fill_amat<L1, L2, LO, SYM>(g.in2, e0, e1 - e0 < CH ? (int)(e1 - e0) : CH, a_lds, lane, wave, NW);
+  __syncthreads();
+  int buf = 0;
+  // Every chunk but the last holds CH (even) edges, so each chunk starts on operand set a.
+  for (int64_t c0 = e0; c0 < e1; c0 += CH) {
+    const int64_t c1 = c0 + CH < e1 ? c0 + CH : e1;
+    const int n_next = e1 - c1 < CH ? (int)(e1 - c1) : CH;
+    const float* ab = a_lds + buf * CH * AL::total;
+    for (int64_t e = c0; e < c1; e += 2) {
+      const int slot = (int)(e - c0);
+      if (e + 1 < e1) load(e + 1, opb);
+      step(e, opa, ab + slot * AL::total, slot);
+      if (e + 1 < c1) {
+        if (e + 2 < e1) load(e + 2, opa);
+        step(e + 1, opb, ab + (slot + 1) * AL::total, slot + 1);
+      }
+    }
+    // the other buffer was last read in the previous chunk, before that chunk's barriers
+    if (n_next > 0) fill_amat<L1, L2, LO, SYM>(g.in2, c1, n_next, a_lds + (buf ^ 1) * CH * AL::total, lane, wave, NW);
+    __syncthreads();
+    const int n = (int)(c1 - c0);
+    for (int k = f; k < n * D2; k += C) {
+      const int slot = k / D2, u = k % D2;
+      float s = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) s += red_lds[(slot * NW + w) * D2 + u];
+      g.grad_in2[(c0 + slot) * D2 + u] = s;
+    }
+    __syncthreads();
+    buf ^= 1;
+  }
+}
+
 // Backward of the node-wise (rows) product with full-width inputs (F1 == F2 == C) and
 // per-path outputs: no channel reduction, so no LDS or barriers. The output gradient
 // of a path is read when the path is processed (the node-wise kernels have no edge
@@ -477,6 +602,22 @@ int launch_tp(const TPArgs& g, bool conv, bool bwd, hipStream_t stream) {
   if (bwd) {
     const bool reduce = (g.grad_in1 && g.F1 == 1 && g.C > 1) || (g.grad_in2 && g.F2 == 1 && g.C > 1);
     const size_t per_edge = reduce ? sizeof(float) * (threads / 64) * (ncomp(L1) + ncomp(L2)) : 0;
+    if constexpr (!SYM && L2 >= 1) {
+      // interaction-layer shape: the compile-time specialisation
+      if (conv && bc2 && !g.reduced && g.grad_w && g.grad_in2 && g.F1 == g.C && threads == g.C &&
+          (g.C == 64 || g.C == 128)) {
+        const bool n1 = g.grad_in1 != nullptr;
+        if (g.C == 128) {
+          if (n1) hipLaunchKernelGGL((tp_bwd_conv_kernel<L1, L2, LO, SYM, 128, true>), grid, block, 0, stream, g);
+          else hipLaunchKernelGGL((tp_bwd_conv_kernel<L1, L2, LO, SYM, 128, false>), grid, block, 0, stream, g);
+        } else {
+          if (n1) hipLaunchKernelGGL((tp_bwd_conv_kernel<L1, L2, LO, SYM, 64, true>), grid, block, 0, stream, g);
+          else hipLaunchKernelGGL((tp_bwd_conv_kernel<L1, L2, LO, SYM, 64, false>), grid, block, 0, stream, g);
+        }
+        FC_LAUNCH_CHECK();
+        return FC_OK;
+      }
+    }
     if (conv) {
       if (bc2)
         hipLaunchKernelGGL((tp_bwd_kernel<L1, L2, LO, SYM, true, true>), grid, block,
