@@ -40,9 +40,9 @@ HBM_PEAK_GBS = 8000.0
 # `bench.py --kernel-only` (first step graph, E = 1,080,166), each counter scaled by its reading for
 # a 2 GiB elementwise copy (FETCH x2.000, WRITE x1.000); see profiles/tp_conv_fwd_l1_fcc25k_hbm_traffic.md.
 MEASURED_TRAFFIC_BYTES = 11.77e9
-# The same for the layer-1 backward op (tp_bwd_kernel 27.085 GB + segment_rows_kernel 5.116 GB) from
+# The same for the layer-1 backward op (tp_bwd_conv_kernel 27.231 GB + segment_rows_kernel 5.116 GB) from
 # the `bench.py --profile-step` counter runs; see profiles/fcc25k_L3_C128_kernel_hbm_mfma.md.
-MEASURED_TRAFFIC_BWD_BYTES = 32.20e9
+MEASURED_TRAFFIC_BWD_BYTES = 32.35e9
 R_MAX = 5.0
 SIGMA_STEP = 0.01
 SKIN = 1.0
@@ -563,9 +563,9 @@ def main():
                      "algorithmic_bytes": byts, "avg_launch_ms": ms,
                      "note": "the north star's TP kernel; by time the layer-1 backward dominates the step "
                              "(roofline_tp_bwd)"},
-        # the step's largest kernel by time: the layer-1 TP backward op = tp_bwd_kernel<2,3,3> (VALU-bound)
+        # the step's largest TP kernel by time: the layer-1 TP backward op = tp_bwd_conv_kernel<2,3,3>
         # + segment_rows_kernel (sender gather); achieved = both kernels' algorithmic bytes / op time
-        "roofline_tp_bwd": {"bound": "hbm", "kernel": "tp_bwd_kernel<2,3,3> + segment_rows_kernel (layer 1)",
+        "roofline_tp_bwd": {"bound": "hbm", "kernel": "tp_bwd_conv_kernel<2,3,3> + segment_rows_kernel (layer 1)",
                             "achieved": gbs_b, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs_b / HBM_PEAK_GBS,
                             "traffic": MEASURED_TRAFFIC_BWD_BYTES,
                             "traffic_launch": "bench.py --profile-step (E=1080166)",

@@ -550,30 +550,17 @@ namespace fc {
 // 32 x 64 outputs each per chunk.
 constexpr int WIDE_BM = 128, WIDE_BN = 64, WIDE_K = 64, WIDE_P = 68;
 
-// GUARD = false: every row and column of the block is in range (m a multiple of 64), so
-// the stores are unconditional and the compiler can count them as outstanding rather
-// than wait for them before the next weight chunk is written to LDS. The last, partial
-// row block runs as a separate GUARD = true launch.
+// Output part shared by the wide kernels: the x block of rows r0 .. r0 + 127 is in As
+// (natural k order, pitch WIDE_P); Bs holds two weight-chunk buffers. Ends with no
+// barrier pending; every thread of the workgroup must call it.
 template <bool GUARD>
-__global__ void __launch_bounds__(256, 2) gemm_wide_kernel(int64_t n, int m, const float* __restrict__ x,
-                                                            const float* __restrict__ w, float scale,
-                                                            float* __restrict__ out, int64_t first_block) {
-  __shared__ __attribute__((aligned(16))) float As[WIDE_BM * WIDE_P];
-  __shared__ __attribute__((aligned(16))) float Bs[2][WIDE_BN * WIDE_P];
+__device__ __forceinline__ void wide_body(const float* As, float (*Bs)[WIDE_BN * WIDE_P], int64_t n, int m,
+                                          const float* __restrict__ w, float scale, float* __restrict__ out,
+                                          int64_t r0) {
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int64_t r0 = (first_block + blockIdx.x) * WIDE_BM;
-  // row (or weight column) q, k = 4 kk .. 4 kk + 3 of one float4 -> LDS positions
   auto put4 = [&](float* base, int q, int k4, float4 v) {
     *reinterpret_cast<float4*>(base + q * WIDE_P + k4) = v;
   };
-  // x block: 128 rows x 16 float4, 8 per thread; rows past n read row n-1 (never stored)
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int e = t + 256 * i, q = e >> 4, k4 = (e & 15) * 4;
-    int64_t row = r0 + q;
-    row = row < n ? row : n - 1;
-    put4(As, q, k4, *reinterpret_cast<const float4*>(x + row * WIDE_K + k4));
-  }
   float4 rb[4];
   auto load_b = [&](int c0) {  // 64 weight rows x 16 float4, 4 per thread
 #pragma unroll
@@ -649,6 +636,231 @@ __global__ void __launch_bounds__(256, 2) gemm_wide_kernel(int64_t n, int m, con
     for (int j = 0; j < 2; ++j) store_one((last & 1) ? r1acc : r0acc, last * WIDE_BN, v, j);
 }
 
+// GUARD = false: every row and column of the block is in range (m a multiple of 64), so
+// the stores are unconditional and the compiler can count them as outstanding rather
+// than wait for them before the next weight chunk is written to LDS. The last, partial
+// row block runs as a separate GUARD = true launch.
+template <bool GUARD>
+__global__ void __launch_bounds__(256, 2) gemm_wide_kernel(int64_t n, int m, const float* __restrict__ x,
+                                                            const float* __restrict__ w, float scale,
+                                                            float* __restrict__ out, int64_t first_block) {
+  __shared__ __attribute__((aligned(16))) float As[WIDE_BM * WIDE_P];
+  __shared__ __attribute__((aligned(16))) float Bs[2][WIDE_BN * WIDE_P];
+  const int t = threadIdx.x;
+  const int64_t r0 = (first_block + blockIdx.x) * WIDE_BM;
+  // x block: 128 rows x 16 float4, 8 per thread; rows past n read row n-1 (never stored)
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int e = t + 256 * i, q = e >> 4, k4 = (e & 15) * 4;
+    int64_t row = r0 + q;
+    row = row < n ? row : n - 1;
+    *reinterpret_cast<float4*>(As + q * WIDE_P + k4) = *reinterpret_cast<const float4*>(x + row * WIDE_K + k4);
+  }
+  wide_body<GUARD>(As, Bs, n, m, w, scale, out, r0);
+}
+
+// ---- Radial MLP with two hidden layers of 64 (reference InteractionLayer.radial_mlp,
+// src/flashcart/nn/layers.py:258-267, applied at :357-363):
+//   pre1 = s0 x W0^T, h1 = silu(pre1), pre2 = s1 h1 W1^T, h2 = silu(pre2), out = s2 h2 W2^T
+// with silu the rescaled SiLU and x (n, n_in), n_in <= 64. The forward forms h1 and h2 of a
+// 128-row block in LDS and hands h2 to the wide output part, so neither hidden layer goes
+// through HBM. The backward (input gradient only) recomputes the hidden layers from x
+// (n_in floats per row) instead of reading saved pre-activations.
+
+// acc[j] (j < NJ) = A rows of this wave (as) x weight rows of column block j (bs + 32 j
+// rows), k = 0..63: MFMA step s contracts k = s (lanes 0-31) and k = 32 + s (lanes 32-63).
+// Only the first ns4 groups of four steps run: with K <= 32 the rest multiply zero padding
+// (K = n_in, the first hidden layer), so ns4 = ceil(K / 4) there and 8 otherwise.
+template <int NJ>
+__device__ __forceinline__ void mfma_k64(const float* as, const float* bs, floatx16 (&acc)[2], int ns4 = 8) {
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[j][v] = 0.f;
+#pragma unroll
+  for (int s4 = 0; s4 < 8; ++s4) {
+    if (s4 >= ns4) break;  // uniform
+    const float4 a4 = *reinterpret_cast<const float4*>(as + 4 * s4);
+    float4 b4[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) b4[j] = *reinterpret_cast<const float4*>(bs + j * 32 * WIDE_P + 4 * s4);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(reinterpret_cast<const float*>(&a4)[q],
+                                                      reinterpret_cast<const float*>(&b4[j])[q], acc[j], 0, 0, 0);
+  }
+}
+
+// Row (within the wave's 32 rows) of accumulator element v of this lane.
+__device__ __forceinline__ int acc_row(int v, int lane) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); }
+
+__device__ __forceinline__ float silu_r(float z) { return kSiluScale * z * sigmoidf_(z); }
+__device__ __forceinline__ float silu_r_grad(float z) {
+  const float sg = sigmoidf_(z);
+  return kSiluScale * sg * (1.0f + z * (1.0f - sg));
+}
+
+// x block (rows r0 .. r0 + 127 that exist; they are contiguous in x) -> As, zero-padded to 64
+// columns; rows past n stay zero (never stored). W0 (64 x n_in) -> B0 and W1 (64 x 64) -> B1 as
+// weight rows (zero-padded k); with trans, W1^T -> B0 and W0^T -> B1 instead. Every thread
+// issues all of its global loads before its first LDS store, so the load latency is paid once.
+__device__ __forceinline__ void mlp_stage_x(float* As, int64_t n, int n_in, const float* __restrict__ x, int64_t r0) {
+  const int t = threadIdx.x;
+  const int rows = n - r0 < WIDE_BM ? (int)(n - r0) : WIDE_BM;
+  const int cnt = rows * n_in;
+  const float* xb = x + r0 * n_in;
+  float v[WIDE_K / 2];  // 128 x 64 / 256 threads at most
+#pragma unroll
+  for (int i = 0; i < WIDE_K / 2; ++i) {
+    const int e = t + 256 * i;
+    v[i] = e < cnt ? xb[e] : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < WIDE_K / 2; ++i) {
+    const int e = t + 256 * i;
+    if (e < WIDE_BM * n_in) {
+      const int q = e / n_in;
+      As[q * WIDE_P + (e - q * n_in)] = v[i];
+    }
+  }
+  for (int e = t; e < WIDE_BM * (WIDE_K - n_in); e += 256) {
+    const int q = e / (WIDE_K - n_in);
+    As[q * WIDE_P + n_in + (e - q * (WIDE_K - n_in))] = 0.f;
+  }
+}
+
+__device__ __forceinline__ void mlp_stage_weights(float* B0, float* B1, int n_in, const float* __restrict__ w0,
+                                                  const float* __restrict__ w1, bool trans) {
+  const int t = threadIdx.x;
+  float a[16], b[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {  // element e = (r, c) of a 64 x 64 square, c = e & 63 along memory
+    const int e = t + 256 * i, r = e >> 6, c = e & 63;
+    a[i] = w1[r * 64 + c];
+    b[i] = c < n_in ? w0[r * n_in + c] : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int e = t + 256 * i, r = e >> 6, c = e & 63;
+    if (!trans) {
+      B0[r * WIDE_P + c] = b[i];  // W0 row r (output), k = c
+      B1[r * WIDE_P + c] = a[i];  // W1 row r, k = c
+    } else {
+      B0[c * WIDE_P + r] = a[i];  // W1^T: row c (input of W1), k = r (output)
+      B1[c * WIDE_P + r] = b[i];  // W0^T: row c (input feature, zero past n_in), k = r
+    }
+  }
+}
+
+// The wave's 32 x 64 accumulator block -> f(value) into its own rows of As.
+template <class F>
+__device__ __forceinline__ void acc_to_rows(const floatx16 (&acc)[2], float* As, int wave, int lane, F f) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+      As[(wave * 32 + acc_row(v, lane)) * WIDE_P + j * 32 + (lane & 31)] = f(acc[j][v]);
+}
+
+template <bool GUARD>
+__global__ void __launch_bounds__(256, 2) radial_mlp_fwd_kernel(int64_t n, int n_in, const float* __restrict__ x,
+                                                                 const float* __restrict__ w0, float s0,
+                                                                 const float* __restrict__ w1, float s1, int m,
+                                                                 const float* __restrict__ w2, float s2,
+                                                                 float* __restrict__ out, int64_t first_block) {
+  __shared__ __attribute__((aligned(16))) float As[WIDE_BM * WIDE_P];
+  __shared__ __attribute__((aligned(16))) float Bs[2][WIDE_BN * WIDE_P];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int64_t r0 = (first_block + blockIdx.x) * WIDE_BM;
+  mlp_stage_x(As, n, n_in, x, r0);
+  mlp_stage_weights(Bs[0], Bs[1], n_in, w0, w1, false);
+  __syncthreads();
+  const int half = (lane >> 5) * (WIDE_K / 2);
+  const float* as = As + (wave * 32 + (lane & 31)) * WIDE_P + half;
+  floatx16 acc[2];
+  const int ns4_in = n_in <= 32 ? (n_in + 3) / 4 : 8;
+  mfma_k64<2>(as, Bs[0] + (lane & 31) * WIDE_P + half, acc, ns4_in);
+  __syncthreads();  // every wave's reads of the x rows are done (each wave rewrites only its own rows)
+  acc_to_rows(acc, As, wave, lane, [&](float a) { return silu_r(a * s0); });
+  __syncthreads();
+  mfma_k64<2>(as, Bs[1] + (lane & 31) * WIDE_P + half, acc);
+  __syncthreads();  // reads of h1 and of both weight buffers done before they are overwritten
+  acc_to_rows(acc, As, wave, lane, [&](float a) { return silu_r(a * s1); });
+  __syncthreads();
+  wide_body<GUARD>(As, Bs, n, m, w2, s2, out, r0);
+}
+
+// Input gradient of the two hidden layers: given gh2 = dL/dh2 (n, 64),
+//   dpre2 = gh2 * silu'(pre2), dh1 = s1 dpre2 W1, dpre1 = dh1 * silu'(pre1), dx = s0 dpre1 W0.
+__global__ void __launch_bounds__(256, 2) radial_mlp_bwd_kernel(int64_t n, int n_in, const float* __restrict__ x,
+                                                                 const float* __restrict__ w0, float s0,
+                                                                 const float* __restrict__ w1, float s1,
+                                                                 const float* __restrict__ gh2,
+                                                                 float* __restrict__ gx) {
+  __shared__ __attribute__((aligned(16))) float As[WIDE_BM * WIDE_P];
+  __shared__ __attribute__((aligned(16))) float B0[WIDE_BN * WIDE_P];
+  __shared__ __attribute__((aligned(16))) float B1[WIDE_BN * WIDE_P];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int64_t r0 = (int64_t)blockIdx.x * WIDE_BM;
+  // this lane's dL/dh2 values (accumulator layout), loaded first so that their latency
+  // overlaps the staging and the two recomputed layers; rows past n contribute nothing
+  float g2[2][16];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int64_t row = r0 + wave * 32 + acc_row(v, lane);
+      g2[j][v] = row < n ? gh2[row * 64 + j * 32 + (lane & 31)] : 0.f;
+    }
+  mlp_stage_x(As, n, n_in, x, r0);
+  mlp_stage_weights(B0, B1, n_in, w0, w1, false);
+  __syncthreads();
+  const int half = (lane >> 5) * (WIDE_K / 2);
+  const float* as = As + (wave * 32 + (lane & 31)) * WIDE_P + half;
+  floatx16 acc[2], d1[2];
+  const int ns4_in = n_in <= 32 ? (n_in + 3) / 4 : 8;
+  mfma_k64<2>(as, B0 + (lane & 31) * WIDE_P + half, acc, ns4_in);
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) d1[j][v] = silu_r_grad(acc[j][v] * s0);
+  __syncthreads();
+  acc_to_rows(acc, As, wave, lane, [&](float a) { return silu_r(a * s0); });
+  __syncthreads();
+  mfma_k64<2>(as, B1 + (lane & 31) * WIDE_P + half, acc);
+  // dpre2 = gh2 * silu'(pre2)
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[j][v] = g2[j][v] * silu_r_grad(acc[j][v] * s1);
+  __syncthreads();  // reads of h1, W0 and W1 done: stage dpre2, W1^T and W0^T
+  acc_to_rows(acc, As, wave, lane, [](float a) { return a; });
+  mlp_stage_weights(B0, B1, n_in, w0, w1, true);
+  __syncthreads();
+  mfma_k64<2>(as, B0 + (lane & 31) * WIDE_P + half, acc);
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[j][v] = acc[j][v] * s1 * d1[j][v];
+  __syncthreads();
+  acc_to_rows(acc, As, wave, lane, [](float a) { return a; });
+  __syncthreads();
+  // dx has n_in columns: one 32-column block when n_in <= 32
+  const int nj = n_in <= 32 ? 1 : 2;
+  if (nj == 1) mfma_k64<1>(as, B1 + (lane & 31) * WIDE_P + half, acc);
+  else mfma_k64<2>(as, B1 + (lane & 31) * WIDE_P + half, acc);
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int64_t row = r0 + wave * 32 + acc_row(v, lane);
+      const int col = j * 32 + (lane & 31);
+      if (j < nj && row < n && col < n_in) gx[row * n_in + col] = acc[j][v] * s0;
+    }
+}
+
 }  // namespace fc
 
 extern "C" int fc_dense_fwd(int64_t n, int32_t k, int32_t m, const float* x, const float* w, float scale,
@@ -683,6 +895,42 @@ extern "C" int fc_dense_fwd(int64_t n, int32_t k, int32_t m, const float* x, con
   g.pre = pre_act;
   g.comps = 1; g.M = (int32_t)n; g.K = k; g.N = m; g.scale = scale;
   return launch_gemm(gb, 1, (hipStream_t)stream);
+}
+
+extern "C" int fc_radial_mlp_fwd(int64_t n, int32_t n_in, const float* x, const float* w0, float s0,
+                                 const float* w1, float s1, int32_t m, const float* w2, float s2, float* out,
+                                 void* stream) {
+  if (n < 0 || n_in < 1 || n_in > WIDE_K || m < 1) return FC_ERR_BAD_DESC;
+  if (n == 0) return FC_OK;
+  if (!x || !w0 || !w1 || !w2 || !out) return FC_ERR_NULL;
+  if (((uintptr_t)w2 & 15) != 0) return FC_ERR_SHAPE;  // weight chunks load as float4
+  const int64_t blocks = (n + WIDE_BM - 1) / WIDE_BM;
+  if (blocks > 0x7fffffff) return FC_ERR_SHAPE;
+  const int64_t full = m % WIDE_BN == 0 ? n / WIDE_BM : 0;
+  if (full > 0) {
+    hipLaunchKernelGGL(radial_mlp_fwd_kernel<false>, dim3((unsigned)full), dim3(256), 0, (hipStream_t)stream, n,
+                       (int)n_in, x, w0, s0, w1, s1, (int)m, w2, s2, out, (int64_t)0);
+    FC_LAUNCH_CHECK();
+  }
+  if (blocks > full) {
+    hipLaunchKernelGGL(radial_mlp_fwd_kernel<true>, dim3((unsigned)(blocks - full)), dim3(256), 0,
+                       (hipStream_t)stream, n, (int)n_in, x, w0, s0, w1, s1, (int)m, w2, s2, out, full);
+    FC_LAUNCH_CHECK();
+  }
+  return FC_OK;
+}
+
+extern "C" int fc_radial_mlp_bwd(int64_t n, int32_t n_in, const float* x, const float* w0, float s0,
+                                 const float* w1, float s1, const float* grad_h2, float* grad_x, void* stream) {
+  if (n < 0 || n_in < 1 || n_in > WIDE_K) return FC_ERR_BAD_DESC;
+  if (n == 0) return FC_OK;
+  if (!x || !w0 || !w1 || !grad_h2 || !grad_x) return FC_ERR_NULL;
+  const int64_t blocks = (n + WIDE_BM - 1) / WIDE_BM;
+  if (blocks > 0x7fffffff) return FC_ERR_SHAPE;
+  hipLaunchKernelGGL(radial_mlp_bwd_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, n, (int)n_in,
+                     x, w0, s0, w1, s1, grad_h2, grad_x);
+  FC_LAUNCH_CHECK();
+  return FC_OK;
 }
 
 extern "C" int fc_dense_dgrad(int64_t n, int32_t k, int32_t m, const float* go, const float* pre_act,

@@ -165,3 +165,50 @@ class _GatedBlock(torch.autograd.Function):
 
 def gated_block(layer, x: Tensor) -> Tensor:
     return _GatedBlock.apply(x, layer)
+
+
+class _RadialMLP(torch.autograd.Function):
+    """The interaction layer's radial MLP, Linear(n_in, 64) -> SiLU -> Linear(64, 64) -> SiLU
+    -> Linear(64, m) (reference ``nn/layers.py:258-267``, applied at ``:357-363``), as one
+    forward kernel whose hidden activations never leave the chip. Backward (input gradient
+    only): dh2 = s2 g W2 (the wide dgrad GEMM), then one kernel that recomputes the hidden
+    layers from x and applies both hidden-layer input gradients."""
+
+    @staticmethod
+    def forward(ctx, x: Tensor, mlp) -> Tensor:
+        l0, l1, l2 = mlp[0], mlp[2], mlp[4]
+        out = _ops.radial_mlp_fwd(x, l0.weight, l0._scale, l1.weight, l1._scale, l2.weight, l2._scale)
+        ctx.save_for_backward(x)
+        ctx.mlp = mlp
+        return out
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, g: Tensor):
+        (x,) = ctx.saved_tensors
+        l0, l1, l2 = ctx.mlp[0], ctx.mlp[2], ctx.mlp[4]
+        gh2 = _ops.dense_bwd(g, g.new_empty(0), l2.weight, l2._scale, 0)
+        return _ops.radial_mlp_bwd(gh2, x, l0.weight, l0._scale, l1.weight, l1._scale), None
+
+
+def radial_mlp_applies(mlp: torch.nn.Sequential, x: Tensor) -> bool:
+    """True for the default radial MLP shape (two hidden layers of 64 with rescaled SiLU,
+    no biases, at most 64 inputs) under the conditions of ``applies``."""
+    from flashcart_amd.nn.layers import SILU_SCALE, LinearLayer, RescaledSiLULayer
+    mods = list(mlp)
+    if len(mods) != 5 or not all(isinstance(mods[i], LinearLayer) for i in (0, 2, 4)):
+        return False
+    if not all(isinstance(mods[i], RescaledSiLULayer) and mods[i]._scale == SILU_SCALE for i in (1, 3)):
+        return False
+    l0, l1, l2 = mods[0], mods[2], mods[4]
+    if any(m.bias is not None for m in (l0, l1, l2)):
+        return False
+    if l0.weight.shape[0] != 64 or tuple(l1.weight.shape) != (64, 64) or l2.weight.shape[1] != 64:
+        return False
+    if not 1 <= l0.weight.shape[1] <= 64 or x.shape[-1] != l0.weight.shape[1]:
+        return False
+    return applies(mlp, x)
+
+
+def radial_mlp(mlp: torch.nn.Sequential, x: Tensor) -> Tensor:
+    return _RadialMLP.apply(x, mlp)

@@ -173,7 +173,10 @@ class InteractionLayer(nn.Module):
         else:
             mlp_input = edge_feats * envelope.unsqueeze(-1)
         node_feats = self.linear_first(node_feats)
-        weights = run_mlp(self.radial_mlp, mlp_input)
+        if fused.radial_mlp_applies(self.radial_mlp, mlp_input):
+            weights = fused.radial_mlp(self.radial_mlp, mlp_input)
+        else:
+            weights = run_mlp(self.radial_mlp, mlp_input)
         aggregated = self.tp(node_feats, edge_attrs, weights, idx_i, idx_j, graph=graph,
                              alpha=1.0 / self._sqrt_avg)
         if out_nodes is not None:

@@ -825,6 +825,59 @@ def _dense_backward(ctx, grad, grad_pre):
 _register_autograd(dense_fwd, _dense_backward, _dense_setup)
 
 
+def _radial_mlp_check(x: Tensor, w0: Tensor, w1: Tensor) -> int:
+    n_in = w0.shape[1]
+    if w0.dim() != 2 or w0.shape[0] != 64 or not 1 <= n_in <= 64 or tuple(w1.shape) != (64, 64):
+        raise RuntimeError(f"radial MLP needs hidden widths 64, 64 and at most 64 inputs; got W0 {tuple(w0.shape)}, "
+                           f"W1 {tuple(w1.shape)}.")
+    if x.shape[-1] != n_in:
+        raise RuntimeError(f"Incorrect last dimension for x. Expected {n_in}, got {x.shape[-1]}.")
+    return n_in
+
+
+@torch.library.custom_op("flashcart::radial_mlp_fwd", mutates_args=())
+def radial_mlp_fwd(x: Tensor, w0: Tensor, s0: float, w1: Tensor, s1: float, w2: Tensor, s2: float) -> Tensor:
+    """s2 silu(s1 silu(s0 x W0^T) W1^T) W2^T in one pass (``fc_radial_mlp_fwd``); the hidden
+    activations are not returned (the backward recomputes them)."""
+    x = _lib.contig("x", x)
+    w0, w1, w2 = _lib.contig("w0", w0), _lib.contig("w1", w1), _lib.contig("w2", w2)
+    n_in = _radial_mlp_check(x, w0, w1)
+    if w2.dim() != 2 or w2.shape[1] != 64:
+        raise RuntimeError(f"W2 must be (m, 64), got {tuple(w2.shape)}.")
+    m = w2.shape[0]
+    x2 = x.reshape(-1, n_in)
+    out = x.new_empty(x2.shape[0], m)
+    _lib_call("fc_radial_mlp_fwd", x2.shape[0], n_in, x2.data_ptr(), w0.data_ptr(), float(s0), w1.data_ptr(),
+              float(s1), m, w2.data_ptr(), float(s2), out.data_ptr(), _lib.stream_of(x))
+    return out.reshape(*x.shape[:-1], m)
+
+
+@radial_mlp_fwd.register_fake
+def _(x, w0, s0, w1, s1, w2, s2):
+    return x.new_empty(*x.shape[:-1], w2.shape[0])
+
+
+@torch.library.custom_op("flashcart::radial_mlp_bwd", mutates_args=())
+def radial_mlp_bwd(grad_h2: Tensor, x: Tensor, w0: Tensor, s0: float, w1: Tensor, s1: float) -> Tensor:
+    """dL/dx of the radial MLP's hidden part from dL/dh2 (``fc_radial_mlp_bwd``)."""
+    x = _lib.contig("x", x)
+    w0, w1 = _lib.contig("w0", w0), _lib.contig("w1", w1)
+    gh = _lib.contig("grad_h2", grad_h2)
+    n_in = _radial_mlp_check(x, w0, w1)
+    x2 = x.reshape(-1, n_in)
+    if gh.numel() != x2.shape[0] * 64:
+        raise RuntimeError(f"grad_h2 must hold {x2.shape[0]} rows of 64, got {tuple(gh.shape)}.")
+    gx = torch.empty_like(x2)
+    _lib_call("fc_radial_mlp_bwd", x2.shape[0], n_in, x2.data_ptr(), w0.data_ptr(), float(s0), w1.data_ptr(),
+              float(s1), gh.data_ptr(), gx.data_ptr(), _lib.stream_of(x))
+    return gx.reshape(x.shape)
+
+
+@radial_mlp_bwd.register_fake
+def _(grad_h2, x, w0, s0, w1, s1):
+    return torch.empty_like(x)
+
+
 def dense_wgrad(grad_out: Tensor, pre: Optional[Tensor], act: int, x: Tensor, scale: float, need_weight: bool,
                 need_bias: bool) -> Tuple[Optional[Tensor], Optional[Tensor]]:
     """(scale * g^T x, column sums of g) with g = grad_out * act'(pre) (act 1) or grad_out

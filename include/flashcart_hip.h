@@ -219,6 +219,18 @@ int fc_dense_fwd(int64_t n, int32_t k, int32_t m, const float* x, const float* w
 int fc_dense_dgrad(int64_t n, int32_t k, int32_t m, const float* grad_out, const float* pre_act,
                    const float* w, float scale, int32_t act, float* grad_x, void* stream);
 
+/* The radial MLP of an interaction layer with two hidden layers of 64 (reference
+ * InteractionLayer.radial_mlp, src/flashcart/nn/layers.py:258-267 and :357-363, i.e. three
+ * fc_dense_fwd calls): out (n, m) = s2 silu(s1 silu(s0 x W0^T) W1^T) W2^T with x (n, n_in),
+ * n_in <= 64, W0 (64, n_in), W1 (64, 64), W2 (m, 64) row-major (W2 16-byte aligned), silu the
+ * rescaled SiLU. The hidden activations stay on chip; nothing but out is written. */
+int fc_radial_mlp_fwd(int64_t n, int32_t n_in, const float* x, const float* w0, float s0, const float* w1,
+                      float s1, int32_t m, const float* w2, float s2, float* out, void* stream);
+/* Input gradient of its hidden part: grad_x (n, n_in) from grad_h2 = dL/dh2 (n, 64), the
+ * hidden layers recomputed from x (replaces the two hidden fc_dense_dgrad calls). */
+int fc_radial_mlp_bwd(int64_t n, int32_t n_in, const float* x, const float* w0, float s0, const float* w1,
+                      float s1, const float* grad_h2, float* grad_x, void* stream);
+
 /* Weight gradients (training). Replaces the weight-gradient part of the reference's
  * linear_bwd and its linear_wgrad kernel (src/flashcart/o3/_linear.py:457-570), and the
  * autograd weight gradient of the torch dense layers (src/flashcart/nn/layers.py:84-145).

@@ -218,6 +218,31 @@ def test_dense(shape):
         assert_close(a, r, 1e-5, 1e-4 * (float(r.abs().max()) + 1), f"dense grad {i}")
 
 
+@pytest.mark.parametrize("n,n_in,m", [(1000, 8, 512), (300, 8, 2176), (257, 40, 200), (128, 64, 256), (5, 8, 64)])
+def test_radial_mlp_fused(n, n_in, m):
+    """The one-pass radial MLP (8 -> 64 -> 64 -> m, rescaled SiLU) and its input gradient
+    against the float64 layer-by-layer chain: partial row blocks, an output width that is
+    not a multiple of 64, more inputs than one MFMA column block."""
+    ops = _ops()
+    gen = torch.Generator().manual_seed(n + m)
+    x64 = torch.randn(n, n_in, generator=gen, dtype=torch.float64, requires_grad=True)
+    w0 = torch.randn(64, n_in, generator=gen, dtype=torch.float64)
+    w1 = torch.randn(64, 64, generator=gen, dtype=torch.float64)
+    w2 = torch.randn(m, 64, generator=gen, dtype=torch.float64)
+    ref = O.dense(O.silu(O.dense(O.silu(O.dense(x64, w0)), w1)), w2)
+    g = torch.randn(ref.shape, generator=gen, dtype=torch.float64)
+    (ref_gx,) = torch.autograd.grad(ref, x64, g)
+    x = x64.detach().float().to(DEV)
+    w0f, w1f, w2f = (t.float().to(DEV) for t in (w0, w1, w2))
+    s0, s1, s2 = float(n_in) ** -0.5, 0.125, 0.125
+    with torch.no_grad():
+        out = ops.radial_mlp_fwd(x, w0f, s0, w1f, s1, w2f, s2)
+        gh2 = ops.dense_bwd(g.float().to(DEV), x.new_empty(0), w2f, s2, 0)
+        gx = ops.radial_mlp_bwd(gh2, x, w0f, s0, w1f, s1)
+    assert_close(out, ref, 1e-5, 2e-5 * float(ref.abs().max()), "radial mlp fwd")
+    assert_close(gx, ref_gx, 1e-5, 2e-5 * float(ref_gx.abs().max()), "radial mlp input grad")
+
+
 def test_edge_geometry_positions_grad():
     ops = _ops()
     from flashcart_amd import _lib
