@@ -92,6 +92,24 @@ def run_mlp(seq: nn.Sequential, x: torch.Tensor) -> torch.Tensor:
     return x
 
 
+class _AddLeading(torch.autograd.Function):
+    """out[:, :k] += r in place on a fresh GEMM output, k = r.shape[-1] (the rank-0 skip
+    connection). Same values as ``cat([out[:, :k] + r, out[:, k:]])``; the backward passes the
+    gradient through (for r its leading columns) instead of zero-filling, copying and adding
+    two slice gradients."""
+
+    @staticmethod
+    def forward(ctx, out: torch.Tensor, r: torch.Tensor) -> torch.Tensor:
+        ctx.k = r.shape[-1]
+        out[:, : ctx.k].add_(r)
+        ctx.mark_dirty(out)
+        return out
+
+    @staticmethod
+    def backward(ctx, g: torch.Tensor):
+        return g, g[:, : ctx.k]
+
+
 class InteractionLayer(nn.Module):
     """Equivariant convolution with radial-MLP tensor-product weights (reference ``nn/layers.py:185-418``).
 
@@ -188,7 +206,8 @@ class InteractionLayer(nn.Module):
             out = self.linear_second(aggregated)
             if self.skip_projection is not None:
                 skip = self.skip_projection(residual_feats)
-                out = torch.cat([out[:, : self.out_features] + skip, out[:, self.out_features:]], dim=-1)
+                out = _AddLeading.apply(out, skip) if torch.is_grad_enabled() else \
+                    torch.cat([out[:, : self.out_features] + skip, out[:, self.out_features:]], dim=-1)
         if self.layer_norm is not None:
             out = self.layer_norm(out)
         return out
