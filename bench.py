@@ -40,9 +40,9 @@ HBM_PEAK_GBS = 8000.0
 # `bench.py --kernel-only` (first step graph, E = 1,080,166), each counter scaled by its reading for
 # a 2 GiB elementwise copy (FETCH x2.000, WRITE x1.000); see profiles/tp_conv_fwd_l1_fcc25k_hbm_traffic.md.
 MEASURED_TRAFFIC_BYTES = 11.77e9
-# The same for the layer-1 backward op (tp_bwd_conv_kernel 27.231 GB + segment_rows_kernel 5.116 GB) from
+# The same for the layer-1 backward op (tp_bwd_conv_kernel 27.248 GB + segment_rows_kernel 5.116 GB) from
 # the `bench.py --profile-step` counter runs; see profiles/fcc25k_L3_C128_kernel_hbm_mfma.md.
-MEASURED_TRAFFIC_BWD_BYTES = 32.35e9
+MEASURED_TRAFFIC_BWD_BYTES = 32.36e9
 R_MAX = 5.0
 SIGMA_STEP = 0.01
 SKIN = 1.0
