@@ -471,7 +471,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU runs are not part of it "
-                                   "(see DESIGN.md for how the path would shard)", "n_gpus": args.gpus}))
+                                   "(periodic systems would shard by spatial domain with a one-layer halo "
+                                   "exchange, molecule batches by molecule)", "n_gpus": args.gpus}))
         sys.exit(2)
     from flashcart_amd import _lib
     _lib.load()
