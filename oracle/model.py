@@ -60,17 +60,28 @@ def rms_norm(sd, prefix, x, l_max, C, eps=1e-6):
     return scaled * g
 
 
-def interaction(sd, prefix, cfg, k, node_feats, edge_attrs, edge_feats, envelope, edge_index):
+def interaction(sd, prefix, cfg, lin, lout, node_feats, edge_attrs, edge_feats, envelope, edge_index,
+                atom_types=None):
+    """InteractionLayer.forward (src/flashcart/nn/layers.py:310-379): linear_first, radial MLP on the
+    envelope-scaled radial features (with the sender/receiver element embeddings appended when the
+    layer is element-conditioned, :346-350), conv TP, / sqrt(avg_neighbors), linear_second, skip
+    projection (rank-0 slice add when lin == 0, :370-375), RMS norm."""
     C = cfg["n_hidden_feats"]
     L = cfg["l_max_edge_attrs"]
-    lin = 0 if k == 0 else cfg["l_max_hidden_feats"]
-    lout = L if cfg.get("correlation", 3) > 1 else (cfg["l_max_hidden_feats"] if k < cfg["n_interactions"] - 1 else 0)
     out_paths, P = _paths(lin, L, lout)
     residual = node_feats
-    mlp_in = edge_feats * envelope.unsqueeze(-1)
+    idx_i, idx_j = edge_index[0], edge_index[1]
+    if f"{prefix}.emb_i.weight" in sd:
+        if atom_types is None:
+            raise ValueError("atom_types required for an element-conditioned interaction")
+        emb_i = sd[f"{prefix}.emb_i.weight"][atom_types][idx_i]
+        emb_j = sd[f"{prefix}.emb_j.weight"][atom_types][idx_j]
+        mlp_in = torch.cat([edge_feats, emb_i, emb_j], dim=-1) * envelope.unsqueeze(-1)
+    else:
+        mlp_in = edge_feats * envelope.unsqueeze(-1)
     h = _o3_linear(sd, f"{prefix}.linear_first", node_feats, lin, lin, C, C)
     w = _mlp(sd, f"{prefix}.radial_mlp", mlp_in, len(cfg.get("hidden_radial", [64, 64])) + 1)
-    agg = O.tensor_product(h, edge_attrs, w, edge_index[0], edge_index[1], lin, L, lout, C, 1)
+    agg = O.tensor_product(h, edge_attrs, w, idx_i, idx_j, lin, L, lout, C, 1)
     agg = agg / sd[f"{prefix}.sqrt_avg_neighbors"].to(agg.dtype)
     out = _o3_linear(sd, f"{prefix}.linear_second", agg, lout, lout, C, C, out_paths)
     if lin == 0:
@@ -91,7 +102,7 @@ def gated(sd, prefix, cfg, x, l_max):
     if cfg.get("gate_activation", "silu") == "silu":
         gates = O.silu(pre)
     else:
-        gates = O.SIGMOID_SCALE * torch.sigmoid(pre)
+        gates = O.stored(O.SIGMOID_SCALE) * torch.sigmoid(pre)
     gates = gates.view(n, l_max + 1, C)
     blocks, off = [], 0
     for l in range(l_max + 1):
@@ -101,7 +112,12 @@ def gated(sd, prefix, cfg, x, l_max):
     return x + _o3_linear(sd, f"{prefix}.output_linear", torch.cat(blocks, dim=-1), l_max, l_max, C, C)
 
 
-def product(sd, prefix, cfg, x, out_l_max):
+def product(sd, prefix, cfg, x, out_l_max, atom_types=None):
+    """ProductLayer.forward (src/flashcart/nn/layers.py:949-995): B_0 = x (times the rank-expanded
+    step-0 path weights when those are learnable, :960-963), B_k = TP(B_{k-1}, x, 1 + delta_k),
+    per-step product linear (or path norm), sum of the selected ranks, final linear (reduced),
+    skip projection, RMS norm. Element-dependent deltas (ProductPathWeights, :703-766) are rows of
+    an embedding indexed by the atom type, so the products then take per-row weights."""
     C = cfg["n_hidden_feats"]
     L = cfg["l_max_edge_attrs"]
     corr = cfg.get("correlation", 3)
@@ -113,16 +129,23 @@ def product(sd, prefix, cfg, x, out_l_max):
         p_out = out_l_max if k == corr - 1 else L
         l2, f2 = (0, 1) if k == 0 else (L, C)
         out_paths, P = _paths(L, l2, p_out)
-        delta = sd.get(f"{prefix}.path_weights.{k}.delta")
-        w = 1.0 + (delta if delta is not None else torch.zeros(P * C, dtype=x.dtype))
+        table = sd.get(f"{prefix}.path_weights.{k}.delta.weight")
+        per_row = table is not None
+        if per_row:
+            if atom_types is None:
+                raise ValueError("atom_types required for element-dependent product weights")
+            w = 1.0 + table[atom_types]
+        else:
+            delta = sd.get(f"{prefix}.path_weights.{k}.delta")
+            w = 1.0 + (delta if delta is not None else torch.zeros(P * C, dtype=x.dtype))
         if k == 0:
-            if reduced:
+            if reduced or per_row:
                 idx = torch.cat([torch.arange(l * C, (l + 1) * C).repeat(2 * l + 1) for l in range(L + 1)])
-                feats = x * w[idx]
+                feats = x * w[..., idx]
             else:
                 feats = x
         else:
-            feats = O.tensor_product(feats, x, w, None, None, L, L, p_out, C, C, shared_weights=True,
+            feats = O.tensor_product(feats, x, w, None, None, L, L, p_out, C, C, shared_weights=not per_row,
                                      reduce_paths=reduced)
         if reduced:
             norm = torch.cat([torch.full(((2 * l + 1) * C,), out_paths[l] ** -0.5) for l in range(p_out + 1)])
@@ -140,14 +163,25 @@ def product(sd, prefix, cfg, x, out_l_max):
     return output
 
 
+def readout(sd, prefix, cfg, outs):
+    """EnergyReadoutLayer.forward (src/flashcart/nn/layers.py:1045-1063): MLP on the concatenated
+    first C columns of every layer's output."""
+    C = cfg["n_hidden_feats"]
+    x = torch.cat([o[:, :C] for o in outs], dim=1)
+    return _mlp(sd, f"{prefix}.readout_mlp", x, len(cfg.get("hidden_readout", [64, 64])) + 1).squeeze(-1)
+
+
 def node_energies(sd: Dict[str, torch.Tensor], cfg: Dict[str, Any], graph: Dict[str, Any]) -> torch.Tensor:
-    if not cfg.get("element_agnostic_interaction", True) or not cfg.get("element_agnostic_product", True):
-        raise NotImplementedError("the oracle covers element-agnostic interactions and products")
+    """FlashCartPotential.forward (src/flashcart/model/flashcart.py:249-317; ranks of each layer
+    from :155-162): interaction in ranks [0, Lh, ...], interaction out L (or the product out ranks
+    when correlation is 1), gate at the interaction's out rank, product out [Lh, ..., 0], readout on
+    the first C columns of every layer, per-element scale."""
     C = cfg["n_hidden_feats"]
     L = cfg["l_max_edge_attrs"]
     Lh = cfg["l_max_hidden_feats"]
     n_int = cfg["n_interactions"]
     ei = graph["edge_index"]
+    types = graph["atom_types"]
     vec = graph.get("vectors")
     if vec is None:
         vec = O.edge_vectors(graph["positions"], graph["cell"], graph["shifts"], ei, graph["batch"],
@@ -158,20 +192,23 @@ def node_energies(sd: Dict[str, torch.Tensor], cfg: Dict[str, Any], graph: Dict[
     feats = O.chebyshev(d, cfg.get("n_radial", 8), cfg["r_max"], cfg.get("r_min", 0.0),
                         cfg.get("radial_mapping", "affine"))
     env = O.cutoff(d, cfg["r_max"], cfg.get("cutoff_poly_order", 6))
-    x = sd["embedding.weight"][graph["atom_types"]]
+    x = sd["embedding.weight"][types]
     use_products = cfg.get("correlation", 3) > 1
+    prod_out = [Lh if k < n_int - 1 else 0 for k in range(n_int)]
+    int_out = [L] * n_int if use_products else prod_out
     outs = []
     for k in range(n_int):
-        y = interaction(sd, f"interactions.{k}", cfg, k, x, attrs, feats, env, ei)
+        y = interaction(sd, f"interactions.{k}", cfg, 0 if k == 0 else Lh, int_out[k], x, attrs, feats, env, ei,
+                        atom_types=types)
         if cfg.get("nonlinearity", False):
-            y = gated(sd, f"nonlinearities.{k}", cfg, y, L if use_products else (Lh if k < n_int - 1 else 0))
+            y = gated(sd, f"nonlinearities.{k}", cfg, y, int_out[k])
         if use_products:
-            x = product(sd, f"products.{k}", cfg, y, Lh if k < n_int - 1 else 0)
+            x = product(sd, f"products.{k}", cfg, y, prod_out[k], atom_types=types)
         else:
             x = y
         outs.append(x[:, :C])
-    e = _mlp(sd, "readout.readout_mlp", torch.cat(outs, dim=1), len(cfg.get("hidden_readout", [64, 64])) + 1)
-    return sd["scale_shift.scales"][graph["atom_types"]] * e.squeeze(-1)
+    e = readout(sd, "readout", cfg, outs)
+    return sd["scale_shift.scales"][types] * e
 
 
 def predict(sd: Dict[str, torch.Tensor], cfg: Dict[str, Any], graph: Dict[str, Any], compute_forces: bool = True,

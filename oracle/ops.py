@@ -33,6 +33,13 @@ SIGMOID_SCALE = 1.8462285453386054
 MIN_EDGE_LENGTH = 1.0e-4
 
 
+def stored(x: float) -> float:
+    """A constant as the reference's modules hold it: in a buffer made under torch's default dtype,
+    float32 (nn/layers.py:24-27, :60-63, :106-110; o3/_linear.py:148-164 via o3/linear.py:68-79),
+    so a model cast to float64 still multiplies by the float32 rounding of the constant."""
+    return float(torch.tensor(x, dtype=torch.float32))
+
+
 def _t(a: np.ndarray, like: torch.Tensor) -> torch.Tensor:
     return torch.as_tensor(a, dtype=like.dtype, device=like.device)
 
@@ -157,7 +164,7 @@ def linear(x: torch.Tensor, weights: Sequence[torch.Tensor], in_l_max: int, out_
         k = in_features * in_paths[l]
         size = (2 * l + 1) * k
         if l <= common:
-            s = float(weight_scale) if weight_scale is not None else float(k) ** -0.5
+            s = stored(float(weight_scale) if weight_scale is not None else float(k) ** -0.5)
             xl = x[:, off:off + size].reshape(n, 2 * l + 1, k)
             outs.append(torch.nn.functional.linear(xl, weights[l] * s).reshape(n, -1))
         off += size
@@ -168,9 +175,9 @@ def linear(x: torch.Tensor, weights: Sequence[torch.Tensor], in_l_max: int, out_
 
 
 def dense(x, weight, bias=None, weight_scale=None):
-    s = float(weight.shape[1]) ** -0.5 if weight_scale is None else weight_scale
+    s = stored(float(weight.shape[1]) ** -0.5 if weight_scale is None else weight_scale)
     return torch.nn.functional.linear(x, weight * s, bias)
 
 
 def silu(x):
-    return SILU_SCALE * torch.nn.functional.silu(x)
+    return stored(SILU_SCALE) * torch.nn.functional.silu(x)

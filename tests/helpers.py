@@ -1,4 +1,7 @@
-"""Shared test helpers: seeded synthetic graphs and comparison utilities."""
+"""Shared test helpers: seeded synthetic graphs, comparison utilities, golden fixtures."""
+
+import json
+import os
 
 import numpy as np
 import torch
@@ -38,3 +41,26 @@ def assert_close(got, want, rtol, atol, what=""):
         raise AssertionError(f"{what}: {int(bad.sum())} / {err.numel()} elements off; worst at flat {k}: "
                              f"got {got.reshape(-1)[k]:.8g} want {want.reshape(-1)[k]:.8g} "
                              f"(max abs err {float(err.max()):.3e})")
+
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def load_golden(name):
+    """One fixture of tests/golden/ (written by tests/golden/make_fixtures.py from the reference's
+    own modules): {"meta": dict, "sd": {...}, "in": {...}, "out": {...}, ...} of CPU tensors."""
+    z = np.load(os.path.join(GOLDEN, f"{name}.npz"))
+    out = {"meta": json.loads(str(z["meta"]))}
+    for key in z.files:
+        if key == "meta":
+            continue
+        group, sub = key.split("/", 1)
+        out.setdefault(group, {})[sub] = torch.from_numpy(z[key].copy())
+    return out
+
+
+def golden_names(kind=None):
+    names = sorted(f[:-4] for f in os.listdir(GOLDEN) if f.endswith(".npz"))
+    if kind is None:
+        return names
+    return [n for n in names if json.loads(str(np.load(os.path.join(GOLDEN, n + ".npz"))["meta"]))["kind"] == kind]
