@@ -103,6 +103,9 @@ _SIGNATURES = {
     "fc_neighbor_list_device_workspace": (c_i64, [c_i64]),
     "fc_neighbor_list_device": (c_i64, [c_i64, c_vp, c_vp, c_vp, ctypes.c_double, c_i64, c_vp, c_vp, c_vp, c_vp,
                                         c_i64, c_vp]),
+    "fc_neighbor_list_device_noalloc_max_atoms": (c_i64, []),
+    "fc_neighbor_list_device_noalloc": (c_i64, [c_i64, c_vp, c_vp, c_vp, ctypes.c_double, c_i64, c_vp, c_vp, c_vp,
+                                                c_vp]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

@@ -86,6 +86,7 @@ extern "C" const char* fc_status_string(int st) {
     case FC_ERR_SHAPE: return "unsupported sizes";
     case FC_ERR_NULL: return "required pointer is NULL";
     case FC_ERR_WORKSPACE: return "workspace missing or too small";
+    case FC_ERR_SCRATCH_LIMIT: return "input exceeds the fixed scratch of an allocation-free entry point";
   }
   return "unknown status";
 }

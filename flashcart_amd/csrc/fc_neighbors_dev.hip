@@ -23,6 +23,7 @@
 //   fill:  one wave per receiver collects its pairs' keys (j, S) in LDS, sorts them
 //          (bitonic) and writes them at its offset.
 #include <cmath>
+#include <mutex>
 
 #include "fc_common.h"
 
@@ -321,15 +322,13 @@ extern "C" int64_t fc_neighbor_list_device_workspace(int64_t n) {
   return nl_layout(n, nullptr, nullptr);
 }
 
-extern "C" int64_t fc_neighbor_list_device(int64_t n, const double* pos, const double* cell, const int32_t* pbc,
-                                           double cutoff, int64_t capacity, int64_t* out_i, int64_t* out_j,
-                                           int32_t* out_shift, void* workspace, int64_t workspace_bytes,
-                                           void* stream) {
-  if (n < 0 || !(cutoff > 0.0) || !cell || !pbc) return -FC_ERR_BAD_DESC;
-  if (n == 0) return 0;
-  if (n > 0x7fffffff || !pos) return -FC_ERR_SHAPE;
-  if (!workspace || workspace_bytes < nl_layout(n, nullptr, nullptr)) return -FC_ERR_WORKSPACE;
-  hipStream_t s = (hipStream_t)stream;
+namespace fc {
+
+// The list from positions in HBM, with its working arrays laid out from `workspace` (at least
+// nl_layout(n) bytes, already checked by the caller). Returns the pair count or -fc_status.
+static int64_t nl_build(int64_t n, const double* pos, const double* cell, const int32_t* pbc, double cutoff,
+                        int64_t capacity, int64_t* out_i, int64_t* out_j, int32_t* out_shift, void* workspace,
+                        hipStream_t s) {
   NLWorkspace ws;
   nl_layout(n, reinterpret_cast<char*>(workspace), &ws);
 
@@ -425,4 +424,71 @@ extern "C" int64_t fc_neighbor_list_device(int64_t n, const double* pos, const d
                      ws.rowptr, out_i, out_j, out_shift);
   if (hipGetLastError() != hipSuccess) return -FC_ERR_LAUNCH;
   return total;
+}
+
+static int64_t nl_check_args(int64_t n, const double* pos, const double* cell, const int32_t* pbc, double cutoff) {
+  if (n < 0 || !(cutoff > 0.0) || !cell || !pbc) return -FC_ERR_BAD_DESC;
+  if (n > 0x7fffffff || (n > 0 && !pos)) return -FC_ERR_SHAPE;
+  return 0;
+}
+
+// Working memory of the allocation-free entry point: one copy of this array per device (a module
+// global), held until the process ends. Host code never passes `scratch` itself to a kernel or a
+// copy (in host code the name is only a stand-in for the symbol): it uses the device address that
+// hipGetSymbolAddress returns for the current device, kept in g_scratch_ptr.
+constexpr int64_t kNLScratchBytes = int64_t(64) << 20;
+static __device__ __align__(256) char scratch[kNLScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+// The current device's address of `scratch` (looked up once per device, with that device current).
+static int nl_scratch_address(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return FC_ERR_LAUNCH;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return FC_ERR_LAUNCH;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return FC_OK;
+}
+
+}  // namespace fc
+
+extern "C" int64_t fc_neighbor_list_device(int64_t n, const double* pos, const double* cell, const int32_t* pbc,
+                                           double cutoff, int64_t capacity, int64_t* out_i, int64_t* out_j,
+                                           int32_t* out_shift, void* workspace, int64_t workspace_bytes,
+                                           void* stream) {
+  const int64_t bad = nl_check_args(n, pos, cell, pbc, cutoff);
+  if (bad) return bad;
+  if (n == 0) return 0;
+  if (!workspace || workspace_bytes < nl_layout(n, nullptr, nullptr)) return -FC_ERR_WORKSPACE;
+  return nl_build(n, pos, cell, pbc, cutoff, capacity, out_i, out_j, out_shift, workspace, (hipStream_t)stream);
+}
+
+extern "C" int64_t fc_neighbor_list_device_noalloc_max_atoms(void) {
+  int64_t lo = 0, hi = int64_t(1) << 31;  // largest n whose working arrays fit the scratch array
+  while (lo < hi) {
+    const int64_t mid = (lo + hi + 1) / 2;
+    if (nl_layout(mid, nullptr, nullptr) <= kNLScratchBytes) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+extern "C" int64_t fc_neighbor_list_device_noalloc(int64_t n, const double* pos, const double* cell,
+                                                   const int32_t* pbc, double cutoff, int64_t capacity,
+                                                   int64_t* out_i, int64_t* out_j, int32_t* out_shift,
+                                                   void* stream) {
+  const int64_t bad = nl_check_args(n, pos, cell, pbc, cutoff);
+  if (bad) return bad;
+  if (n == 0) return 0;
+  if (nl_layout(n, nullptr, nullptr) > kNLScratchBytes) return -FC_ERR_SCRATCH_LIMIT;
+  void* base = nullptr;
+  const int st = nl_scratch_address(&base);
+  if (st != FC_OK) return -st;
+  return nl_build(n, pos, cell, pbc, cutoff, capacity, out_i, out_j, out_shift, base, (hipStream_t)stream);
 }

@@ -29,7 +29,8 @@ typedef enum fc_status {
   FC_ERR_LAUNCH = 3,         /* hipGetLastError() reported a launch failure */
   FC_ERR_SHAPE = 4,          /* sizes the kernels do not support (e.g. > 1024 channels) */
   FC_ERR_NULL = 5,           /* a required pointer is NULL */
-  FC_ERR_WORKSPACE = 6       /* workspace missing or too small */
+  FC_ERR_WORKSPACE = 6,      /* workspace missing or too small */
+  FC_ERR_SCRATCH_LIMIT = 7   /* input larger than an allocation-free entry point's fixed scratch */
 } fc_status;
 
 /* Library version (major*10000 + minor*100 + patch) and the maximal supported rank. */
@@ -327,6 +328,19 @@ int64_t fc_neighbor_list_device(int64_t n, const double* pos, const double* cell
                                 double cutoff, int64_t capacity, int64_t* out_i, int64_t* out_j,
                                 int32_t* out_shift, void* workspace, int64_t workspace_bytes,
                                 void* stream);
+
+/* Allocation-free variant of fc_neighbor_list_device. No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (tight MD / serving loops, harnesses that
+ * forbid hipMalloc). The same pairs in the same order, with the working arrays in a fixed
+ * 64 MiB array of device memory that the library holds on each device it runs on until the
+ * process ends, instead of a caller workspace. Inputs and outputs as fc_neighbor_list_device;
+ * allocates and frees nothing. n above fc_neighbor_list_device_noalloc_max_atoms() (about
+ * 640k atoms) returns -FC_ERR_SCRATCH_LIMIT. Every call on a device shares that device's
+ * array, so calls that overlap on one device (other streams, other host threads) race. */
+int64_t fc_neighbor_list_device_noalloc_max_atoms(void);
+int64_t fc_neighbor_list_device_noalloc(int64_t n, const double* pos, const double* cell, const int32_t* pbc,
+                                        double cutoff, int64_t capacity, int64_t* out_i, int64_t* out_j,
+                                        int32_t* out_shift, void* stream);
 
 #ifdef __cplusplus
 }
