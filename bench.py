@@ -43,70 +43,16 @@ MEASURED_TRAFFIC_BYTES = 11.77e9
 # The same for the layer-1 backward op (tp_bwd_conv_kernel 27.248 GB + segment_rows_kernel 5.116 GB) from
 # the `bench.py --profile-step` counter runs; see profiles/fcc25k_L3_C128_kernel_hbm_mfma.md.
 MEASURED_TRAFFIC_BWD_BYTES = 32.36e9
-R_MAX = 5.0
-SIGMA_STEP = 0.01
-SKIN = 1.0
+from flashcart_amd.data.synthetic import FCC25K_R_MAX as R_MAX  # noqa: E402
+from flashcart_amd.data.synthetic import FCC25K_SIGMA_STEP as SIGMA_STEP  # noqa: E402
+from flashcart_amd.data.synthetic import FCC25K_SKIN as SKIN  # noqa: E402
+from flashcart_amd.data.synthetic import StepGraphs  # noqa: E402
+from flashcart_amd.data.synthetic import fcc25k_model as build_model  # noqa: E402
+from flashcart_amd.data.synthetic import fcc25k_system as make_system  # noqa: E402
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
-
-
-def make_system(nx=25, ny=25, nz=10, seed=0):
-    from flashcart_amd.data.synthetic import fcc_alloy
-    return fcc_alloy(nx, ny, nz, a=3.6, jitter=0.05, seed=seed)
-
-
-class StepGraphs:
-    """Per-step graphs with exact r_max connectivity from a skin list (host side)."""
-
-    def __init__(self, numbers, pos, cell, pbc, elements, n_steps, seed=1):
-        from flashcart_amd.data.neighbors import neighbor_pairs
-        from flashcart_amd.data.graph import numbers_to_types
-        self.types = torch.as_tensor(numbers_to_types(numbers, elements))
-        self.numbers = numbers
-        self.cell = cell
-        self.pbc = pbc
-        rng = np.random.default_rng(seed)
-        self.graphs = []
-        ref_pos, skin_list = None, None
-        cur = pos.copy()
-        n_rebuild = 0
-        for k in range(n_steps):
-            cur = cur + rng.normal(0.0, SIGMA_STEP, size=cur.shape)
-            if ref_pos is None or np.max(np.linalg.norm(cur - ref_pos, axis=1)) >= SKIN / 2:
-                ref_pos = cur.copy()
-                skin_list = neighbor_pairs(cur, cell, pbc, R_MAX + SKIN)
-                n_rebuild += 1
-            ei, sh = skin_list
-            v = cur[ei[1]] - cur[ei[0]] + sh @ cell
-            keep = np.einsum("ij,ij->i", v, v) < R_MAX * R_MAX
-            self.graphs.append((cur.astype(np.float64), ei[:, keep].copy(), sh[keep].copy()))
-        self.n_rebuild = n_rebuild
-
-    def graph(self, k, device):
-        from flashcart_amd.data.graph import AtomicGraph
-        pos, ei, sh = self.graphs[k]
-        n = pos.shape[0]
-        return AtomicGraph(
-            positions=torch.as_tensor(pos, dtype=torch.float32, device=device),
-            cell=torch.as_tensor(self.cell, dtype=torch.float32, device=device).unsqueeze(0),
-            pbc=torch.as_tensor(self.pbc, device=device).unsqueeze(0),
-            shifts=torch.as_tensor(sh, dtype=torch.long, device=device),
-            edge_index=torch.as_tensor(ei, dtype=torch.long, device=device),
-            atom_types=self.types.to(device), atomic_numbers=torch.as_tensor(self.numbers, device=device),
-            n_atoms=torch.tensor([n], dtype=torch.long, device=device), use_shifts=True)
-
-
-def build_model(avg_neighbors, channels=128, l_max=3):
-    from flashcart_amd.data.synthetic import model_config
-    from flashcart_amd.model import FlashCartPotential
-    cfg = model_config(["Cu", "Ni", "Fe", "Cr"], channels, l_max, r_max=R_MAX, avg_neighbors=avg_neighbors)
-    torch.manual_seed(1234)
-    model = FlashCartPotential.from_config(cfg)
-    for p in model.parameters():
-        p.requires_grad_(False)
-    return model, cfg
 
 
 def tp_conv_bytes(n_nodes, n_send, E, d1, d2, P, C, nout):

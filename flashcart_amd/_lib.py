@@ -66,6 +66,7 @@ _SIGNATURES = {
     "fc_status_string": (c_cp, [c_int]),
     "fc_irreps_fwd": (c_int, [c_i64, c_i32, c_vp, c_vp, c_vp]),
     "fc_irreps_bwd": (c_int, [c_i64, c_i32, c_vp, c_vp, c_vp, c_vp]),
+    "fc_irreps_dbwd": (c_int, [c_i64, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "fc_radial_fwd": (c_int, [ctypes.POINTER(RadialDesc), c_i64, c_vp, c_vp, c_vp, c_vp]),
     "fc_radial_bwd": (c_int, [ctypes.POINTER(RadialDesc), c_i64, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "fc_edge_geometry_fwd": (c_int, [ctypes.POINTER(EdgeDesc), c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),

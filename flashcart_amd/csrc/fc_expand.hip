@@ -281,6 +281,35 @@ __device__ __forceinline__ void expand_all_hvp(float x, float y, float z, const 
   });
 }
 
+// Backward of irreps_bwd (gx = J(x)^T g): along a cotangent v of gx,
+//   d/dg = J(x) v            (the directional derivative of every component),
+//   d/dx = sum_a g_a H_a(x) v (Hessian-vector products of the components).
+// Either output may be NULL (not wanted).
+template <int L>
+__global__ void irreps_dbwd_kernel(int64_t n, const float* __restrict__ g, const float* __restrict__ x,
+                                   const float* __restrict__ v, float* __restrict__ d_g, float* __restrict__ d_x) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float x0 = x[3 * i], x1 = x[3 * i + 1], x2 = x[3 * i + 2];
+  const float du[3] = {v[3 * i], v[3 * i + 1], v[3 * i + 2]};
+  if (d_g) {
+    float dt[ncomp(L)];
+    expand_all_jvp<L>(x0, x1, x2, du, dt);
+#pragma unroll
+    for (int k = 0; k < ncomp(L); ++k) d_g[i * ncomp(L) + k] = dt[k];
+  }
+  if (d_x) {
+    float gi[ncomp(L)];
+#pragma unroll
+    for (int k = 0; k < ncomp(L); ++k) gi[k] = g[i * ncomp(L) + k];
+    float h[3] = {0.f, 0.f, 0.f};
+    expand_all_hvp<L>(x0, x1, x2, gi, du, h);
+    d_x[3 * i] = h[0];
+    d_x[3 * i + 1] = h[1];
+    d_x[3 * i + 2] = h[2];
+  }
+}
+
 // First and second derivatives of the radial basis with respect to d.
 __device__ __forceinline__ void radial_d12(const RadialParams& p, float d, float* df, float* d2f) {
   const int n = p.n_radial;
@@ -458,6 +487,7 @@ int launch_by_l(int l, int64_t n, hipStream_t s, Args... args) {
 
 template <int L> struct IrrepsFwd { static constexpr auto fn = irreps_fwd_kernel<L>; };
 template <int L> struct IrrepsBwd { static constexpr auto fn = irreps_bwd_kernel<L>; };
+template <int L> struct IrrepsDbwd { static constexpr auto fn = irreps_dbwd_kernel<L>; };
 
 static int check_radial(const fc_radial_desc* d) {
   if (!d) return FC_ERR_NULL;
@@ -503,6 +533,14 @@ extern "C" int fc_irreps_bwd(int64_t n, int32_t l_max, const float* g, const flo
   if (n < 0) return FC_ERR_SHAPE;
   if (n > 0 && (!g || !x || !gx)) return FC_ERR_NULL;
   return launch_by_l<IrrepsBwd>(l_max, n, (hipStream_t)stream, g, x, gx);
+}
+
+extern "C" int fc_irreps_dbwd(int64_t n, int32_t l_max, const float* g, const float* x, const float* v,
+                              float* d_g, float* d_x, void* stream) {
+  if (n < 0) return FC_ERR_SHAPE;
+  if (n > 0 && (!x || !v || (d_x && !g))) return FC_ERR_NULL;
+  if (!d_g && !d_x) return FC_OK;
+  return launch_by_l<IrrepsDbwd>(l_max, n, (hipStream_t)stream, g, x, v, d_g, d_x);
 }
 
 extern "C" int fc_radial_fwd(const fc_radial_desc* desc, int64_t n, const float* d, float* feats, float* env,

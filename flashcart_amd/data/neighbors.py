@@ -53,6 +53,16 @@ def neighbor_pairs(positions: np.ndarray, cell: np.ndarray, pbc, cutoff: float, 
 _last_device_count = {}  # atom count -> pairs of the last device build (output size hint)
 
 
+_FC_ERR_SHAPE = 4  # fc_status, include/flashcart_hip.h
+
+
+def host_fallback_needed(status: int) -> bool:
+    """Whether fc_neighbor_list_device's return value asks for the host list: -FC_ERR_SHAPE
+    means an atom with more than 1,024 pairs or a shift component of 512 or more (sizes the
+    device kernels do not hold); every other negative value is an error of its own."""
+    return status == -_FC_ERR_SHAPE
+
+
 def neighbor_pairs_device(positions: torch.Tensor, cell, pbc, cutoff: float, eps: float = 1e-7):
     """The pairs of ``neighbor_pairs`` built on the GPU from positions in HBM
     (``fc_neighbor_list_device``): (edge_index (2, E) int64, unit_shifts (E, 3) int32) on
@@ -82,6 +92,12 @@ def neighbor_pairs_device(positions: torch.Tensor, cell, pbc, cutoff: float, eps
         cnt = lib.fc_neighbor_list_device(n, pos.data_ptr(), cell_np.ctypes.data, flags.ctypes.data, float(cutoff),
                                           cap, ei[0].data_ptr(), ei[1].data_ptr(), sh.data_ptr(), ws.data_ptr(),
                                           ws_bytes, _lib.stream_of(pos))
+        if host_fallback_needed(cnt):
+            # more pairs for one atom than the device list holds in LDS (1024), or a periodic
+            # shift component >= 512: the host cell list builds the same pairs in the same order
+            ei_h, sh_h = neighbor_pairs(pos.cpu().numpy(), cell_np, pbc, cutoff)
+            return (torch.as_tensor(ei_h, device=pos.device),
+                    torch.as_tensor(np.ascontiguousarray(sh_h), dtype=torch.int32, device=pos.device))
         if cnt < 0:
             _lib.check(-cnt, "fc_neighbor_list_device")
         _last_device_count[n] = int(cnt)

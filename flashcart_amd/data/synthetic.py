@@ -9,6 +9,9 @@
 * ``model_config``: the packaged default architecture (l_max_hidden_feats=2,
   correlation=3, sigmoid gates, layer norm, cosine Chebyshev radial basis, radial and
   readout widths [64, 64]) with the given channels, edge rank and cutoff.
+* ``fcc25k_system`` / ``StepGraphs`` / ``fcc25k_model``: the benchmark workload of
+  BASELINE configuration 4 (25x25x10 fcc cells, a = 3.6 A, MD-style steps of N(0, 0.01^2) A,
+  C = 128, L_max = 3, seed 1234), shared by bench.py and the full-size parity test.
 """
 
 from __future__ import annotations
@@ -16,6 +19,7 @@ from __future__ import annotations
 from typing import Dict, List, Tuple
 
 import numpy as np
+import torch
 
 _Z = {"H": 1, "C": 6, "N": 7, "O": 8, "Cr": 24, "Fe": 26, "Ni": 28, "Cu": 29}
 
@@ -99,3 +103,73 @@ def model_config(elements, n_hidden_feats: int, l_max_edge_attrs: int, r_max: fl
         cutoff_poly_order=6, avg_neighbors=float(avg_neighbors), atomic_shifts=[0.0] * len(elements),
         fit_atomic_shifts=False, use_triton=True,
     )
+
+
+FCC25K_R_MAX = 5.0
+FCC25K_SIGMA_STEP = 0.01
+FCC25K_SKIN = 1.0
+FCC25K_ELEMENTS = ("Cu", "Ni", "Fe", "Cr")
+
+
+def fcc25k_system(nx=25, ny=25, nz=10, seed=0):
+    """fcc random alloy, a = 3.6 A, jitter 0.05 A, 4 species."""
+    return fcc_alloy(nx, ny, nz, a=3.6, jitter=0.05, seed=seed)
+
+
+class StepGraphs:
+    """Per-step graphs of an MD-style run with exact r_max connectivity from a skin list (host side).
+
+    Step k perturbs the previous positions by N(0, sigma^2) (rng seed ``seed``); the host cell list
+    at r_max + skin is rebuilt when an atom moved more than skin / 2 since the last build, and each
+    step keeps the pairs within r_max (in the list's (i, j, S) order)."""
+
+    def __init__(self, numbers, pos, cell, pbc, elements, n_steps, seed=1, r_max=FCC25K_R_MAX,
+                 sigma=FCC25K_SIGMA_STEP, skin=FCC25K_SKIN):
+        from flashcart_amd.data.graph import numbers_to_types
+        from flashcart_amd.data.neighbors import neighbor_pairs
+        self.types = torch.as_tensor(numbers_to_types(numbers, elements))
+        self.numbers = numbers
+        self.cell = cell
+        self.pbc = pbc
+        rng = np.random.default_rng(seed)
+        self.graphs = []
+        ref_pos, skin_list = None, None
+        cur = pos.copy()
+        n_rebuild = 0
+        for _ in range(n_steps):
+            cur = cur + rng.normal(0.0, sigma, size=cur.shape)
+            if ref_pos is None or np.max(np.linalg.norm(cur - ref_pos, axis=1)) >= skin / 2:
+                ref_pos = cur.copy()
+                skin_list = neighbor_pairs(cur, cell, pbc, r_max + skin)
+                n_rebuild += 1
+            ei, sh = skin_list
+            v = cur[ei[1]] - cur[ei[0]] + sh @ cell
+            keep = np.einsum("ij,ij->i", v, v) < r_max * r_max
+            self.graphs.append((cur.astype(np.float64), ei[:, keep].copy(), sh[keep].copy()))
+        self.n_rebuild = n_rebuild
+
+    def graph(self, k, device="cpu"):
+        """Step k as an AtomicGraph with float32 positions and cell."""
+        from flashcart_amd.data.graph import AtomicGraph
+        pos, ei, sh = self.graphs[k]
+        n = pos.shape[0]
+        return AtomicGraph(
+            positions=torch.as_tensor(pos, dtype=torch.float32, device=device),
+            cell=torch.as_tensor(self.cell, dtype=torch.float32, device=device).unsqueeze(0),
+            pbc=torch.as_tensor(self.pbc, device=device).unsqueeze(0),
+            shifts=torch.as_tensor(sh, dtype=torch.long, device=device),
+            edge_index=torch.as_tensor(ei, dtype=torch.long, device=device),
+            atom_types=self.types.to(device), atomic_numbers=torch.as_tensor(self.numbers, device=device),
+            n_atoms=torch.tensor([n], dtype=torch.long, device=device), use_shifts=True)
+
+
+def fcc25k_model(avg_neighbors, channels=128, l_max=3):
+    """The benchmark model: default architecture, random init from torch.manual_seed(1234),
+    frozen parameters (inference)."""
+    from flashcart_amd.model import FlashCartPotential
+    cfg = model_config(list(FCC25K_ELEMENTS), channels, l_max, r_max=FCC25K_R_MAX, avg_neighbors=avg_neighbors)
+    torch.manual_seed(1234)
+    model = FlashCartPotential.from_config(cfg)
+    for p in model.parameters():
+        p.requires_grad_(False)
+    return model, cfg

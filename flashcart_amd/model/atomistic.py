@@ -128,7 +128,15 @@ class AtomisticModel(nn.Module):
         reference's cached compiled functions, a new shape (atom or edge count) captures
         a new graph. ``compile_mode``, ``fullgraph`` and ``dynamic`` are accepted for API
         compatibility; shapes are always static.
+
+        Per-structure energies are segment sums over ``batch``, which must be sorted (atoms of
+        a structure contiguous, as ``batch_graphs`` and the reference's ``Batch.from_data_list``
+        build it); a plain dict graph is checked for that here.
         """
+        if isinstance(graph, dict):
+            b = graph["batch"]
+            if b.numel() > 1 and not bool((b[1:] >= b[:-1]).all()):
+                raise ValueError("graph['batch'] must be sorted: the atoms of each structure contiguous.")
         if create_graph:
             from flashcart_amd.nn import fused
             with fused.disabled():
@@ -148,8 +156,11 @@ class AtomisticModel(nn.Module):
                              if not torch.is_tensor(v) and k not in ("_source", "csr")
                              and isinstance(v, (bool, int, float, str))))
         key = flags + plain + tuple(sorted((k, tuple(v.shape), v.dtype, str(v.device)) for k, v in tensors.items()))
-        # captured kernels read the parameters in place: re-capture if they were reallocated
-        key += tuple(p.data_ptr() for p in self.parameters())[:1]
+        # Captured kernels read parameters and buffers in place (a re-capture when any of them was
+        # reallocated); host-side constants baked into the launches (each interaction's
+        # 1/sqrt(avg_neighbors), re-read when its buffer changes) are part of the key.
+        key += tuple(t.data_ptr() for t in self.parameters()) + tuple(t.data_ptr() for t in self.buffers())
+        key += tuple(m._inv_sqrt_avg() for m in self.modules() if hasattr(m, "_inv_sqrt_avg"))
         cache = self.__dict__.setdefault("_replay_cache", {})
         entry = cache.get(key)
         if entry is None:
@@ -190,10 +201,13 @@ class AtomisticModel(nn.Module):
         out = {"node_energies": node_energies}
         n_atoms = gd["n_atoms"]
         if node_energies.shape[0] == gd["batch"].shape[0]:
-            ptr = gd.get("ptr")
-            if ptr is None:
-                ptr = torch.cat([n_atoms.new_zeros(1), torch.cumsum(n_atoms, 0)])
-            out["energy"] = _ops.segment_sum(node_energies, ptr, gd["batch"])
+            # Segment bounds from `batch` itself (the vector the forces' backward follows), so
+            # energies and forces always agree; the segmented sum needs `batch` sorted, as every
+            # graph builder here (and the reference's Batch.from_data_list) makes it.
+            batch = gd["batch"]
+            ptr = torch.searchsorted(batch, torch.arange(n_atoms.shape[0] + 1, device=batch.device,
+                                                         dtype=batch.dtype))
+            out["energy"] = _ops.segment_sum(node_energies, ptr, batch)
         else:
             out["energy"] = node_energies.sum().reshape(1)
         inputs, names = [], []

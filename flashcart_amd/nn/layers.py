@@ -137,7 +137,8 @@ class InteractionLayer(nn.Module):
             raise ValueError(f"avg_neighbors must be positive. Provided: {avg_neighbors}.")
         self.register_buffer("sqrt_avg_neighbors",
                              torch.tensor(float(avg_neighbors) ** 0.5, dtype=torch.get_default_dtype()))
-        self._sqrt_avg = float(torch.tensor(float(avg_neighbors) ** 0.5, dtype=torch.get_default_dtype()))
+        self._alpha_key = None  # (storage, version) of the buffer that self._alpha was read from
+        self._alpha = 1.0
         self.out_dim = sum((2 * l + 1) * out_features for l in range(out_l_max + 1))
         out_paths, n_total_paths = o3.utils.count_output_paths(in1_l_max, in2_l_max, out_l_max)
         if n_elements is not None and element_features is None:
@@ -172,11 +173,21 @@ class InteractionLayer(nn.Module):
             self.emb_i = None
             self.emb_j = None
 
-    def _load_from_state_dict(self, state_dict, prefix, *args, **kwargs):
-        super()._load_from_state_dict(state_dict, prefix, *args, **kwargs)
-        key = prefix + "sqrt_avg_neighbors"
-        if key in state_dict:
-            self._sqrt_avg = float(state_dict[key])
+    @property
+    def _sqrt_avg(self) -> float:
+        return 1.0 / self._inv_sqrt_avg()
+
+    def _inv_sqrt_avg(self) -> float:
+        """1 / sqrt_avg_neighbors for the TP kernel's output factor. The buffer is read again
+        (one device-to-host copy) only when it was replaced or written in place since the last
+        read: load_state_dict, set_avg_neighbors and the reference's broadcast_pre_fit_state
+        (``copy_``) all bump its version counter."""
+        buf = self.sqrt_avg_neighbors
+        key = (buf.data_ptr(), buf.device, buf._version)
+        if key != self._alpha_key:
+            self._alpha = 1.0 / float(buf.detach().float())
+            self._alpha_key = key
+        return self._alpha
 
     def forward(self, node_feats: torch.Tensor, edge_attrs: torch.Tensor, edge_feats: torch.Tensor,
                 edge_index: torch.Tensor, envelope: torch.Tensor, atom_types: Optional[torch.Tensor] = None,
@@ -196,7 +207,7 @@ class InteractionLayer(nn.Module):
         else:
             weights = run_mlp(self.radial_mlp, mlp_input)
         aggregated = self.tp(node_feats, edge_attrs, weights, idx_i, idx_j, graph=graph,
-                             alpha=1.0 / self._sqrt_avg)
+                             alpha=self._inv_sqrt_avg())
         if out_nodes is not None:
             aggregated = aggregated[:out_nodes]
         if self.skip_projection is not None and self.in1_l_max > 0:
@@ -216,7 +227,6 @@ class InteractionLayer(nn.Module):
         if avg_neighbors <= 0.0:
             raise ValueError(f"avg_neighbors must be positive. Provided: {avg_neighbors}.")
         self.sqrt_avg_neighbors.fill_(float(avg_neighbors) ** 0.5)
-        self._sqrt_avg = float(self.sqrt_avg_neighbors.detach().cpu())
 
 
 class RMSLayerNorm(nn.Module):

@@ -171,6 +171,25 @@ def _(grad_output, x, l_max):
     return torch.empty_like(x)
 
 
+@torch.library.custom_op("flashcart::irreps_dbwd", mutates_args=())
+def irreps_dbwd(grad_output: Tensor, x: Tensor, v: Tensor, l_max: int) -> Tuple[Tensor, Tensor]:
+    """Backward of irreps_bwd along v (reference flashcart::irreps_dbwd, o3/_irreps.py:146-176):
+    (d grad_output = J(x) v, d x = sum_a grad_output_a H_a(x) v)."""
+    x = _lib.contig("x", x)
+    g = _lib.contig("grad_output", grad_output)
+    vv = _lib.contig("v", v)
+    d_g = x.new_empty(x.shape[0], (l_max + 1) ** 2)
+    d_x = torch.empty_like(x)
+    _lib_call("fc_irreps_dbwd", x.shape[0], l_max, g.data_ptr(), x.data_ptr(), vv.data_ptr(), d_g.data_ptr(),
+              d_x.data_ptr(), _lib.stream_of(x))
+    return d_g, d_x
+
+
+@irreps_dbwd.register_fake
+def _(grad_output, x, v, l_max):
+    return x.new_empty(x.shape[0], (l_max + 1) ** 2), torch.empty_like(x)
+
+
 def _irreps_setup(ctx, inputs, output):
     x, l_max = inputs
     ctx.save_for_backward(x)
@@ -576,11 +595,12 @@ def _pad4(weights):
     return ws
 
 
-@torch.library.custom_op("flashcart::linear_fwd", mutates_args=())
+@torch.library.custom_op("flashcart::equiv_linear_fwd", mutates_args=())
 def linear_fwd_op(x: Tensor, w0: Tensor, w1: Optional[Tensor], w2: Optional[Tensor], w3: Optional[Tensor],
                   in_l_max: int, out_l_max: int, in_features: int, out_features: int, in_paths: List[int],
                   scale: List[float], alpha: float = 1.0, residual: Optional[Tensor] = None) -> Tensor:
-    """out = linear(x) (+ residual, a tensor of the output's shape added in the GEMM epilogue)."""
+    """out = linear(x) (+ residual, a tensor of the output's shape added in the GEMM epilogue): the
+    build's own layers call this op (the reference-schema ``flashcart::linear_fwd`` is below)."""
     in_dim, out_dim = _linear_dims(in_l_max, out_l_max, in_features, out_features, in_paths)
     if x.shape[-1] != in_dim:
         raise RuntimeError(f"Incorrect last dimension for x. Expected {in_dim}, got {x.shape[-1]}.")
@@ -601,7 +621,7 @@ def _(x, w0, w1, w2, w3, in_l_max, out_l_max, in_features, out_features, in_path
     return x.new_empty(x.shape[0], out_dim)
 
 
-@torch.library.custom_op("flashcart::linear_bwd", mutates_args=())
+@torch.library.custom_op("flashcart::equiv_linear_dgrad", mutates_args=())
 def linear_bwd_op(grad_out: Tensor, w0: Tensor, w1: Optional[Tensor], w2: Optional[Tensor], w3: Optional[Tensor],
                   in_l_max: int, out_l_max: int, in_features: int, out_features: int, in_paths: List[int],
                   scale: List[float], alpha: float = 1.0, residual: Optional[Tensor] = None) -> Tensor:
@@ -627,7 +647,7 @@ def _(grad_out, w0, w1, w2, w3, in_l_max, out_l_max, in_features, out_features, 
 def linear_fwd(x: Tensor, weights: List[Tensor], in_l_max: int, out_l_max: int, in_features: int,
                out_features: int, in_paths: List[int], scale: List[float], alpha: float = 1.0,
                residual: Optional[Tensor] = None) -> Tensor:
-    """out_l = alpha * scale_l * x_l @ W_l^T for every shared rank (torch.ops.flashcart.linear_fwd),
+    """out_l = alpha * scale_l * x_l @ W_l^T for every shared rank (torch.ops.flashcart.equiv_linear_fwd),
     plus ``residual`` (same shape as the output) when given."""
     return linear_fwd_op(x, *_pad4(weights), in_l_max, out_l_max, in_features, out_features, list(in_paths),
                          [float(s) for s in scale], float(alpha), residual)
@@ -717,6 +737,263 @@ def linear_wgrad(grad_out: Tensor, x: Tensor, weights: List[Tensor], in_l_max: i
               int(n_ws), _lib.stream_of(go))
     return outs
 
+
+
+# ---------------------------------------------------------------------------
+# The reference's linear ops, same names and schemas (src/flashcart/o3/_linear.py:328-385,
+# :457-538, :571-699, autograd chain :777-778), on the same MFMA kernels
+# ---------------------------------------------------------------------------
+
+_PRECISIONS = ("ieee", "tf32", "tf32x3")
+_scale_cache: dict = {}
+
+
+def _scale_values(scale: Tensor, n: int) -> List[float]:
+    """Host copy of the per-rank scale tensor, read again only when the tensor was replaced or
+    written in place (one device-to-host copy per change, none per call)."""
+    key = (scale.data_ptr(), scale.device, scale._version, n)
+    vals = _scale_cache.get(key)
+    if vals is None:
+        if scale.numel() < n:
+            raise RuntimeError(f"Expected {n} scales, got {scale.numel()}.")
+        vals = [float(v) for v in scale.detach().reshape(-1)[:n].cpu()]
+        if len(_scale_cache) > 256:
+            _scale_cache.clear()
+        _scale_cache[key] = vals
+    return vals
+
+
+def _ref_linear_layout(x: Tensor, weights: List[Tensor], use_fp64: bool, dot_input_precision: str,
+                       in_offsets, out_offsets, weight_offsets, m_values, f_in_values, f_out_values, out_size=None):
+    """The descriptor of the reference's metadata lists (make_linear_metadata, _linear.py:113-166):
+    rank l of n active ranks has 2l+1 components, f_in_values[l] input columns (channels x paths)
+    and f_out_values[l] = out_features outputs; returns (n, in_active_end, out_l_max, desc args)."""
+    if use_fp64:
+        raise NotImplementedError("flashcart_amd's linear kernels compute in float32 (use_fp64=False).")
+    if dot_input_precision not in _PRECISIONS:
+        raise ValueError(f"dot_input_precision must be one of {_PRECISIONS}. Provided: {dot_input_precision!r}.")
+    n = len(in_offsets)
+    lists = (out_offsets, weight_offsets, m_values, f_in_values, f_out_values)
+    if any(len(v) != n for v in lists) or n > 4:
+        raise RuntimeError("linear metadata lists must have one entry per active rank (at most 4).")
+    if len(weights) < n:
+        raise RuntimeError(f"Expected at least {n} weight tensors, got {len(weights)}.")
+    fout = int(f_out_values[0]) if n else 1
+    i_off = o_off = w_off = 0
+    for l in range(n):
+        if (int(m_values[l]) != 2 * l + 1 or int(in_offsets[l]) != i_off or int(out_offsets[l]) != o_off
+                or int(weight_offsets[l]) != w_off or int(f_out_values[l]) != fout):
+            raise ValueError("linear metadata does not describe the standard layout (make_linear_metadata).")
+        if tuple(weights[l].shape) != (fout, int(f_in_values[l])):
+            raise RuntimeError(f"Weight[{l}] shape mismatch: expected ({fout}, {int(f_in_values[l])}), "
+                               f"got {tuple(weights[l].shape)}.")
+        i_off += (2 * l + 1) * int(f_in_values[l])
+        o_off += (2 * l + 1) * fout
+        w_off += fout * int(f_in_values[l])
+    if x.shape[-1] < i_off:
+        raise RuntimeError(f"Incorrect last dimension for x. Expected at least {i_off}, got {x.shape[-1]}.")
+    out_l_max = n - 1
+    if out_size is not None:
+        r = int(round((int(out_size) / max(fout, 1)) ** 0.5)) - 1
+        if r < n - 1 or (r + 1) ** 2 * fout != int(out_size):
+            raise ValueError(f"out_size={out_size} is not (out_l_max+1)^2 * {fout} for out_l_max >= {n - 1}.")
+        out_l_max = r
+    return n, i_off, out_l_max, fout
+
+
+def _ref_desc(n, out_l_max, fout, f_in_values, weights, scale):
+    return _lib.linear_desc(n - 1, out_l_max, 1, fout, [int(v) for v in f_in_values[:n]], weights[:n],
+                            _scale_values(scale, n))
+
+
+@torch.library.custom_op("flashcart::linear_fwd", mutates_args=())
+def linear_fwd_ref(x: Tensor, weights: List[Tensor], meta: Tensor, out_size: int, use_fp64: bool,
+                   dot_input_precision: str, in_offsets: List[int], out_offsets: List[int],
+                   weight_offsets: List[int], m_values: List[int], f_in_values: List[int],
+                   f_out_values: List[int], scale: Tensor) -> Tensor:
+    """out_l = scale_l * x_l @ W_l^T for the active ranks, zeros above (the reference's op;
+    ``meta`` holds the same columns as the lists and is not read)."""
+    n, in_end, out_l_max, fout = _ref_linear_layout(x, weights, use_fp64, dot_input_precision, in_offsets,
+                                                    out_offsets, weight_offsets, m_values, f_in_values,
+                                                    f_out_values, out_size)
+    x = _lib.contig("x", x)
+    if n == 0:
+        return x.new_zeros(x.shape[0], int(out_size))
+    if x.shape[1] != in_end:  # input ranks above the output's: not read
+        x = x[:, :in_end].contiguous()
+    ws = [_lib.contig(f"weight[{l}]", w) for l, w in enumerate(weights[:n])]
+    out = x.new_empty(x.shape[0], int(out_size))
+    _lib_call("fc_linear_fwd", _ref_desc(n, out_l_max, fout, f_in_values, ws, scale), x.shape[0], x.data_ptr(),
+              1.0, None, out.data_ptr(), _lib.stream_of(x))
+    return out
+
+
+@linear_fwd_ref.register_fake
+def _(x, weights, meta, out_size, use_fp64, dot_input_precision, in_offsets, out_offsets, weight_offsets, m_values,
+      f_in_values, f_out_values, scale):
+    return x.new_empty(x.shape[0], int(out_size))
+
+
+def _ref_grad_x(grad_out, x, ws, n, in_end, fout, f_in_values, scale):
+    """scale_l * go_l @ W_l into the active input columns, zeros beyond."""
+    go = _lib.contig("grad_out", grad_out)
+    out_l_max = int(round((go.shape[1] / fout) ** 0.5)) - 1
+    gx = go.new_empty(go.shape[0], in_end)
+    _lib_call("fc_linear_dgrad", _ref_desc(n, out_l_max, fout, f_in_values, ws, scale), go.shape[0],
+              go.data_ptr(), 1.0, None, gx.data_ptr(), _lib.stream_of(go))
+    if x.shape[1] != in_end:
+        gx = torch.cat([gx, gx.new_zeros(gx.shape[0], x.shape[1] - in_end)], dim=1)
+    return gx
+
+
+def _ref_grad_w(grad_out, b, ws, n, in_end, fout, f_in_values, scale):
+    """scale_l * sum over rows of go_l^T b_l for every active rank (split-K MFMA)."""
+    b = _lib.contig("x", b)
+    if b.shape[1] != in_end:
+        b = b[:, :in_end].contiguous()
+    out_l_max = int(round((grad_out.shape[1] / fout) ** 0.5)) - 1
+    with torch.no_grad():
+        return linear_wgrad(grad_out, b, ws, n - 1, out_l_max, 1, fout, [int(v) for v in f_in_values[:n]],
+                            _scale_values(scale, n), 1.0, [True] * n)
+
+
+@torch.library.custom_op("flashcart::linear_bwd", mutates_args=())
+def linear_bwd_ref(grad_out: Tensor, x: Tensor, weights: List[Tensor], need_x: bool, need_weight: bool,
+                   use_fp64: bool, dot_input_precision: str, in_offsets: List[int], out_offsets: List[int],
+                   weight_offsets: List[int], m_values: List[int], f_in_values: List[int],
+                   f_out_values: List[int], scale: Tensor) -> Tuple[Tensor, List[Tensor]]:
+    """(grad_x, grad_weights) of linear_fwd, empty (0,) tensors for the unrequested ones."""
+    n, in_end, _, fout = _ref_linear_layout(x, weights, use_fp64, dot_input_precision, in_offsets, out_offsets,
+                                            weight_offsets, m_values, f_in_values, f_out_values)
+    if n == 0 or not (need_x or need_weight):
+        gx = torch.zeros_like(x) if need_x else x.new_empty((0,))
+        gws = [torch.zeros_like(w) for w in weights] if need_weight else [w.new_empty(0) for w in weights]
+        return gx, gws
+    ws = [_lib.contig(f"weight[{l}]", w) for l, w in enumerate(weights[:n])]
+    gx = _ref_grad_x(grad_out, x, ws, n, in_end, fout, f_in_values, scale) if need_x else x.new_empty((0,))
+    if need_weight:
+        gws = _ref_grad_w(grad_out, x, ws, n, in_end, fout, f_in_values, scale)
+        gws = gws + [torch.zeros_like(w) for w in weights[n:]]
+    else:
+        gws = [w.new_empty(0) for w in weights]
+    return gx, gws
+
+
+@linear_bwd_ref.register_fake
+def _(grad_out, x, weights, need_x, need_weight, use_fp64, dot_input_precision, in_offsets, out_offsets,
+      weight_offsets, m_values, f_in_values, f_out_values, scale):
+    gx = torch.empty_like(x) if need_x else x.new_empty((0,))
+    return gx, [torch.empty_like(w) if need_weight else w.new_empty(0) for w in weights]
+
+
+@torch.library.custom_op("flashcart::linear_dbwd", mutates_args=())
+def linear_dbwd_ref(grad_out: Tensor, x: Tensor, weights: List[Tensor], v_grad_x: Tensor,
+                    v_grad_weight: List[Tensor], use_fp64: bool, dot_input_precision: str, need_d_grad_out: bool,
+                    need_d_x: bool, need_d_weight: bool, has_v_grad_x: bool, has_v_grad_weight: bool,
+                    in_offsets: List[int], out_offsets: List[int], weight_offsets: List[int], m_values: List[int],
+                    f_in_values: List[int], f_out_values: List[int],
+                    scale: Tensor) -> Tuple[Tensor, Tensor, List[Tensor]]:
+    """Backward of linear_bwd along cotangents (v_grad_x, v_grad_weight):
+    d grad_out_l = s_l (v_gx_l W_l^T + x_l v_gW_l^T), d x_l = s_l go_l v_gW_l, d W_l = s_l go_l^T v_gx_l."""
+    n, in_end, _, fout = _ref_linear_layout(x, weights, use_fp64, dot_input_precision, in_offsets, out_offsets,
+                                            weight_offsets, m_values, f_in_values, f_out_values)
+    go = _lib.contig("grad_out", grad_out)
+    ws = [_lib.contig(f"weight[{l}]", w) for l, w in enumerate(weights[:n])]
+    vws = [_lib.contig(f"v_grad_weight[{l}]", v) for l, v in enumerate(v_grad_weight[:n])] if has_v_grad_weight \
+        else []
+    out_l_max = int(round((go.shape[1] / max(fout, 1)) ** 0.5)) - 1
+
+    def fwd(inp, mats, residual=None):
+        a = _lib.contig("input", inp)
+        if a.shape[1] != in_end:
+            a = a[:, :in_end].contiguous()
+        out = a.new_empty(a.shape[0], go.shape[1])
+        _lib_call("fc_linear_fwd", _ref_desc(n, out_l_max, fout, f_in_values, mats, scale), a.shape[0],
+                  a.data_ptr(), 1.0, _lib.ptr(residual), out.data_ptr(), _lib.stream_of(a))
+        return out
+
+    if not need_d_grad_out:
+        d_go = go.new_empty((0,))
+    elif n == 0 or not (has_v_grad_x or has_v_grad_weight):
+        d_go = torch.zeros_like(go)
+    else:
+        d_go = fwd(x, vws) if has_v_grad_weight else None
+        if has_v_grad_x:
+            d_go = fwd(v_grad_x, ws, d_go)
+    if not need_d_x:
+        d_x = x.new_empty((0,))
+    elif n == 0 or not has_v_grad_weight:
+        d_x = torch.zeros_like(x)
+    else:
+        d_x = _ref_grad_x(go, x, vws, n, in_end, fout, f_in_values, scale)
+    if not need_d_weight:
+        d_ws = [w.new_empty(0) for w in weights]
+    elif n == 0 or not has_v_grad_x:
+        d_ws = [torch.zeros_like(w) for w in weights]
+    else:
+        d_ws = _ref_grad_w(go, v_grad_x, ws, n, in_end, fout, f_in_values, scale) + \
+            [torch.zeros_like(w) for w in weights[n:]]
+    return d_go, d_x, d_ws
+
+
+@linear_dbwd_ref.register_fake
+def _(grad_out, x, weights, v_grad_x, v_grad_weight, use_fp64, dot_input_precision, need_d_grad_out, need_d_x,
+      need_d_weight, has_v_grad_x, has_v_grad_weight, in_offsets, out_offsets, weight_offsets, m_values,
+      f_in_values, f_out_values, scale):
+    return (torch.empty_like(grad_out) if need_d_grad_out else grad_out.new_empty((0,)),
+            torch.empty_like(x) if need_d_x else x.new_empty((0,)),
+            [torch.empty_like(w) if need_d_weight else w.new_empty(0) for w in weights])
+
+
+_REF_LIN_META = ("in_offsets", "out_offsets", "weight_offsets", "m_values", "f_in_values", "f_out_values")
+
+
+def _linear_ref_setup(ctx, inputs, output):
+    (x, weights, meta, out_size, use_fp64, prec, *lists, scale) = inputs
+    ctx.save_for_backward(x, *weights, scale)
+    ctx.opts = (bool(use_fp64), prec)
+    ctx.lists = [list(v) for v in lists]
+
+
+def _linear_ref_backward(ctx, grad_out):
+    """The reference's linear_bwd (o3/_linear.py:409-455): one linear_bwd op call for the
+    gradients that are needed."""
+    x, *weights, scale = ctx.saved_tensors
+    need_x, need_w = bool(ctx.needs_input_grad[0]), bool(ctx.needs_input_grad[1])
+    if not (need_x or need_w):
+        return (None,) * 13
+    gx, gws = torch.ops.flashcart.linear_bwd(grad_out, x, weights, need_x, need_w, *ctx.opts, *ctx.lists, scale)
+    return (gx if need_x else None, gws if need_w else None) + (None,) * 11
+
+
+def _linear_bwd_ref_setup(ctx, inputs, output):
+    (go, x, weights, need_x, need_w, use_fp64, prec, *lists, scale) = inputs
+    ctx.set_materialize_grads(False)
+    ctx.save_for_backward(go, x, *weights, scale)
+    ctx.need_out = (bool(need_x), bool(need_w))
+    ctx.opts = (bool(use_fp64), prec)
+    ctx.lists = [list(v) for v in lists]
+
+
+def _linear_bwd_ref_backward(ctx, v_gx, v_gws):
+    """The reference's linear_dbwd autograd (o3/_linear.py:700-760)."""
+    go, x, *weights, scale = ctx.saved_tensors
+    need = ctx.needs_input_grad
+    nd_go, nd_x, nd_w = bool(need[0]), bool(need[1]), bool(need[2])
+    if not (nd_go or nd_x or nd_w):
+        return (None,) * 14
+    has_gx = v_gx is not None and v_gx.numel() != 0 and ctx.need_out[0]
+    has_gw = v_gws is not None and any(v is not None and v.numel() != 0 for v in v_gws) and ctx.need_out[1]
+    vgx = v_gx if has_gx else x.new_empty((0,))
+    vgw = [(v if v is not None and v.numel() != 0 else torch.zeros_like(w)) for v, w in zip(v_gws, weights)] \
+        if has_gw else [w.new_empty(0) for w in weights]
+    d_go, d_x, d_ws = torch.ops.flashcart.linear_dbwd(go, x, weights, vgx, vgw, *ctx.opts, nd_go, nd_x, nd_w,
+                                                        has_gx, has_gw, *ctx.lists, scale)
+    return (d_go if nd_go else None, d_x if nd_x else None, d_ws if nd_w else None) + (None,) * 11
+
+
+linear_fwd_ref.register_autograd(_linear_ref_backward, setup_context=_linear_ref_setup)
+linear_bwd_ref.register_autograd(_linear_bwd_ref_backward, setup_context=_linear_bwd_ref_setup)
 
 
 # ---------------------------------------------------------------------------

@@ -179,11 +179,13 @@ def _irreps_bwd_setup(ctx, inputs, output):
 
 
 def _irreps_dbwd(ctx, c):
-    """Backward of irreps_bwd (reference irreps_dbwd, src/flashcart/o3/_irreps.py:146-199)."""
+    """Backward of irreps_bwd: the irreps_dbwd op (reference src/flashcart/o3/_irreps.py:146-199)."""
     g, x = ctx.saved_tensors
     need = ctx.needs_input_grad
-    gp, gg = M.vjp_of_vjp(lambda xx: M.expansion(xx, ctx.l_max), [x], [0], [g], [c], [need[1]], [need[0]])
-    return gg[0], gp[0], None
+    if c is None or not (need[0] or need[1]):
+        return None, None, None
+    d_g, d_x = _ops.irreps_dbwd(g, x, c, ctx.l_max)
+    return (d_g if need[0] else None), (d_x if need[1] else None), None
 
 
 _ops._register_autograd(_ops.irreps_bwd, _irreps_dbwd, _irreps_bwd_setup)

@@ -48,6 +48,12 @@ const char* fc_status_string(int status);
 int fc_irreps_fwd(int64_t n, int32_t l_max, const float* x, float* out, void* stream);
 int fc_irreps_bwd(int64_t n, int32_t l_max, const float* grad_out, const float* x, float* grad_x,
                   void* stream);
+/* Backward of fc_irreps_bwd along a cotangent v (n, 3) of grad_x: replaces
+ * torch.ops.flashcart.irreps_dbwd (reference src/flashcart/o3/_irreps.py:146-199; kernel
+ * _codegen_irreps.py irreps_dbwd). d_grad_out (n, (l_max+1)^2) = J(x) v, d_x (n, 3) =
+ * sum_a grad_out_a H_a(x) v; either output may be NULL. */
+int fc_irreps_dbwd(int64_t n, int32_t l_max, const float* grad_out, const float* x, const float* v,
+                   float* d_grad_out, float* d_x, void* stream);
 
 /* ------------------------------------------------------------------------- */
 /* Radial basis and cutoff envelope: replaces ChebyshevBasis.forward,          */

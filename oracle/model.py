@@ -60,12 +60,36 @@ def rms_norm(sd, prefix, x, l_max, C, eps=1e-6):
     return scaled * g
 
 
+def _conv_chunked(sd, prefix, cfg, h, edge_attrs, mlp_in, idx_i, idx_j, lin, L, lout, C, chunk):
+    """Radial MLP + convolution TP over ranges of ``chunk`` receivers (edges sorted by receiver),
+    each under torch.utils.checkpoint: same sums as the one-shot form, but the per-edge weights
+    and path outputs of one range at a time (recomputed for the backward)."""
+    from torch.utils.checkpoint import checkpoint
+
+    rows = h.shape[0]
+    n_mlp = len(cfg.get("hidden_radial", [64, 64])) + 1
+    bounds = torch.searchsorted(idx_i, torch.arange(0, rows + chunk, chunk).clamp_max(rows)).tolist()
+
+    def part(h_, attrs_c, mlp_c, ii, jj, n_out):
+        w = _mlp(sd, f"{prefix}.radial_mlp", mlp_c, n_mlp)
+        return O.tensor_product(h_, attrs_c, w, ii, jj, lin, L, lout, C, 1, out_rows=n_out)
+
+    outs = []
+    for k, a in enumerate(range(0, rows, chunk)):
+        e0, e1 = bounds[k], bounds[k + 1]
+        n_out = min(rows, a + chunk) - a
+        outs.append(checkpoint(part, h, edge_attrs[e0:e1], mlp_in[e0:e1], idx_i[e0:e1] - a, idx_j[e0:e1], n_out,
+                               use_reentrant=False))
+    return torch.cat(outs, dim=0)
+
+
 def interaction(sd, prefix, cfg, lin, lout, node_feats, edge_attrs, edge_feats, envelope, edge_index,
-                atom_types=None):
+                atom_types=None, chunk=None):
     """InteractionLayer.forward (src/flashcart/nn/layers.py:310-379): linear_first, radial MLP on the
     envelope-scaled radial features (with the sender/receiver element embeddings appended when the
     layer is element-conditioned, :346-350), conv TP, / sqrt(avg_neighbors), linear_second, skip
-    projection (rank-0 slice add when lin == 0, :370-375), RMS norm."""
+    projection (rank-0 slice add when lin == 0, :370-375), RMS norm. ``chunk``: evaluate the radial
+    MLP and the convolution per range of that many receivers (large graphs)."""
     C = cfg["n_hidden_feats"]
     L = cfg["l_max_edge_attrs"]
     out_paths, P = _paths(lin, L, lout)
@@ -80,8 +104,11 @@ def interaction(sd, prefix, cfg, lin, lout, node_feats, edge_attrs, edge_feats, 
     else:
         mlp_in = edge_feats * envelope.unsqueeze(-1)
     h = _o3_linear(sd, f"{prefix}.linear_first", node_feats, lin, lin, C, C)
-    w = _mlp(sd, f"{prefix}.radial_mlp", mlp_in, len(cfg.get("hidden_radial", [64, 64])) + 1)
-    agg = O.tensor_product(h, edge_attrs, w, idx_i, idx_j, lin, L, lout, C, 1)
+    if chunk:
+        agg = _conv_chunked(sd, prefix, cfg, h, edge_attrs, mlp_in, idx_i, idx_j, lin, L, lout, C, chunk)
+    else:
+        w = _mlp(sd, f"{prefix}.radial_mlp", mlp_in, len(cfg.get("hidden_radial", [64, 64])) + 1)
+        agg = O.tensor_product(h, edge_attrs, w, idx_i, idx_j, lin, L, lout, C, 1)
     agg = agg / sd[f"{prefix}.sqrt_avg_neighbors"].to(agg.dtype)
     out = _o3_linear(sd, f"{prefix}.linear_second", agg, lout, lout, C, C, out_paths)
     if lin == 0:
@@ -171,7 +198,8 @@ def readout(sd, prefix, cfg, outs):
     return _mlp(sd, f"{prefix}.readout_mlp", x, len(cfg.get("hidden_readout", [64, 64])) + 1).squeeze(-1)
 
 
-def node_energies(sd: Dict[str, torch.Tensor], cfg: Dict[str, Any], graph: Dict[str, Any]) -> torch.Tensor:
+def node_energies(sd: Dict[str, torch.Tensor], cfg: Dict[str, Any], graph: Dict[str, Any],
+                  chunk: Optional[int] = None) -> torch.Tensor:
     """FlashCartPotential.forward (src/flashcart/model/flashcart.py:249-317; ranks of each layer
     from :155-162): interaction in ranks [0, Lh, ...], interaction out L (or the product out ranks
     when correlation is 1), gate at the interaction's out rank, product out [Lh, ..., 0], readout on
@@ -199,7 +227,7 @@ def node_energies(sd: Dict[str, torch.Tensor], cfg: Dict[str, Any], graph: Dict[
     outs = []
     for k in range(n_int):
         y = interaction(sd, f"interactions.{k}", cfg, 0 if k == 0 else Lh, int_out[k], x, attrs, feats, env, ei,
-                        atom_types=types)
+                        atom_types=types, chunk=chunk)
         if cfg.get("nonlinearity", False):
             y = gated(sd, f"nonlinearities.{k}", cfg, y, int_out[k])
         if use_products:
@@ -212,7 +240,8 @@ def node_energies(sd: Dict[str, torch.Tensor], cfg: Dict[str, Any], graph: Dict[
 
 
 def predict(sd: Dict[str, torch.Tensor], cfg: Dict[str, Any], graph: Dict[str, Any], compute_forces: bool = True,
-            dtype: torch.dtype = torch.float64, compute_stress: bool = False) -> Dict[str, torch.Tensor]:
+            dtype: torch.dtype = torch.float64, compute_stress: bool = False,
+            chunk: Optional[int] = None) -> Dict[str, torch.Tensor]:
     """Energies (per structure and per atom), forces and optionally stress, on CPU in ``dtype``.
 
     Stress follows src/flashcart/model/atomistic.py:200-210,290-302: positions and cell
@@ -233,7 +262,7 @@ def predict(sd: Dict[str, torch.Tensor], cfg: Dict[str, Any], graph: Dict[str, A
     else:
         g["positions"] = pos
         g["cell"] = cell
-    e_node = node_energies(sd, cfg, g)
+    e_node = node_energies(sd, cfg, g, chunk=chunk)
     n_graphs = int(g["n_atoms"].shape[0])
     energy = O.scatter_sum(e_node, g["batch"], n_graphs)
     out = {"node_energies": e_node.detach(), "energy": energy.detach()}

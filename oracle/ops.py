@@ -120,8 +120,9 @@ def _path_tensor_t(l1, l2, lo, dtype):
 
 
 def tensor_product(in1, in2, weights, idx_i, idx_j, in1_l_max, in2_l_max, out_l_max, in1_features,
-                   in2_features, symmetric_product=False, shared_weights=False, reduce_paths=False):
-    rows = in1.shape[0]
+                   in2_features, symmetric_product=False, shared_weights=False, reduce_paths=False, out_rows=None):
+    """``out_rows``: rows of a convolution's output (default: the rows of in1)."""
+    rows = in1.shape[0] if out_rows is None else out_rows
     conv = idx_i is not None and idx_j is not None
     if conv:
         in1 = in1.index_select(0, idx_j)

@@ -110,8 +110,10 @@ def test_silu_gate_correlation2(frozen, monkeypatch):
 @pytest.mark.parametrize("frozen", [False, True])
 def test_predict_replay(frozen):
     """predict(use_compile=True) captures the whole prediction as a HIP graph: replays with
-    new positions (and eager work and synchronisations in between) must match eager
-    predictions on the same inputs, energies, forces and stress alike."""
+    new positions (and eager work and synchronisations in between) must match the oracle on
+    the same inputs (energies, forces and stress at the north-star bars) and the eager
+    prediction. avg_neighbors changed between replays (set_avg_neighbors, and an in-place
+    copy into the buffer as the reference's broadcast_pre_fit_state does) must reach the replay."""
     numbers, pos, cell, pbc = water_box(12, seed=4)
     cfg = model_config(["H", "O"], 16, 2, avg_neighbors=20.0)
     g = AtomicGraph.from_arrays(numbers, pos, cfg["elements"], 5.0, cell=cell, pbc=pbc).to(DEV)
@@ -119,17 +121,28 @@ def test_predict_replay(frozen):
     m.requires_grad_(not frozen)
     gen = torch.Generator(device="cpu").manual_seed(0)
     base = g.positions.clone()
-    for it in range(5):
+    for it in range(6):
         g.positions = base + 0.02 * torch.randn(base.shape, generator=gen).to(DEV)
         if it == 2:  # a new edge-list tensor: the CSR graph replays
             g.edge_index = g.edge_index.clone()
         if it == 3:  # modified in place (same contents): replays as well
             g.edge_index.add_(0)
+            m.interactions[0].set_avg_neighbors(12.5)
+        if it == 5:
+            with torch.no_grad():
+                m.interactions[1].sqrt_avg_neighbors.copy_(torch.tensor(31.0 ** 0.5))
         got = m.predict(g, compute_forces=True, compute_stress=True, use_compile=True)
         junk = torch.randn(1000, 1000, device=DEV) @ torch.randn(1000, 1000, device=DEV)  # eager work between
         torch.cuda.synchronize()
-        ref = m.predict(g, compute_forces=True, compute_stress=True)
+        eager = m.predict(g, compute_forces=True, compute_stress=True)
         del junk
         for k in ("energy", "forces", "stress", "node_energies"):
-            assert_close(got[k], ref[k].double(), 1e-6, 1e-6 * (float(ref[k].abs().max()) + 1.0), f"replay {it} {k}")
-    assert len(m._replay_cache) == 1
+            assert_close(got[k], eager[k].double(), 1e-6, 1e-6 * (float(eager[k].abs().max()) + 1.0),
+                         f"replay {it} {k} vs eager")
+        ref = OM.predict(m.state_dict(), m.to_model_config(), g.to("cpu").to_dict(), compute_forces=True,
+                         compute_stress=True)
+        assert_close(got["energy"], ref["energy"], E_REL, 1e-6, f"replay {it} energy vs oracle")
+        assert_close(got["forces"], ref["forces"], 0.0, F_ABS, f"replay {it} forces vs oracle")
+        assert_close(got["stress"], ref["stress"], 1e-5, 1e-5 * float(ref["stress"].abs().max()),
+                     f"replay {it} stress vs oracle")
+    assert len(m._replay_cache) == 3  # one capture per avg_neighbors state

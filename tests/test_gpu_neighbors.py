@@ -11,12 +11,15 @@ import torch
 
 from flashcart_amd.data.neighbors import NeighborList, neighbor_pairs, neighbor_pairs_device
 from flashcart_amd.data.synthetic import fcc_alloy, molecules, water_box
+from oracle.neighbors import brute_force_pairs
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
 def _same(pos, cell, pbc, cutoff, what):
+    """Device list == host list, and on systems small enough for it == the brute-force oracle
+    (the edge-set contract of the reference, in canonical (i, j, S) order)."""
     ei_h, sh_h = neighbor_pairs(pos, cell, pbc, cutoff)
     ei_d, sh_d = neighbor_pairs_device(torch.as_tensor(np.asarray(pos, dtype=np.float64), device=DEV), cell, pbc,
                                        cutoff)
@@ -24,6 +27,11 @@ def _same(pos, cell, pbc, cutoff, what):
     assert ei_d.shape == (2, ei_h.shape[1]), f"{what}: {ei_d.shape[1]} pairs on the device, {ei_h.shape[1]} on the host"
     assert np.array_equal(ei_d.cpu().numpy(), ei_h), f"{what}: edge_index differs"
     assert np.array_equal(sh_d.cpu().numpy(), sh_h), f"{what}: shifts differ"
+    if len(pos) <= 2000 and np.any(pbc) and abs(np.linalg.det(np.asarray(cell, dtype=float))) > 1e-7 \
+            or not np.any(pbc):
+        got = [tuple(int(v) for v in row) for row in
+               np.concatenate([ei_d.cpu().numpy().T, sh_d.cpu().numpy().astype(np.int64)], axis=1)]
+        assert got == brute_force_pairs(pos, cell, pbc, cutoff), f"{what}: differs from the brute-force oracle"
     return ei_h.shape[1]
 
 
@@ -80,6 +88,14 @@ def test_cfg4_size():
     z, pos, cell, pbc = fcc_alloy(25, 25, 10, a=3.6, jitter=0.05, seed=0)
     n_pairs = _same(pos, cell, pbc, 6.0, "fcc 25k, r_max + skin")
     assert n_pairs > 25_000 * 70
+
+
+def test_dense_atoms_fall_back_to_the_host_list():
+    """More than 1,024 pairs per atom (fcc within 15 A: about 1,200): the device list reports
+    its size limit and neighbor_pairs_device returns the host list's pairs instead."""
+    z, pos, cell, pbc = fcc_alloy(9, 9, 9, seed=8)
+    n = _same(pos, cell, pbc, 15.0, "fcc, 15 A cutoff")
+    assert n > 1100 * len(pos)
 
 
 def test_empty_and_single_atom():

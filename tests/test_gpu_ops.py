@@ -21,6 +21,12 @@ def _ops():
     return _ops
 
 
+def _close(got, want, what, rel=2e-5):
+    """float32 GPU result against a float64 reference, relative to the reference's largest entry."""
+    want = want.detach().double().cpu()
+    assert_close(got, want, rel, rel * max(float(want.abs().max()) if want.numel() else 0.0, 1e-30), what)
+
+
 @pytest.mark.parametrize("l_max", [0, 1, 2, 3])
 def test_irreps_fwd_bwd(l_max):
     ops = _ops()
@@ -425,3 +431,74 @@ def test_dense_wgrad(n, k, m, act, bias):
         assert_close(gb, wb, 0.0, 2e-5 * float(wb.abs().max()), "dense bias grad")
     else:
         assert gb is None
+
+
+@pytest.mark.parametrize("lin,lout,fin,fout,in_paths", [(3, 3, 16, 16, [3, 5, 5, 4]), (3, 1, 8, 12, None),
+                                                        (1, 3, 8, 8, None), (2, 0, 4, 8, [2, 3, 1])])
+def test_reference_linear_ops(lin, lout, fin, fout, in_paths):
+    """torch.ops.flashcart.linear_fwd / linear_bwd / linear_dbwd called with the reference's
+    arguments (metadata, scale tensor and lists of o3.LinearLayer, as its triton_linear passes
+    them, src/flashcart/o3/_linear.py:860-897) against the oracle: outputs, both gradients of
+    linear_bwd, and the second derivatives reached through the registered autograd chain."""
+    from flashcart_amd import o3
+    import flashcart_amd.o3._second_order  # noqa: F401
+
+    torch.manual_seed(3)
+    lay = o3.LinearLayer(lin, lout, fin, fout, in_paths=in_paths).to(DEV)
+    n = 37
+    x = torch.randn(n, lay.in_dim, device=DEV, dtype=torch.float32)
+    ws = [w.detach().clone() for w in lay.weight]
+    args = (lay.meta, lay.out_dim, False, "ieee", *lay.meta_lists, lay.scale)
+    out = torch.ops.flashcart.linear_fwd(x, ws, *args)
+    xd = x.double().cpu().requires_grad_()
+    wd = [w.double().cpu().requires_grad_() for w in ws]
+    ref = O.linear(xd, wd, lin, lout, fin, fout, in_paths)
+    _close(out, ref, "linear_fwd")
+    go = torch.randn(n, lay.out_dim, device=DEV)
+    gx, gws = torch.ops.flashcart.linear_bwd(go, x, ws, True, True, False, "ieee", *lay.meta_lists, lay.scale)
+    rgx, *rgw = torch.autograd.grad(ref, [xd] + wd, go.double().cpu(), create_graph=True)
+    _close(gx, rgx, "linear_bwd grad_x")
+    for l, (a, b) in enumerate(zip(gws, rgw)):
+        _close(a, b, f"linear_bwd grad_weight[{l}]")
+    # second order through the registered autograd (linear_fwd -> linear_bwd -> linear_dbwd)
+    xa = x.clone().requires_grad_()
+    wa = [w.clone().requires_grad_() for w in ws]
+    goa = go.clone().requires_grad_()
+    o = torch.ops.flashcart.linear_fwd(xa, wa, *args)
+    g1 = torch.autograd.grad(o, [xa] + wa, goa, create_graph=True)
+    cots = [torch.randn_like(t) for t in g1]
+    s2 = sum((a * c).sum() for a, c in zip(g1, cots))
+    got2 = torch.autograd.grad(s2, [goa, xa] + wa, allow_unused=True)
+    god = go.double().cpu().requires_grad_()
+    rg1 = torch.autograd.grad(O.linear(xd, wd, lin, lout, fin, fout, in_paths), [xd] + wd, god, create_graph=True)
+    rs2 = sum((a * c.double().cpu()).sum() for a, c in zip(rg1, cots))
+    want2 = torch.autograd.grad(rs2, [god, xd] + wd, allow_unused=True)
+    for k, (a, b) in enumerate(zip(got2, want2)):
+        b = torch.zeros_like(a).double().cpu() if b is None else b
+        _close(torch.zeros_like(b) if a is None else a, b, f"linear_dbwd input {k}")
+    with pytest.raises(NotImplementedError):
+        torch.ops.flashcart.linear_fwd(x, ws, lay.meta, lay.out_dim, True, "ieee", *lay.meta_lists, lay.scale)
+    with pytest.raises(ValueError, match="dot_input_precision"):
+        torch.ops.flashcart.linear_fwd(x, ws, lay.meta, lay.out_dim, False, "bf16", *lay.meta_lists, lay.scale)
+
+
+def test_irreps_dbwd_op():
+    """torch.ops.flashcart.irreps_dbwd (the Eq. (1) expansion's second derivative on the GPU)
+    against double autograd of the oracle's expansion, l_max 0..3."""
+    from tests.helpers import unit_vectors
+    import flashcart_amd.o3._second_order  # noqa: F401
+
+    for l_max in range(4):
+        u = unit_vectors(300, seed=l_max)
+        g = torch.randn(300, (l_max + 1) ** 2, dtype=torch.float64)
+        v = torch.randn(300, 3, dtype=torch.float64)
+        d_g, d_x = torch.ops.flashcart.irreps_dbwd(g.float().to(DEV), u.float().to(DEV), v.float().to(DEV), l_max)
+        if l_max == 0:  # the expansion is the constant 1: both derivatives vanish
+            assert float(d_g.abs().max()) == 0.0 and float(d_x.abs().max()) == 0.0
+            continue
+        ud = u.clone().requires_grad_()
+        gd = g.clone().requires_grad_()
+        (gx,) = torch.autograd.grad(O.irreps(ud, l_max), ud, gd, create_graph=True)
+        want_g, want_x = torch.autograd.grad((gx * v).sum(), [gd, ud], allow_unused=True)
+        _close(d_g, want_g, f"irreps_dbwd d_grad_output l={l_max}")
+        _close(d_x, torch.zeros_like(ud) if want_x is None else want_x, f"irreps_dbwd d_x l={l_max}")

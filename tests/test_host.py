@@ -203,3 +203,38 @@ def test_checkpoint_round_trip(tmp_path):
     for (k, a), (k2, b) in zip(m.state_dict().items(), m2.state_dict().items()):
         assert k == k2 and torch.equal(a, b)
     assert m2.interactions[0]._sqrt_avg == m.interactions[0]._sqrt_avg
+
+
+def test_device_neighbor_list_host_fallback_decision():
+    """Only the device list's size limit (-FC_ERR_SHAPE: > 1024 pairs for one atom or a shift
+    component >= 512) sends the build to the host list; other failures stay errors."""
+    from flashcart_amd.data.neighbors import host_fallback_needed
+
+    assert host_fallback_needed(-4)
+    assert not any(host_fallback_needed(s) for s in (0, 17, -1, -3, -5, -6, -7))
+
+
+def test_linear_and_irreps_op_schemas_follow_reference():
+    """torch.ops.flashcart.linear_fwd / linear_bwd / linear_dbwd / irreps_dbwd take the
+    reference's positional arguments (src/flashcart/o3/_linear.py:328-343, :457-472, :571-591;
+    src/flashcart/o3/_irreps.py:153-159) and return its outputs."""
+    import flashcart_amd.o3._second_order  # noqa: F401  (registers the double backward)
+
+    lists = ["in_offsets", "out_offsets", "weight_offsets", "m_values", "f_in_values", "f_out_values"]
+    want = {
+        "linear_fwd": ["x", "weights", "meta", "out_size", "use_fp64", "dot_input_precision"] + lists + ["scale"],
+        "linear_bwd": ["grad_out", "x", "weights", "need_x", "need_weight", "use_fp64",
+                       "dot_input_precision"] + lists + ["scale"],
+        "linear_dbwd": ["grad_out", "x", "weights", "v_grad_x", "v_grad_weight", "use_fp64", "dot_input_precision",
+                        "need_d_grad_out", "need_d_x", "need_d_weight", "has_v_grad_x",
+                        "has_v_grad_weight"] + lists + ["scale"],
+        "irreps_dbwd": ["grad_output", "x", "v", "l_max"],
+    }
+    n_out = {"linear_fwd": 1, "linear_bwd": 2, "linear_dbwd": 3, "irreps_dbwd": 2}
+    for name, ref in want.items():
+        schema = getattr(torch.ops.flashcart, name).default._schema
+        assert [a.name for a in schema.arguments] == ref, name
+        assert len(schema.returns) == n_out[name], name
+    # the build's own residual / alpha variants live under names of their own
+    assert [a.name for a in torch.ops.flashcart.equiv_linear_fwd.default._schema.arguments][-2:] == ["alpha",
+                                                                                                      "residual"]
