@@ -50,14 +50,77 @@ from flashcart_amd.data.synthetic import StepGraphs  # noqa: E402
 from flashcart_amd.data.synthetic import fcc25k_model as build_model  # noqa: E402
 from flashcart_amd.data.synthetic import fcc25k_system as make_system  # noqa: E402
 
+# The counter runs' graph (the first step graph: N = 25,000, E = 1,080,166) and the compulsory
+# bytes of the layer-1 convolution on it (d1 = 9, d2 = 16, P = 17, C = 128, 71 output rows).
+TRAFFIC_E = 1080166
+
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
 def tp_conv_bytes(n_nodes, n_send, E, d1, d2, P, C, nout):
-    """Compulsory HBM bytes of one convolution TP forward launch (fp32, int32 indices)."""
+    """Compulsory HBM bytes of one convolution TP forward (fp32, int32 indices): in1 rows, edge
+    attributes, per-edge weights and the receiver outputs once each, the sender index and rowptr."""
     return 4 * (n_send * d1 * C + E * d2 + E * P * C + n_nodes * nout * C) + 4 * E + 4 * (n_nodes + 1)
+
+
+def tp_conv_bwd_bytes(n_nodes, E, d1, d2, P, C, nout):
+    """Compulsory HBM bytes of one convolution TP backward with all three gradients (the
+    per-edge formula of the hot-path survey's measurement table,
+    4 (N o C + 2 N d1 C + 2 E d2 + 2 E P C) + 8 E + 4 (N + 1)): the output gradient read once,
+    in1 read and its gradient written, edge attributes read and their gradient written, weights
+    read and their gradient written, two index arrays and rowptr. Per-edge sender messages or any
+    other intermediate of an implementation are not counted."""
+    return 4 * (n_nodes * nout * C + 2 * n_nodes * d1 * C + 2 * E * d2 + 2 * E * P * C) + 8 * E + 4 * (n_nodes + 1)
+
+
+TRAFFIC_ALG_FWD = tp_conv_bytes(25000, 25000, TRAFFIC_E, 9, 16, 17, 128, 71)
+TRAFFIC_ALG_BWD = tp_conv_bwd_bytes(25000, TRAFFIC_E, 9, 16, 17, 128, 71)
+
+
+def device_time_ms(fn, reps, dev, warmup=3):
+    """Average device time of ``fn`` replayed from a captured HIP graph: HIP events on the
+    stream the replays run on bracket ``reps`` replays (no host launch overhead inside)."""
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        for _ in range(warmup):
+            fn()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    graph.replay()
+    torch.cuda.synchronize(dev)
+    stream = torch.cuda.current_stream(dev)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(reps):
+        graph.replay()
+    ev1.record(stream)
+    torch.cuda.synchronize(dev)
+    return ev0.elapsed_time(ev1) / reps
+
+
+def calibration_kernels(dev, reps):
+    """Two kernels of known HBM bytes for scaling the FETCH_SIZE / WRITE_SIZE counters: a
+    streaming copy (2 GiB read, 2 GiB written) and a row gather by a random permutation
+    (index_select of 2^22 rows of 512 B: 2 GiB of rows + 32 MiB of int64 indices read,
+    2 GiB written), the access pattern of the convolution's in1 rows."""
+    src = torch.ones(2 ** 29, device=dev)  # 2 GiB
+    dst = torch.empty_like(src)
+    rows = src.view(2 ** 22, 128)
+    perm = torch.randperm(2 ** 22, device=dev)
+    out = torch.empty_like(rows)
+    for _ in range(reps):
+        torch.mul(src, 1.0, out=dst)
+    for _ in range(reps):
+        torch.index_select(rows, 0, perm, out=out)
+    torch.cuda.synchronize(dev)
+    return {"copy_bytes_each_way": src.numel() * 4, "gather_bytes_read": src.numel() * 4 + perm.numel() * 8,
+            "gather_bytes_written": src.numel() * 4}
 
 
 def measure_dominant(model, graph, dev, reps=10, with_backward=False):
@@ -94,7 +157,8 @@ def measure_dominant(model, graph, dev, reps=10, with_backward=False):
     if not with_backward:
         return ms, byts
     # The backward op as the energy+forces step runs it (gradients for in1, in2 and the
-    # weights): tp_bwd_kernel, then the sender-ordered segmented sum of the per-edge messages.
+    # weights): the backward kernel, then the sender-ordered segmented sum of the per-edge
+    # messages; achieved bandwidth on the compulsory bytes of the three gradients.
     go = torch.randn(n, tp.out_dim, device=dev, generator=g)
     bargs = (go,) + args[:17] + (False, True, True, True) + args[18:]
     for _ in range(2):
@@ -106,34 +170,32 @@ def measure_dominant(model, graph, dev, reps=10, with_backward=False):
     ev1.record(stream)
     torch.cuda.synchronize(dev)
     ms_b = ev0.elapsed_time(ev1) / reps
-    # tp_bwd_kernel: the forward's reads plus the weight gradient, the per-edge sender messages
-    # and the edge-attribute gradient written; segment_rows_kernel: messages read, in1 gradient written
-    kern = byts + 4 * (E * P * C + E * d1 * C + E * d2)
-    seg = 4 * (E * d1 * C + n * d1 * C) + 4 * E + 4 * (n + 1)
-    return ms, byts, ms_b, kern + seg
+    return ms, byts, ms_b, tp_conv_bwd_bytes(n, E, d1, d2, P, C, nout)
 
 
-def cpu_baseline(model, cfg, avg_neighbors, budget_s=20.0):
-    """Oracle (CPU PyTorch restatement of the reference path), float32, on a 256-atom sample."""
+def cpu_baseline(model, cfg, avg_neighbors, budget_s=20.0, cells=(8, 8, 8)):
+    """Oracle (CPU PyTorch restatement of the reference path), float32, on a bounded sample of the
+    same system: fcc 8x8x8 cells = 2,048 atoms of the same model, at least 3 calls after 1 warmup."""
     from flashcart_amd.data.graph import AtomicGraph
     from oracle import model as OM
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    numbers, pos, cell, pbc = make_system(4, 4, 4, seed=5)
+    numbers, pos, cell, pbc = make_system(*cells, seed=5)
     g = AtomicGraph.from_arrays(numbers, pos, cfg["elements"], R_MAX, cell=cell, pbc=pbc)
     sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
     mcfg = model.to_model_config()
     gd = g.to_dict()
-    OM.predict(sd, mcfg, gd, dtype=torch.float32)  # warmup
+    OM.predict(sd, mcfg, gd, dtype=torch.float32, chunk=512)  # warmup
     t0 = time.perf_counter()
     calls = 0
     while calls < 3 or (time.perf_counter() - t0 < budget_s and calls < 50):
-        OM.predict(sd, mcfg, gd, dtype=torch.float32)
+        OM.predict(sd, mcfg, gd, dtype=torch.float32, chunk=512)
         calls += 1
     dt = time.perf_counter() - t0
     n = len(numbers)
     return {"value": n * calls / dt, "unit": "atom-steps/s", "cores": cores, "kind": "port",
-            "sample": f"oracle (CPU PyTorch restatement of the reference path), float32, fcc 4x4x4 = {n} atoms, "
+            "sample": f"oracle (CPU PyTorch restatement of the reference path), float32, fcc {cells[0]}x{cells[1]}x"
+                      f"{cells[2]} = {n} atoms, "
                       f"{int(g.edge_index.shape[1])} edges, same model config and weights, {calls} calls after "
                       f"1 warmup, {dt:.1f} s, torch threads = {cores}"}
 
@@ -164,15 +226,38 @@ def _oracle_rate(sd, mcfg, gd, n_atoms, budget_s=20.0):
     return n_atoms * calls / dt, cores, calls, dt
 
 
-def run_other_workload(name, args, dev):
-    """Throughput of the other BASELINE configurations (parity-tested in tests/test_gpu_configs.py).
-    Prints one JSON line per call; the default invocation measures the 25k-atom configuration."""
+CONFIG_LINES = ("cfg1_tp_standalone", "cfg2_expansion_radial", "cfg3_water_1536", "cfg5_molecules_512")
+
+
+def _cpu_rate(fn, units, budget_s=8.0):
+    """Units per second of ``fn`` on the host cores (1 warmup, then calls within ``budget_s``)."""
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    fn()
+    calls, t0 = 0, time.perf_counter()
+    while calls < 3 or (time.perf_counter() - t0 < budget_s and calls < 200):
+        fn()
+        calls += 1
+    dt = time.perf_counter() - t0
+    return units * calls / dt, cores, calls, dt
+
+
+def config_line(name, dev, steps, warmup, cpu):
+    """One BASELINE configuration other than the metric's: throughput from device time (HIP
+    events around HIP-graph replays, so that host launch work is not counted), the roofline
+    fraction of its tensor-product work on the compulsory bytes, and (``cpu``) the oracle on
+    the host cores on the same inputs or a stated sample."""
     from flashcart_amd import o3
     from flashcart_amd.data import AtomicGraph, batch_graphs
     from flashcart_amd.data.synthetic import model_config, molecules, water_box
-    res = {"workload": name, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "dtype": "f32",
-           "data": "synthetic (seeded)"}
+    from flashcart_amd.o3 import _ops
+    from flashcart_amd.o3._graph import build_graph
+    from oracle import ops as O
+    res = {"workload": name}
     if name == "cfg1_tp_standalone":
+        # TensorProduct(2, 2, 2, 32, 1), conv mode: 512 receivers x 8 sorted in-edges, E = 4096;
+        # forward and the gradients of both inputs (the weight gradient is formed as well, so the
+        # compulsory-byte formula of the forward + full backward applies unchanged)
         rng = np.random.default_rng(0)
         n_recv, E, C = 512, 4096, 32
         ii = np.repeat(np.arange(n_recv), 8)
@@ -181,47 +266,141 @@ def run_other_workload(name, args, dev):
         tp = o3.TensorProduct(2, 2, 2, C, 1)
         v = rng.standard_normal((E, 3))
         v = torch.as_tensor(v / np.linalg.norm(v, axis=1, keepdims=True), dtype=torch.float32, device=dev)
-        in2 = o3.Irreps(2).forward_normalized(v).requires_grad_(True)
-        in1 = torch.randn(n_recv, 9 * C, device=dev, requires_grad=True)
-        w = torch.randn(E, tp.n_total_paths * C, device=dev)
-        go = torch.randn(n_recv, tp.out_dim, device=dev)
-        idx_i = torch.as_tensor(ii, device=dev)
-        idx_j = torch.as_tensor(jj, device=dev)
-        from flashcart_amd.o3._graph import build_graph
-        graph = build_graph(torch.stack([idx_i, idx_j]), n_recv)
+        in2 = o3.Irreps(2).forward_normalized(v)
+        gen = torch.Generator(device=dev).manual_seed(0)
+        in1 = torch.randn(n_recv, 9 * C, device=dev, generator=gen)
+        w = torch.randn(E, tp.n_total_paths * C, device=dev, generator=gen)
+        go = torch.randn(n_recv, tp.out_dim, device=dev, generator=gen)
+        ei = torch.stack([torch.as_tensor(ii, device=dev), torch.as_tensor(jj, device=dev)])
+        csr = build_graph(ei, n_recv)
+        args = (in1, in2, w, csr.idx_i, csr.idx_j, 2, 2, 2, C, 1, False, False, *tp.op_meta, False, csr.rowptr,
+                csr.sender_perm, csr.sender_ptr, 1.0)
 
         def step():
-            out = tp(in1, in2, w, graph=graph)
-            return torch.autograd.grad(out, [in1, in2], go)
-        dt, _ = _timed(step, args.steps, args.warmup, dev)
-        fwd = 4 * (n_recv * 288 + E * 9 + E * 352 + n_recv * 1120) + 4 * E + 4 * (n_recv + 1)
-        bwd = 4 * (n_recv * 1120 + 2 * n_recv * 288 + 2 * E * 9 + 2 * E * 352) + 8 * E + 4 * (n_recv + 1)
-        ms = 1e3 * dt / args.steps
-        res.update({"metric": "TP forward + input gradients per second (E=4096, 2x2->2, C=32)",
-                    "value": args.steps / dt, "unit": "calls/s", "ms_per_step": ms,
-                    "roofline": {"bound": "hbm (launch-bound at this size)", "algorithmic_bytes": fwd + bwd,
-                                 "achieved": (fwd + bwd) / (ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s"}})
+            _ops.tp_fwd(*args)
+            return _ops.tp_bwd(go, *args[:17], False, True, True, True, *args[18:])
+        ms = device_time_ms(step, steps, dev)
+        fwd = tp_conv_bytes(n_recv, n_recv, E, 9, 9, tp.n_total_paths, C, tp.out_dim // C)
+        bwd = tp_conv_bwd_bytes(n_recv, E, 9, 9, tp.n_total_paths, C, tp.out_dim // C)
+        res.update({"metric": "TP forward + gradients per second (E=4096, 2x2->2, C=32, conv)", "value": 1e3 / ms,
+                    "unit": "calls/s", "ms_per_step": ms,
+                    "roofline": {"bound": "hbm", "kernel": "tp_fwd + tp_bwd (conv, one call each)",
+                                 "algorithmic_bytes": fwd + bwd, "achieved": (fwd + bwd) / (ms * 1e-3) / 1e9,
+                                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                 "frac": (fwd + bwd) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                 "note": "24 MB per call: bound by launch and tail latency, not bandwidth"}})
+        if cpu:
+            c1, c2, cw = in1.cpu().requires_grad_(), in2.cpu().requires_grad_(), w.cpu().requires_grad_()
+            cgo, ci, cj = go.cpu(), ei[0].cpu(), ei[1].cpu()
+
+            def cstep():
+                out = O.tensor_product(c1, c2, cw, ci, cj, 2, 2, 2, C, 1)
+                return torch.autograd.grad(out, [c1, c2, cw], cgo)
+            rate, cores, calls, cdt = _cpu_rate(cstep, 1)
+            res["cpu_baseline"] = {"value": rate, "unit": "calls/s", "cores": cores, "kind": "port",
+                                   "sample": f"oracle float32, same inputs, {calls} calls in {cdt:.1f} s"}
     elif name == "cfg2_expansion_radial":
+        # E = 200,000 edge vectors (|v| ~ U[0.8, 5.0] A, direction uniform): Eq. (1) l <= 3, 8 Bessel
+        # functions, polynomial cutoff p = 6 at 5 A, one fused kernel
+        from flashcart_amd import _lib as L
         rng = np.random.default_rng(0)
         E = 200_000
         d = rng.uniform(0.8, 5.0, size=E)
         r = rng.standard_normal((E, 3))
         r /= np.linalg.norm(r, axis=1, keepdims=True)
         vec = torch.as_tensor(d[:, None] * r, dtype=torch.float32, device=dev)
-        from flashcart_amd import _lib as L
-        from flashcart_amd.o3 import _ops
         idx = torch.arange(E, dtype=torch.int32, device=dev)
         rowptr = torch.arange(E + 1, dtype=torch.int32, device=dev)
-
-        def step():
-            return _ops.edge_geometry(None, None, idx, idx, vec, rowptr, idx, rowptr, 3, L.BASIS_BESSEL, 8, 0.0,
-                                      5.0, 6)
-        dt, _ = _timed(step, args.steps, args.warmup, dev)
-        ms = 1e3 * dt / args.steps
+        ms = device_time_ms(lambda: _ops.edge_geometry(None, None, idx, idx, vec, rowptr, idx, rowptr, 3,
+                                                        L.BASIS_BESSEL, 8, 0.0, 5.0, 6), steps, dev)
+        byts = 112 * E
         res.update({"metric": "edges/s (expansion l<=3 + 8 Bessel + cutoff p=6, fused, E=200k)",
-                    "value": E * args.steps / dt, "unit": "edges/s", "ms_per_step": ms,
-                    "roofline": {"bound": "hbm (launch-bound at this size)", "algorithmic_bytes": 112 * E,
-                                 "achieved": 112 * E / (ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s"}})
+                    "value": E / (ms * 1e-3), "unit": "edges/s", "ms_per_step": ms,
+                    "roofline": {"bound": "hbm", "kernel": "edge_fwd_kernel (vector given)", "algorithmic_bytes": byts,
+                                 "achieved": byts / (ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                 "frac": byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                 "note": "22.4 MB per launch: a few microseconds, bound by launch latency"}})
+        if cpu:
+            cv = vec.cpu()
+
+            def cstep():
+                dd = cv.norm(dim=-1)
+                u = cv / dd.unsqueeze(-1)
+                return O.irreps(u, 3), O.bessel(dd, 8, 5.0), O.cutoff(dd, 5.0, 6)
+            rate, cores, calls, cdt = _cpu_rate(cstep, E)
+            res["cpu_baseline"] = {"value": rate, "unit": "edges/s", "cores": cores, "kind": "port",
+                                   "sample": f"oracle float32, same 200k edges, {calls} calls in {cdt:.1f} s"}
+    else:
+        if name == "cfg3_water_1536":
+            z, p, cell, pbc = water_box(512, seed=0)
+            elements, C, L = ["H", "O"], 64, 2
+            graph = AtomicGraph.from_arrays(z, p, elements, R_MAX, cell=cell, pbc=pbc)
+            oracle_graph = graph
+        else:
+            mols = molecules(512, seed=0)
+            elements, C, L = ["H", "C", "N", "O"], 64, 2
+            gs = [AtomicGraph.from_arrays(zz, pp, elements, R_MAX) for zz, pp in mols]
+            graph = batch_graphs(gs)
+            oracle_graph = batch_graphs(gs[:16])
+        n_atoms = graph.num_nodes
+        avg = graph.edge_index.shape[1] / n_atoms
+        from flashcart_amd.model import FlashCartPotential
+        torch.manual_seed(1234)
+        model = FlashCartPotential.from_config(model_config(elements, C, L, r_max=R_MAX, avg_neighbors=avg))
+        for q in model.parameters():
+            q.requires_grad_(False)
+        model = model.to(dev)
+        gdev = graph.to(dev)
+        dt_eager, _ = _timed(lambda: model.predict(gdev, compute_forces=True), steps, warmup, dev)
+        # fixed topology: the whole prediction replayed as one HIP graph (predict(use_compile=True))
+        for _ in range(warmup):
+            model.predict(gdev, compute_forces=True, use_compile=True)
+        stream = torch.cuda.current_stream(dev)
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize(dev)
+        ev0.record(stream)
+        for _ in range(steps):
+            out = model.predict(gdev, compute_forces=True, use_compile=True)
+        ev1.record(stream)
+        torch.cuda.synchronize(dev)
+        ms = ev0.elapsed_time(ev1) / steps
+        if not bool(torch.isfinite(out["energy"]).all()):
+            raise RuntimeError(f"{name}: non-finite energy")
+        f_ms, f_b, b_ms, b_b = measure_dominant(model, gdev, dev, with_backward=True)
+        res.update({"metric": "atom-steps/s (energy+forces)", "value": n_atoms / (ms * 1e-3), "unit": "atom-steps/s",
+                    "ms_per_step": ms, "mode": "HIP graph replay of predict (use_compile=True)",
+                    "eager": {"value": n_atoms * steps / dt_eager, "ms_per_step": 1e3 * dt_eager / steps},
+                    "config": {"n_atoms": n_atoms, "n_graphs": graph.num_graphs,
+                               "n_edges": int(graph.edge_index.shape[1]), "channels": C, "l_max_edge_attrs": L},
+                    "roofline": {"bound": "hbm", "kernel": "layer-1 TP convolution forward", "algorithmic_bytes": f_b,
+                                 "avg_launch_ms": f_ms, "achieved": f_b / (f_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS,
+                                 "unit": "GB/s", "frac": f_b / (f_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
+                    "roofline_tp_bwd": {"bound": "hbm", "kernel": "layer-1 TP convolution backward op",
+                                        "algorithmic_bytes": b_b, "avg_launch_ms": b_ms,
+                                        "achieved": b_b / (b_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                        "frac": b_b / (b_ms * 1e-3) / 1e9 / HBM_PEAK_GBS}})
+        if cpu:
+            sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+            rate, cores, calls, cdt = _oracle_rate(sd, model.to_model_config(), oracle_graph.to_dict(),
+                                                   oracle_graph.num_nodes)
+            res["cpu_baseline"] = {"value": rate, "unit": "atom-steps/s", "cores": cores, "kind": "port",
+                                   "sample": f"oracle float32 on {oracle_graph.num_nodes} atoms "
+                                             f"({oracle_graph.num_graphs} graphs), {calls} calls, {cdt:.1f} s"}
+    if cpu:
+        res["speedup_vs_cpu"] = res["value"] / res["cpu_baseline"]["value"]
+    return res
+
+
+def run_other_workload(name, args, dev):
+    """Throughput of the other BASELINE configurations (parity-tested in tests/test_gpu_configs.py).
+    Prints one JSON line per call; the default invocation measures the 25k-atom configuration."""
+    from flashcart_amd import o3
+    from flashcart_amd.data import AtomicGraph, batch_graphs
+    from flashcart_amd.data.synthetic import model_config, molecules, water_box
+    res = {"workload": name, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "dtype": "f32",
+           "data": "synthetic (seeded)"}
+    if name in CONFIG_LINES:
+        res.update(config_line(name, dev, args.steps, args.warmup, not args.no_cpu_baseline))
     elif name.startswith("train_"):
         run_training(name, args, dev, res)
     elif name == "lammps_fcc25k":
@@ -279,46 +458,7 @@ def run_other_workload(name, args, dev):
                                    "sample": f"host cell list (fc_neighbor_list), same system, {calls} builds"}
             res["speedup_vs_cpu"] = res["value"] / rate
     else:
-        if name == "cfg3_water_1536":
-            z, p, cell, pbc = water_box(512, seed=0)
-            elements, C, L = ["H", "O"], 64, 2
-            graph = AtomicGraph.from_arrays(z, p, elements, R_MAX, cell=cell, pbc=pbc)
-            oracle_graph = graph
-        elif name == "cfg5_molecules_512":
-            mols = molecules(512, seed=0)
-            elements, C, L = ["H", "C", "N", "O"], 64, 2
-            gs = [AtomicGraph.from_arrays(zz, pp, elements, R_MAX) for zz, pp in mols]
-            graph = batch_graphs(gs)
-            oracle_graph = batch_graphs(gs[:16])
-        else:
-            raise SystemExit(f"unknown workload {name}")
-        n_atoms = graph.num_nodes
-        avg = graph.edge_index.shape[1] / n_atoms
-        from flashcart_amd.model import FlashCartPotential
-        torch.manual_seed(1234)
-        model = FlashCartPotential.from_config(model_config(elements, C, L, r_max=R_MAX, avg_neighbors=avg))
-        for q in model.parameters():
-            q.requires_grad_(False)
-        model = model.to(dev)
-        gdev = graph.to(dev)
-        dt_eager, _ = _timed(lambda: model.predict(gdev, compute_forces=True), args.steps, args.warmup, dev)
-        # fixed topology: the whole prediction replayed as one HIP graph (predict(use_compile=True))
-        dt, out = _timed(lambda: model.predict(gdev, compute_forces=True, use_compile=True), args.steps,
-                         args.warmup, dev)
-        res.update({"metric": "atom-steps/s (energy+forces)", "value": n_atoms * args.steps / dt,
-                    "unit": "atom-steps/s", "ms_per_step": 1e3 * dt / args.steps,
-                    "mode": "HIP graph replay of predict (use_compile=True)",
-                    "eager": {"value": n_atoms * args.steps / dt_eager, "ms_per_step": 1e3 * dt_eager / args.steps},
-                    "config": {"n_atoms": n_atoms, "n_graphs": graph.num_graphs,
-                               "n_edges": int(graph.edge_index.shape[1]), "channels": C, "l_max_edge_attrs": L}})
-        if not args.no_cpu_baseline:
-            sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
-            rate, cores, calls, cdt = _oracle_rate(sd, model.to_model_config(), oracle_graph.to_dict(),
-                                                   oracle_graph.num_nodes)
-            res["cpu_baseline"] = {"value": rate, "unit": "atom-steps/s", "cores": cores, "kind": "port",
-                                   "sample": f"oracle float32 on {oracle_graph.num_nodes} atoms "
-                                             f"({oracle_graph.num_graphs} graphs), {calls} calls, {cdt:.1f} s"}
-            res["speedup_vs_cpu"] = res["value"] / rate
+        raise SystemExit(f"unknown workload {name}")
     print(json.dumps(res), flush=True)
 
 
@@ -412,8 +552,10 @@ def main():
     ap.add_argument("--kernel-only", action="store_true",
                     help="only launch the dominant kernel (5x) and a 2 GiB device copy (5x), for counter runs")
     ap.add_argument("--profile-step", action="store_true",
-                    help="two energy+forces steps on the first step graph, then a 2 GiB device copy (2x) "
-                         "for counter calibration, for per-kernel counter runs")
+                    help="two energy+forces steps on the first step graph, then the calibration kernels (2x), "
+                         "for per-kernel counter runs")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="measure only the metric's configuration (no lines for the other BASELINE configurations)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU runs are not part of it "
@@ -434,26 +576,18 @@ def main():
         model = model.to(dev)
         for _ in range(2):
             model.predict(g, compute_forces=True)
-        src = torch.ones(2 ** 29, device=dev)  # 2 GiB
-        dst = torch.empty_like(src)
-        for _ in range(2):  # plain elementwise copy (reads and writes 2 GiB) for counter calibration
-            torch.mul(src, 1.0, out=dst)
-        torch.cuda.synchronize(dev)
+        cal = calibration_kernels(dev, 2)
         print(json.dumps({"profile_step": True, "n_atoms": len(numbers), "n_edges": int(g.edge_index.shape[1]),
-                          "copy_bytes_each_way": src.numel() * 4}), flush=True)
+                          **cal}), flush=True)
         return
     if args.kernel_only:
         sg = StepGraphs(numbers, pos, cell, pbc, ["Cu", "Ni", "Fe", "Cr"], 1)
         model, _ = build_model(43.0)
         g = sg.graph(0, dev)
-        ms, byts = measure_dominant(model.to(dev), g, dev, reps=5)
-        src = torch.ones(2 ** 29, device=dev)  # 2 GiB
-        dst = torch.empty_like(src)
-        for _ in range(5):  # a plain elementwise copy kernel (reads and writes 2 GiB) for counter calibration
-            torch.mul(src, 1.0, out=dst)
-        torch.cuda.synchronize(dev)
+        ms, byts, ms_b, byts_b = measure_dominant(model.to(dev), g, dev, reps=5, with_backward=True)
+        cal = calibration_kernels(dev, 5)
         print(json.dumps({"kernel_only": True, "avg_launch_ms": ms, "algorithmic_bytes": byts,
-                          "copy_bytes_each_way": src.numel() * 4}), flush=True)
+                          "avg_bwd_op_ms": ms_b, "algorithmic_bytes_bwd": byts_b, **cal}), flush=True)
         return
     n_steps = args.warmup + args.steps
     log(f"building {n_steps} step graphs for {len(numbers)} atoms")
@@ -506,19 +640,26 @@ def main():
                    "l_max_hidden_feats": 2, "n_interactions": 2, "r_max": R_MAX, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": "tp_fwd_kernel<2,3,3> (conv, layer 1)", "achieved": gbs,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
-                     "traffic": MEASURED_TRAFFIC_BYTES, "traffic_launch": "bench.py --kernel-only (E=1080166)",
+                     "traffic": MEASURED_TRAFFIC_BYTES, "traffic_launch": f"bench.py --kernel-only (E={TRAFFIC_E})",
+                     "traffic_over_algorithmic": MEASURED_TRAFFIC_BYTES / TRAFFIC_ALG_FWD,
                      "algorithmic_bytes": byts, "avg_launch_ms": ms,
                      "note": "the north star's TP kernel; by time the layer-1 backward dominates the step "
                              "(roofline_tp_bwd)"},
-        # the step's largest TP kernel by time: the layer-1 TP backward op = tp_bwd_conv_kernel<2,3,3>
-        # + segment_rows_kernel (sender gather); achieved = both kernels' algorithmic bytes / op time
+        # the step's largest TP kernel by time: the layer-1 TP backward op (backward kernel + the
+        # sender-ordered sum of its per-edge messages), on the compulsory bytes of its three gradients
         "roofline_tp_bwd": {"bound": "hbm", "kernel": "tp_bwd_conv_kernel<2,3,3> + segment_rows_kernel (layer 1)",
                             "achieved": gbs_b, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs_b / HBM_PEAK_GBS,
                             "traffic": MEASURED_TRAFFIC_BWD_BYTES,
-                            "traffic_launch": "bench.py --profile-step (E=1080166)",
+                            "traffic_launch": f"bench.py --kernel-only (E={TRAFFIC_E})",
+                            "traffic_over_algorithmic": MEASURED_TRAFFIC_BWD_BYTES / TRAFFIC_ALG_BWD,
                             "algorithmic_bytes": byts_b, "avg_launch_ms": ms_b},
         "energy": e,
     }
+    if not args.no_configs:
+        result["configs"] = {}
+        for name in CONFIG_LINES:
+            log(f"configuration {name}")
+            result["configs"][name] = config_line(name, dev, 30, 5, not args.no_cpu_baseline)
     if not args.no_cpu_baseline:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(model.cpu(), cfg, avg_nbr)

@@ -745,22 +745,12 @@ def linear_wgrad(grad_out: Tensor, x: Tensor, weights: List[Tensor], in_l_max: i
 # ---------------------------------------------------------------------------
 
 _PRECISIONS = ("ieee", "tf32", "tf32x3")
-_scale_cache: dict = {}
-
-
 def _scale_values(scale: Tensor, n: int) -> List[float]:
-    """Host copy of the per-rank scale tensor, read again only when the tensor was replaced or
-    written in place (one device-to-host copy per change, none per call)."""
-    key = (scale.data_ptr(), scale.device, scale._version, n)
-    vals = _scale_cache.get(key)
-    if vals is None:
-        if scale.numel() < n:
-            raise RuntimeError(f"Expected {n} scales, got {scale.numel()}.")
-        vals = [float(v) for v in scale.detach().reshape(-1)[:n].cpu()]
-        if len(_scale_cache) > 256:
-            _scale_cache.clear()
-        _scale_cache[key] = vals
-    return vals
+    """Host copy of the per-rank scale tensor (one small device-to-host copy per call of the
+    reference-schema ops; the build's own layers keep their scales on the host)."""
+    if scale.numel() < n:
+        raise RuntimeError(f"Expected {n} scales, got {scale.numel()}.")
+    return [float(v) for v in scale.detach().reshape(-1)[:n].cpu()]
 
 
 def _ref_linear_layout(x: Tensor, weights: List[Tensor], use_fp64: bool, dot_input_precision: str,
@@ -1000,16 +990,6 @@ linear_bwd_ref.register_autograd(_linear_bwd_ref_backward, setup_context=_linear
 # Dense layer with optional rescaled-SiLU epilogue (radial / readout MLPs)
 # ---------------------------------------------------------------------------
 
-LIBRARY_GEMM_MIN_FLOP = 2e10
-
-
-def _use_library_gemm(n: int, k: int, m: int, act: int, bias) -> bool:
-    """Large plain GEMMs (the radial MLP output layer) go to the vendor GEMM; layers with a
-    fused activation or bias epilogue stay on the library's MFMA kernel."""
-    return act == 0 and bias is None and 2.0 * n * k * m >= LIBRARY_GEMM_MIN_FLOP and \
-        not torch.backends.cuda.matmul.allow_tf32
-
-
 @torch.library.custom_op("flashcart::dense_fwd", mutates_args=())
 def dense_fwd(x: Tensor, weight: Tensor, bias: Optional[Tensor], scale: float, act: int) -> Tuple[Tensor, Tensor]:
     """(activated output, pre-activation (empty when act == 0))."""
@@ -1021,13 +1001,6 @@ def dense_fwd(x: Tensor, weight: Tensor, bias: Optional[Tensor], scale: float, a
         raise RuntimeError(f"Incorrect last dimension for x. Expected {k}, got {x.shape[-1]}.")
     lead = x.shape[:-1]
     x2 = x.reshape(-1, k)
-    # K = 64 (the radial output layer) runs on the library's wide-output kernel, which
-    # overlaps its output stores with the MFMA work; other large plain GEMMs on hipBLASLt
-    if k != 64 and _use_library_gemm(x2.shape[0], k, m, act, b):
-        # Plain GEMM (no activation, no bias): hipBLASLt, with the weight pre-scaled as the
-        # reference's F.linear(x, W * s) does. fp32 inputs, IEEE fp32 products.
-        out = torch.mm(x2, (w * scale).t())
-        return out.reshape(*lead, m), x.new_empty(0)
     out = x.new_empty(x2.shape[0], m)
     pre = x.new_empty(x2.shape[0], m) if act else x.new_empty(0)
     _lib_call("fc_dense_fwd", x2.shape[0], k, m, x2.data_ptr(), w.data_ptr(), float(scale), _lib.ptr(b), int(act),
@@ -1048,10 +1021,16 @@ def dense_bwd(grad_out: Tensor, pre: Tensor, weight: Tensor, scale: float, act: 
     m, k = w.shape
     lead = go.shape[:-1]
     go2 = go.reshape(-1, m)
-    if _use_library_gemm(go2.shape[0], k, m, act, None):
-        return torch.mm(go2, w * scale).reshape(*lead, k)
-    pr = _lib.contig("pre", pre).reshape(-1, m) if act else None
     gx = go.new_empty(go2.shape[0], k)
+    if act == 0:
+        # gx = go @ (W s): the forward kernel with the transposed weight as its (k, m) matrix, whose
+        # operands both stage through LDS as 128-bit rows (the radial output layer's input
+        # gradient, K = P x C = 2,176 -> 64, runs 6% faster this way than on the k-major path)
+        wt = w.t().contiguous()  # (k, m): a few microseconds for the radial output layer's 2,176 x 64
+        _lib_call("fc_dense_fwd", go2.shape[0], m, k, go2.data_ptr(), wt.data_ptr(), float(scale), None, 0, None,
+                  gx.data_ptr(), _lib.stream_of(go))
+        return gx.reshape(*lead, k)
+    pr = _lib.contig("pre", pre).reshape(-1, m)
     _lib_call("fc_dense_dgrad", go2.shape[0], k, m, go2.data_ptr(), _lib.ptr(pr), w.data_ptr(), float(scale),
               int(act), gx.data_ptr(), _lib.stream_of(go))
     return gx.reshape(*lead, k)
