@@ -156,3 +156,17 @@ def test_initial_parameters(name):
         got = sd[k].detach().cpu()
         assert got.dtype == want.dtype, k
         assert torch.equal(got, want), k
+
+
+def test_fullsize_fixture_matches_the_benchmark_workload():
+    """tests/golden/fcc25k_step0.npz (the oracle at the benchmark's full size) belongs to the
+    workload bench.py times: same first-step graph and same seed-1234 parameters."""
+    from tests.golden.make_fullsize import graph_digest, params_digest, workload
+
+    fx = load_golden("fcc25k_step0")
+    g, model = workload()
+    m = fx["meta"]
+    assert (g.num_nodes, int(g.edge_index.shape[1])) == (m["n_atoms"], m["n_edges"])
+    assert graph_digest(g) == m["graph_sha256"]
+    assert params_digest(model) == m["params_sha256"]
+    assert m["f32_vs_f64"]["energy_rel"] < 1e-5
