@@ -119,6 +119,51 @@ def _path_tensor_t(l1, l2, lo, dtype):
     return torch.as_tensor(path_tensor(l1, l2, lo), dtype=dtype)
 
 
+# How tensor_product evaluates each path: "einsum" contracts the dense path tensor in one call;
+# "components" follows the op sequence of the reference's generated CPU module
+# (src/flashcart/o3/_codegen_tensor_product.py:833-1012): every output component as a sum of
+# products of input component columns, then stack, path weight, cat and scatter_sum. Both give
+# the same values; the CPU baseline times the second. Set with components_form().
+TP_FORM = "einsum"
+
+
+class components_form:
+    """Context manager: tensor_product evaluates per output component (the reference's CPU
+    op sequence) inside the block."""
+
+    def __enter__(self):
+        global TP_FORM
+        self._prev, TP_FORM = TP_FORM, "components"
+        return self
+
+    def __exit__(self, *exc):
+        global TP_FORM
+        TP_FORM = self._prev
+
+
+@lru_cache(maxsize=None)
+def _path_terms(l1, l2, lo):
+    """Nonzero coefficients of the path tensor, per output component: [(b, c, coeff), ...]."""
+    B = path_tensor(l1, l2, lo)
+    return tuple(tuple((int(b), int(c), float(B[a, b, c])) for b, c in zip(*np.nonzero(np.abs(B[a]) > 1e-14)))
+                 for a in range(B.shape[0]))
+
+
+def _path_components(x, y, l1, l2, lo):
+    """out_a = sum over (b, c) of B[a, b, c] * x[:, b] * y[:, c], column by column: x (n, 2l1+1, C),
+    y (n, 2l2+1, C or 1) -> (n, 2lo+1, C)."""
+    xs = [x[:, b] for b in range(x.shape[1])]
+    ys = [y[:, c] for c in range(y.shape[1])]
+    comps = []
+    for terms in _path_terms(l1, l2, lo):
+        acc = None
+        for b, c, k in terms:
+            t = k * xs[b] * ys[c]
+            acc = t if acc is None else acc + t
+        comps.append(acc if acc is not None else torch.zeros_like(xs[0] * ys[0]))
+    return torch.stack(comps, dim=1)
+
+
 def tensor_product(in1, in2, weights, idx_i, idx_j, in1_l_max, in2_l_max, out_l_max, in1_features,
                    in2_features, symmetric_product=False, shared_weights=False, reduce_paths=False, out_rows=None):
     """``out_rows``: rows of a convolution's output (default: the rows of in1)."""
@@ -129,16 +174,23 @@ def tensor_product(in1, in2, weights, idx_i, idx_j, in1_l_max, in2_l_max, out_l_
     n = in1.shape[0]
     C = max(in1_features, in2_features)
 
+    components = TP_FORM == "components"
+
     def blocks(x, lmax, f):
-        return [x[:, l * l * f:(l + 1) * (l + 1) * f].reshape(n, 2 * l + 1, f).expand(n, 2 * l + 1, C)
+        return [x[:, l * l * f:(l + 1) * (l + 1) * f].reshape(n, 2 * l + 1, f) if components else
+                x[:, l * l * f:(l + 1) * (l + 1) * f].reshape(n, 2 * l + 1, f).expand(n, 2 * l + 1, C)
                 for l in range(lmax + 1)]
 
     b1, b2 = blocks(in1, in1_l_max, in1_features), blocks(in2, in2_l_max, in2_features)
     buckets: List[List[torch.Tensor]] = [[] for _ in range(out_l_max + 1)]
     for p, (l1, l2, lo, swap) in enumerate(enumerate_paths(in1_l_max, in2_l_max, out_l_max, symmetric_product)):
         x, y = (b2[l1], b1[l2]) if swap else (b1[l1], b2[l2])
-        B = _path_tensor_t(l1, l2, lo, in1.dtype)
-        out = torch.einsum("abc,nbf,ncf->naf", B, x, y)
+        if components:
+            out = _path_components(x, y, l1, l2, lo)
+            out = out.expand(n, 2 * lo + 1, C) if out.shape[-1] != C else out
+        else:
+            B = _path_tensor_t(l1, l2, lo, in1.dtype)
+            out = torch.einsum("abc,nbf,ncf->naf", B, x, y)
         w = weights[p * C:(p + 1) * C] if shared_weights else weights[:, p * C:(p + 1) * C].unsqueeze(1)
         buckets[lo].append(out * w)
     flats = []

@@ -42,8 +42,18 @@ def _prefixed(sd, prefix="m"):
     return {f"{prefix}.{k}": v for k, v in sd.items()}
 
 
+@pytest.mark.parametrize("form", ["einsum", "components"])
 @pytest.mark.parametrize("name", golden_names("tp"))
-def test_tensor_product(name):
+def test_tensor_product(name, form):
+    """Both evaluation forms of the oracle's tensor product (the dense einsum, and the
+    per-component op sequence that the CPU baseline times) against the reference."""
+    import contextlib
+
+    with (O.components_form() if form == "components" else contextlib.nullcontext()):
+        _tensor_product(name)
+
+
+def _tensor_product(name):
     fx = load_golden(name)
     m = fx["meta"]
     ins = _leaves(fx["in"])
@@ -128,14 +138,18 @@ def golden_graph(fx):
     return g
 
 
+@pytest.mark.parametrize("form", ["einsum", "components"])
 @pytest.mark.parametrize("name", golden_names("potential"))
-def test_potential(name):
+def test_potential(name, form):
     """Site energies, energies, forces and stress of the whole potential (FlashCartPotential's
     wiring of the reference's layers, through the reference's AtomisticModel.predict)."""
     fx = load_golden(name)
     cfg = fx["meta"]["config"]
     stress = fx["meta"]["stress"]
-    ref = OM.predict(fx["sd"], cfg, golden_graph(fx), compute_forces=True, compute_stress=stress)
+    import contextlib
+
+    with (O.components_form() if form == "components" else contextlib.nullcontext()):
+        ref = OM.predict(fx["sd"], cfg, golden_graph(fx), compute_forces=True, compute_stress=stress)
     for key in ("node_energies", "energy", "forces") + (("stress",) if stress else ()):
         _close(ref[key], fx["out"][key], key)
 

@@ -187,7 +187,7 @@ class PairData(MLIAPData):
 
 
 @pytest.mark.parametrize("use_f", [False, True], ids=["update_pair_forces", "data_f"])
-def test_lammps_mliap_matches_periodic_prediction(use_f):
+def test_lammps_mliap_matches_periodic_oracle(use_f):
     from flashcart_amd.calculators import FlashCartLAMMPSUnified
     z, p, cell, pbc = fcc_alloy(2, 2, 2, seed=9)
     cfg = model_config(["Cu", "Ni", "Fe", "Cr"], 16, 3, avg_neighbors=42.0)
@@ -195,7 +195,9 @@ def test_lammps_mliap_matches_periodic_prediction(use_f):
     with torch.no_grad():
         model.scale_shift.shifts.copy_(torch.tensor([0.1, -0.2, 0.3, -0.4]))
     g = AtomicGraph.from_arrays(z, p, cfg["elements"], 5.0, cell=cell, pbc=pbc)
-    ref = model.to(DEV).predict(g.to(DEV), compute_forces=True)
+    # the oracle's periodic prediction (float64, CPU) of the same structure and parameters
+    ref = OM.predict(model.state_dict(), model.to_model_config(), g.to_dict(), compute_forces=True)
+    model = model.to(DEV)
     unified = FlashCartLAMMPSUnified(model, add_atomic_offsets=True)
     data = MLIAPData(g, len(z), with_f=True) if use_f else PairData(g, len(z))
     data.rij = torch.as_tensor(data.rij, dtype=torch.float32, device=DEV)  # device array, as KOKKOS hands over
@@ -211,15 +213,17 @@ def test_lammps_mliap_matches_periodic_prediction(use_f):
     assert_close(torch.as_tensor(forces), ref["forces"], 0.0, 1e-4, "LAMMPS forces")
 
 
-def test_single_rank_mliap_data_matches_prediction():
+def test_single_rank_mliap_data_matches_oracle():
     """The packaged single-rank ML-IAP layout (``SingleRankMLIAPData``: ghosts per periodic
-    image, device arrays, pair forces kept on the device) reproduces the periodic prediction."""
+    image, device arrays, pair forces kept on the device) reproduces the oracle's periodic
+    prediction of the same structure."""
     from flashcart_amd.calculators import FlashCartLAMMPSUnified, SingleRankMLIAPData
     z, p, cell, pbc = fcc_alloy(3, 2, 2, seed=11)
     cfg = model_config(["Cu", "Ni", "Fe", "Cr"], 16, 3, avg_neighbors=42.0)
     model = _model(cfg, 31)
     g = AtomicGraph.from_arrays(z, p, cfg["elements"], 5.0, cell=cell, pbc=pbc)
-    ref = model.to(DEV).predict(g.to(DEV), compute_forces=True)
+    ref = OM.predict(model.state_dict(), model.to_model_config(), g.to_dict(), compute_forces=True)
+    model = model.to(DEV)
     data = SingleRankMLIAPData(g, device=DEV)
     FlashCartLAMMPSUnified(model).compute_forces(data)
     assert data.ntotal > data.nlocal and data.pair_forces.is_cuda
