@@ -166,6 +166,35 @@ def contig(name: str, t: torch.Tensor, dtype: torch.dtype = torch.float32) -> to
     return t if t.is_contiguous() else t.contiguous()
 
 
+# Per-edge tensors of a molecular-dynamics run change size every step (the edge count drifts by
+# ~0.1% per step at 1M edges) and the largest are several GB. Exact-size requests make the
+# caching allocator reserve a new segment for each new size until device memory runs out and
+# it has to flush (~0.5 s per step once that happens). Rows are therefore allocated in steps of
+# 1/8 of a power of two, so one set of segments serves every edge count within ~12% of it.
+ROUNDED_ROWS_MIN_BYTES = 64 << 20
+
+
+def rounded_rows(rows: int) -> int:
+    """``rows`` rounded up to a multiple of 2^(floor(log2(rows)) - 3) (at most 12.5% more)."""
+    if rows < 16:
+        return rows
+    q = 1 << (rows.bit_length() - 4)
+    return -(-rows // q) * q
+
+
+def rows_empty(like: torch.Tensor, rows: int, *cols: int, dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """Uninitialised (rows, *cols) tensor on ``like``'s device: the leading rows of a buffer of
+    rounded_rows(rows) rows when it is ROUNDED_ROWS_MIN_BYTES or larger (a contiguous view)."""
+    dtype = like.dtype if dtype is None else dtype
+    width = 1
+    for c in cols:
+        width *= int(c)
+    rows = int(rows)
+    if rows * width * torch.empty((), dtype=dtype).element_size() < ROUNDED_ROWS_MIN_BYTES:
+        return like.new_empty((rows, *cols), dtype=dtype)
+    return like.new_empty((rounded_rows(rows), *cols), dtype=dtype)[:rows]
+
+
 def tp_desc(in1_l_max, in2_l_max, out_l_max, in1_features, in2_features, symmetric, shared, reduced) -> TPDesc:
     return TPDesc(int(in1_l_max), int(in2_l_max), int(out_l_max), int(in1_features), int(in2_features),
                   int(bool(symmetric)), int(bool(shared)), int(bool(reduced)))

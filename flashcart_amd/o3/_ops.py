@@ -290,9 +290,9 @@ def edge_geometry(positions: Optional[Tensor], shift_vec: Optional[Tensor], idx_
     if ref is None:
         raise ValueError("edge_geometry needs positions or vectors.")
     E = ii.shape[0]
-    attrs = ref.new_empty(E, (l_max + 1) ** 2)
-    feats = ref.new_empty(E, n_radial) if basis != _lib.BASIS_NONE else ref.new_empty(0)
-    env = ref.new_empty(E) if poly_order > 0 else ref.new_empty(0)
+    attrs = _lib.rows_empty(ref, E, (l_max + 1) ** 2)
+    feats = _lib.rows_empty(ref, E, n_radial) if basis != _lib.BASIS_NONE else ref.new_empty(0)
+    env = _lib.rows_empty(ref, E) if poly_order > 0 else ref.new_empty(0)
     desc = _edge_desc(l_max, basis, n_radial, r_min, r_max, poly_order)
     _lib_call("fc_edge_geometry_fwd", desc, E, _lib.ptr(pos), _lib.ptr(sv), ii.data_ptr(), jj.data_ptr(),
               _lib.ptr(vec), attrs.data_ptr(), _lib.ptr(feats) if feats.numel() else None,
@@ -327,7 +327,7 @@ def edge_geometry_bwd(g_attrs: Optional[Tensor], g_feats: Optional[Tensor], g_en
     gf = _lib.contig("grad_feats", g_feats) if (g_feats is not None and basis != _lib.BASIS_NONE) else None
     ge = _lib.contig("grad_env", g_env) if (g_env is not None and poly_order > 0) else None
     E = ii.shape[0]
-    gvec = ref.new_empty(E, 3)
+    gvec = _lib.rows_empty(ref, E, 3)
     desc = _edge_desc(l_max, basis, n_radial, r_min, r_max, poly_order)
     stream = _lib.stream_of(ref)
     _lib_call("fc_edge_geometry_bwd", desc, E, _lib.ptr(pos), _lib.ptr(sv), ii.data_ptr(), jj.data_ptr(),
@@ -491,14 +491,14 @@ def tp_bwd(grad_out: Tensor, in1: Tensor, in2: Tensor, weights: Tensor, idx_i: O
     csr, keep = (None, None)
     if conv:
         csr, keep = _tp_csr(in1, idx_i, idx_j, rowptr, sender_perm, sender_ptr, need_senders=need_grad_in1)
-    g1 = torch.empty_like(in1) if need_grad_in1 else in1.new_empty(0)
-    g2 = torch.empty_like(in2) if need_grad_in2 else in2.new_empty(0)
-    gw = torch.empty_like(w) if need_grad_weights else w.new_empty(0)
+    g1 = _lib.rows_empty(in1, *in1.shape) if need_grad_in1 else in1.new_empty(0)
+    g2 = _lib.rows_empty(in2, *in2.shape) if need_grad_in2 else in2.new_empty(0)
+    gw = _lib.rows_empty(w, *w.shape) if need_grad_weights else w.new_empty(0)
     lib = _lib.load()
     n_ws = lib.fc_tp_bwd_workspace(desc, csr, in1.shape[0], int(need_grad_in1), int(need_grad_weights))
     if n_ws < 0:
         _lib.check(-n_ws, "fc_tp_bwd_workspace")
-    ws = in1.new_empty(max(int(n_ws), 1))
+    ws = _lib.rows_empty(in1, max(int(n_ws), 1))
     _lib_call("fc_tp_bwd", desc, csr, in1.shape[0], go.data_ptr(), in1.data_ptr(), in2.data_ptr(), w.data_ptr(),
               float(alpha), g1.data_ptr() if need_grad_in1 else None, g2.data_ptr() if need_grad_in2 else None,
               gw.data_ptr() if need_grad_weights else None, ws.data_ptr(), int(n_ws), _lib.stream_of(in1))
@@ -1001,8 +1001,8 @@ def dense_fwd(x: Tensor, weight: Tensor, bias: Optional[Tensor], scale: float, a
         raise RuntimeError(f"Incorrect last dimension for x. Expected {k}, got {x.shape[-1]}.")
     lead = x.shape[:-1]
     x2 = x.reshape(-1, k)
-    out = x.new_empty(x2.shape[0], m)
-    pre = x.new_empty(x2.shape[0], m) if act else x.new_empty(0)
+    out = _lib.rows_empty(x, x2.shape[0], m)
+    pre = _lib.rows_empty(x, x2.shape[0], m) if act else x.new_empty(0)
     _lib_call("fc_dense_fwd", x2.shape[0], k, m, x2.data_ptr(), w.data_ptr(), float(scale), _lib.ptr(b), int(act),
               pre.data_ptr() if act else None, out.data_ptr(), _lib.stream_of(x))
     return out.reshape(*lead, m), (pre.reshape(*lead, m) if act else pre)
@@ -1021,7 +1021,7 @@ def dense_bwd(grad_out: Tensor, pre: Tensor, weight: Tensor, scale: float, act: 
     m, k = w.shape
     lead = go.shape[:-1]
     go2 = go.reshape(-1, m)
-    gx = go.new_empty(go2.shape[0], k)
+    gx = _lib.rows_empty(go, go2.shape[0], k)
     if act == 0:
         # gx = go @ (W s): the forward kernel with the transposed weight as its (k, m) matrix, whose
         # operands both stage through LDS as 128-bit rows (the radial output layer's input
@@ -1102,7 +1102,7 @@ def radial_mlp_fwd(x: Tensor, w0: Tensor, s0: float, w1: Tensor, s1: float, w2: 
         raise RuntimeError(f"W2 must be (m, 64), got {tuple(w2.shape)}.")
     m = w2.shape[0]
     x2 = x.reshape(-1, n_in)
-    out = x.new_empty(x2.shape[0], m)
+    out = _lib.rows_empty(x, x2.shape[0], m)
     _lib_call("fc_radial_mlp_fwd", x2.shape[0], n_in, x2.data_ptr(), w0.data_ptr(), float(s0), w1.data_ptr(),
               float(s1), m, w2.data_ptr(), float(s2), out.data_ptr(), _lib.stream_of(x))
     return out.reshape(*x.shape[:-1], m)
@@ -1123,7 +1123,7 @@ def radial_mlp_bwd(grad_h2: Tensor, x: Tensor, w0: Tensor, s0: float, w1: Tensor
     x2 = x.reshape(-1, n_in)
     if gh.numel() != x2.shape[0] * 64:
         raise RuntimeError(f"grad_h2 must hold {x2.shape[0]} rows of 64, got {tuple(gh.shape)}.")
-    gx = torch.empty_like(x2)
+    gx = _lib.rows_empty(x2, *x2.shape)
     _lib_call("fc_radial_mlp_bwd", x2.shape[0], n_in, x2.data_ptr(), w0.data_ptr(), float(s0), w1.data_ptr(),
               float(s1), gh.data_ptr(), gx.data_ptr(), _lib.stream_of(x))
     return gx.reshape(x.shape)
@@ -1155,7 +1155,7 @@ def dense_wgrad(grad_out: Tensor, pre: Optional[Tensor], act: int, x: Tensor, sc
     n_ws = lib.fc_dense_wgrad_workspace(n, k, m, int(need_bias))
     if n_ws < 0:
         _lib.check(-n_ws, "fc_dense_wgrad_workspace")
-    buf = go.new_empty(max(int(n_ws), 1))
+    buf = _lib.rows_empty(go, max(int(n_ws), 1))
     _lib_call("fc_dense_wgrad", n, k, m, go.data_ptr(), _lib.ptr(pr), int(act), xx.data_ptr(), float(scale),
               gw.data_ptr(), _lib.ptr(gb), buf.data_ptr(), int(n_ws), _lib.stream_of(go))
     return (gw if need_weight else None), gb

@@ -238,3 +238,22 @@ def test_linear_and_irreps_op_schemas_follow_reference():
     # the build's own residual / alpha variants live under names of their own
     assert [a.name for a in torch.ops.flashcart.equiv_linear_fwd.default._schema.arguments][-2:] == ["alpha",
                                                                                                       "residual"]
+
+
+def test_rounded_row_allocations():
+    from flashcart_amd import _lib
+    assert [_lib.rounded_rows(n) for n in (0, 1, 15, 16, 17, 31, 32, 33)] == [0, 1, 15, 16, 18, 32, 32, 36]
+    for n in [1080166, 1081496, 1100110, 1179648, 1179649, 7, 4096, 123457]:
+        r = _lib.rounded_rows(n)
+        q = 1 << max(n.bit_length() - 4, 0)
+        assert n <= r < n + q and r % q == 0 and (r - n) <= n / 8
+    # edge counts of an MD run drifting by ~0.1% per step share one rounded size
+    assert len({_lib.rounded_rows(n) for n in range(1080166, 1179648, 997)}) == 1
+    like = torch.empty(0)
+    small = _lib.rows_empty(like, 1000, 16)
+    assert small.shape == (1000, 16) and small.untyped_storage().nbytes() == 1000 * 16 * 4
+    big = _lib.rows_empty(like, 1080166, 16)
+    assert big.shape == (1080166, 16) and big.is_contiguous() and big.storage_offset() == 0
+    assert big.untyped_storage().nbytes() == _lib.rounded_rows(1080166) * 16 * 4
+    flat = _lib.rows_empty(like, 20_000_000, dtype=torch.int32)
+    assert flat.shape == (20_000_000,) and flat.dtype == torch.int32
