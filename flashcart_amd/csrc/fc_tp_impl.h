@@ -604,8 +604,8 @@ int launch_tp(const TPArgs& g, bool conv, bool bwd, hipStream_t stream) {
     const size_t per_edge = reduce ? sizeof(float) * (threads / 64) * (ncomp(L1) + ncomp(L2)) : 0;
     if constexpr (!SYM && L2 >= 1) {
       // interaction-layer shape: the compile-time specialisation
-      if (conv && bc2 && !g.reduced && g.grad_w && g.grad_in2 && g.F1 == g.C && threads == g.C &&
-          (g.C == 64 || g.C == 128)) {
+      if (conv && bc2 && !g.reduced && !g.shared_w && g.grad_w && g.grad_in2 && g.F1 == g.C && threads == g.C &&
+          (g.C == 64 || g.C == 128)) {  // per-edge weights: the kernel reads w[e] rows
         const bool n1 = g.grad_in1 != nullptr;
         if (g.C == 128) {
           if (n1) hipLaunchKernelGGL((tp_bwd_conv_kernel<L1, L2, LO, SYM, 128, true>), grid, block, 0, stream, g);

@@ -121,6 +121,13 @@ def test_tp_conv_reduced_shared():
     _tp_case(2, 2, 2, 8, 1, shared=True, reduced=True, conv=True, seed=3)
 
 
+@pytest.mark.parametrize("f1", [64, 128])
+def test_tp_conv_shared_weights_full_width(f1):
+    """Shared weights at the interaction layer's channel counts: the per-edge-weight backward
+    specialisation does not apply (it reads one weight row per edge)."""
+    _tp_case(2, 3, 3, f1, 1, shared=True, conv=True, seed=5)
+
+
 ROW_CASES = [
     dict(l1=3, l2=3, lo=3, f1=8, f2=8, shared=True), dict(l1=3, l2=3, lo=2, f1=8, f2=8, shared=True),
     dict(l1=3, l2=3, lo=0, f1=8, f2=8, shared=True), dict(l1=3, l2=0, lo=3, f1=8, f2=1, shared=True),
