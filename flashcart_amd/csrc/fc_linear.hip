@@ -771,22 +771,22 @@ int launch_gemm(GemmBatch gb, int n_ranks, hipStream_t s) {
   return launch_gemm_cfg<64, 128, 1, 4, 1>(gb, n_ranks, s);
 }
 
-// dst[r, off:off+width] = src ? src[r, off:off+width] : 0 (same row stride)
+// dst[r, off:off+width] = src ? src[r, off:off+width] : 0 (same row stride): one wave per
+// row, lanes along the columns (no per-element division)
 __global__ void fill_rows_kernel(int64_t rows, int64_t row_stride, int64_t off, int64_t width,
                                  const float* __restrict__ src, float* __restrict__ dst) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= rows * width) return;
-  const int64_t k = (t / width) * row_stride + off + (t % width);
-  dst[k] = src ? src[k] : 0.f;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const int64_t base = r * row_stride + off;
+  for (int64_t c = threadIdx.x & 63; c < width; c += 64) dst[base + c] = src ? src[base + c] : 0.f;
 }
 
 // Output columns the map does not produce: zero, or the residual's values.
 int fill_columns(int64_t rows, int64_t row_stride, int64_t off, int64_t width, const float* residual, float* dst,
                  hipStream_t s) {
   if (rows * width == 0 || residual == dst) return FC_OK;
-  const int bs = 256;
-  hipLaunchKernelGGL(fill_rows_kernel, dim3((unsigned)((rows * width + bs - 1) / bs)), dim3(bs), 0, s, rows,
-                     row_stride, off, width, residual, dst);
+  hipLaunchKernelGGL(fill_rows_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, rows, row_stride, off, width,
+                     residual, dst);
   FC_LAUNCH_CHECK();
   return FC_OK;
 }
@@ -1005,7 +1005,8 @@ __device__ __forceinline__ void wide_body(const float* As, float (*Bs)[WIDE_BN *
 // GUARD = false: every row and column of the block is in range (m a multiple of 64), so
 // the stores are unconditional and the compiler can count them as outstanding rather
 // than wait for them before the next weight chunk is written to LDS. The last, partial
-// row block runs as a separate GUARD = true launch.
+// row block runs as a separate GUARD = true launch. (The radial MLP forward instead takes
+// the guarded body for its partial block inside the one launch; there it costs no spills.)
 template <bool GUARD>
 __global__ void __launch_bounds__(256, 2) gemm_wide_kernel(int64_t n, int m, const float* __restrict__ x,
                                                             const float* __restrict__ w, float scale,
@@ -1155,7 +1156,8 @@ __global__ void __launch_bounds__(256, 2) radial_mlp_fwd_kernel(int64_t n, int n
   __syncthreads();  // reads of h1 and of both weight buffers done before they are overwritten
   acc_to_rows(acc, As, wave, lane, [&](float a) { return silu_r(a * s1); });
   __syncthreads();
-  wide_body<GUARD>(As, Bs, n, m, w2, s2, out, r0);
+  if (GUARD || r0 + WIDE_BM > n) wide_body<true>(As, Bs, n, m, w2, s2, out, r0);
+  else wide_body<false>(As, Bs, n, m, w2, s2, out, r0);
 }
 
 // Input gradient of the two hidden layers: given gh2 = dL/dh2 (n, 64),
@@ -1272,17 +1274,14 @@ extern "C" int fc_radial_mlp_fwd(int64_t n, int32_t n_in, const float* x, const 
   if (((uintptr_t)w2 & 15) != 0) return FC_ERR_SHAPE;  // weight chunks load as float4
   const int64_t blocks = (n + WIDE_BM - 1) / WIDE_BM;
   if (blocks > 0x7fffffff) return FC_ERR_SHAPE;
-  const int64_t full = m % WIDE_BN == 0 ? n / WIDE_BM : 0;
-  if (full > 0) {
-    hipLaunchKernelGGL(radial_mlp_fwd_kernel<false>, dim3((unsigned)full), dim3(256), 0, (hipStream_t)stream, n,
+  // one launch (the partial last row block is guarded inside it)
+  if (m % WIDE_BN == 0)
+    hipLaunchKernelGGL(radial_mlp_fwd_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, n,
                        (int)n_in, x, w0, s0, w1, s1, (int)m, w2, s2, out, (int64_t)0);
-    FC_LAUNCH_CHECK();
-  }
-  if (blocks > full) {
-    hipLaunchKernelGGL(radial_mlp_fwd_kernel<true>, dim3((unsigned)(blocks - full)), dim3(256), 0,
-                       (hipStream_t)stream, n, (int)n_in, x, w0, s0, w1, s1, (int)m, w2, s2, out, full);
-    FC_LAUNCH_CHECK();
-  }
+  else
+    hipLaunchKernelGGL(radial_mlp_fwd_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, n,
+                       (int)n_in, x, w0, s0, w1, s1, (int)m, w2, s2, out, (int64_t)0);
+  FC_LAUNCH_CHECK();
   return FC_OK;
 }
 
