@@ -762,8 +762,15 @@ int launch_gemm(GemmBatch gb, int n_ranks, hipStream_t s) {
   // Measured on the model's shapes (MI355X, fp32): the pipelined kernel with 16x16x4 blocks
   // runs 3-13% faster than the register-staged one; 128 x 64 tiles for maps at most 64 wide
   // (the radial output layer's input gradient: 112 vs 99 TFLOP/s), 64 x 128 otherwise.
+  // Launches with fewer 128-row tiles than two per CU (the 1,536-atom water box) take 64 x 64
+  // tiles instead, for twice the workgroups.
   if (pipe_ok(gb, n_ranks)) {
-    if (max_n <= 64) return launch_pipe_cfg<128, 64, 4, 1, 16>(gb, n_ranks, s);
+    if (max_n <= 64) {
+      int64_t tiles128 = 0;
+      for (int l = 0; l < n_ranks; ++l) tiles128 += (gb.r[l].M + 127) / 128;
+      if (tiles128 < 2 * (int64_t)device_cu_count()) return launch_pipe_cfg<64, 64, 2, 2, 16>(gb, n_ranks, s);
+      return launch_pipe_cfg<128, 64, 4, 1, 16>(gb, n_ranks, s);
+    }
     return launch_pipe_cfg<64, 128, 2, 2, 16>(gb, n_ranks, s);
   }
   if (max_n <= 64) return launch_gemm_cfg<64, 64, 2, 2, 1>(gb, n_ranks, s);
