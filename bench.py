@@ -36,13 +36,13 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-# HBM bytes per launch of the dominant kernel from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of
-# `bench.py --kernel-only` (first step graph, E = 1,080,166), each counter scaled by its reading for
-# a 2 GiB elementwise copy (FETCH x2.000, WRITE x1.000); see profiles/tp_conv_fwd_l1_fcc25k_hbm_traffic.md.
-MEASURED_TRAFFIC_BYTES = 11.77e9
-# The same for the layer-1 backward op (tp_bwd_conv_kernel 27.248 GB + segment_rows_kernel 5.116 GB) from
-# the `bench.py --profile-step` counter runs; see profiles/fcc25k_L3_C128_kernel_hbm_mfma.md.
-MEASURED_TRAFFIC_BWD_BYTES = 32.36e9
+# HBM bytes per launch of the dominant kernel from rocprofv3 memory-request counters of
+# `bench.py --kernel-only` (first step graph, E = 1,080,166): read bytes by request size
+# (TCC_EA0_RDREQ_32B/64B/128B), written bytes from TCC_EA0_WRREQ / WRREQ_64B; a 2 GiB copy reads
+# back 2.148 / 2.147 GB. See profiles/hbm_counter_method.md and profiles/tp_conv_l1_fcc25k_kernel_only.md.
+MEASURED_TRAFFIC_BYTES = 11.67e9
+# The same for the layer-1 backward op (tp_bwd_conv_kernel 27.220 GB + segment_rows_kernel 5.104 GB).
+MEASURED_TRAFFIC_BWD_BYTES = 32.32e9
 from flashcart_amd.data.synthetic import FCC25K_R_MAX as R_MAX  # noqa: E402
 from flashcart_amd.data.synthetic import FCC25K_SIGMA_STEP as SIGMA_STEP  # noqa: E402
 from flashcart_amd.data.synthetic import FCC25K_SKIN as SKIN  # noqa: E402
@@ -105,10 +105,10 @@ def device_time_ms(fn, reps, dev, warmup=3):
 
 
 def calibration_kernels(dev, reps):
-    """Two kernels of known HBM bytes for scaling the FETCH_SIZE / WRITE_SIZE counters: a
-    streaming copy (2 GiB read, 2 GiB written) and a row gather by a random permutation
-    (index_select of 2^22 rows of 512 B: 2 GiB of rows + 32 MiB of int64 indices read,
-    2 GiB written), the access pattern of the convolution's in1 rows."""
+    """Two kernels of known HBM bytes that check the memory-request counters: a streaming copy
+    (2 GiB read, 2 GiB written) and a row gather by a random permutation (index_select of 2^22
+    rows of 512 B: 2 GiB of rows + 32 MiB of int64 indices read, 2 GiB written), the access
+    pattern of the convolution's in1 rows."""
     src = torch.ones(2 ** 29, device=dev)  # 2 GiB
     dst = torch.empty_like(src)
     rows = src.view(2 ** 22, 128)
@@ -559,7 +559,8 @@ def main():
     ap.add_argument("--workload", choices=WORKLOADS, default="cfg4_fcc25k",
                     help="cfg4_fcc25k (the metric's configuration) or one of the other BASELINE configurations")
     ap.add_argument("--kernel-only", action="store_true",
-                    help="only launch the dominant kernel (5x) and a 2 GiB device copy (5x), for counter runs")
+                    help="only launch the layer-1 convolution forward and backward ops (7x each) and the two "
+                         "calibration kernels (5x each), for counter runs")
     ap.add_argument("--profile-step", action="store_true",
                     help="two energy+forces steps on the first step graph, then the calibration kernels (2x), "
                          "for per-kernel counter runs")

@@ -257,3 +257,31 @@ def test_rounded_row_allocations():
     assert big.untyped_storage().nbytes() == _lib.rounded_rows(1080166) * 16 * 4
     flat = _lib.rows_empty(like, 20_000_000, dtype=torch.int32)
     assert flat.shape == (20_000_000,) and flat.dtype == torch.int32
+
+
+def test_alias_as_flashcart():
+    """The reference's module names resolve to this package after alias_as_flashcart()."""
+    import sys
+
+    import flashcart_amd
+
+    saved = {k: v for k, v in sys.modules.items() if k == "flashcart" or k.startswith("flashcart.")}
+    try:
+        for k in saved:
+            del sys.modules[k]
+        flashcart_amd.alias_as_flashcart()
+        import flashcart
+        import flashcart.data
+        import flashcart.o3
+        from flashcart.model import FlashCartPotential
+        from flashcart.nn import InteractionLayer
+        from flashcart.utils.lammps import lammps_data_slot
+
+        assert flashcart is flashcart_amd and flashcart.o3.TensorProduct is flashcart_amd.o3.TensorProduct
+        assert FlashCartPotential.__module__.startswith("flashcart_amd.model")
+        assert InteractionLayer is flashcart_amd.nn.InteractionLayer
+        assert flashcart.data.NeighborList is flashcart_amd.data.NeighborList and callable(lammps_data_slot)
+    finally:
+        for k in [k for k in sys.modules if k == "flashcart" or k.startswith("flashcart.")]:
+            del sys.modules[k]
+        sys.modules.update(saved)
