@@ -378,15 +378,22 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmBatch gb) {
 // activation epilogue.
 //
 // LDS layout per stage: A, and B when k-contiguous (trans_b), as rows of 8 chunks of 4
-// floats (one 32-float K step); chunk c of row r sits at position c ^ pipe_swz(r), so the 16
-// (or 8) rows read together at one chunk fall in distinct banks. A k-major B (the input
-// gradient) sits as 32 rows of BN floats; chunk p of row k at p ^ (8 * ((k / 4) % 2)), which
-// puts the two half-waves' rows k and k + 4 in different bank halves.
+// floats (one 32-float K step); chunk c of row r sits at position c ^ ((r / 2) % 8), so the
+// rows read together at one chunk fall in distinct banks (SQ_LDS_BANK_CONFLICT reads 0; the
+// (r % 8)-based swizzle it replaces stalled the LDS ~0.55 of the busy cycles). A k-major B (the input
+// gradient) sits as 32 rows of BN floats; chunk p of row k at p ^ pipe_kswz(k), which puts the
+// rows that the lane groups of one k step read (4 apart) in different parts of the bank row.
 // K-step mapping: MFMA k-pair q (0..3) of quad s4 (0..3) takes k = 8 s4 + 4 h + q in lane
 // half h, in A and B alike, so each lane reads four k values as one 128-bit chunk.
 
-__device__ __forceinline__ int pipe_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
-__device__ __forceinline__ int pipe_kswz(int k) { return ((k >> 2) & 1) << 3; }
+__device__ __forceinline__ int pipe_swz(int r) { return (r >> 1) & 7; }
+// k-major B rows: the lane groups reading one k step sit 4 rows apart (2 groups for 32x32x2
+// blocks, 4 for 16x16x4); XOR-ing the chunk index by the group puts each group's 128-byte
+// (32x32) or 64-byte (16x16) column run in its own part of the bank row.
+template <int MI>
+__device__ __forceinline__ int pipe_kswz(int k) {
+  return MI == 32 ? ((k >> 2) & 1) << 3 : ((k >> 2) & 3) << 2;
+}
 
 // One 16-byte direct load per lane into LDS at lds + 16 * lane (lds: byte offset, wave-uniform).
 // Issued as inline assembly so that the compiler does not track it: it would otherwise wait for
@@ -488,7 +495,7 @@ __global__ void __launch_bounds__(256, (BM + BN) * 32 * 4 * 3 <= 80 * 1024 ? 2 :
     for (int j = 0; j < B_DMA; ++j) {
       const int s = (j * 4 + wave) * 64 + lane;
       if constexpr (KB) {
-        const int kk = s / BQ, p = (s % BQ) ^ pipe_kswz(kk);
+        const int kk = s / BQ, p = (s % BQ) ^ pipe_kswz<MI>(kk);
         const int col = min(pt.c0 + 4 * p, g.N - 4);
         b_src[j] = g.B + (int64_t)kk * g.N + col;
       } else {
@@ -546,7 +553,7 @@ __global__ void __launch_bounds__(256, (BM + BN) * 32 * 4 * 3 <= 80 * 1024 ? 2 :
         const int col = wn * TN + j * MI + (lane & (MI - 1));
         if constexpr (KB) {
           const int k = 4 * ch;  // rows k..k+3 share (k / 4) % 2
-          const float* p = bs + k * BN + 4 * ((col >> 2) ^ pipe_kswz(k)) + (col & 3);
+          const float* p = bs + k * BN + 4 * ((col >> 2) ^ pipe_kswz<MI>(k)) + (col & 3);
           b4[j] = make_float4(p[0], p[BN], p[2 * BN], p[3 * BN]);
         } else {
           b4[j] = *reinterpret_cast<const float4*>(bs + col * 32 + 4 * (ch ^ pipe_swz(col)));
