@@ -983,13 +983,21 @@ __device__ __forceinline__ void wide_body(const float* As, float (*Bs)[WIDE_BN *
 #pragma unroll
       for (int v = 0; v < 16; ++v) cur[j][v] = 0.f;
     const float* bs = Bs[buf] + (lane & 31) * WIDE_P + half;
+    // operands of MFMA group s4 + 1 are read from LDS while group s4 multiplies
+    float4 a4n = *reinterpret_cast<const float4*>(as), b4n[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) b4n[j] = *reinterpret_cast<const float4*>(bs + j * 32 * WIDE_P);
 #pragma unroll
     for (int s4 = 0; s4 < 8; ++s4) {  // 32 MFMA steps, four per 128-bit read
-      const int o = 4 * s4;
-      const float4 a4 = *reinterpret_cast<const float4*>(as + o);
-      float4 b4[2];
+      const float4 a4 = a4n;
+      float4 b4[2] = {b4n[0], b4n[1]};
+      if (s4 + 1 < 8) {
+        const int o = 4 * (s4 + 1);
+        a4n = *reinterpret_cast<const float4*>(as + o);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) b4[j] = *reinterpret_cast<const float4*>(bs + j * 32 * WIDE_P + o);
+        for (int j = 0; j < 2; ++j) b4n[j] = *reinterpret_cast<const float4*>(bs + j * 32 * WIDE_P + o);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // keep those reads ahead of this group's MFMAs
 #pragma unroll
       for (int q = 0; q < 4; ++q)
 #pragma unroll
@@ -1058,13 +1066,23 @@ __device__ __forceinline__ void mfma_k64(const float* as, const float* bs, float
   for (int j = 0; j < NJ; ++j)
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[j][v] = 0.f;
+  // operands of group s4 + 1 are read from LDS while group s4 multiplies
+  float4 a4n = *reinterpret_cast<const float4*>(as), b4n[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) b4n[j] = *reinterpret_cast<const float4*>(bs + j * 32 * WIDE_P);
 #pragma unroll
   for (int s4 = 0; s4 < 8; ++s4) {
     if (s4 >= ns4) break;  // uniform
-    const float4 a4 = *reinterpret_cast<const float4*>(as + 4 * s4);
+    const float4 a4 = a4n;
     float4 b4[NJ];
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) b4[j] = *reinterpret_cast<const float4*>(bs + j * 32 * WIDE_P + 4 * s4);
+    for (int j = 0; j < NJ; ++j) b4[j] = b4n[j];
+    if (s4 + 1 < ns4) {
+      a4n = *reinterpret_cast<const float4*>(as + 4 * (s4 + 1));
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) b4n[j] = *reinterpret_cast<const float4*>(bs + j * 32 * WIDE_P + 4 * (s4 + 1));
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep those reads ahead of this group's MFMAs
 #pragma unroll
     for (int q = 0; q < 4; ++q)
 #pragma unroll
