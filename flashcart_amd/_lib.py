@@ -35,7 +35,7 @@ class EdgeDesc(ctypes.Structure):
 class CSR(ctypes.Structure):
     _fields_ = [
         ("n_nodes", c_i64), ("n_edges", c_i64), ("idx_j", c_vp), ("rowptr", c_vp),
-        ("sender_perm", c_vp), ("sender_ptr", c_vp), ("n_sender_rows", c_i64),
+        ("sender_perm", c_vp), ("sender_ptr", c_vp), ("n_sender_rows", c_i64), ("pair_slot", c_vp),
     ]
 
 
@@ -74,6 +74,8 @@ _SIGNATURES = {
     "fc_edge_geometry_dbwd": (c_int, [ctypes.POINTER(EdgeDesc), c_i64] + [c_vp] * 14),
     "fc_csr_from_sorted": (c_int, [c_i64, c_vp, c_i64, c_vp, c_vp]),
     "fc_edge_grad_to_nodes": (c_int, [ctypes.POINTER(CSR), c_vp, c_vp, c_vp]),
+    "fc_edge_pairs_workspace": (c_i64, [c_i64]),
+    "fc_edge_pairs": (c_int, [ctypes.POINTER(CSR), c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp]),
     "fc_tp_num_paths": (c_int, [ctypes.POINTER(TPDesc)]),
     "fc_tp_out_dim": (c_i64, [ctypes.POINTER(TPDesc)]),
     "fc_tp_fwd": (c_int, [ctypes.POINTER(TPDesc), ctypes.POINTER(CSR), c_i64, c_vp, c_vp, c_vp, c_f32, c_vp, c_vp]),
@@ -216,6 +218,6 @@ def radial_desc(basis: int, n_radial: int, r_min: float, r_max: float, poly_orde
 
 
 def csr_struct(n_nodes: int, n_edges: int, idx_j, rowptr, sender_perm=None, sender_ptr=None,
-               n_sender_rows: Optional[int] = None) -> CSR:
+               n_sender_rows: Optional[int] = None, pair_slot=None) -> CSR:
     return CSR(int(n_nodes), int(n_edges), ptr(idx_j), ptr(rowptr), ptr(sender_perm), ptr(sender_ptr),
-               int(n_nodes if n_sender_rows is None else n_sender_rows))
+               int(n_nodes if n_sender_rows is None else n_sender_rows), ptr(pair_slot))

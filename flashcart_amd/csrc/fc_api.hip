@@ -115,9 +115,10 @@ extern "C" int fc_tp_fwd(const fc_tp_desc* d, const fc_csr* graph, int64_t n_row
   if (conv && (!graph->rowptr || !graph->idx_j)) return FC_ERR_NULL;
   const int64_t items = conv ? graph->n_edges : rows;
   if (items > 0 && (!in1 || !in2 || !w)) return FC_ERR_NULL;
+  if (conv && graph->pair_slot && d->shared_weights) return FC_ERR_BAD_DESC;
   TPArgs g = make_args(d, rows);
   g.in1 = in1; g.in2 = in2; g.w = w; g.out = out; g.alpha = alpha;
-  if (conv) { g.idx_j = graph->idx_j; g.rowptr = graph->rowptr; }
+  if (conv) { g.idx_j = graph->idx_j; g.rowptr = graph->rowptr; g.wslot = graph->pair_slot; }
   return dispatch(d, g, conv, false, (hipStream_t)stream);
 }
 
@@ -151,6 +152,7 @@ extern "C" int fc_tp_bwd(const fc_tp_desc* d, const fc_csr* graph, int64_t n_row
   if (conv && gin1 && (!graph->sender_perm || !graph->sender_ptr)) return FC_ERR_NULL;
   if (rows > 0 && !go) return FC_ERR_NULL;
   if (items > 0 && (!in1 || !in2 || !w)) return FC_ERR_NULL;
+  if (conv && graph->pair_slot && d->shared_weights) return FC_ERR_BAD_DESC;
 
   TPArgs g = make_args(d, rows);
   g.in1 = in1; g.in2 = in2; g.w = w; g.grad_out = go; g.alpha = alpha;
@@ -163,7 +165,7 @@ extern "C" int fc_tp_bwd(const fc_tp_desc* d, const fc_csr* graph, int64_t n_row
   g.grad_in1 = conv ? msg : gin1;
   g.grad_in2 = gin2;
   g.grad_w = (gw && d->shared_weights) ? wtmp : gw;
-  if (conv) { g.idx_j = graph->idx_j; g.rowptr = graph->rowptr; }
+  if (conv) { g.idx_j = graph->idx_j; g.rowptr = graph->rowptr; g.wslot = graph->pair_slot; }
   if (rows > 0) {
     st = dispatch(d, g, conv, true, s);
     if (st != FC_OK) return st;

@@ -25,6 +25,8 @@ struct TPArgs {
   const float* w;
   const int32_t* idx_j;    // conv: sender per edge
   const int32_t* rowptr;   // conv: receiver CSR, n_rows + 1 entries
+  const int32_t* wslot;    // conv, optional: edge e reads weight row wslot[e] / 2 and writes its
+                           // weight gradient to row wslot[e] (the two edges of a pair share a row)
   const float* grad_out;   // bwd only
   float* out;              // fwd output
   float* grad_in1;         // bwd: rows mode -> grad wrt in1 rows; conv mode -> per-edge messages
@@ -51,6 +53,14 @@ struct TPConfig {
   static constexpr int NOUT_RED = PL::NOUT_RED;
 };
 
+// Weight row of edge e, and the row of its weight gradient (pair-major when edges share weights).
+__device__ __forceinline__ int64_t weight_row(const TPArgs& g, int64_t e) {
+  return g.wslot ? (int64_t)(g.wslot[e] >> 1) : e;
+}
+__device__ __forceinline__ int64_t weight_grad_row(const TPArgs& g, int64_t e) {
+  return g.wslot ? (int64_t)g.wslot[e] : e;
+}
+
 // Operands of one edge (or row) for one lane.
 template <int D1, int D2, int NP>
 struct EdgeOps {
@@ -73,7 +83,7 @@ __device__ __forceinline__ void load_edge(const TPArgs& g, int64_t e, int f1, in
 #pragma unroll
     for (int u = 0; u < D2; ++u) o.y[u] = active ? g.in2[e * s2 + u * g.F2 + f2] : 0.f;
   }
-  const float* wr = g.shared_w ? g.w : g.w + e * (int64_t)NP * g.C;
+  const float* wr = g.shared_w ? g.w : g.w + weight_row(g, e) * (int64_t)NP * g.C;
 #pragma unroll
   for (int i = 0; i < NP; ++i) o.w[i] = active ? wr[i * g.C + fw] : 0.f;
 }
@@ -326,7 +336,7 @@ __global__ void __launch_bounds__(256, 2) tp_bwd_kernel(TPArgs g) {
             float s = 0.f;
 #pragma unroll
             for (int b = 0; b < T::N1; ++b) s = fmaf(v[b], xp[b], s);
-            if (active) g.grad_w[e * sw + i * C + f] = s;
+            if (active) g.grad_w[weight_grad_row(g, e) * sw + i * C + f] = s;
           }
           if (need1) {
 #pragma unroll
@@ -431,7 +441,7 @@ __global__ void __launch_bounds__(C, 2) tp_bwd_conv_kernel(TPArgs g) {
   auto load = [&](int64_t e, EdgeOps<D1, D2, NP>& o) {
     const int64_t j = (int64_t)g.idx_j[e];
     const float* xr = g.in1 + j * S1 + f;
-    const float* wr = g.w + e * SW + f;
+    const float* wr = g.w + weight_row(g, e) * SW + f;
 #pragma unroll
     for (int u = 0; u < D1; ++u) o.x[u] = xr[u * C];
 #pragma unroll
@@ -444,7 +454,7 @@ __global__ void __launch_bounds__(C, 2) tp_bwd_conv_kernel(TPArgs g) {
     for (int u = 0; u < D1; ++u) gx[u] = 0.f;
 #pragma unroll
     for (int u = 0; u < R2; ++u) gy[u] = 0.f;
-    float* gwr = g.grad_w + e * SW + f;
+    float* gwr = g.grad_w + weight_grad_row(g, e) * SW + f;
     static_for<NP>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
       constexpr PathDesc P = PL::at(i);

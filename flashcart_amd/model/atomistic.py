@@ -63,18 +63,33 @@ class _PredictReplay:
         self.flags = flags
         self.topology = None
         self._src_edges = None
+        self.pair_counts = None  # device counters of the edge pairing replayed with the topology
+        self.paired = False
         side = torch.cuda.Stream()  # default priority
         side.wait_stream(torch.cuda.current_stream())
         if not gd.get("lammps_exchange", False):
-            from flashcart_amd.o3._graph import build_graph
+            from flashcart_amd.o3._graph import build_graph, launch_edge_pairs, pairable, pairs_complete
             n_rows = int(self.inputs["atom_types"].shape[0])
+            want_pairs, pair_shifts = (model.edge_pair_shifts(model._prepare_predict_graph(base, *flags))
+                                       if hasattr(model, "edge_pair_shifts") else (False, None))
             with torch.cuda.stream(side):
-                build_graph(self.inputs["edge_index"], n_rows)  # warm-up outside the capture
+                warm = build_graph(self.inputs["edge_index"], n_rows)  # warm-up outside the capture
+                want_pairs = want_pairs and pairable(warm, pair_shifts)
+                if want_pairs:
+                    launch_edge_pairs(warm, pair_shifts)
             torch.cuda.current_stream().wait_stream(side)
             self.topology = torch.cuda.CUDAGraph()
             with torch.cuda.graph(self.topology):
-                base["csr"] = build_graph(self.inputs["edge_index"], n_rows)
+                csr = build_graph(self.inputs["edge_index"], n_rows)
+                pend = launch_edge_pairs(csr, pair_shifts) if want_pairs else None
+                base["csr"] = csr
             self.topology.replay()  # capturing records the work without running it
+            if pend is not None:
+                # the captured prediction takes the pairing whenever this first edge list pairs up;
+                # a later edge list whose pairing state differs is evaluated eagerly (__call__)
+                self.pair_counts = pend[1]
+                self.paired = pairs_complete(pend[1], csr.n_edges)
+                csr.set_edge_pairs(pair_shifts, pend[0] if self.paired else None)
             self._src_edges = (tensors["edge_index"], tensors["edge_index"]._version)
 
         def run():
@@ -92,7 +107,7 @@ class _PredictReplay:
 
     def __call__(self, tensors):
         edges = tensors["edge_index"]
-        same_edges = (self.topology is not None and self._src_edges[0] is edges
+        same_edges = (self.topology is not None and self._src_edges is not None and self._src_edges[0] is edges
                       and self._src_edges[1] == edges._version)
         for k, buf in self.inputs.items():
             if not (same_edges and k == "edge_index"):
@@ -100,6 +115,11 @@ class _PredictReplay:
         if self.topology is not None and not same_edges:
             self.topology.replay()
             self._src_edges = (edges, edges._version)
+            if self.pair_counts is not None:
+                from flashcart_amd.o3._graph import pairs_complete
+                if pairs_complete(self.pair_counts, int(edges.shape[1])) != self.paired:
+                    self._src_edges = None  # replay the topology again next time
+                    return None
         self.graph.replay()
         return {k: v.clone() for k, v in self.outputs.items()}
 
@@ -166,7 +186,11 @@ class AtomisticModel(nn.Module):
         if entry is None:
             entry = _PredictReplay(self, gd, tensors, flags)
             cache[key] = entry
-        return entry(tensors)
+        out = entry(tensors)
+        if out is None:  # the captured edge pairing does not hold for this edge list
+            gd = self._prepare_predict_graph(gd, compute_forces, compute_stress, compute_edge_forces)
+            return self._predict_impl(gd, compute_forces, compute_stress, compute_edge_forces)
+        return out
 
     def _prepare_predict_graph(self, graph, compute_forces, compute_stress, compute_edge_forces):
         gd = _graph_dict(graph)

@@ -25,6 +25,7 @@ from flashcart_amd.nn.layers import (
     ProductLayer,
     ScaleShiftEnergyLayer,
 )
+from flashcart_amd.nn import fused
 from flashcart_amd.nn.radial import ChebyshevBasis, PolynomialCutoff
 from flashcart_amd.o3 import _ops
 from flashcart_amd.o3._graph import GraphCSR, build_graph
@@ -121,6 +122,23 @@ class FlashCartPotential(AtomisticModel):
                 src.csr = csr
         return csr
 
+    def wants_edge_pairs(self, positions: torch.Tensor) -> bool:
+        """True when an interaction layer would form its radial weights once per edge pair
+        (``fused.paired_conv_applies``); the edge list is then paired with its reverse edges."""
+        return any(fused.paired_conv_applies(m, positions) for m in self.interactions)
+
+    def edge_pair_shifts(self, graph: Dict[str, Any]):
+        """(True, the shifts the edge list is paired by, or None) when ``forward`` would pair the
+        edges of this graph dict, else (False, None)."""
+        if graph.get("vectors") is not None or bool(graph.get("lammps_exchange", False)):
+            return False, None
+        if not self.wants_edge_pairs(graph["positions"]):
+            return False, None
+        use_shifts = graph.get("use_shifts", True)
+        if not isinstance(use_shifts, bool):
+            use_shifts = uses_periodic_shifts(use_shifts)
+        return True, (graph["shifts"] if use_shifts else None)
+
     def forward(self, graph: Dict[str, Any]) -> torch.Tensor:
         if not isinstance(graph, Mapping):
             raise TypeError(f"{self.__class__.__name__}.forward expects a tensor dictionary. Use predict() for graphs.")
@@ -138,12 +156,16 @@ class FlashCartPotential(AtomisticModel):
         basis = self.radial_basis.basis_kind
         geo = (self.l_max_edge_attrs, basis, self.n_radial, float(self.r_min), self.r_max, self.cutoff_poly_order)
         vectors = graph.get("vectors")
+        pairs = None
         if vectors is None:
             positions = graph["positions"]
             use_shifts = graph.get("use_shifts", True)
             if not isinstance(use_shifts, bool):
                 use_shifts = uses_periodic_shifts(use_shifts)
-            sv = shift_vectors(graph["cell"], graph["shifts"], edge_index[0], batch) if use_shifts else None
+            if not is_lammps and self.wants_edge_pairs(positions):
+                pairs = csr.edge_pairs(graph["shifts"] if use_shifts else None)
+            sv = shift_vectors(graph["cell"], graph["shifts"], edge_index[0], batch,
+                               antisymmetric=pairs is not None) if use_shifts else None
             edge_attrs, edge_feats, envelope = _ops.edge_geometry(
                 positions, sv, csr.idx_i, csr.idx_j, None, csr.rowptr, csr.sender_perm, csr.sender_ptr, *geo)
         else:
@@ -158,7 +180,7 @@ class FlashCartPotential(AtomisticModel):
                 msg = lammps_exchange_features(node_feats, nlocal, ntotal)
             feats = interaction(msg, edge_attrs, edge_feats, edge_index, envelope,
                                 atom_types=atom_types if not self.element_agnostic_interaction else None,
-                                out_nodes=nlocal, graph=csr)
+                                out_nodes=nlocal, graph=csr, edge_pairs=pairs)
             if self.nonlinearity:
                 feats = self.nonlinearities[k](feats)
             if self.use_products:

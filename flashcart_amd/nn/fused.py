@@ -212,3 +212,77 @@ def radial_mlp_applies(mlp: torch.nn.Sequential, x: Tensor) -> bool:
 
 def radial_mlp(mlp: torch.nn.Sequential, x: Tensor) -> Tensor:
     return _RadialMLP.apply(x, mlp)
+
+
+class _PairedConv(torch.autograd.Function):
+    """Radial MLP + convolution tensor product of an interaction layer over edge pairs.
+
+    The radial MLP input of an edge depends only on its length, which both edges of a pair
+    (i <- j, S) / (j <- i, -S) share bitwise, so the weights are formed once per pair
+    (``x``: the MLP inputs of the pairs' lower edges) and both edges read them
+    (``tp_fwd(..., pair_slot)``): half the MLP work and half the weight stream written. The
+    forward output equals the per-edge path's. Backward: the convolution's weight gradient
+    comes out pair-major and the output layer's input gradient sums each pair inside its
+    GEMM (``dense_bwd_pairs``); the hidden layers' backward then runs over the pairs.
+    Reference: ``nn/layers.py:351-369`` (the MLP of every edge, then the convolution).
+    """
+
+    @staticmethod
+    def forward(ctx, in1: Tensor, in2: Tensor, x: Tensor, layer, graph, slot: Tensor, alpha: float) -> Tensor:
+        l0, l1, l2 = layer.radial_mlp[0], layer.radial_mlp[2], layer.radial_mlp[4]
+        w = _ops.radial_mlp_fwd(x, l0.weight, l0._scale, l1.weight, l1._scale, l2.weight, l2._scale)
+        tp = layer.tp
+        out = _ops.tp_fwd(in1, in2, w, graph.idx_i, graph.idx_j, tp.in1_l_max, tp.in2_l_max, tp.out_l_max,
+                          tp.in1_features, tp.in2_features, tp.symmetric_product, tp.shared_weights, *tp.op_meta,
+                          tp.reduce_paths, graph.rowptr, graph.sender_perm, graph.sender_ptr, float(alpha), slot)
+        ctx.save_for_backward(in1, in2, x, w, slot)
+        ctx.layer, ctx.graph, ctx.alpha = layer, graph, float(alpha)
+        return out
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, g: Tensor):
+        in1, in2, x, w, slot = ctx.saved_tensors
+        layer, graph = ctx.layer, ctx.graph
+        n1, n2, nx = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[2]
+        tp = layer.tp
+        g1, g2, gw = _ops.tp_bwd(g.contiguous(), in1, in2, w, graph.idx_i, graph.idx_j, tp.in1_l_max, tp.in2_l_max,
+                                 tp.out_l_max, tp.in1_features, tp.in2_features, tp.symmetric_product,
+                                 tp.shared_weights, *tp.op_meta, tp.reduce_paths, bool(n1), bool(n2), bool(nx),
+                                 graph.rowptr, graph.sender_perm, graph.sender_ptr, ctx.alpha, slot)
+        gx = None
+        if nx:
+            l0, l1, l2 = layer.radial_mlp[0], layer.radial_mlp[2], layer.radial_mlp[4]
+            gh2 = _ops.dense_bwd_pairs(gw, l2.weight, l2._scale)
+            del gw
+            gx = _ops.radial_mlp_bwd(gh2, x, l0.weight, l0._scale, l1.weight, l1._scale)
+        return (g1 if n1 else None), (g2 if n2 else None), gx, None, None, None, None
+
+
+def paired_conv_applies(layer, node_feats: Tensor) -> bool:
+    """True when an interaction layer may form its radial weights once per edge pair: the
+    MLP input is the edge length alone (no element embeddings), the radial MLP has the fused
+    kernel's shape, the convolution takes per-edge weights, no parameter of the MLP needs a
+    gradient and no second derivative is wanted."""
+    if getattr(_state, "off", False) or torch.compiler.is_compiling():
+        return False
+    if layer.emb_i is not None or layer.tp.shared_weights or not node_feats.is_cuda:
+        return False
+    mlp = layer.radial_mlp
+    if any(p.requires_grad for p in mlp.parameters()):
+        return False
+    from flashcart_amd.nn.layers import SILU_SCALE, LinearLayer, RescaledSiLULayer
+    mods = list(mlp)
+    if len(mods) != 5 or not all(isinstance(mods[i], LinearLayer) for i in (0, 2, 4)):
+        return False
+    if not all(isinstance(mods[i], RescaledSiLULayer) and mods[i]._scale == SILU_SCALE for i in (1, 3)):
+        return False
+    l0, l1, l2 = mods[0], mods[2], mods[4]
+    if any(m.bias is not None for m in (l0, l1, l2)):
+        return False
+    return (l0.weight.shape[0] == 64 and tuple(l1.weight.shape) == (64, 64) and l2.weight.shape[1] == 64
+            and 1 <= l0.weight.shape[1] <= 64)
+
+
+def paired_conv(layer, in1: Tensor, in2: Tensor, x_pairs: Tensor, graph, pairs, alpha: float) -> Tensor:
+    return _PairedConv.apply(in1, in2, x_pairs, layer, graph, pairs.slot, alpha)

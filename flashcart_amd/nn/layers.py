@@ -16,7 +16,7 @@ import torch.nn.functional as F
 
 from flashcart_amd import o3
 from flashcart_amd.o3 import _ops
-from flashcart_amd.o3._graph import GraphCSR
+from flashcart_amd.o3._graph import EdgePairs, GraphCSR
 from flashcart_amd.nn import fused
 
 SILU_SCALE = 1.6765324703310907      # reference nn/layers.py:23
@@ -191,9 +191,19 @@ class InteractionLayer(nn.Module):
 
     def forward(self, node_feats: torch.Tensor, edge_attrs: torch.Tensor, edge_feats: torch.Tensor,
                 edge_index: torch.Tensor, envelope: torch.Tensor, atom_types: Optional[torch.Tensor] = None,
-                out_nodes: Optional[int] = None, graph: Optional[GraphCSR] = None) -> torch.Tensor:
+                out_nodes: Optional[int] = None, graph: Optional[GraphCSR] = None,
+                edge_pairs: Optional[EdgePairs] = None) -> torch.Tensor:
+        """``edge_pairs`` (with ``graph``): the reverse-edge pairing of a full neighbour list whose
+        edge lengths agree bitwise within each pair; the radial weights are then formed once per
+        pair where ``fused.paired_conv_applies`` (same outputs, half the radial MLP work)."""
         idx_i, idx_j = edge_index[0], edge_index[1]
         residual_feats = node_feats if out_nodes is None else node_feats[:out_nodes]
+        if edge_pairs is not None and graph is not None and fused.paired_conv_applies(self, node_feats):
+            pe = edge_pairs.edge
+            mlp_pairs = edge_feats.index_select(0, pe) * envelope.index_select(0, pe).unsqueeze(-1)
+            aggregated = fused.paired_conv(self, self.linear_first(node_feats), edge_attrs, mlp_pairs, graph,
+                                           edge_pairs, self._inv_sqrt_avg())
+            return self._finish(aggregated, residual_feats, out_nodes)
         if self.emb_i is not None:
             if atom_types is None:
                 raise ValueError(f"atom_types required when n_elements is set. Provided: {atom_types}.")
@@ -208,6 +218,10 @@ class InteractionLayer(nn.Module):
             weights = run_mlp(self.radial_mlp, mlp_input)
         aggregated = self.tp(node_feats, edge_attrs, weights, idx_i, idx_j, graph=graph,
                              alpha=self._inv_sqrt_avg())
+        return self._finish(aggregated, residual_feats, out_nodes)
+
+    def _finish(self, aggregated: torch.Tensor, residual_feats: torch.Tensor,
+                out_nodes: Optional[int]) -> torch.Tensor:
         if out_nodes is not None:
             aggregated = aggregated[:out_nodes]
         if self.skip_projection is not None and self.in1_l_max > 0:

@@ -18,6 +18,24 @@ from flashcart_amd import _lib
 
 
 @dataclass
+class EdgePairs:
+    """Edges (i <- j, S) and (j <- i, -S) of a full neighbour list.
+
+    The radial MLP of an interaction layer reads only the edge length, which is bitwise the
+    same for both edges of a pair when the shift vectors are exact negations of each other
+    (``utils.geometry.shift_vectors(..., antisymmetric=True)``); the pair's weights are then
+    formed once and read by both edges (``fc_csr.pair_slot``). No counterpart in the
+    reference, which forms the weights of every edge (src/flashcart/nn/layers.py:357-364).
+    """
+    slot: torch.Tensor   # int32 (E,): 2p for the lower edge of pair p, 2p + 1 for its reverse
+    edge: torch.Tensor   # int32 (P,): the lower edge of each pair, in edge order
+
+    @property
+    def n_pairs(self) -> int:
+        return int(self.edge.shape[0])
+
+
+@dataclass
 class GraphCSR:
     n_nodes: int           # receiver rows
     n_sender_rows: int     # rows of the sender features (>= n_nodes with ghosts)
@@ -34,6 +52,71 @@ class GraphCSR:
     def struct(self) -> "_lib.CSR":
         return _lib.csr_struct(self.n_nodes, self.n_edges, self.idx_j, self.rowptr, self.sender_perm,
                                self.sender_ptr, self.n_sender_rows)
+
+    def edge_pairs(self, shifts: Optional[torch.Tensor]) -> Optional[EdgePairs]:
+        """The pairing of this edge list (cached per shift tensor), or None when some edge has no
+        unique reverse (ghost senders, half lists, duplicate edges)."""
+        cache = self.__dict__.setdefault("_pairs", {})
+        key = _shift_key(shifts)
+        if key not in cache:
+            cache.clear()
+            cache[key] = find_edge_pairs(self, shifts)
+        return cache[key]
+
+    def set_edge_pairs(self, shifts: Optional[torch.Tensor], pairs: Optional[EdgePairs]) -> None:
+        """Record the pairing of this edge list for ``shifts`` (computed elsewhere, e.g. in a graph)."""
+        self.__dict__["_pairs"] = {_shift_key(shifts): pairs}
+
+
+def _shift_key(shifts: Optional[torch.Tensor]):
+    return None if shifts is None else (shifts.data_ptr(), tuple(shifts.shape), shifts._version)
+
+
+def pairable(csr: GraphCSR, shifts: Optional[torch.Tensor]) -> bool:
+    """Shapes and types under which ``fc_edge_pairs`` can pair the whole edge list."""
+    n_edges = csr.n_edges
+    if n_edges == 0 or n_edges % 2:
+        return False
+    return shifts is None or (not shifts.is_floating_point() and not shifts.is_complex()
+                              and tuple(shifts.shape) == (n_edges, 3))
+
+
+def launch_edge_pairs(csr: GraphCSR, shifts: Optional[torch.Tensor]):
+    """Launch ``fc_edge_pairs`` without waiting for it (usable under HIP graph capture):
+    returns the pairing and its device counters [unpaired edges, pairs]; the pairing is valid
+    only when the counters read [0, E / 2] (``pairs_complete``)."""
+    n_edges = csr.n_edges
+    dev = csr.idx_i.device
+    sh = None if shifts is None else shifts.to(device=dev, dtype=torch.int32).contiguous()
+    lib = _lib.load()
+    n_ws = int(lib.fc_edge_pairs_workspace(n_edges))
+    if n_ws < 0:
+        _lib.check(-n_ws, "fc_edge_pairs_workspace")
+    slot = torch.empty(n_edges, dtype=torch.int32, device=dev)
+    edge = torch.empty(n_edges // 2, dtype=torch.int32, device=dev)
+    counts = torch.empty(2, dtype=torch.int32, device=dev)
+    ws = torch.empty(max(n_ws, 1), dtype=torch.int32, device=dev)
+    keep = csr.struct()
+    _lib.check(lib.fc_edge_pairs(keep, csr.idx_i.data_ptr(), _lib.ptr(sh), slot.data_ptr(), edge.data_ptr(),
+                                 n_edges // 2, counts.data_ptr(), ws.data_ptr(), n_ws, _lib.stream_of(csr.idx_i)),
+               "fc_edge_pairs")
+    return EdgePairs(slot, edge), counts
+
+
+def pairs_complete(counts: torch.Tensor, n_edges: int) -> bool:
+    """Host check of ``launch_edge_pairs``'s counters (one synchronisation)."""
+    unpaired, n_pairs = (int(v) for v in counts.tolist())
+    return unpaired == 0 and 2 * n_pairs == n_edges
+
+
+def find_edge_pairs(csr: GraphCSR, shifts: Optional[torch.Tensor]) -> Optional[EdgePairs]:
+    """Pair every edge with its reverse on the GPU (``fc_edge_pairs``); None unless all edges
+    pair up. ``shifts``: integer cell translations (E, 3), or None without periodic shifts.
+    Reads the two pair counters back to the host (one synchronisation)."""
+    if not pairable(csr, shifts):
+        return None
+    pairs, counts = launch_edge_pairs(csr, shifts)
+    return pairs if pairs_complete(counts, csr.n_edges) else None
 
 
 def rowptr_from_sorted(idx_sorted: torch.Tensor, n_rows: int) -> torch.Tensor:

@@ -392,7 +392,7 @@ _register_autograd(edge_geometry, _edge_backward, _edge_setup)
 # ---------------------------------------------------------------------------
 
 def _tp_csr(in1: Tensor, idx_i: Tensor, idx_j: Tensor, rowptr: Optional[Tensor], sender_perm: Optional[Tensor],
-            sender_ptr: Optional[Tensor], need_senders: bool):
+            sender_ptr: Optional[Tensor], need_senders: bool, pair_slot: Optional[Tensor] = None):
     n = in1.shape[0]
     jj = _i32("idx_j", idx_j)
     if rowptr is None or (need_senders and (sender_perm is None or sender_ptr is None)):
@@ -404,12 +404,15 @@ def _tp_csr(in1: Tensor, idx_i: Tensor, idx_j: Tensor, rowptr: Optional[Tensor],
     sq = _i32("sender_ptr", sender_ptr)
     if rp.shape[0] != n + 1:
         raise ValueError(f"rowptr must have in1.shape[0] + 1 = {n + 1} entries, got {rp.shape[0]}.")
-    keep = (jj, rp, sp, sq)
-    return _lib.csr_struct(n, jj.shape[0], jj, rp, sp, sq, n), keep
+    ps = _i32("pair_slot", pair_slot)
+    if ps is not None and ps.shape[0] != jj.shape[0]:
+        raise ValueError(f"pair_slot must have one entry per edge ({jj.shape[0]}), got {ps.shape[0]}.")
+    keep = (jj, rp, sp, sq, ps)
+    return _lib.csr_struct(n, jj.shape[0], jj, rp, sp, sq, n, ps), keep
 
 
 def _check_tp_inputs(in1, in2, weights, idx_i, idx_j, in1_l_max, in2_l_max, out_l_max, in1_features,
-                     in2_features, symmetric_product, shared_weights):
+                     in2_features, symmetric_product, shared_weights, paired=False):
     conv = idx_i is not None and idx_j is not None
     c = max(in1_features, in2_features)
     _, n_paths = count_output_paths(in1_l_max, in2_l_max, out_l_max, symmetric_product)
@@ -422,11 +425,14 @@ def _check_tp_inputs(in1, in2, weights, idx_i, idx_j, in1_l_max, in2_l_max, out_
     elif in2.shape[0] != in1.shape[0]:
         raise ValueError("idx_i and idx_j must be provided when in1 and in2 have different batch sizes. "
                          f"Got in1_batch={in1.shape[0]}, in2_batch={in2.shape[0]}.")
+    if paired and (shared_weights or not conv or items % 2):
+        raise ValueError("pair_slot needs a convolution with per-edge weights over an even number of edges.")
+    w_rows = items // 2 if paired else items
     if shared_weights:
         if weights.dim() != 1 or weights.shape[0] != n_paths * c:
             raise ValueError(f"Shared weights must be 1D of size {n_paths * c}, got {tuple(weights.shape)}.")
-    elif weights.dim() != 2 or weights.shape[0] != items or weights.shape[1] != n_paths * c:
-        raise ValueError(f"Non-shared weights must have shape ({items}, {n_paths * c}), got {tuple(weights.shape)}.")
+    elif weights.dim() != 2 or weights.shape[0] != w_rows or weights.shape[1] != n_paths * c:
+        raise ValueError(f"Non-shared weights must have shape ({w_rows}, {n_paths * c}), got {tuple(weights.shape)}.")
     return conv
 
 
@@ -436,14 +442,15 @@ def tp_fwd(in1: Tensor, in2: Tensor, weights: Tensor, idx_i: Optional[Tensor], i
            symmetric_product: bool, shared_weights: bool, in1_offs: List[int], in2_offs: List[int],
            out_sizes: List[int], n_paths_per_l: List[int], n_total_paths: int, reduce_paths: bool = False,
            rowptr: Optional[Tensor] = None, sender_perm: Optional[Tensor] = None,
-           sender_ptr: Optional[Tensor] = None, alpha: float = 1.0) -> Tensor:
+           sender_ptr: Optional[Tensor] = None, alpha: float = 1.0, pair_slot: Optional[Tensor] = None) -> Tensor:
     """Reference schema (src/flashcart/o3/_tensor_product.py:332-352) plus optional CSR
-    arrays (``rowptr``, ``sender_perm``, ``sender_ptr``, see ``o3._graph``) and ``alpha``,
-    a scale applied to the output."""
+    arrays (``rowptr``, ``sender_perm``, ``sender_ptr``, see ``o3._graph``), ``alpha``,
+    a scale applied to the output, and ``pair_slot`` (``o3._graph.EdgePairs.slot``): the two
+    edges of a pair read one weight row, so ``weights`` holds E / 2 rows."""
     _check_tp_meta((in1_l_max, in2_l_max, out_l_max, in1_features, in2_features, symmetric_product, reduce_paths),
                    in1_offs, in2_offs, out_sizes, n_paths_per_l, n_total_paths)
     conv = _check_tp_inputs(in1, in2, weights, idx_i, idx_j, in1_l_max, in2_l_max, out_l_max, in1_features,
-                            in2_features, symmetric_product, shared_weights)
+                            in2_features, symmetric_product, shared_weights, pair_slot is not None)
     in1 = _lib.contig("in1", in1)
     in2 = _lib.contig("in2", in2)
     w = _lib.contig("weights", weights)
@@ -453,7 +460,8 @@ def tp_fwd(in1: Tensor, in2: Tensor, weights: Tensor, idx_i: Optional[Tensor], i
                                                   symmetric_product, reduce_paths))
     csr, keep = (None, None)
     if conv:
-        csr, keep = _tp_csr(in1, idx_i, idx_j, rowptr, sender_perm, sender_ptr, need_senders=False)
+        csr, keep = _tp_csr(in1, idx_i, idx_j, rowptr, sender_perm, sender_ptr, need_senders=False,
+                            pair_slot=pair_slot)
     _lib_call("fc_tp_fwd", desc, csr, in1.shape[0], in1.data_ptr(), in2.data_ptr(), w.data_ptr(), float(alpha),
               out.data_ptr(), _lib.stream_of(in1))
     return out
@@ -462,7 +470,7 @@ def tp_fwd(in1: Tensor, in2: Tensor, weights: Tensor, idx_i: Optional[Tensor], i
 @tp_fwd.register_fake
 def _(in1, in2, weights, idx_i, idx_j, in1_l_max, in2_l_max, out_l_max, in1_features, in2_features,
       symmetric_product, shared_weights, in1_offs, in2_offs, out_sizes, n_paths_per_l, n_total_paths,
-      reduce_paths=False, rowptr=None, sender_perm=None, sender_ptr=None, alpha=1.0):
+      reduce_paths=False, rowptr=None, sender_perm=None, sender_ptr=None, alpha=1.0, pair_slot=None):
     return in1.new_empty(in1.shape[0], _tp_out_dim(in1_l_max, in2_l_max, out_l_max, in1_features, in2_features,
                                                    symmetric_product, reduce_paths))
 
@@ -474,11 +482,14 @@ def tp_bwd(grad_out: Tensor, in1: Tensor, in2: Tensor, weights: Tensor, idx_i: O
            in2_offs: List[int], out_sizes: List[int], n_paths_per_l: List[int], n_total_paths: int,
            reduce_paths: bool, need_grad_in1: bool, need_grad_in2: bool, need_grad_weights: bool,
            rowptr: Optional[Tensor] = None, sender_perm: Optional[Tensor] = None,
-           sender_ptr: Optional[Tensor] = None, alpha: float = 1.0) -> Tuple[Tensor, Tensor, Tensor]:
+           sender_ptr: Optional[Tensor] = None, alpha: float = 1.0,
+           pair_slot: Optional[Tensor] = None) -> Tuple[Tensor, Tensor, Tensor]:
     """Gradients wrt (in1, in2, weights); unrequested ones are returned as empty (0,) tensors.
 
     Reference schema (src/flashcart/o3/_tensor_product.py:588-611) plus the optional
-    CSR arrays and ``alpha`` of ``tp_fwd``."""
+    CSR arrays, ``alpha`` and ``pair_slot`` of ``tp_fwd``. With ``pair_slot`` the weight
+    gradient has one row per edge, pair-major (row 2p + s holds edge s of pair p): the sum
+    of its two rows per pair is the gradient of the (E / 2)-row weights."""
     _check_tp_meta((in1_l_max, in2_l_max, out_l_max, in1_features, in2_features, symmetric_product, reduce_paths),
                    in1_offs, in2_offs, out_sizes, n_paths_per_l, n_total_paths)
     conv = idx_i is not None and idx_j is not None
@@ -490,10 +501,14 @@ def tp_bwd(grad_out: Tensor, in1: Tensor, in2: Tensor, weights: Tensor, idx_i: O
                         shared_weights, reduce_paths)
     csr, keep = (None, None)
     if conv:
-        csr, keep = _tp_csr(in1, idx_i, idx_j, rowptr, sender_perm, sender_ptr, need_senders=need_grad_in1)
+        csr, keep = _tp_csr(in1, idx_i, idx_j, rowptr, sender_perm, sender_ptr, need_senders=need_grad_in1,
+                            pair_slot=pair_slot)
+    elif pair_slot is not None:
+        raise ValueError("pair_slot needs a convolution (idx_i, idx_j).")
     g1 = _lib.rows_empty(in1, *in1.shape) if need_grad_in1 else in1.new_empty(0)
     g2 = _lib.rows_empty(in2, *in2.shape) if need_grad_in2 else in2.new_empty(0)
-    gw = _lib.rows_empty(w, *w.shape) if need_grad_weights else w.new_empty(0)
+    gw_rows = 2 * w.shape[0] if pair_slot is not None else w.shape[0]
+    gw = _lib.rows_empty(w, gw_rows, *w.shape[1:]) if need_grad_weights else w.new_empty(0)
     lib = _lib.load()
     n_ws = lib.fc_tp_bwd_workspace(desc, csr, in1.shape[0], int(need_grad_in1), int(need_grad_weights))
     if n_ws < 0:
@@ -509,29 +524,32 @@ def tp_bwd(grad_out: Tensor, in1: Tensor, in2: Tensor, weights: Tensor, idx_i: O
 def _(grad_out, in1, in2, weights, idx_i, idx_j, in1_l_max, in2_l_max, out_l_max, in1_features, in2_features,
       symmetric_product, shared_weights, in1_offs, in2_offs, out_sizes, n_paths_per_l, n_total_paths,
       reduce_paths, need_grad_in1, need_grad_in2, need_grad_weights, rowptr=None, sender_perm=None,
-      sender_ptr=None, alpha=1.0):
+      sender_ptr=None, alpha=1.0, pair_slot=None):
+    gw_rows = 2 * weights.shape[0] if pair_slot is not None else weights.shape[0]
     return (torch.empty_like(in1) if need_grad_in1 else in1.new_empty(0),
             torch.empty_like(in2) if need_grad_in2 else in2.new_empty(0),
-            torch.empty_like(weights) if need_grad_weights else weights.new_empty(0))
+            weights.new_empty(gw_rows, *weights.shape[1:]) if need_grad_weights else weights.new_empty(0))
 
 
 def _tp_setup(ctx, inputs, output):
     (in1, in2, weights, idx_i, idx_j, l1, l2, lo, f1, f2, sym, shared, o1, o2, osz, npl, ntot, red,
-     rowptr, sperm, sptr, alpha) = inputs
-    ctx.save_for_backward(in1, in2, weights, idx_i, idx_j, rowptr, sperm, sptr)
+     rowptr, sperm, sptr, alpha, pair_slot) = inputs
+    ctx.save_for_backward(in1, in2, weights, idx_i, idx_j, rowptr, sperm, sptr, pair_slot)
     ctx.cfg = (int(l1), int(l2), int(lo), int(f1), int(f2), bool(sym), bool(shared), list(o1), list(o2),
                list(osz), list(npl), int(ntot), bool(red))
     ctx.alpha = float(alpha)
 
 
 def _tp_backward(ctx, grad):
-    in1, in2, weights, idx_i, idx_j, rowptr, sperm, sptr = ctx.saved_tensors
+    in1, in2, weights, idx_i, idx_j, rowptr, sperm, sptr, pair_slot = ctx.saved_tensors
     n1, n2, nw = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[2]
-    none_tail = (None,) * 19
+    none_tail = (None,) * 20
     if not (n1 or n2 or nw):
         return (None, None, None) + none_tail
     g1, g2, gw = tp_bwd(grad, in1, in2, weights, idx_i, idx_j, *ctx.cfg, bool(n1), bool(n2), bool(nw),
-                        rowptr, sperm, sptr, ctx.alpha)
+                        rowptr, sperm, sptr, ctx.alpha, pair_slot)
+    if nw and pair_slot is not None:
+        gw = gw.view(-1, 2, gw.shape[-1]).sum(1)  # both edges of a pair read its weight row
     return (g1 if n1 else None, g2 if n2 else None, gw if nw else None) + none_tail
 
 
@@ -1039,6 +1057,25 @@ def dense_bwd(grad_out: Tensor, pre: Tensor, weight: Tensor, scale: float, act: 
 @dense_bwd.register_fake
 def _(grad_out, pre, weight, scale, act):
     return grad_out.new_empty(*grad_out.shape[:-1], weight.shape[1])
+
+
+def dense_bwd_pairs(grad_pairs: Tensor, weight: Tensor, scale: float) -> Tensor:
+    """Input gradient of a bias-free linear layer whose output rows are shared by pairs of
+    consumers: gx[p] = scale (g[2p] + g[2p + 1]) W for a pair-major (2P, m) gradient ``g``
+    (``tp_bwd`` with ``pair_slot``). One GEMM over the (P, 2m) view with the stacked weight
+    [W; W], so the pair sum happens in the K loop."""
+    go = _lib.contig("grad_pairs", grad_pairs)
+    w = _lib.contig("weight", weight)
+    m, k = w.shape
+    if go.dim() != 2 or go.shape[1] != m or go.shape[0] % 2:
+        raise RuntimeError(f"grad_pairs must be (2P, {m}), got {tuple(go.shape)}.")
+    n_pairs = go.shape[0] // 2
+    wt = w.t().contiguous()
+    wt2 = torch.cat([wt, wt], dim=1)  # (k, 2m): the forward kernel's (N, K) weight
+    gx = _lib.rows_empty(go, n_pairs, k)
+    _lib_call("fc_dense_fwd", n_pairs, 2 * m, k, go.data_ptr(), wt2.data_ptr(), float(scale), None, 0, None,
+              gx.data_ptr(), _lib.stream_of(go))
+    return gx
 
 
 def _dense_setup(ctx, inputs, output):

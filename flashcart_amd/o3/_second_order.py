@@ -51,8 +51,9 @@ def _acc(*terms):
 
 def _tp_bwd_setup(ctx, inputs, output):
     (go, in1, in2, w, idx_i, idx_j, l1, l2, lo, f1, f2, sym, shared, o1, o2, osz, npl, ntot, red,
-     n1, n2, nw, rowptr, sperm, sptr, alpha) = inputs
+     n1, n2, nw, rowptr, sperm, sptr, alpha, pair_slot) = inputs
     ctx.save_for_backward(go, in1, in2, w, idx_i, idx_j, rowptr, sperm, sptr)
+    ctx.paired = pair_slot is not None
     ctx.cfg = (int(l1), int(l2), int(lo), int(f1), int(f2), bool(sym), bool(shared), list(o1), list(o2),
                list(osz), list(npl), int(ntot), bool(red))
     ctx.alpha = float(alpha)
@@ -67,7 +68,10 @@ def _tp_dbwd(ctx, c1, c2, cw):
     c2 = _live(c2) if ctx.computed[1] else None
     cw = _live(cw) if ctx.computed[2] else None
     cfg, alpha = ctx.cfg, ctx.alpha
-    tail = (None,) * 22
+    tail = (None,) * 23
+    if ctx.paired:
+        raise NotImplementedError("second derivatives of a tensor product with shared pair weights (pair_slot) "
+                                  "are not implemented; run without edge pairs under create_graph.")
 
     def fwd(a, b, ww):
         return _ops.tp_fwd(a, b, ww, ii, jj, *cfg, rp, sp, sq, alpha)

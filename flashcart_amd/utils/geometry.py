@@ -15,16 +15,21 @@ def uses_periodic_shifts(pbc: object) -> bool:
     return bool(np.any(pbc))
 
 
-def shift_vectors(cell: torch.Tensor, shifts: torch.Tensor, idx_i: torch.Tensor, batch: torch.Tensor) -> torch.Tensor:
+def shift_vectors(cell: torch.Tensor, shifts: torch.Tensor, idx_i: torch.Tensor, batch: torch.Tensor,
+                  antisymmetric: bool = False) -> torch.Tensor:
     """Cartesian periodic translation S . cell[batch[i]] of every edge (reference ``geometry.py:52``).
 
     One structure: a single (E,3) x (3,3) product; several: per-edge sums of the three
     scaled lattice vectors (a per-edge batched 1x3 @ 3x3 product is far slower).
+    ``antisymmetric``: the per-edge sums also for one structure, each element evaluated as
+    (s0 c0 + s1 c1) + s2 c2 with one rounding per operation, so the translation of -S is the
+    exact negation of that of S (a library matrix product does not promise one summation
+    order for all rows).
     """
     s = shifts.to(cell.dtype)
-    if cell.shape[0] == 1:
+    if cell.shape[0] == 1 and not antisymmetric:
         return s @ cell[0]
-    c = cell[batch[idx_i]]
+    c = cell[0].unsqueeze(0) if cell.shape[0] == 1 else cell[batch[idx_i]]
     return s[:, 0:1] * c[:, 0] + s[:, 1:2] * c[:, 1] + s[:, 2:3] * c[:, 2]
 
 

@@ -128,7 +128,23 @@ typedef struct fc_csr {
   const int32_t* sender_perm;  /* edge ids ordered by sender (stable), n_edges */
   const int32_t* sender_ptr;   /* sender CSR into sender_perm (n_sender_rows+1) */
   int64_t n_sender_rows;       /* rows of in1 (senders may include ghost atoms) */
+  const int32_t* pair_slot;    /* optional (NULL: edge e uses weight row e). Per-edge weights shared
+                                  by the two edges of a pair (fc_edge_pairs): edge e reads weight row
+                                  pair_slot[e] / 2 and writes its weight gradient to row pair_slot[e],
+                                  so the gradient has 2 rows per pair. No counterpart in the reference,
+                                  which forms the weights of every edge (nn/layers.py:357-364). */
 } fc_csr;
+
+/* Edge pairs of a full neighbour list (no counterpart in the reference): the reverse of
+ * edge (i <- j, S) is the edge (j <- i, -S) of receiver j; shifts (n_edges, 3) may be NULL
+ * (no periodic shifts). Writes pair_slot[e] = 2p for the lower edge of pair p and 2p + 1
+ * for its reverse (-1: no unique mutual reverse), pair_edge[p] = the lower edge (pairs
+ * numbered in its order, at most max_pairs written), counts[0] = edges without a reverse,
+ * counts[1] = pairs. Index work only; workspace of fc_edge_pairs_workspace(n_edges) int32. */
+int64_t fc_edge_pairs_workspace(int64_t n_edges);
+int fc_edge_pairs(const fc_csr* graph, const int32_t* idx_i, const int32_t* shifts, int32_t* pair_slot,
+                  int32_t* pair_edge, int64_t max_pairs, int32_t* counts, int32_t* workspace,
+                  int64_t workspace_ints, void* stream);
 
 /* rowptr[n] = first edge with idx_sorted[e] >= n, for n in [0, n_nodes]. */
 int fc_csr_from_sorted(int64_t n_edges, const int32_t* idx_sorted, int64_t n_nodes,

@@ -1,0 +1,252 @@
+"""Edge pairs (i <- j, S) / (j <- i, -S) and the radial weights shared within a pair.
+
+``fc_edge_pairs`` is index work, checked bit for bit against a plain restatement here. The
+premise of sharing (both edges of a pair have bitwise the same radial-MLP input) is checked on
+the device geometry itself; the tensor product with ``pair_slot`` is checked bit for bit
+against the same product with the weights expanded per edge; the potential with pairs against
+the float64 oracle at the north-star bars, and against its own unpaired evaluation.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from flashcart_amd.data import AtomicGraph, batch_graphs
+from flashcart_amd.data.synthetic import fcc_alloy, model_config, molecules, water_box
+from oracle import model as OM
+from tests.helpers import assert_close, random_csr_graph
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _np_pairs(ii, jj, shifts):
+    """Restatement of fc_edge_pairs: the reverse of edge e is the first edge of receiver jj[e]
+    with sender ii[e] and shift -S; pairs are mutual reverses, numbered by their lower edge."""
+    ii, jj = np.asarray(ii), np.asarray(jj)
+    n_edges = ii.shape[0]
+    s = np.zeros((n_edges, 3), np.int64) if shifts is None else np.asarray(shifts, np.int64)
+    starts = {}
+    for e in range(n_edges):
+        starts.setdefault(int(ii[e]), []).append(e)
+    rev = np.full(n_edges, -1, np.int64)
+    for e in range(n_edges):
+        for k in starts.get(int(jj[e]), []):
+            if k != e and jj[k] == ii[e] and (s[k] == -s[e]).all():
+                rev[e] = k
+                break
+    slot = np.full(n_edges, -1, np.int64)
+    edge = []
+    bad = 0
+    for e in range(n_edges):
+        r = rev[e]
+        if r < 0 or rev[r] != e:
+            bad += 1
+            continue
+        if r > e:
+            p = len(edge)
+            edge.append(e)
+            slot[e], slot[r] = 2 * p, 2 * p + 1
+    return slot, np.asarray(edge, np.int64), bad
+
+
+def _graphs():
+    numbers, pos, cell, pbc = fcc_alloy(2, 2, 2, seed=3)  # 7.2 A box, r_max 5: several images per pair
+    yield "fcc_small_cell", AtomicGraph.from_arrays(numbers, pos, ["Cu", "Ni", "Fe", "Cr"], 5.0, cell=cell, pbc=pbc)
+    numbers, pos, cell, pbc = water_box(64, seed=1)
+    yield "water", AtomicGraph.from_arrays(numbers, pos, ["H", "O"], 5.0, cell=cell, pbc=pbc)
+    mols = molecules(6, seed=2)
+    yield "molecules", batch_graphs([AtomicGraph.from_arrays(z, p, ["H", "C", "N", "O"], 5.0) for z, p in mols])
+
+
+def _csr(g):
+    from flashcart_amd.o3._graph import build_graph
+    return build_graph(g.edge_index.to(DEV), int(g.atom_types.shape[0]))
+
+
+@pytest.mark.parametrize("name,graph", list(_graphs()), ids=lambda v: v if isinstance(v, str) else "")
+def test_pairs_match_restatement(name, graph):
+    from flashcart_amd.o3._graph import launch_edge_pairs
+    csr = _csr(graph)
+    use_shifts = bool(graph.to_dict().get("use_shifts", True))
+    shifts = graph.shifts.to(DEV) if use_shifts else None
+    print(f"pairs: {name}, {csr.n_edges} edges", flush=True)
+    pairs, counts = launch_edge_pairs(csr, shifts)
+    slot, edge, bad = _np_pairs(graph.edge_index[0].numpy(), graph.edge_index[1].numpy(),
+                                graph.shifts.numpy() if use_shifts else None)
+    assert bad == 0 and 2 * len(edge) == csr.n_edges
+    assert counts.tolist() == [0, len(edge)]
+    assert np.array_equal(pairs.slot.cpu().numpy(), slot)
+    assert np.array_equal(pairs.edge.cpu().numpy(), edge)
+    assert csr.edge_pairs(shifts) is not None
+
+
+def test_incomplete_pairings_are_refused():
+    from flashcart_amd.o3._graph import build_graph, find_edge_pairs, launch_edge_pairs
+    # random directed edges: most have no reverse
+    ei = random_csr_graph(40, [3, 5, 0, 8], seed=4)
+    csr = build_graph(ei.to(DEV), 40)
+    pairs, counts = launch_edge_pairs(csr, None)
+    slot, edge, bad = _np_pairs(ei[0].numpy(), ei[1].numpy(), None)
+    assert counts.tolist() == [bad, len(edge)] and bad > 0
+    assert np.array_equal(pairs.slot.cpu().numpy(), slot)
+    assert find_edge_pairs(csr, None) is None
+    # a symmetric list with one pair's shift broken
+    numbers, pos, cell, pbc = fcc_alloy(2, 2, 2, seed=3)
+    g = AtomicGraph.from_arrays(numbers, pos, ["Cu", "Ni", "Fe", "Cr"], 5.0, cell=cell, pbc=pbc)
+    csr = _csr(g)
+    shifts = g.shifts.clone()
+    shifts[7, 0] += 5
+    assert find_edge_pairs(csr, shifts.to(DEV)) is None
+    assert find_edge_pairs(csr, g.shifts.to(DEV)) is not None
+    # ghost senders (rows beyond the receivers) have no reverse
+    ei = torch.tensor([[0, 0, 1, 1], [1, 2, 0, 3]])
+    csr = build_graph(ei.to(DEV), 2, n_sender_rows=4)
+    assert find_edge_pairs(csr, None) is None
+    # empty and odd edge lists
+    csr = build_graph(torch.zeros(2, 0, dtype=torch.long, device=DEV), 3)
+    assert find_edge_pairs(csr, None) is None
+    assert launch_edge_pairs(csr, None)[1].tolist() == [0, 0]
+
+
+def test_pair_edges_have_identical_radial_inputs():
+    """The premise: with antisymmetric shift vectors both edges of a pair get bitwise the same
+    edge length, radial features and envelope from the device edge geometry."""
+    from flashcart_amd.o3 import _ops
+    from flashcart_amd.utils.geometry import shift_vectors
+    numbers, pos, cell, pbc = fcc_alloy(3, 3, 3, seed=5, jitter=0.3)
+    g = AtomicGraph.from_arrays(numbers, pos, ["Cu", "Ni", "Fe", "Cr"], 5.0, cell=cell, pbc=pbc).to(DEV)
+    csr = _csr(g)
+    pairs = csr.edge_pairs(g.shifts)
+    assert pairs is not None
+    sv = shift_vectors(g.cell, g.shifts, csr.idx_i, g.batch, antisymmetric=True)
+    posd = g.positions.to(torch.float32) + 1e-3 * torch.randn_like(g.positions.to(torch.float32))
+    attrs, feats, env = _ops.edge_geometry(posd, sv, csr.idx_i, csr.idx_j, None, csr.rowptr, csr.sender_perm,
+                                           csr.sender_ptr, 3, 1, 8, 0.0, 5.0, 6)
+    order = torch.empty_like(pairs.slot, dtype=torch.long)
+    order[pairs.slot.long()] = torch.arange(csr.n_edges, device=DEV)  # order[2p], order[2p + 1]: pair p
+    lo, hi = order[0::2], order[1::2]
+    assert torch.equal(lo, pairs.edge.long())
+    assert torch.equal(feats[lo], feats[hi]) and torch.equal(env[lo], env[hi])
+    # edge attributes of the reverse edge: (-1)^l times the forward ones, l of each component
+    sign = torch.tensor([1.0] + [-1.0] * 3 + [1.0] * 5 + [-1.0] * 7, device=DEV)
+    assert torch.equal(attrs[hi], attrs[lo] * sign)
+
+
+def _tp(l1, l2, lo, c):
+    from flashcart_amd.o3 import TensorProduct
+    return TensorProduct(l1, l2, lo, c, 1, shared_weights=False, reduce_paths=False)
+
+
+@pytest.mark.parametrize("l1,c", [(2, 128), (0, 64), (1, 32)])
+def test_tp_with_pair_slot_equals_expanded_weights(l1, c):
+    """Forward and backward with pair_slot are the per-edge computation with the pair's weight row,
+    bit for bit; the weight gradient comes back pair-major."""
+    from flashcart_amd.o3 import _ops
+    numbers, pos, cell, pbc = fcc_alloy(2, 2, 2, seed=3)
+    g = AtomicGraph.from_arrays(numbers, pos, ["Cu", "Ni", "Fe", "Cr"], 5.0, cell=cell, pbc=pbc).to(DEV)
+    csr = _csr(g)
+    pairs = csr.edge_pairs(g.shifts)
+    tp = _tp(l1, 3, 3, c)
+    n, e = csr.n_nodes, csr.n_edges
+    gen = torch.Generator(device=DEV).manual_seed(11)
+    x = torch.randn(n, tp.in1_dim, device=DEV, generator=gen)
+    y = torch.randn(e, 16, device=DEV, generator=gen)
+    wp = torch.randn(pairs.n_pairs, tp.n_total_paths * c, device=DEV, generator=gen)
+    w_edge = wp[(pairs.slot // 2).long()]
+    args = (tp.in1_l_max, tp.in2_l_max, tp.out_l_max, tp.in1_features, tp.in2_features, False, False,
+            *tp.op_meta, False)
+    csr_args = (csr.rowptr, csr.sender_perm, csr.sender_ptr)
+    out_p = _ops.tp_fwd(x, y, wp, csr.idx_i, csr.idx_j, *args, *csr_args, 0.3, pairs.slot)
+    out_e = _ops.tp_fwd(x, y, w_edge, csr.idx_i, csr.idx_j, *args, *csr_args, 0.3)
+    assert torch.equal(out_p, out_e)
+    go = torch.randn_like(out_e)
+    g1p, g2p, gwp = _ops.tp_bwd(go, x, y, wp, csr.idx_i, csr.idx_j, *args, True, True, True, *csr_args, 0.3,
+                                pairs.slot)
+    g1e, g2e, gwe = _ops.tp_bwd(go, x, y, w_edge, csr.idx_i, csr.idx_j, *args, True, True, True, *csr_args, 0.3)
+    assert torch.equal(g1p, g1e) and torch.equal(g2p, g2e)
+    assert gwp.shape == gwe.shape and torch.equal(gwp[pairs.slot.long()], gwe)
+    # through autograd the pair-shared weights get the sum of both edges' gradients
+    wq = wp.clone().requires_grad_(True)
+    _ops.tp_fwd(x, y, wq, csr.idx_i, csr.idx_j, *args, *csr_args, 0.3, pairs.slot).backward(go)
+    want = gwe.new_zeros(wp.shape).index_add_(0, (pairs.slot // 2).long(), gwe)
+    assert_close(wq.grad, want, 1e-6, 1e-6, "pair weight gradient")
+
+
+def _model(cfg, seed=1234):
+    from flashcart_amd.model import FlashCartPotential
+    torch.manual_seed(seed)
+    m = FlashCartPotential.from_config(cfg)
+    g = torch.Generator().manual_seed(seed + 1)
+    with torch.no_grad():
+        for name, p in m.named_parameters():
+            if "output_linear" in name or "layer_norm.weights" in name:
+                p.copy_(torch.randn(p.shape, generator=g) * 0.5 + (1.0 if "layer_norm" in name else 0.0))
+    return m
+
+
+@pytest.mark.parametrize("case", ["fcc_L3_C128", "water_L2_C64", "molecules_L2_C32"])
+def test_paired_potential_matches_oracle_and_unpaired(case):
+    if case == "fcc_L3_C128":
+        numbers, pos, cell, pbc = fcc_alloy(2, 2, 2, seed=3)
+        cfg = model_config(["Cu", "Ni", "Fe", "Cr"], 128, 3, avg_neighbors=42.0)
+        graph = AtomicGraph.from_arrays(numbers, pos, cfg["elements"], 5.0, cell=cell, pbc=pbc)
+    elif case == "water_L2_C64":
+        numbers, pos, cell, pbc = water_box(64, seed=1)
+        cfg = model_config(["H", "O"], 64, 2, avg_neighbors=50.0)
+        graph = AtomicGraph.from_arrays(numbers, pos, cfg["elements"], 5.0, cell=cell, pbc=pbc)
+    else:
+        cfg = model_config(["H", "C", "N", "O"], 32, 2, avg_neighbors=12.0)
+        graph = batch_graphs([AtomicGraph.from_arrays(z, p, cfg["elements"], 5.0) for z, p in molecules(5, seed=7)])
+    model = _model(cfg)
+    ref = OM.predict(model.state_dict(), model.to_model_config(), graph.to_dict(), compute_forces=True)
+    m = model.to(DEV)
+    m.requires_grad_(False)
+    gd = graph.to(DEV)
+    print(f"paired potential: {case}", flush=True)
+    out = m.predict(gd, compute_forces=True)
+    csr = gd.csr
+    assert any(v is not None for v in csr.__dict__.get("_pairs", {}).values()), "the paired path was not taken"
+    assert_close(out["energy"], ref["energy"], 1e-5, 1e-6, "energy")
+    assert_close(out["forces"], ref["forces"], 0.0, 1e-4, "forces")
+    # the same potential with the radial MLP parameters trainable takes the per-edge path
+    for layer in m.interactions:
+        layer.radial_mlp.requires_grad_(True)
+    assert not m.wants_edge_pairs(gd.positions)
+    un = m.predict(graph.to(DEV), compute_forces=True)
+    assert_close(out["energy"], un["energy"], 2e-6, 1e-6, "paired vs per-edge energy")
+    assert_close(out["forces"], un["forces"], 1e-5, 2e-5, "paired vs per-edge forces")
+
+
+def test_replay_falls_back_when_pairing_breaks():
+    """A captured prediction takes the pairing of its first edge list; an edge list of the same
+    size that does not pair up is evaluated eagerly (and correctly)."""
+    numbers, pos, cell, pbc = fcc_alloy(2, 2, 2, seed=3)
+    cfg = model_config(["Cu", "Ni", "Fe", "Cr"], 16, 3, avg_neighbors=42.0)
+    graph = AtomicGraph.from_arrays(numbers, pos, cfg["elements"], 5.0, cell=cell, pbc=pbc)
+    model = _model(cfg)
+    sd, mc = model.state_dict(), model.to_model_config()
+    m = model.to(DEV)
+    m.requires_grad_(False)
+    gd = graph.to(DEV)
+    out0 = m.predict(gd, compute_forces=True, use_compile=True)
+    entry = next(iter(m._replay_cache.values()))
+    assert entry.paired
+    ref0 = OM.predict(sd, mc, graph.to_dict(), compute_forces=True)
+    assert_close(out0["forces"], ref0["forces"], 0.0, 1e-4, "replayed forces")
+    # break one pair: redirect an edge to a different sender (same edge count, receivers sorted)
+    broken = graph.to_dict()
+    ei = broken["edge_index"].clone()
+    e = 5
+    ei[1, e] = (ei[1, e] + 1) % int(broken["atom_types"].shape[0])
+    if ei[1, e] == ei[0, e]:
+        ei[1, e] = (ei[1, e] + 1) % int(broken["atom_types"].shape[0])
+    broken["edge_index"] = ei
+    ref1 = OM.predict(sd, mc, broken, compute_forces=True)
+    bd = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in broken.items()}
+    out1 = m.predict(bd, compute_forces=True, use_compile=True)
+    assert_close(out1["energy"], ref1["energy"], 1e-5, 1e-6, "fallback energy")
+    assert_close(out1["forces"], ref1["forces"], 0.0, 1e-4, "fallback forces")
+    # and back to a pairable list: replayed again
+    out2 = m.predict(gd, compute_forces=True, use_compile=True)
+    assert_close(out2["forces"], ref0["forces"], 0.0, 1e-4, "replayed forces after fallback")
