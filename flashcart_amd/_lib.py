@@ -76,6 +76,8 @@ _SIGNATURES = {
     "fc_edge_grad_to_nodes": (c_int, [ctypes.POINTER(CSR), c_vp, c_vp, c_vp]),
     "fc_edge_pairs_workspace": (c_i64, [c_i64]),
     "fc_edge_pairs": (c_int, [ctypes.POINTER(CSR), c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp]),
+    "fc_pair_inputs_fwd": (c_int, [c_i64, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "fc_pair_inputs_bwd": (c_int, [c_i64, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "fc_tp_num_paths": (c_int, [ctypes.POINTER(TPDesc)]),
     "fc_tp_out_dim": (c_i64, [ctypes.POINTER(TPDesc)]),
     "fc_tp_fwd": (c_int, [ctypes.POINTER(TPDesc), ctypes.POINTER(CSR), c_i64, c_vp, c_vp, c_vp, c_f32, c_vp, c_vp]),
@@ -89,6 +91,10 @@ _SIGNATURES = {
     "fc_dense_fwd": (c_int, [c_i64, c_i32, c_i32, c_vp, c_vp, c_f32, c_vp, c_i32, c_vp, c_vp, c_vp]),
     "fc_dense_dgrad": (c_int, [c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_f32, c_i32, c_vp, c_vp]),
     "fc_radial_mlp_fwd": (c_int, [c_i64, c_i32, c_vp, c_vp, c_f32, c_vp, c_f32, c_i32, c_vp, c_f32, c_vp, c_vp]),
+    "fc_radial_mlp_hidden_fwd": (c_int, [c_i64, c_i32, c_vp, c_vp, c_f32, c_vp, c_f32, c_vp, c_vp]),
+    "fc_species_density_fwd": (c_int, [ctypes.POINTER(CSR), c_i32, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "fc_species_density_bwd": (c_int, [ctypes.POINTER(CSR), c_i32, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
+                                       c_vp]),
     "fc_radial_mlp_bwd": (c_int, [c_i64, c_i32, c_vp, c_vp, c_f32, c_vp, c_f32, c_vp, c_vp, c_vp]),
     "fc_linear_wgrad_workspace": (c_i64, [ctypes.POINTER(LinearDesc), c_i64, ctypes.POINTER(c_vp)]),
     "fc_linear_wgrad": (c_int, [ctypes.POINTER(LinearDesc), c_i64, c_vp, c_vp, c_f32, ctypes.POINTER(c_vp), c_vp,

@@ -1163,7 +1163,9 @@ __device__ __forceinline__ void acc_to_rows(const floatx16 (&acc)[2], float* As,
       As[(wave * 32 + acc_row(v, lane)) * WIDE_P + j * 32 + (lane & 31)] = f(acc[j][v]);
 }
 
-template <bool GUARD>
+// HIDDEN: stop after the second hidden layer and write its activation h2 (n x 64) instead of
+// the output layer (the first interaction layer's species density takes h2 itself).
+template <bool GUARD, bool HIDDEN = false>
 __global__ void __launch_bounds__(256, 2) radial_mlp_fwd_kernel(int64_t n, int n_in, const float* __restrict__ x,
                                                                  const float* __restrict__ w0, float s0,
                                                                  const float* __restrict__ w1, float s1, int m,
@@ -1185,6 +1187,16 @@ __global__ void __launch_bounds__(256, 2) radial_mlp_fwd_kernel(int64_t n, int n
   acc_to_rows(acc, As, wave, lane, [&](float a) { return silu_r(a * s0); });
   __syncthreads();
   mfma_k64<2>(as, Bs[1] + (lane & 31) * WIDE_P + half, acc);
+  if constexpr (HIDDEN) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t row = r0 + wave * 32 + acc_row(v, lane);
+        if (row < n) out[row * 64 + j * 32 + (lane & 31)] = silu_r(acc[j][v] * s1);
+      }
+    return;
+  }
   __syncthreads();  // reads of h1 and of both weight buffers done before they are overwritten
   acc_to_rows(acc, As, wave, lane, [&](float a) { return silu_r(a * s1); });
   __syncthreads();
@@ -1313,6 +1325,19 @@ extern "C" int fc_radial_mlp_fwd(int64_t n, int32_t n_in, const float* x, const 
   else
     hipLaunchKernelGGL(radial_mlp_fwd_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, n,
                        (int)n_in, x, w0, s0, w1, s1, (int)m, w2, s2, out, (int64_t)0);
+  FC_LAUNCH_CHECK();
+  return FC_OK;
+}
+
+extern "C" int fc_radial_mlp_hidden_fwd(int64_t n, int32_t n_in, const float* x, const float* w0, float s0,
+                                        const float* w1, float s1, float* h2, void* stream) {
+  if (n < 0 || n_in < 1 || n_in > WIDE_K) return FC_ERR_BAD_DESC;
+  if (n == 0) return FC_OK;
+  if (!x || !w0 || !w1 || !h2) return FC_ERR_NULL;
+  const int64_t blocks = (n + WIDE_BM - 1) / WIDE_BM;
+  if (blocks > 0x7fffffff) return FC_ERR_SHAPE;
+  hipLaunchKernelGGL((radial_mlp_fwd_kernel<true, true>), dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, n,
+                     (int)n_in, x, w0, s0, w1, s1, 64, (const float*)nullptr, 1.0f, h2, (int64_t)0);
   FC_LAUNCH_CHECK();
   return FC_OK;
 }

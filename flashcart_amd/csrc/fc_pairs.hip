@@ -153,9 +153,84 @@ __global__ void __launch_bounds__(kPairBlock) pair_assign_kernel(int64_t n_edges
   }
 }
 
+// Radial-MLP inputs of the pairs: x[p, k] = feats[e_p, k] * env[e_p] with e_p = pair_edge[p].
+__global__ void pair_inputs_fwd_kernel(int64_t n_pairs, int width, const int32_t* __restrict__ pair_edge,
+                                       const float* __restrict__ feats, const float* __restrict__ env,
+                                       float* __restrict__ x) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n_pairs * width) return;
+  const int64_t p = t / width;
+  const int k = (int)(t - p * width);
+  const int64_t e = pair_edge[p];
+  x[t] = feats[e * width + k] * env[e];
+}
+
+// Its backward for every edge: the lower edge of pair p takes the pair's gradient, the other
+// edge of the pair none (each edge row written once, no fill needed). G lanes per edge (G a
+// power of two >= width, at most 64), lane k handling column k; the envelope gradient is the
+// sum over the group's lanes.
+template <int G>
+__global__ void pair_inputs_bwd_kernel(int64_t n_edges, int width, const int32_t* __restrict__ pair_slot,
+                                       const float* __restrict__ feats, const float* __restrict__ env,
+                                       const float* __restrict__ gx, float* __restrict__ g_feats,
+                                       float* __restrict__ g_env) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t e = t / G;
+  const int k = (int)(t % G);
+  const bool on = e < n_edges && k < width;
+  float g = 0.f, f = 0.f, en = 0.f;
+  if (on) {
+    const int32_t s = pair_slot[e];
+    en = env[e];
+    f = feats[e * width + k];
+    g = (s & 1) == 0 ? gx[(int64_t)(s >> 1) * width + k] : 0.f;
+    if (g_feats) g_feats[e * width + k] = g * en;
+  }
+  float acc = g * f;
+#pragma unroll
+  for (int o = G / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+  if (g_env && e < n_edges && k == 0) g_env[e] = acc;
+}
+
 }  // namespace fc
 
 using namespace fc;
+
+extern "C" int fc_pair_inputs_fwd(int64_t n_pairs, int32_t width, const int32_t* pair_edge, const float* feats,
+                                  const float* env, float* x, void* stream) {
+  if (n_pairs < 0 || width < 1) return FC_ERR_SHAPE;
+  if (n_pairs == 0) return FC_OK;
+  if (!pair_edge || !feats || !env || !x) return FC_ERR_NULL;
+  const int64_t n = n_pairs * width;
+  hipLaunchKernelGGL(pair_inputs_fwd_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     n_pairs, width, pair_edge, feats, env, x);
+  FC_LAUNCH_CHECK();
+  return FC_OK;
+}
+
+extern "C" int fc_pair_inputs_bwd(int64_t n_edges, int32_t width, const int32_t* pair_slot, const float* feats,
+                                  const float* env, const float* gx, float* g_feats, float* g_env, void* stream) {
+  if (n_edges < 0 || width < 1) return FC_ERR_SHAPE;
+  if (n_edges == 0 || (!g_feats && !g_env)) return FC_OK;
+  if (!pair_slot || !feats || !env || !gx) return FC_ERR_NULL;
+  if (width > 64) return FC_ERR_SHAPE;
+  int g = 1;
+  while (g < width) g <<= 1;
+  const int64_t threads = n_edges * g;
+  const dim3 grid((unsigned)((threads + 255) / 256)), block(256);
+  hipStream_t s = (hipStream_t)stream;
+  switch (g) {
+    case 1: hipLaunchKernelGGL(pair_inputs_bwd_kernel<1>, grid, block, 0, s, n_edges, width, pair_slot, feats, env, gx, g_feats, g_env); break;
+    case 2: hipLaunchKernelGGL(pair_inputs_bwd_kernel<2>, grid, block, 0, s, n_edges, width, pair_slot, feats, env, gx, g_feats, g_env); break;
+    case 4: hipLaunchKernelGGL(pair_inputs_bwd_kernel<4>, grid, block, 0, s, n_edges, width, pair_slot, feats, env, gx, g_feats, g_env); break;
+    case 8: hipLaunchKernelGGL(pair_inputs_bwd_kernel<8>, grid, block, 0, s, n_edges, width, pair_slot, feats, env, gx, g_feats, g_env); break;
+    case 16: hipLaunchKernelGGL(pair_inputs_bwd_kernel<16>, grid, block, 0, s, n_edges, width, pair_slot, feats, env, gx, g_feats, g_env); break;
+    case 32: hipLaunchKernelGGL(pair_inputs_bwd_kernel<32>, grid, block, 0, s, n_edges, width, pair_slot, feats, env, gx, g_feats, g_env); break;
+    default: hipLaunchKernelGGL(pair_inputs_bwd_kernel<64>, grid, block, 0, s, n_edges, width, pair_slot, feats, env, gx, g_feats, g_env); break;
+  }
+  FC_LAUNCH_CHECK();
+  return FC_OK;
+}
 
 extern "C" int64_t fc_edge_pairs_workspace(int64_t n_edges) {
   if (n_edges < 0) return -FC_ERR_SHAPE;

@@ -172,6 +172,10 @@ class FlashCartPotential(AtomisticModel):
             edge_attrs, edge_feats, envelope = _ops.edge_geometry(
                 None, None, csr.idx_i, csr.idx_j, vectors, csr.rowptr, csr.sender_perm, csr.sender_ptr, *geo)
         node_feats = self.embedding(atom_types)
+        species = None
+        if pairs is not None and not self.embedding.weight.requires_grad:
+            # the first layer's sender features are embedding rows: species density (fused.species_conv)
+            species = (torch.index_select(atom_types.to(torch.int32), 0, csr.idx_j), self.embedding.weight)
         outputs = []
         for k, interaction in enumerate(self.interactions):
             msg = node_feats
@@ -180,7 +184,7 @@ class FlashCartPotential(AtomisticModel):
                 msg = lammps_exchange_features(node_feats, nlocal, ntotal)
             feats = interaction(msg, edge_attrs, edge_feats, edge_index, envelope,
                                 atom_types=atom_types if not self.element_agnostic_interaction else None,
-                                out_nodes=nlocal, graph=csr, edge_pairs=pairs)
+                                out_nodes=nlocal, graph=csr, edge_pairs=pairs, species=species if k == 0 else None)
             if self.nonlinearity:
                 feats = self.nonlinearities[k](feats)
             if self.use_products:

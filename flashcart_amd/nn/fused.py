@@ -21,7 +21,7 @@ only the order of floating-point additions in the backward differs.
 
 import contextlib
 import threading
-from typing import Optional
+from typing import List, Optional
 
 import torch
 from torch import Tensor
@@ -286,3 +286,83 @@ def paired_conv_applies(layer, node_feats: Tensor) -> bool:
 
 def paired_conv(layer, in1: Tensor, in2: Tensor, x_pairs: Tensor, graph, pairs, alpha: float) -> Tensor:
     return _PairedConv.apply(in1, in2, x_pairs, layer, graph, pairs.slot, alpha)
+
+
+def species_weights(x_table: Tensor, w2: Tensor, channels: int, l_max: int) -> List[Tensor]:
+    """B_l[c, Z * 64 + k] = x_table[Z, c] W2[l C + c, k]: the first layer's convolution and radial
+    output layer folded into one matrix per rank (the path (0, l, l) takes weight row block l)."""
+    n_species = x_table.shape[0]
+    xt = x_table.t().unsqueeze(-1)  # (C, Z, 1)
+    return [(xt * w2[l * channels:(l + 1) * channels].unsqueeze(1)).reshape(channels, n_species * 64).contiguous()
+            for l in range(l_max + 1)]
+
+
+class _SpeciesConv(torch.autograd.Function):
+    """Radial MLP + 0 x L -> L convolution of the first interaction layer, whose sender features
+    x_table[Z_j] depend on the sender's species alone, as a species density
+    (``csrc/fc_species.hip``): the radial MLP up to its last hidden activation h (per edge pair),
+    the receiver density dens[i, (l, m), Z, k] = sum_{e -> i, Z_j = Z} h_e[k] y_e[(l, m)], and one
+    equivariant linear map per rank with the matrices of ``species_weights``
+    (out_l = alpha s2 dens_l @ B_l^T). Same function as the per-edge path, with sums in another
+    order; the E x paths x C weights are never formed. Reference ``nn/layers.py:351-369``.
+    """
+
+    @staticmethod
+    def forward(ctx, y: Tensor, x_pairs: Tensor, layer, graph, pairs, edge_species: Tensor,
+                x_table: Tensor, alpha: float) -> Tensor:
+        from flashcart_amd import _lib
+        tp = layer.tp
+        l0, l1, l2 = layer.radial_mlp[0], layer.radial_mlp[2], layer.radial_mlp[4]
+        n_sp, c = x_table.shape[0], tp.in1_features
+        lm = min(tp.in2_l_max, tp.out_l_max)
+        h = _ops.radial_mlp_hidden_fwd(x_pairs, l0.weight, l0._scale, l1.weight, l1._scale)
+        csr = _lib.csr_struct(graph.n_nodes, graph.n_edges, graph.idx_j, graph.rowptr, pair_slot=pairs.slot)
+        dens = _ops.species_density_fwd(csr, lm, tp.in2_l_max, n_sp, edge_species, h, y, graph.n_nodes)
+        mats = species_weights(x_table, l2.weight, c, lm)
+        cfg = (lm, lm, 64, c, [n_sp] * (lm + 1), [float(alpha) * l2._scale] * (lm + 1))
+        out = _ops.linear_fwd(dens, mats, *cfg)
+        ctx.save_for_backward(y, x_pairs, h, edge_species, pairs.slot, *mats)
+        ctx.layer, ctx.graph, ctx.cfg, ctx.n_sp = layer, graph, cfg, n_sp
+        return out
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, g: Tensor):
+        from flashcart_amd import _lib
+        y, x_pairs, h, edge_species, slot, *mats = ctx.saved_tensors
+        layer, graph, cfg = ctx.layer, ctx.graph, ctx.cfg
+        if not (ctx.needs_input_grad[0] or ctx.needs_input_grad[1]):
+            return (None,) * 8
+        g_dens = _ops.linear_bwd(g.contiguous(), mats, *cfg)
+        csr = _lib.csr_struct(graph.n_nodes, graph.n_edges, graph.idx_j, graph.rowptr, pair_slot=slot)
+        g_h, g_y = _ops.species_density_bwd(csr, cfg[0], layer.tp.in2_l_max, ctx.n_sp, edge_species, h, y, g_dens)
+        del g_dens
+        gx = None
+        if ctx.needs_input_grad[1]:
+            l0, l1 = layer.radial_mlp[0], layer.radial_mlp[2]
+            gh2 = g_h.view(-1, 2, 64).sum(1)  # both edges of a pair read its h row
+            gx = _ops.radial_mlp_bwd(gh2, x_pairs, l0.weight, l0._scale, l1.weight, l1._scale)
+        return (g_y if ctx.needs_input_grad[0] else None), gx, None, None, None, None, None, None
+
+
+MAX_DENSITY_SPECIES = 8
+
+
+def species_conv_applies(layer, node_feats: Tensor, n_species: int) -> bool:
+    """True when the first interaction layer may run as a species density: the conditions of
+    ``paired_conv_applies``, rank-0 sender features of one channel block through a frozen
+    ``linear_first``, single-channel edge attributes, unreduced paths, at most
+    ``MAX_DENSITY_SPECIES`` species."""
+    tp = layer.tp
+    if layer.in1_l_max != 0 or tp.in1_l_max != 0 or tp.in2_features != 1 or tp.reduce_paths or tp.symmetric_product:
+        return False
+    if not 1 <= n_species <= MAX_DENSITY_SPECIES:
+        return False
+    if any(p.requires_grad for p in layer.linear_first.parameters()):
+        return False
+    return paired_conv_applies(layer, node_feats)
+
+
+def species_conv(layer, edge_attrs: Tensor, x_pairs: Tensor, graph, pairs, edge_species: Tensor,
+                 x_table: Tensor, alpha: float) -> Tensor:
+    return _SpeciesConv.apply(edge_attrs, x_pairs, layer, graph, pairs, edge_species, x_table, alpha)

@@ -8,7 +8,7 @@ readout MLP layers with their fused rescaled-SiLU epilogue. Element-wise glue
 (gates, norm scaling, residual sums) uses PyTorch tensor ops on the same device.
 """
 
-from typing import Iterator, List, Optional
+from typing import Iterator, List, Optional, Tuple
 
 import torch
 import torch.nn as nn
@@ -192,17 +192,24 @@ class InteractionLayer(nn.Module):
     def forward(self, node_feats: torch.Tensor, edge_attrs: torch.Tensor, edge_feats: torch.Tensor,
                 edge_index: torch.Tensor, envelope: torch.Tensor, atom_types: Optional[torch.Tensor] = None,
                 out_nodes: Optional[int] = None, graph: Optional[GraphCSR] = None,
-                edge_pairs: Optional[EdgePairs] = None) -> torch.Tensor:
+                edge_pairs: Optional[EdgePairs] = None,
+                species: Optional[Tuple[torch.Tensor, torch.Tensor]] = None) -> torch.Tensor:
         """``edge_pairs`` (with ``graph``): the reverse-edge pairing of a full neighbour list whose
         edge lengths agree bitwise within each pair; the radial weights are then formed once per
-        pair where ``fused.paired_conv_applies`` (same outputs, half the radial MLP work)."""
+        pair where ``fused.paired_conv_applies`` (same outputs, half the radial MLP work).
+        ``species = (edge_species, table)``: ``node_feats`` is ``table[atom_types]`` and
+        ``edge_species[e]`` the sender's row of ``table``; with pairs the layer then runs as a
+        species density where ``fused.species_conv_applies``."""
         idx_i, idx_j = edge_index[0], edge_index[1]
         residual_feats = node_feats if out_nodes is None else node_feats[:out_nodes]
         if edge_pairs is not None and graph is not None and fused.paired_conv_applies(self, node_feats):
-            pe = edge_pairs.edge
-            mlp_pairs = edge_feats.index_select(0, pe) * envelope.index_select(0, pe).unsqueeze(-1)
-            aggregated = fused.paired_conv(self, self.linear_first(node_feats), edge_attrs, mlp_pairs, graph,
-                                           edge_pairs, self._inv_sqrt_avg())
+            mlp_pairs = _ops.pair_inputs(edge_feats, envelope, edge_pairs.edge, edge_pairs.slot)
+            if species is not None and fused.species_conv_applies(self, node_feats, species[1].shape[0]):
+                aggregated = fused.species_conv(self, edge_attrs, mlp_pairs, graph, edge_pairs, species[0],
+                                                self.linear_first(species[1]), self._inv_sqrt_avg())
+            else:
+                aggregated = fused.paired_conv(self, self.linear_first(node_feats), edge_attrs, mlp_pairs, graph,
+                                               edge_pairs, self._inv_sqrt_avg())
             return self._finish(aggregated, residual_feats, out_nodes)
         if self.emb_i is not None:
             if atom_types is None:

@@ -1078,6 +1078,43 @@ def dense_bwd_pairs(grad_pairs: Tensor, weight: Tensor, scale: float) -> Tensor:
     return gx
 
 
+class _PairInputs(torch.autograd.Function):
+    """x[p] = feats[pair_edge[p]] * env[pair_edge[p]]: the radial-MLP input of each edge pair
+    (``fc_pair_inputs_fwd``); backward per edge, the lower edge of each pair taking the pair's
+    gradient (``fc_pair_inputs_bwd``). First-order only."""
+
+    @staticmethod
+    def forward(ctx, feats: Tensor, env: Tensor, pair_edge: Tensor, pair_slot: Tensor) -> Tensor:
+        f = _lib.contig("feats", feats)
+        en = _lib.contig("env", env)
+        pe = _i32("pair_edge", pair_edge)
+        width = f.shape[-1]
+        x = _lib.rows_empty(f, pe.shape[0], width)
+        _lib_call("fc_pair_inputs_fwd", pe.shape[0], width, pe.data_ptr(), f.data_ptr(), en.data_ptr(), x.data_ptr(),
+                  _lib.stream_of(f))
+        ctx.save_for_backward(f, en, _i32("pair_slot", pair_slot))
+        return x
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, gx: Tensor):
+        f, en, slot = ctx.saved_tensors
+        nf, ne = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        if not (nf or ne):
+            return None, None, None, None
+        gxc = _lib.contig("grad", gx)
+        g_f = _lib.rows_empty(f, *f.shape) if nf else None
+        g_e = _lib.rows_empty(en, *en.shape) if ne else None
+        _lib_call("fc_pair_inputs_bwd", f.shape[0], f.shape[-1], slot.data_ptr(), f.data_ptr(), en.data_ptr(),
+                  gxc.data_ptr(), _lib.ptr(g_f), _lib.ptr(g_e), _lib.stream_of(f))
+        return g_f, g_e, None, None
+
+
+def pair_inputs(feats: Tensor, env: Tensor, pair_edge: Tensor, pair_slot: Tensor) -> Tensor:
+    """Radial-MLP inputs feats * env of the lower edge of each pair (``o3._graph.EdgePairs``)."""
+    return _PairInputs.apply(feats, env, pair_edge, pair_slot)
+
+
 def _dense_setup(ctx, inputs, output):
     x, weight, bias, scale, act = inputs
     ctx.save_for_backward(x, weight, output[1])
@@ -1169,6 +1206,44 @@ def radial_mlp_bwd(grad_h2: Tensor, x: Tensor, w0: Tensor, s0: float, w1: Tensor
 @radial_mlp_bwd.register_fake
 def _(grad_h2, x, w0, s0, w1, s1):
     return torch.empty_like(x)
+
+
+def radial_mlp_hidden_fwd(x: Tensor, w0: Tensor, s0: float, w1: Tensor, s1: float) -> Tensor:
+    """h2 = silu(s1 silu(s0 x W0^T) W1^T) (n, 64): the radial MLP without its output layer
+    (``fc_radial_mlp_hidden_fwd``)."""
+    x = _lib.contig("x", x)
+    w0, w1 = _lib.contig("w0", w0), _lib.contig("w1", w1)
+    n_in = _radial_mlp_check(x, w0, w1)
+    x2 = x.reshape(-1, n_in)
+    h = _lib.rows_empty(x2, x2.shape[0], 64)
+    _lib_call("fc_radial_mlp_hidden_fwd", x2.shape[0], n_in, x2.data_ptr(), w0.data_ptr(), float(s0), w1.data_ptr(),
+              float(s1), h.data_ptr(), _lib.stream_of(x))
+    return h
+
+
+def species_density_fwd(csr, l_max: int, y_l_max: int, n_species: int, edge_species: Tensor, h: Tensor,
+                        y: Tensor, n_nodes: int) -> Tensor:
+    """dens[i, (l, m), Z, k] = sum over the receiver's edges of species-Z senders of h[pair, k] y[e, (l, m)]
+    (``fc_species_density_fwd``; ``csr`` a CSR struct carrying the edge pairing)."""
+    zj = _i32("edge_species", edge_species)
+    hh, yy = _lib.contig("h", h), _lib.contig("y", y)
+    dens = _lib.rows_empty(hh, n_nodes, (l_max + 1) ** 2 * n_species * 64)
+    _lib_call("fc_species_density_fwd", csr, int(l_max), int(y_l_max), int(n_species), zj.data_ptr(), hh.data_ptr(),
+              yy.data_ptr(), dens.data_ptr(), _lib.stream_of(hh))
+    return dens
+
+
+def species_density_bwd(csr, l_max: int, y_l_max: int, n_species: int, edge_species: Tensor, h: Tensor, y: Tensor,
+                        g_dens: Tensor) -> Tuple[Tensor, Tensor]:
+    """(dL/dh per edge, pair-major rows; dL/dy) of ``species_density_fwd`` (``fc_species_density_bwd``)."""
+    zj = _i32("edge_species", edge_species)
+    hh, yy, gd = _lib.contig("h", h), _lib.contig("y", y), _lib.contig("g_dens", g_dens)
+    n_edges = yy.shape[0]
+    g_h = _lib.rows_empty(hh, n_edges, 64)
+    g_y = _lib.rows_empty(yy, n_edges, yy.shape[1])
+    _lib_call("fc_species_density_bwd", csr, int(l_max), int(y_l_max), int(n_species), zj.data_ptr(), hh.data_ptr(),
+              yy.data_ptr(), gd.data_ptr(), g_h.data_ptr(), g_y.data_ptr(), _lib.stream_of(hh))
+    return g_h, g_y
 
 
 def dense_wgrad(grad_out: Tensor, pre: Optional[Tensor], act: int, x: Tensor, scale: float, need_weight: bool,

@@ -146,6 +146,35 @@ int fc_edge_pairs(const fc_csr* graph, const int32_t* idx_i, const int32_t* shif
                   int32_t* pair_edge, int64_t max_pairs, int32_t* counts, int32_t* workspace,
                   int64_t workspace_ints, void* stream);
 
+/* Radial-MLP inputs of edge pairs (no counterpart in the reference, which forms
+ * edge_feats * envelope for every edge, src/flashcart/nn/layers.py:350-356):
+ *   x[p, k] = feats[pair_edge[p], k] * env[pair_edge[p]]                 (n_pairs, width)
+ * and its backward for all n_edges edges: the lower edge of each pair (even pair_slot) gets
+ *   g_feats[e, k] = gx[p, k] * env[e],  g_env[e] = sum_k gx[p, k] feats[e, k],
+ * the other edge zeros. Either backward output may be NULL. */
+int fc_pair_inputs_fwd(int64_t n_pairs, int32_t width, const int32_t* pair_edge, const float* feats,
+                       const float* env, float* x, void* stream);
+int fc_pair_inputs_bwd(int64_t n_edges, int32_t width, const int32_t* pair_slot, const float* feats,
+                       const float* env, const float* gx, float* g_feats, float* g_env, void* stream);
+
+/* First interaction layer as a species density. Replaces the radial output layer and the
+ * 0 x L -> L convolution of the first InteractionLayer (reference src/flashcart/nn/layers.py
+ * :351-369) when its sender features depend on the species alone: with h (n_pairs, 64) the last
+ * hidden activation of the radial MLP per edge pair (graph->pair_slot required),
+ * y (n_edges, (y_l_max+1)^2) the edge attributes and edge_species[e] the species of the sender,
+ *   dens[i, (l, m), Z, k] = sum_{e -> i, species Z} h[pair(e), k] y[e, (l, m)],  l <= l_max,
+ * rows of (l_max+1)^2 x n_species x 64 floats (n_species <= 8), receiver-segmented, no atomics.
+ * The layer output is then fc_linear_fwd over dens (in_features 64, in_paths n_species). */
+int fc_species_density_fwd(const fc_csr* graph, int32_t l_max, int32_t y_l_max, int32_t n_species,
+                           const int32_t* edge_species, const float* h, const float* y, float* dens,
+                           void* stream);
+/* Its backward from g_dens = dL/d dens: g_h (n_edges, 64) per edge at row pair_slot[e] (the two
+ * rows of a pair sum to the gradient of its h row) and g_y (n_edges, (y_l_max+1)^2) (zero above
+ * l_max). */
+int fc_species_density_bwd(const fc_csr* graph, int32_t l_max, int32_t y_l_max, int32_t n_species,
+                           const int32_t* edge_species, const float* h, const float* y, const float* g_dens,
+                           float* g_h, float* g_y, void* stream);
+
 /* rowptr[n] = first edge with idx_sorted[e] >= n, for n in [0, n_nodes]. */
 int fc_csr_from_sorted(int64_t n_edges, const int32_t* idx_sorted, int64_t n_nodes,
                        int32_t* rowptr, void* stream);
@@ -249,6 +278,10 @@ int fc_dense_dgrad(int64_t n, int32_t k, int32_t m, const float* grad_out, const
  * rescaled SiLU. The hidden activations stay on chip; nothing but out is written. */
 int fc_radial_mlp_fwd(int64_t n, int32_t n_in, const float* x, const float* w0, float s0, const float* w1,
                       float s1, int32_t m, const float* w2, float s2, float* out, void* stream);
+/* Its hidden part alone: h2 (n, 64) = silu(s1 silu(s0 x W0^T) W1^T), the input of the output
+ * layer (no counterpart in the reference; the first layer's species density reads it). */
+int fc_radial_mlp_hidden_fwd(int64_t n, int32_t n_in, const float* x, const float* w0, float s0,
+                             const float* w1, float s1, float* h2, void* stream);
 /* Input gradient of its hidden part: grad_x (n, n_in) from grad_h2 = dL/dh2 (n, 64), the
  * hidden layers recomputed from x (replaces the two hidden fc_dense_dgrad calls). */
 int fc_radial_mlp_bwd(int64_t n, int32_t n_in, const float* x, const float* w0, float s0, const float* w1,

@@ -215,7 +215,9 @@ def test_paired_potential_matches_oracle_and_unpaired(case):
     assert not m.wants_edge_pairs(gd.positions)
     un = m.predict(graph.to(DEV), compute_forces=True)
     assert_close(out["energy"], un["energy"], 2e-6, 1e-6, "paired vs per-edge energy")
-    assert_close(out["forces"], un["forces"], 1e-5, 2e-5, "paired vs per-edge forces")
+    # float32 round-off of force sums whose terms reach the largest force
+    assert_close(out["forces"], un["forces"], 0.0, 5e-6 * float(un["forces"].abs().max()) + 1e-6,
+                 "paired vs per-edge forces")
 
 
 def test_replay_falls_back_when_pairing_breaks():
@@ -250,3 +252,90 @@ def test_replay_falls_back_when_pairing_breaks():
     # and back to a pairable list: replayed again
     out2 = m.predict(gd, compute_forces=True, use_compile=True)
     assert_close(out2["forces"], ref0["forces"], 0.0, 1e-4, "replayed forces after fallback")
+
+
+def test_pair_inputs_op():
+    """fc_pair_inputs_fwd/bwd against the same gather written with torch indexing."""
+    from flashcart_amd.o3 import _ops
+    numbers, pos, cell, pbc = fcc_alloy(2, 2, 2, seed=3)
+    g = AtomicGraph.from_arrays(numbers, pos, ["Cu", "Ni", "Fe", "Cr"], 5.0, cell=cell, pbc=pbc).to(DEV)
+    csr = _csr(g)
+    pairs = csr.edge_pairs(g.shifts)
+    gen = torch.Generator(device=DEV).manual_seed(2)
+    feats = torch.randn(csr.n_edges, 8, device=DEV, generator=gen, requires_grad=True)
+    env = torch.rand(csr.n_edges, device=DEV, generator=gen, requires_grad=True)
+    x = _ops.pair_inputs(feats, env, pairs.edge, pairs.slot)
+    pe = pairs.edge.long()
+    ref = feats[pe] * env[pe].unsqueeze(-1)
+    assert torch.equal(x, ref)
+    gx = torch.randn_like(x)
+    gf, ge = torch.autograd.grad(x, (feats, env), gx)
+    rf, re = torch.autograd.grad(ref, (feats, env), gx)
+    assert torch.equal(gf, rf)
+    assert_close(ge, re, 1e-6, 1e-6, "envelope gradient")
+
+
+@pytest.mark.parametrize("l_max,y_l_max", [(3, 3), (2, 3), (1, 1)])
+def test_species_density_op(l_max, y_l_max):
+    """fc_species_density_fwd/bwd against their definitions evaluated in float64 with torch."""
+    from flashcart_amd import _lib
+    from flashcart_amd.o3 import _ops
+    numbers, pos, cell, pbc = fcc_alloy(2, 2, 2, seed=3)
+    g = AtomicGraph.from_arrays(numbers, pos, ["Cu", "Ni", "Fe", "Cr"], 5.0, cell=cell, pbc=pbc).to(DEV)
+    csr = _csr(g)
+    pairs = csr.edge_pairs(g.shifts)
+    n, e, n_sp = csr.n_nodes, csr.n_edges, 3
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    zj = torch.randint(0, n_sp, (e,), device=DEV, generator=gen, dtype=torch.int32)
+    h = torch.randn(pairs.n_pairs, 64, device=DEV, generator=gen)
+    dy = (y_l_max + 1) ** 2
+    y = torch.randn(e, dy, device=DEV, generator=gen)
+    d = (l_max + 1) ** 2
+    st = _lib.csr_struct(n, e, csr.idx_j, csr.rowptr, pair_slot=pairs.slot)
+    dens = _ops.species_density_fwd(st, l_max, y_l_max, n_sp, zj, h, y, n)
+    he = h.double()[(pairs.slot // 2).long()]                       # (E, 64)
+    contrib = he[:, None, :] * y.double()[:, :d, None]              # (E, d, 64)
+    onehot = torch.nn.functional.one_hot(zj.long(), n_sp).double()  # (E, Z)
+    per_edge = contrib[:, :, None, :] * onehot[:, None, :, None]    # (E, d, Z, 64)
+    want = torch.zeros(n, d, n_sp, 64, dtype=torch.float64, device=DEV).index_add_(0, csr.idx_i.long(), per_edge)
+    assert_close(dens.view(n, d, n_sp, 64), want, 1e-5, 1e-5, "density")
+    gd = torch.randn(n, d * n_sp * 64, device=DEV, generator=gen)
+    g_h, g_y = _ops.species_density_bwd(st, l_max, y_l_max, n_sp, zj, h, y, gd)
+    gde = gd.double().view(n, d, n_sp, 64)[csr.idx_i.long()]        # (E, d, Z, 64)
+    gsel = (gde * onehot[:, None, :, None]).sum(2)                  # (E, d, 64)
+    want_h = (gsel * y.double()[:, :d, None]).sum(1)                # (E, 64) per edge
+    want_y = torch.zeros(e, dy, dtype=torch.float64, device=DEV)
+    want_y[:, :d] = (gsel * he[:, None, :]).sum(2)
+    assert_close(g_h[pairs.slot.long()], want_h, 1e-5, 1e-5, "dL/dh per edge")
+    assert_close(g_y, want_y, 1e-5, 1e-5, "dL/dy")
+
+
+def test_species_conv_matches_paired_conv():
+    """The first interaction layer as a species density against the same layer over edge pairs:
+    outputs and input gradients (edge attributes, radial inputs) at float32 round-off."""
+    from flashcart_amd.nn import fused
+    from flashcart_amd.o3 import _ops
+    numbers, pos, cell, pbc = fcc_alloy(3, 3, 3, seed=4)
+    cfg = model_config(["Cu", "Ni", "Fe", "Cr"], 128, 3, avg_neighbors=42.0)
+    g = AtomicGraph.from_arrays(numbers, pos, cfg["elements"], 5.0, cell=cell, pbc=pbc).to(DEV)
+    model = _model(cfg).to(DEV)
+    model.requires_grad_(False)
+    layer = model.interactions[0]
+    csr = _csr(g)
+    pairs = csr.edge_pairs(g.shifts)
+    gen = torch.Generator(device=DEV).manual_seed(8)
+    y = torch.randn(csr.n_edges, 16, device=DEV, generator=gen, requires_grad=True)
+    xp = torch.rand(pairs.n_pairs, 8, device=DEV, generator=gen, requires_grad=True)
+    table = model.embedding.weight
+    zj = torch.index_select(g.atom_types.to(torch.int32), 0, csr.idx_j)
+    alpha = layer._inv_sqrt_avg()
+    node = model.embedding(g.atom_types)
+    assert fused.species_conv_applies(layer, node, table.shape[0])
+    out_s = fused.species_conv(layer, y, xp, csr, pairs, zj, layer.linear_first(table), alpha)
+    out_p = fused.paired_conv(layer, layer.linear_first(node), y, xp, csr, pairs, alpha)
+    assert_close(out_s, out_p, 1e-5, 1e-5 * float(out_p.abs().max()), "species vs paired output")
+    go = torch.randn_like(out_p)
+    gs = torch.autograd.grad(out_s, (y, xp), go)
+    gp = torch.autograd.grad(out_p, (y, xp), go)
+    for a, b, what in zip(gs, gp, ("edge attributes", "radial inputs")):
+        assert_close(a, b, 1e-5, 1e-5 * float(b.abs().max()), f"species vs paired gradient of {what}")
