@@ -288,23 +288,49 @@ def paired_conv(layer, in1: Tensor, in2: Tensor, x_pairs: Tensor, graph, pairs, 
     return _PairedConv.apply(in1, in2, x_pairs, layer, graph, pairs.slot, alpha)
 
 
-def species_weights(x_table: Tensor, w2: Tensor, channels: int, l_max: int) -> List[Tensor]:
-    """B_l[c, Z * 64 + k] = x_table[Z, c] W2[l C + c, k]: the first layer's convolution and radial
-    output layer folded into one matrix per rank (the path (0, l, l) takes weight row block l)."""
-    n_species = x_table.shape[0]
-    xt = x_table.t().unsqueeze(-1)  # (C, Z, 1)
-    return [(xt * w2[l * channels:(l + 1) * channels].unsqueeze(1)).reshape(channels, n_species * 64).contiguous()
-            for l in range(l_max + 1)]
+def species_maps(layer, x_table: Tensor, alpha: float):
+    """Matrices and scales of the first interaction layer's species density, with its
+    ``linear_second`` folded in: per rank l,
+        M_l[o, Z * 64 + k] = sum_c Wsec_l[o, c] x_table[Z, c] W2[l C + c, k],
+        scale_l = alpha s2 s_l,
+    so that linear_second(TP(...))_l = scale_l dens_l @ M_l^T (the path (0, l, l) takes block l
+    of the radial output layer W2). Cached on the layer while the parameters, the table and
+    alpha are unchanged (recomputed under graph capture, which then replays the computation)."""
+    tp, lin, w2 = layer.tp, layer.linear_second, layer.radial_mlp[4].weight
+    c = tp.in1_features
+    lm = min(tp.in2_l_max, tp.out_l_max)
+    common = min(lm, lin.out_l_max)
+    srcs = [x_table, w2, *lin.weight]
+    key = tuple((t.data_ptr(), t._version) for t in srcs) + (float(alpha),)
+    capturing = torch.cuda.is_current_stream_capturing()
+    hit = layer.__dict__.get("_species_maps")
+    if not capturing and hit is not None and hit[0] == key:
+        return hit[1]
+    n_sp = x_table.shape[0]
+    mats = []
+    for l in range(common + 1):
+        # Bt[(Z, k), c] = x_table[Z, c] W2[l C + c, k]; M_l = Wsec_l @ Bt^T on the MFMA dense kernel
+        bt = (x_table.unsqueeze(1) * w2[l * c:(l + 1) * c].t().unsqueeze(0)).reshape(n_sp * 64, c).contiguous()
+        m, _ = _ops.dense_fwd(lin.weight[l].detach(), bt, None, 1.0, 0)
+        mats.append(m.contiguous())
+    s2 = layer.radial_mlp[4]._scale
+    cfg = (lm, lin.out_l_max, 64, lin.out_features, [n_sp] * (lm + 1),
+           [float(alpha) * s2 * lin._scale_list[l] for l in range(common + 1)])
+    out = (mats, cfg)
+    if not capturing:
+        layer.__dict__["_species_maps"] = (key, out)
+    return out
 
 
 class _SpeciesConv(torch.autograd.Function):
-    """Radial MLP + 0 x L -> L convolution of the first interaction layer, whose sender features
-    x_table[Z_j] depend on the sender's species alone, as a species density
-    (``csrc/fc_species.hip``): the radial MLP up to its last hidden activation h (per edge pair),
-    the receiver density dens[i, (l, m), Z, k] = sum_{e -> i, Z_j = Z} h_e[k] y_e[(l, m)], and one
-    equivariant linear map per rank with the matrices of ``species_weights``
-    (out_l = alpha s2 dens_l @ B_l^T). Same function as the per-edge path, with sums in another
-    order; the E x paths x C weights are never formed. Reference ``nn/layers.py:351-369``.
+    """Radial MLP + 0 x L -> L convolution + ``linear_second`` of the first interaction layer,
+    whose sender features x_table[Z_j] depend on the sender's species alone, as a species
+    density (``csrc/fc_species.hip``): the radial MLP up to its last hidden activation h (per edge
+    pair), the receiver density dens[i, (l, m), Z, k] = sum_{e -> i, Z_j = Z} h_e[k] y_e[(l, m)],
+    and one equivariant linear map per rank with the matrices of ``species_maps``. Same function
+    as the per-edge path followed by ``linear_second``, with sums in another order; the
+    E x paths x C weights and the convolution output are never formed. Reference
+    ``nn/layers.py:351-369``.
     """
 
     @staticmethod
@@ -312,14 +338,13 @@ class _SpeciesConv(torch.autograd.Function):
                 x_table: Tensor, alpha: float) -> Tensor:
         from flashcart_amd import _lib
         tp = layer.tp
-        l0, l1, l2 = layer.radial_mlp[0], layer.radial_mlp[2], layer.radial_mlp[4]
-        n_sp, c = x_table.shape[0], tp.in1_features
+        l0, l1 = layer.radial_mlp[0], layer.radial_mlp[2]
+        n_sp = x_table.shape[0]
         lm = min(tp.in2_l_max, tp.out_l_max)
         h = _ops.radial_mlp_hidden_fwd(x_pairs, l0.weight, l0._scale, l1.weight, l1._scale)
         csr = _lib.csr_struct(graph.n_nodes, graph.n_edges, graph.idx_j, graph.rowptr, pair_slot=pairs.slot)
         dens = _ops.species_density_fwd(csr, lm, tp.in2_l_max, n_sp, edge_species, h, y, graph.n_nodes)
-        mats = species_weights(x_table, l2.weight, c, lm)
-        cfg = (lm, lm, 64, c, [n_sp] * (lm + 1), [float(alpha) * l2._scale] * (lm + 1))
+        mats, cfg = species_maps(layer, x_table, alpha)
         out = _ops.linear_fwd(dens, mats, *cfg)
         ctx.save_for_backward(y, x_pairs, h, edge_species, pairs.slot, *mats)
         ctx.layer, ctx.graph, ctx.cfg, ctx.n_sp = layer, graph, cfg, n_sp
@@ -353,12 +378,15 @@ def species_conv_applies(layer, node_feats: Tensor, n_species: int) -> bool:
     ``paired_conv_applies``, rank-0 sender features of one channel block through a frozen
     ``linear_first``, single-channel edge attributes, unreduced paths, at most
     ``MAX_DENSITY_SPECIES`` species."""
-    tp = layer.tp
+    tp, lin = layer.tp, layer.linear_second
     if layer.in1_l_max != 0 or tp.in1_l_max != 0 or tp.in2_features != 1 or tp.reduce_paths or tp.symmetric_product:
+        return False
+    lm = min(tp.in2_l_max, tp.out_l_max)
+    if lin.in_l_max != lm or lin.in_paths != [1] * (lm + 1) or lin.in_features != tp.in1_features:
         return False
     if not 1 <= n_species <= MAX_DENSITY_SPECIES:
         return False
-    if any(p.requires_grad for p in layer.linear_first.parameters()):
+    if any(p.requires_grad for p in layer.linear_first.parameters()) or any(p.requires_grad for p in lin.parameters()):
         return False
     return paired_conv_applies(layer, node_feats)
 

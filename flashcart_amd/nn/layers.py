@@ -204,9 +204,11 @@ class InteractionLayer(nn.Module):
         residual_feats = node_feats if out_nodes is None else node_feats[:out_nodes]
         if edge_pairs is not None and graph is not None and fused.paired_conv_applies(self, node_feats):
             mlp_pairs = _ops.pair_inputs(edge_feats, envelope, edge_pairs.edge, edge_pairs.slot)
-            if species is not None and fused.species_conv_applies(self, node_feats, species[1].shape[0]):
-                aggregated = fused.species_conv(self, edge_attrs, mlp_pairs, graph, edge_pairs, species[0],
-                                                self.linear_first(species[1]), self._inv_sqrt_avg())
+            if species is not None and out_nodes is None and \
+                    fused.species_conv_applies(self, node_feats, species[1].shape[0]):
+                mapped = fused.species_conv(self, edge_attrs, mlp_pairs, graph, edge_pairs, species[0],
+                                            self.linear_first(species[1]), self._inv_sqrt_avg())
+                return self._finish(mapped, residual_feats, out_nodes, mapped=True)
             else:
                 aggregated = fused.paired_conv(self, self.linear_first(node_feats), edge_attrs, mlp_pairs, graph,
                                                edge_pairs, self._inv_sqrt_avg())
@@ -228,14 +230,18 @@ class InteractionLayer(nn.Module):
         return self._finish(aggregated, residual_feats, out_nodes)
 
     def _finish(self, aggregated: torch.Tensor, residual_feats: torch.Tensor,
-                out_nodes: Optional[int]) -> torch.Tensor:
+                out_nodes: Optional[int], mapped: bool = False) -> torch.Tensor:
+        """linear_second, skip connection and norm; ``mapped``: ``aggregated`` is already the
+        output of linear_second (the species density folds it in)."""
         if out_nodes is not None:
             aggregated = aggregated[:out_nodes]
-        if self.skip_projection is not None and self.in1_l_max > 0:
+        if self.skip_projection is not None and self.in1_l_max > 0 and not mapped:
             # the skip projection enters linear_second's GEMM epilogue as its residual
             out = self.linear_second(aggregated, residual=self.skip_projection(residual_feats))
+        elif mapped and self.skip_projection is not None and self.in1_l_max > 0:
+            out = aggregated + self.skip_projection(residual_feats)
         else:
-            out = self.linear_second(aggregated)
+            out = aggregated if mapped else self.linear_second(aggregated)
             if self.skip_projection is not None:
                 skip = self.skip_projection(residual_feats)
                 out = _AddLeading.apply(out, skip) if torch.is_grad_enabled() else \

@@ -214,7 +214,7 @@ def test_paired_potential_matches_oracle_and_unpaired(case):
         layer.radial_mlp.requires_grad_(True)
     assert not m.wants_edge_pairs(gd.positions)
     un = m.predict(graph.to(DEV), compute_forces=True)
-    assert_close(out["energy"], un["energy"], 2e-6, 1e-6, "paired vs per-edge energy")
+    assert_close(out["energy"], un["energy"], 5e-6, 1e-6, "paired vs per-edge energy")
     # float32 round-off of force sums whose terms reach the largest force
     assert_close(out["forces"], un["forces"], 0.0, 5e-6 * float(un["forces"].abs().max()) + 1e-6,
                  "paired vs per-edge forces")
@@ -311,8 +311,9 @@ def test_species_density_op(l_max, y_l_max):
 
 
 def test_species_conv_matches_paired_conv():
-    """The first interaction layer as a species density against the same layer over edge pairs:
-    outputs and input gradients (edge attributes, radial inputs) at float32 round-off."""
+    """The first interaction layer as a species density (linear_second folded in) against the same
+    layer over edge pairs followed by linear_second: outputs and input gradients (edge attributes,
+    radial inputs) at float32 round-off; a second call reuses the cached maps."""
     from flashcart_amd.nn import fused
     from flashcart_amd.o3 import _ops
     numbers, pos, cell, pbc = fcc_alloy(3, 3, 3, seed=4)
@@ -332,7 +333,9 @@ def test_species_conv_matches_paired_conv():
     node = model.embedding(g.atom_types)
     assert fused.species_conv_applies(layer, node, table.shape[0])
     out_s = fused.species_conv(layer, y, xp, csr, pairs, zj, layer.linear_first(table), alpha)
-    out_p = fused.paired_conv(layer, layer.linear_first(node), y, xp, csr, pairs, alpha)
+    out_p = layer.linear_second(fused.paired_conv(layer, layer.linear_first(node), y, xp, csr, pairs, alpha))
+    again = fused.species_conv(layer, y, xp, csr, pairs, zj, layer.linear_first(table), alpha)
+    assert torch.equal(out_s, again)
     assert_close(out_s, out_p, 1e-5, 1e-5 * float(out_p.abs().max()), "species vs paired output")
     go = torch.randn_like(out_p)
     gs = torch.autograd.grad(out_s, (y, xp), go)
