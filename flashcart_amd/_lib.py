@@ -89,6 +89,7 @@ _SIGNATURES = {
     "fc_linear_fwd": (c_int, [ctypes.POINTER(LinearDesc), c_i64, c_vp, c_f32, c_vp, c_vp, c_vp]),
     "fc_linear_dgrad": (c_int, [ctypes.POINTER(LinearDesc), c_i64, c_vp, c_f32, c_vp, c_vp, c_vp]),
     "fc_dense_fwd": (c_int, [c_i64, c_i32, c_i32, c_vp, c_vp, c_f32, c_vp, c_i32, c_vp, c_vp, c_vp]),
+    "fc_dense_fwd_pairsum": (c_int, [c_i64, c_i32, c_i32, c_vp, c_vp, c_f32, c_vp, c_vp]),
     "fc_dense_dgrad": (c_int, [c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_f32, c_i32, c_vp, c_vp]),
     "fc_radial_mlp_fwd": (c_int, [c_i64, c_i32, c_vp, c_vp, c_f32, c_vp, c_f32, c_i32, c_vp, c_f32, c_vp, c_vp]),
     "fc_radial_mlp_hidden_fwd": (c_int, [c_i64, c_i32, c_vp, c_vp, c_f32, c_vp, c_f32, c_vp, c_vp]),

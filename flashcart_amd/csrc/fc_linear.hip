@@ -58,6 +58,7 @@ struct GemmBatch {
   int32_t trans_b;    // 1: B(k, o) = W[o*K + k] (forward); 0: B(k, o) = W[k*N + o] (input gradient)
   int32_t act;        // 1: rescaled SiLU epilogue (fwd)
   int32_t act_bwd;    // 1: rescaled SiLU derivative prologue on A (dgrad)
+  int32_t pair_sum;   // 1: A rows hold two K-long halves, multiplied as their sum (pipelined kernel only)
 };
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
@@ -427,8 +428,12 @@ struct PipeTile {
   int ri, r0, c0, K;
 };
 
-template <int BM, int BN, int WM, int WN, int MI, bool KB>
-__global__ void __launch_bounds__(256, (BM + BN) * 32 * 4 * 3 <= 80 * 1024 ? 2 : 1) gemm_pipe_kernel(GemmBatch gb, int32_t tiles_per_xcd) {
+// PS (pair sum): every A row holds two halves of K floats, A[r, 0:K] and A[r, K:2K], and the
+// product is taken with their sum; both halves go to LDS by direct loads and are added as the
+// MFMA operands are read, so the MFMA work is that of K (the radial output layer's input
+// gradient over edge pairs, whose two edges share the layer's output row).
+template <int BM, int BN, int WM, int WN, int MI, bool KB, bool PS = false>
+__global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 80 * 1024 ? 2 : 1) gemm_pipe_kernel(GemmBatch gb, int32_t tiles_per_xcd) {
   static_assert(WM * WN == 4, "four waves");
   static_assert(MI == 32 || MI == 16, "MFMA block: 32x32x2 or 16x16x4");
   constexpr int TM = BM / WM, TN = BN / WN;
@@ -437,12 +442,13 @@ __global__ void __launch_bounds__(256, (BM + BN) * 32 * 4 * 3 <= 80 * 1024 ? 2 :
   typedef float accv __attribute__((ext_vector_type(NV)));
   constexpr int A_DMA = BM * 8 / 256;  // 16-byte chunks per thread and K step
   constexpr int B_DMA = BN * 8 / 256;
-  constexpr int L = A_DMA + B_DMA;     // direct loads per wave and K step
+  constexpr int AH = PS ? 2 : 1;       // A halves
+  constexpr int L = AH * A_DMA + B_DMA;  // direct loads per wave and K step
   static_assert(A_DMA >= 1 && B_DMA >= 1 && L <= 15, "tile shape");
   constexpr int BQ = BN / 4;           // chunks per k-major B row
-  __shared__ __attribute__((aligned(16))) float As0[BM * 32];
-  __shared__ __attribute__((aligned(16))) float As1[BM * 32];
-  __shared__ __attribute__((aligned(16))) float As2[BM * 32];
+  __shared__ __attribute__((aligned(16))) float As0[AH * BM * 32];
+  __shared__ __attribute__((aligned(16))) float As1[AH * BM * 32];
+  __shared__ __attribute__((aligned(16))) float As2[AH * BM * 32];
   __shared__ __attribute__((aligned(16))) float Bs0[BN * 32];
   __shared__ __attribute__((aligned(16))) float Bs1[BN * 32];
   __shared__ __attribute__((aligned(16))) float Bs2[BN * 32];
@@ -510,6 +516,10 @@ __global__ void __launch_bounds__(256, (BM + BN) * 32 * 4 * 3 <= 80 * 1024 ? 2 :
     const int64_t bstep = KB ? (int64_t)p_k * gb.r[pt.ri].N : (int64_t)p_k;
 #pragma unroll
     for (int j = 0; j < A_DMA; ++j) lds_dma16(a_src[j] + p_k, as + (j * 4 + wave) * 256);
+    if constexpr (PS) {
+#pragma unroll
+      for (int j = 0; j < A_DMA; ++j) lds_dma16(a_src[j] + pt.K + p_k, as + BM * 32 + (j * 4 + wave) * 256);
+    }
 #pragma unroll
     for (int j = 0; j < B_DMA; ++j) lds_dma16(b_src[j] + bstep, bs + (j * 4 + wave) * 256);
     ++n_issued;
@@ -547,6 +557,10 @@ __global__ void __launch_bounds__(256, (BM + BN) * 32 * 4 * 3 <= 80 * 1024 ? 2 :
       for (int i = 0; i < FM; ++i) {
         const int row = wm * TM + i * MI + (lane & (MI - 1));
         a4[i] = *reinterpret_cast<const float4*>(as + row * 32 + 4 * (ch ^ pipe_swz(row)));
+        if constexpr (PS) {
+          const float4 hi = *reinterpret_cast<const float4*>(as + BM * 32 + row * 32 + 4 * (ch ^ pipe_swz(row)));
+          a4[i].x += hi.x; a4[i].y += hi.y; a4[i].z += hi.z; a4[i].w += hi.w;
+        }
       }
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
@@ -706,7 +720,7 @@ static bool pipe_ok(const GemmBatch& gb, int n_ranks) {
   return true;
 }
 
-template <int BM, int BN, int WM, int WN, int MI>
+template <int BM, int BN, int WM, int WN, int MI, bool PS = false>
 int launch_pipe_cfg(GemmBatch gb, int n_ranks, hipStream_t s) {
   int64_t total = 0;
   for (int l = 0; l < n_ranks; ++l) {
@@ -724,8 +738,8 @@ int launch_pipe_cfg(GemmBatch gb, int n_ranks, hipStream_t s) {
   if (grid > total) grid = total;
   if (grid >= 8) grid -= grid % 8;
   const int32_t per_xcd = (int32_t)((total + 7) / 8);
-  if (gb.trans_b) hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WM, WN, MI, false>), dim3((unsigned)grid), dim3(256), 0, s, gb, per_xcd);
-  else hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WM, WN, MI, true>), dim3((unsigned)grid), dim3(256), 0, s, gb, per_xcd);
+  if (gb.trans_b) hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WM, WN, MI, false, PS>), dim3((unsigned)grid), dim3(256), 0, s, gb, per_xcd);
+  else hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WM, WN, MI, true, PS>), dim3((unsigned)grid), dim3(256), 0, s, gb, per_xcd);
   FC_LAUNCH_CHECK();
   return FC_OK;
 }
@@ -771,6 +785,10 @@ int launch_gemm(GemmBatch gb, int n_ranks, hipStream_t s) {
   // (the radial output layer's input gradient: 112 vs 99 TFLOP/s), 64 x 128 otherwise.
   // Launches with fewer 128-row tiles than two per CU (the 1,536-atom water box) take 64 x 64
   // tiles instead, for twice the workgroups.
+  if (gb.pair_sum) {  // forward layout, at most 64 output columns, pipelined kernel only
+    if (!gb.trans_b || max_n > 64 || !pipe_ok(gb, n_ranks)) return FC_ERR_SHAPE;
+    return launch_pipe_cfg<64, 64, 2, 2, 16, true>(gb, n_ranks, s);
+  }
   if (pipe_ok(gb, n_ranks)) {
     if (max_n <= 64) {
       int64_t tiles128 = 0;
@@ -1305,6 +1323,23 @@ extern "C" int fc_dense_fwd(int64_t n, int32_t k, int32_t m, const float* x, con
   g.B = w;
   g.D = out; g.d_row = m; g.d_comp = 0;
   g.pre = pre_act;
+  g.comps = 1; g.M = (int32_t)n; g.K = k; g.N = m; g.scale = scale;
+  return launch_gemm(gb, 1, (hipStream_t)stream);
+}
+
+extern "C" int fc_dense_fwd_pairsum(int64_t n, int32_t k, int32_t m, const float* x, const float* w, float scale,
+                                    float* out, void* stream) {
+  if (n < 0 || k < 1 || m < 1 || m > 64) return FC_ERR_BAD_DESC;
+  if (n == 0) return FC_OK;
+  if (!x || !w || !out) return FC_ERR_NULL;
+  if (n > 0x7fffffff || (k & 31) || (m & 3) || ((uintptr_t)x & 15) || ((uintptr_t)w & 15)) return FC_ERR_SHAPE;
+  GemmBatch gb{};
+  gb.trans_b = 1;
+  gb.pair_sum = 1;
+  GemmRank& g = gb.r[0];
+  g.A = x; g.a_row = 2 * (int64_t)k; g.a_comp = 0;
+  g.B = w;
+  g.D = out; g.d_row = m; g.d_comp = 0;
   g.comps = 1; g.M = (int32_t)n; g.K = k; g.N = m; g.scale = scale;
   return launch_gemm(gb, 1, (hipStream_t)stream);
 }

@@ -1062,19 +1062,23 @@ def _(grad_out, pre, weight, scale, act):
 def dense_bwd_pairs(grad_pairs: Tensor, weight: Tensor, scale: float) -> Tensor:
     """Input gradient of a bias-free linear layer whose output rows are shared by pairs of
     consumers: gx[p] = scale (g[2p] + g[2p + 1]) W for a pair-major (2P, m) gradient ``g``
-    (``tp_bwd`` with ``pair_slot``). One GEMM over the (P, 2m) view with the stacked weight
-    [W; W], so the pair sum happens in the K loop."""
+    (``tp_bwd`` with ``pair_slot``). One GEMM over the (P, 2m) view that adds the two halves of
+    each row as its operands are read (``fc_dense_fwd_pairsum``): the MFMA work of P rows."""
     go = _lib.contig("grad_pairs", grad_pairs)
     w = _lib.contig("weight", weight)
     m, k = w.shape
     if go.dim() != 2 or go.shape[1] != m or go.shape[0] % 2:
         raise RuntimeError(f"grad_pairs must be (2P, {m}), got {tuple(go.shape)}.")
     n_pairs = go.shape[0] // 2
-    wt = w.t().contiguous()
-    wt2 = torch.cat([wt, wt], dim=1)  # (k, 2m): the forward kernel's (N, K) weight
+    wt = w.t().contiguous()  # (k, m): the forward kernel's (N, K) weight
     gx = _lib.rows_empty(go, n_pairs, k)
-    _lib_call("fc_dense_fwd", n_pairs, 2 * m, k, go.data_ptr(), wt2.data_ptr(), float(scale), None, 0, None,
-              gx.data_ptr(), _lib.stream_of(go))
+    if m % 32 == 0 and k <= 64 and k % 4 == 0 and go.data_ptr() % 16 == 0:
+        _lib_call("fc_dense_fwd_pairsum", n_pairs, m, k, go.data_ptr(), wt.data_ptr(), float(scale), gx.data_ptr(),
+                  _lib.stream_of(go))
+    else:  # other widths: one GEMM over K = 2m with the stacked weight [W; W]
+        wt2 = torch.cat([wt, wt], dim=1)
+        _lib_call("fc_dense_fwd", n_pairs, 2 * m, k, go.data_ptr(), wt2.data_ptr(), float(scale), None, 0, None,
+                  gx.data_ptr(), _lib.stream_of(go))
     return gx
 
 

@@ -267,6 +267,12 @@ int fc_linear_dgrad(const fc_linear_desc* desc, int64_t n_rows, const float* gra
  * receives the value before the activation when non-NULL. */
 int fc_dense_fwd(int64_t n, int32_t k, int32_t m, const float* x, const float* w, float scale,
                  const float* bias, int32_t act, float* pre_act, float* out, void* stream);
+/* out (n, m) = scale * (x[:, 0:k] + x[:, k:2k]) @ W^T for x (n, 2k), W (m, k), m <= 64, k a
+ * multiple of 32, x and W 16-byte aligned: a dense layer applied to the sum of two row halves
+ * without forming it (no counterpart in the reference; the radial output layer's input gradient
+ * over edge pairs, whose two edges' weight gradients sit side by side). */
+int fc_dense_fwd_pairsum(int64_t n, int32_t k, int32_t m, const float* x, const float* w, float scale,
+                         float* out, void* stream);
 /* grad_x (n, k) = (grad_out * act'(pre_act)) @ W * scale. */
 int fc_dense_dgrad(int64_t n, int32_t k, int32_t m, const float* grad_out, const float* pre_act,
                    const float* w, float scale, int32_t act, float* grad_x, void* stream);

@@ -342,3 +342,16 @@ def test_species_conv_matches_paired_conv():
     gp = torch.autograd.grad(out_p, (y, xp), go)
     for a, b, what in zip(gs, gp, ("edge attributes", "radial inputs")):
         assert_close(a, b, 1e-5, 1e-5 * float(b.abs().max()), f"species vs paired gradient of {what}")
+
+
+@pytest.mark.parametrize("m", [2176, 272])
+def test_dense_bwd_pairs(m):
+    """The pair-summed input gradient (fc_dense_fwd_pairsum, and the stacked-weight form for
+    widths that are not multiples of 32) against torch float64."""
+    from flashcart_amd.o3 import _ops
+    gen = torch.Generator(device=DEV).manual_seed(9)
+    g = torch.randn(2 * 1001, m, device=DEV, generator=gen)
+    w = torch.randn(m, 64, device=DEV, generator=gen)
+    got = _ops.dense_bwd_pairs(g, w, 0.37)
+    want = 0.37 * (g.double()[0::2] + g.double()[1::2]) @ w.double()
+    assert_close(got, want, 1e-5, 1e-5 * float(want.abs().max()), "pair-summed input gradient")
