@@ -75,7 +75,7 @@ _SIGNATURES = {
     "fc_csr_from_sorted": (c_int, [c_i64, c_vp, c_i64, c_vp, c_vp]),
     "fc_edge_grad_to_nodes": (c_int, [ctypes.POINTER(CSR), c_vp, c_vp, c_vp]),
     "fc_edge_pairs_workspace": (c_i64, [c_i64]),
-    "fc_edge_pairs": (c_int, [ctypes.POINTER(CSR), c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp]),
+    "fc_edge_pairs": (c_int, [ctypes.POINTER(CSR), c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp]),
     "fc_pair_inputs_fwd": (c_int, [c_i64, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "fc_pair_inputs_bwd": (c_int, [c_i64, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "fc_tp_num_paths": (c_int, [ctypes.POINTER(TPDesc)]),
@@ -89,13 +89,14 @@ _SIGNATURES = {
     "fc_linear_fwd": (c_int, [ctypes.POINTER(LinearDesc), c_i64, c_vp, c_f32, c_vp, c_vp, c_vp]),
     "fc_linear_dgrad": (c_int, [ctypes.POINTER(LinearDesc), c_i64, c_vp, c_f32, c_vp, c_vp, c_vp]),
     "fc_dense_fwd": (c_int, [c_i64, c_i32, c_i32, c_vp, c_vp, c_f32, c_vp, c_i32, c_vp, c_vp, c_vp]),
-    "fc_dense_fwd_pairsum": (c_int, [c_i64, c_i32, c_i32, c_vp, c_vp, c_f32, c_vp, c_vp]),
+    "fc_dense_fwd_pairsum": (c_int, [c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp, c_f32, c_vp, c_vp]),
     "fc_dense_dgrad": (c_int, [c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_f32, c_i32, c_vp, c_vp]),
     "fc_radial_mlp_fwd": (c_int, [c_i64, c_i32, c_vp, c_vp, c_f32, c_vp, c_f32, c_i32, c_vp, c_f32, c_vp, c_vp]),
     "fc_radial_mlp_hidden_fwd": (c_int, [c_i64, c_i32, c_vp, c_vp, c_f32, c_vp, c_f32, c_vp, c_vp]),
     "fc_species_density_fwd": (c_int, [ctypes.POINTER(CSR), c_i32, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "fc_species_density_bwd": (c_int, [ctypes.POINTER(CSR), c_i32, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                        c_vp]),
+    "fc_radial_mlp_bwd_pairsum": (c_int, [c_i64, c_i32, c_vp, c_vp, c_f32, c_vp, c_f32, c_vp, c_vp, c_vp]),
     "fc_radial_mlp_bwd": (c_int, [c_i64, c_i32, c_vp, c_vp, c_f32, c_vp, c_f32, c_vp, c_vp, c_vp]),
     "fc_linear_wgrad_workspace": (c_i64, [ctypes.POINTER(LinearDesc), c_i64, ctypes.POINTER(c_vp)]),
     "fc_linear_wgrad": (c_int, [ctypes.POINTER(LinearDesc), c_i64, c_vp, c_vp, c_f32, ctypes.POINTER(c_vp), c_vp,

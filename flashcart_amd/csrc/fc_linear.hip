@@ -45,6 +45,8 @@ struct GemmRank {
   float* pre;       // dense fwd: pre-activation output (same layout as D)
   const float* R;   // residual added to the result (same layout as D; may be D itself)
   int64_t a_row, a_comp, d_row, d_comp;
+  const int32_t* a_lo;  // pair sum (gb.pair_sum) with gathered halves: A row r's halves are rows a_lo[r]
+  const int32_t* a_hi;  // and a_hi[r] of A (a_row floats apart); NULL: A row r holds both halves
   int32_t M;        // rows = n * comps
   int32_t comps, K, N;
   float scale;
@@ -428,10 +430,11 @@ struct PipeTile {
   int ri, r0, c0, K;
 };
 
-// PS (pair sum): every A row holds two halves of K floats, A[r, 0:K] and A[r, K:2K], and the
-// product is taken with their sum; both halves go to LDS by direct loads and are added as the
-// MFMA operands are read, so the MFMA work is that of K (the radial output layer's input
-// gradient over edge pairs, whose two edges share the layer's output row).
+// PS (pair sum): every A row is the sum of two halves of K floats, A[r, 0:K] and A[r, K:2K], or
+// rows a_lo[r] and a_hi[r] of A when the rank gives those index arrays; both halves go to LDS by
+// direct loads and are added as the MFMA operands are read, so the MFMA work is that of K (the
+// radial output layer's input gradient over edge pairs, whose two edges share the layer's
+// output row).
 template <int BM, int BN, int WM, int WN, int MI, bool KB, bool PS = false>
 __global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 80 * 1024 ? 2 : 1) gemm_pipe_kernel(GemmBatch gb, int32_t tiles_per_xcd) {
   static_assert(WM * WN == 4, "four waves");
@@ -484,6 +487,7 @@ __global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 
   int p_tile = t_first, p_k = 0, n_issued = 0;
   PipeTile pt{0, 0, 0, 32};
   const float* a_src[A_DMA];
+  const float* a_src2[PS ? A_DMA : 1];  // second halves
   const float* b_src[B_DMA];
   auto p_setup = [&]() {
     if (p_tile >= t_end) return;
@@ -494,8 +498,18 @@ __global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 
       const int s = (j * 4 + wave) * 64 + lane;
       const int row = s >> 3, c = (s & 7) ^ pipe_swz(row);
       const int grow = min(pt.r0 + row, g.M - 1);
+      if constexpr (PS) {
+        if (g.a_lo) {
+          // Gathered halves. Using these loads waits for every outstanding vector load, the
+          // direct loads of the ring included (once per tile).
+          a_src[j] = g.A + (int64_t)g.a_lo[grow] * g.a_row + 4 * c;
+          a_src2[j] = g.A + (int64_t)g.a_hi[grow] * g.a_row + 4 * c;
+          continue;
+        }
+      }
       const int n = grow / g.comps, cc = grow - n * g.comps;
       a_src[j] = g.A + (int64_t)n * g.a_row + (int64_t)cc * g.a_comp + 4 * c;
+      if constexpr (PS) a_src2[j] = a_src[j] + g.K;
     }
 #pragma unroll
     for (int j = 0; j < B_DMA; ++j) {
@@ -518,7 +532,7 @@ __global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 
     for (int j = 0; j < A_DMA; ++j) lds_dma16(a_src[j] + p_k, as + (j * 4 + wave) * 256);
     if constexpr (PS) {
 #pragma unroll
-      for (int j = 0; j < A_DMA; ++j) lds_dma16(a_src[j] + pt.K + p_k, as + BM * 32 + (j * 4 + wave) * 256);
+      for (int j = 0; j < A_DMA; ++j) lds_dma16(a_src2[j] + p_k, as + BM * 32 + (j * 4 + wave) * 256);
     }
 #pragma unroll
     for (int j = 0; j < B_DMA; ++j) lds_dma16(b_src[j] + bstep, bs + (j * 4 + wave) * 256);
@@ -1224,6 +1238,8 @@ __global__ void __launch_bounds__(256, 2) radial_mlp_fwd_kernel(int64_t n, int n
 
 // Input gradient of the two hidden layers: given gh2 = dL/dh2 (n, 64),
 //   dpre2 = gh2 * silu'(pre2), dh1 = s1 dpre2 W1, dpre1 = dh1 * silu'(pre1), dx = s0 dpre1 W0.
+// PAIRS: gh2 holds two rows per input row (rows 2r and 2r + 1, summed).
+template <bool PAIRS = false>
 __global__ void __launch_bounds__(256, 2) radial_mlp_bwd_kernel(int64_t n, int n_in, const float* __restrict__ x,
                                                                  const float* __restrict__ w0, float s0,
                                                                  const float* __restrict__ w1, float s1,
@@ -1242,7 +1258,11 @@ __global__ void __launch_bounds__(256, 2) radial_mlp_bwd_kernel(int64_t n, int n
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int64_t row = r0 + wave * 32 + acc_row(v, lane);
-      g2[j][v] = row < n ? gh2[row * 64 + j * 32 + (lane & 31)] : 0.f;
+      if constexpr (PAIRS)
+        g2[j][v] = row < n ? gh2[2 * row * 64 + j * 32 + (lane & 31)] + gh2[(2 * row + 1) * 64 + j * 32 + (lane & 31)]
+                           : 0.f;
+      else
+        g2[j][v] = row < n ? gh2[row * 64 + j * 32 + (lane & 31)] : 0.f;
     }
   mlp_stage_x(As, n, n_in, x, r0);
   mlp_stage_weights(B0, B1, n_in, w0, w1, false);
@@ -1327,17 +1347,19 @@ extern "C" int fc_dense_fwd(int64_t n, int32_t k, int32_t m, const float* x, con
   return launch_gemm(gb, 1, (hipStream_t)stream);
 }
 
-extern "C" int fc_dense_fwd_pairsum(int64_t n, int32_t k, int32_t m, const float* x, const float* w, float scale,
-                                    float* out, void* stream) {
+extern "C" int fc_dense_fwd_pairsum(int64_t n, int32_t k, int32_t m, const float* x, const int32_t* rows_lo,
+                                    const int32_t* rows_hi, const float* w, float scale, float* out, void* stream) {
   if (n < 0 || k < 1 || m < 1 || m > 64) return FC_ERR_BAD_DESC;
   if (n == 0) return FC_OK;
   if (!x || !w || !out) return FC_ERR_NULL;
+  if ((rows_lo == nullptr) != (rows_hi == nullptr)) return FC_ERR_NULL;
   if (n > 0x7fffffff || (k & 31) || (m & 3) || ((uintptr_t)x & 15) || ((uintptr_t)w & 15)) return FC_ERR_SHAPE;
   GemmBatch gb{};
   gb.trans_b = 1;
   gb.pair_sum = 1;
   GemmRank& g = gb.r[0];
-  g.A = x; g.a_row = 2 * (int64_t)k; g.a_comp = 0;
+  g.A = x; g.a_row = (rows_lo ? 1 : 2) * (int64_t)k; g.a_comp = 0;
+  g.a_lo = rows_lo; g.a_hi = rows_hi;
   g.B = w;
   g.D = out; g.d_row = m; g.d_comp = 0;
   g.comps = 1; g.M = (int32_t)n; g.K = k; g.N = m; g.scale = scale;
@@ -1384,8 +1406,22 @@ extern "C" int fc_radial_mlp_bwd(int64_t n, int32_t n_in, const float* x, const 
   if (!x || !w0 || !w1 || !grad_h2 || !grad_x) return FC_ERR_NULL;
   const int64_t blocks = (n + WIDE_BM - 1) / WIDE_BM;
   if (blocks > 0x7fffffff) return FC_ERR_SHAPE;
-  hipLaunchKernelGGL(radial_mlp_bwd_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, n, (int)n_in,
-                     x, w0, s0, w1, s1, grad_h2, grad_x);
+  hipLaunchKernelGGL(radial_mlp_bwd_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, n,
+                     (int)n_in, x, w0, s0, w1, s1, grad_h2, grad_x);
+  FC_LAUNCH_CHECK();
+  return FC_OK;
+}
+
+extern "C" int fc_radial_mlp_bwd_pairsum(int64_t n, int32_t n_in, const float* x, const float* w0, float s0,
+                                         const float* w1, float s1, const float* grad_h2, float* grad_x,
+                                         void* stream) {
+  if (n < 0 || n_in < 1 || n_in > WIDE_K) return FC_ERR_BAD_DESC;
+  if (n == 0) return FC_OK;
+  if (!x || !w0 || !w1 || !grad_h2 || !grad_x) return FC_ERR_NULL;
+  const int64_t blocks = (n + WIDE_BM - 1) / WIDE_BM;
+  if (blocks > 0x7fffffff) return FC_ERR_SHAPE;
+  hipLaunchKernelGGL(radial_mlp_bwd_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, n,
+                     (int)n_in, x, w0, s0, w1, s1, grad_h2, grad_x);
   FC_LAUNCH_CHECK();
   return FC_OK;
 }

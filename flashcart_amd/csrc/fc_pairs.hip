@@ -6,7 +6,8 @@
 // x^2 + y^2 + z^2 does not see the sign). Both edges of a pair therefore get identical
 // per-edge weights, which are formed once per pair. This file finds the pairs:
 //   pair_slot[e] = 2p (the edge with the lower index) or 2p + 1 (its reverse), pairs
-//   numbered in the order of their lower edge, and pair_edge[p] = that lower edge;
+//   numbered in the order of their lower edge, pair_edge[p] = that lower edge and
+//   pair_upper[p] = its reverse;
 //   counts[0] = edges without a (unique, mutual) reverse, counts[1] = pairs.
 // The caller uses the pairing only when counts[0] == 0. Index work only: the result is
 // exact and independent of the launch shape.
@@ -117,7 +118,8 @@ __global__ void __launch_bounds__(kPairBlock) pair_scan_kernel(int64_t n_tiles, 
 __global__ void __launch_bounds__(kPairBlock) pair_assign_kernel(int64_t n_edges, const int32_t* __restrict__ rev,
                                                                  const int32_t* __restrict__ tile_off,
                                                                  int64_t max_pairs, int32_t* __restrict__ pair_slot,
-                                                                 int32_t* __restrict__ pair_edge) {
+                                                                 int32_t* __restrict__ pair_edge,
+                                                                 int32_t* __restrict__ pair_upper) {
   __shared__ int lds[kPairBlock];
   const int t = threadIdx.x;
   const int64_t base = (int64_t)blockIdx.x * kPairTile + (int64_t)t * kPairPerThread;  // contiguous per thread
@@ -146,6 +148,7 @@ __global__ void __launch_bounds__(kPairBlock) pair_assign_kernel(int64_t n_edges
     const int64_t e = base + q;
     if (p < max_pairs) {
       pair_edge[p] = (int32_t)e;
+      if (pair_upper) pair_upper[p] = rev[e];
       pair_slot[e] = (int32_t)(2 * p);
       pair_slot[rev[e]] = (int32_t)(2 * p + 1);
     }
@@ -239,8 +242,8 @@ extern "C" int64_t fc_edge_pairs_workspace(int64_t n_edges) {
 }
 
 extern "C" int fc_edge_pairs(const fc_csr* gr, const int32_t* idx_i, const int32_t* shifts, int32_t* pair_slot,
-                             int32_t* pair_edge, int64_t max_pairs, int32_t* counts, int32_t* workspace,
-                             int64_t workspace_ints, void* stream) {
+                             int32_t* pair_edge, int32_t* pair_upper, int64_t max_pairs, int32_t* counts,
+                             int32_t* workspace, int64_t workspace_ints, void* stream) {
   if (!gr || !counts) return FC_ERR_NULL;
   const int64_t E = gr->n_edges;
   if (E < 0 || gr->n_nodes < 0 || max_pairs < 0) return FC_ERR_SHAPE;
@@ -265,7 +268,7 @@ extern "C" int fc_edge_pairs(const fc_csr* gr, const int32_t* idx_i, const int32
   FC_LAUNCH_CHECK();
   if (E > 0) {
     hipLaunchKernelGGL(pair_assign_kernel, dim3((unsigned)tiles), dim3(kPairBlock), 0, s, E, rev, tile_pairs,
-                       max_pairs, pair_slot, pair_edge);
+                       max_pairs, pair_slot, pair_edge, pair_upper);
     FC_LAUNCH_CHECK();
   }
   return FC_OK;

@@ -35,7 +35,7 @@ __global__ void __launch_bounds__(256) species_density_fwd_kernel(int64_t n_rows
                                                                   const int32_t* __restrict__ zj,
                                                                   const float* __restrict__ h,
                                                                   const float* __restrict__ y, float* __restrict__ dens) {
-  constexpr int U = 8, ZW = kSpeciesMax / 4;  // species per wave
+  constexpr int U = 16, ZW = kSpeciesMax / 4;  // species per wave
   const int64_t row = xcd_row(n_rows);
   if (row >= n_rows) return;
   const int k = threadIdx.x & 63;
@@ -55,8 +55,13 @@ __global__ void __launch_bounds__(256) species_density_fwd_kernel(int64_t n_rows
       z[u] = b + u < e1 ? zj[e] : -1;
       sl[u] = pair_slot[e];
     }
+    // h only where this wave takes the edge (uniform branches; the loads are all issued before
+    // the first FMA waits for them)
 #pragma unroll
-    for (int u = 0; u < U; ++u) hk[u] = h[(int64_t)(sl[u] >> 1) * kHid + k];
+    for (int u = 0; u < U; ++u) {
+      hk[u] = 0.f;
+      if ((z[u] & 3) == wave && z[u] < 4 * ZW) hk[u] = h[(int64_t)(sl[u] >> 1) * kHid + k];
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
 #pragma unroll

@@ -25,8 +25,8 @@ struct TPArgs {
   const float* w;
   const int32_t* idx_j;    // conv: sender per edge
   const int32_t* rowptr;   // conv: receiver CSR, n_rows + 1 entries
-  const int32_t* wslot;    // conv, optional: edge e reads weight row wslot[e] / 2 and writes its
-                           // weight gradient to row wslot[e] (the two edges of a pair share a row)
+  const int32_t* wslot;    // conv, optional: edge e reads weight row wslot[e] / 2 (the two edges of a
+                           // pair share a row); its weight gradient stays at row e
   const float* grad_out;   // bwd only
   float* out;              // fwd output
   float* grad_in1;         // bwd: rows mode -> grad wrt in1 rows; conv mode -> per-edge messages
@@ -53,12 +53,9 @@ struct TPConfig {
   static constexpr int NOUT_RED = PL::NOUT_RED;
 };
 
-// Weight row of edge e, and the row of its weight gradient (pair-major when edges share weights).
+// Weight row of edge e (the pair's row when edges share weights).
 __device__ __forceinline__ int64_t weight_row(const TPArgs& g, int64_t e) {
   return g.wslot ? (int64_t)(g.wslot[e] >> 1) : e;
-}
-__device__ __forceinline__ int64_t weight_grad_row(const TPArgs& g, int64_t e) {
-  return g.wslot ? (int64_t)g.wslot[e] : e;
 }
 
 // Operands of one edge (or row) for one lane.
@@ -336,7 +333,7 @@ __global__ void __launch_bounds__(256, 2) tp_bwd_kernel(TPArgs g) {
             float s = 0.f;
 #pragma unroll
             for (int b = 0; b < T::N1; ++b) s = fmaf(v[b], xp[b], s);
-            if (active) g.grad_w[weight_grad_row(g, e) * sw + i * C + f] = s;
+            if (active) g.grad_w[e * sw + i * C + f] = s;
           }
           if (need1) {
 #pragma unroll
@@ -454,7 +451,7 @@ __global__ void __launch_bounds__(C, 2) tp_bwd_conv_kernel(TPArgs g) {
     for (int u = 0; u < D1; ++u) gx[u] = 0.f;
 #pragma unroll
     for (int u = 0; u < R2; ++u) gy[u] = 0.f;
-    float* gwr = g.grad_w + weight_grad_row(g, e) * SW + f;
+    float* gwr = g.grad_w + e * SW + f;
     static_for<NP>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
       constexpr PathDesc P = PL::at(i);

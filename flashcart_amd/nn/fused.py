@@ -228,21 +228,22 @@ class _PairedConv(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, in1: Tensor, in2: Tensor, x: Tensor, layer, graph, slot: Tensor, alpha: float) -> Tensor:
+    def forward(ctx, in1: Tensor, in2: Tensor, x: Tensor, layer, graph, pairs, alpha: float) -> Tensor:
+        slot = pairs.slot
         l0, l1, l2 = layer.radial_mlp[0], layer.radial_mlp[2], layer.radial_mlp[4]
         w = _ops.radial_mlp_fwd(x, l0.weight, l0._scale, l1.weight, l1._scale, l2.weight, l2._scale)
         tp = layer.tp
         out = _ops.tp_fwd(in1, in2, w, graph.idx_i, graph.idx_j, tp.in1_l_max, tp.in2_l_max, tp.out_l_max,
                           tp.in1_features, tp.in2_features, tp.symmetric_product, tp.shared_weights, *tp.op_meta,
                           tp.reduce_paths, graph.rowptr, graph.sender_perm, graph.sender_ptr, float(alpha), slot)
-        ctx.save_for_backward(in1, in2, x, w, slot)
+        ctx.save_for_backward(in1, in2, x, w, slot, pairs.edge, pairs.upper)
         ctx.layer, ctx.graph, ctx.alpha = layer, graph, float(alpha)
         return out
 
     @staticmethod
     @once_differentiable
     def backward(ctx, g: Tensor):
-        in1, in2, x, w, slot = ctx.saved_tensors
+        in1, in2, x, w, slot, pairs_lo, pairs_hi = ctx.saved_tensors
         layer, graph = ctx.layer, ctx.graph
         n1, n2, nx = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[2]
         tp = layer.tp
@@ -253,7 +254,7 @@ class _PairedConv(torch.autograd.Function):
         gx = None
         if nx:
             l0, l1, l2 = layer.radial_mlp[0], layer.radial_mlp[2], layer.radial_mlp[4]
-            gh2 = _ops.dense_bwd_pairs(gw, l2.weight, l2._scale)
+            gh2 = _ops.dense_bwd_pairs(gw, l2.weight, l2._scale, pairs_lo, pairs_hi)
             del gw
             gx = _ops.radial_mlp_bwd(gh2, x, l0.weight, l0._scale, l1.weight, l1._scale)
         return (g1 if n1 else None), (g2 if n2 else None), gx, None, None, None, None
@@ -285,7 +286,7 @@ def paired_conv_applies(layer, node_feats: Tensor) -> bool:
 
 
 def paired_conv(layer, in1: Tensor, in2: Tensor, x_pairs: Tensor, graph, pairs, alpha: float) -> Tensor:
-    return _PairedConv.apply(in1, in2, x_pairs, layer, graph, pairs.slot, alpha)
+    return _PairedConv.apply(in1, in2, x_pairs, layer, graph, pairs, alpha)
 
 
 def species_maps(layer, x_table: Tensor, alpha: float):
@@ -365,8 +366,8 @@ class _SpeciesConv(torch.autograd.Function):
         gx = None
         if ctx.needs_input_grad[1]:
             l0, l1 = layer.radial_mlp[0], layer.radial_mlp[2]
-            gh2 = g_h.view(-1, 2, 64).sum(1)  # both edges of a pair read its h row
-            gx = _ops.radial_mlp_bwd(gh2, x_pairs, l0.weight, l0._scale, l1.weight, l1._scale)
+            # both edges of a pair read its h row: rows 2p and 2p + 1 of g_h summed in the kernel
+            gx = _ops.radial_mlp_bwd_pairsum(g_h, x_pairs, l0.weight, l0._scale, l1.weight, l1._scale)
         return (g_y if ctx.needs_input_grad[0] else None), gx, None, None, None, None, None, None
 
 

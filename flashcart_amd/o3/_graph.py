@@ -29,6 +29,7 @@ class EdgePairs:
     """
     slot: torch.Tensor   # int32 (E,): 2p for the lower edge of pair p, 2p + 1 for its reverse
     edge: torch.Tensor   # int32 (P,): the lower edge of each pair, in edge order
+    upper: torch.Tensor  # int32 (P,): the other edge of each pair
 
     @property
     def n_pairs(self) -> int:
@@ -94,13 +95,15 @@ def launch_edge_pairs(csr: GraphCSR, shifts: Optional[torch.Tensor]):
         _lib.check(-n_ws, "fc_edge_pairs_workspace")
     slot = torch.empty(n_edges, dtype=torch.int32, device=dev)
     edge = torch.empty(n_edges // 2, dtype=torch.int32, device=dev)
+    upper = torch.empty(n_edges // 2, dtype=torch.int32, device=dev)
     counts = torch.empty(2, dtype=torch.int32, device=dev)
     ws = torch.empty(max(n_ws, 1), dtype=torch.int32, device=dev)
     keep = csr.struct()
     _lib.check(lib.fc_edge_pairs(keep, csr.idx_i.data_ptr(), _lib.ptr(sh), slot.data_ptr(), edge.data_ptr(),
-                                 n_edges // 2, counts.data_ptr(), ws.data_ptr(), n_ws, _lib.stream_of(csr.idx_i)),
+                                 upper.data_ptr(), n_edges // 2, counts.data_ptr(), ws.data_ptr(), n_ws,
+                                 _lib.stream_of(csr.idx_i)),
                "fc_edge_pairs")
-    return EdgePairs(slot, edge), counts
+    return EdgePairs(slot, edge, upper), counts
 
 
 def pairs_complete(counts: torch.Tensor, n_edges: int) -> bool:

@@ -488,8 +488,8 @@ def tp_bwd(grad_out: Tensor, in1: Tensor, in2: Tensor, weights: Tensor, idx_i: O
 
     Reference schema (src/flashcart/o3/_tensor_product.py:588-611) plus the optional
     CSR arrays, ``alpha`` and ``pair_slot`` of ``tp_fwd``. With ``pair_slot`` the weight
-    gradient has one row per edge, pair-major (row 2p + s holds edge s of pair p): the sum
-    of its two rows per pair is the gradient of the (E / 2)-row weights."""
+    gradient has one row per edge (edge order); the sum of a pair's two rows is the gradient
+    of the pair's weight row."""
     _check_tp_meta((in1_l_max, in2_l_max, out_l_max, in1_features, in2_features, symmetric_product, reduce_paths),
                    in1_offs, in2_offs, out_sizes, n_paths_per_l, n_total_paths)
     conv = idx_i is not None and idx_j is not None
@@ -507,7 +507,7 @@ def tp_bwd(grad_out: Tensor, in1: Tensor, in2: Tensor, weights: Tensor, idx_i: O
         raise ValueError("pair_slot needs a convolution (idx_i, idx_j).")
     g1 = _lib.rows_empty(in1, *in1.shape) if need_grad_in1 else in1.new_empty(0)
     g2 = _lib.rows_empty(in2, *in2.shape) if need_grad_in2 else in2.new_empty(0)
-    gw_rows = 2 * w.shape[0] if pair_slot is not None else w.shape[0]
+    gw_rows = 2 * w.shape[0] if pair_slot is not None else w.shape[0]  # per edge either way
     gw = _lib.rows_empty(w, gw_rows, *w.shape[1:]) if need_grad_weights else w.new_empty(0)
     lib = _lib.load()
     n_ws = lib.fc_tp_bwd_workspace(desc, csr, in1.shape[0], int(need_grad_in1), int(need_grad_weights))
@@ -548,8 +548,8 @@ def _tp_backward(ctx, grad):
         return (None, None, None) + none_tail
     g1, g2, gw = tp_bwd(grad, in1, in2, weights, idx_i, idx_j, *ctx.cfg, bool(n1), bool(n2), bool(nw),
                         rowptr, sperm, sptr, ctx.alpha, pair_slot)
-    if nw and pair_slot is not None:
-        gw = gw.view(-1, 2, gw.shape[-1]).sum(1)  # both edges of a pair read its weight row
+    if nw and pair_slot is not None:  # both edges of a pair read its weight row (two terms: order-free)
+        gw = gw.new_zeros(weights.shape).index_add_(0, (pair_slot // 2).long(), gw)
     return (g1 if n1 else None, g2 if n2 else None, gw if nw else None) + none_tail
 
 
@@ -1059,26 +1059,31 @@ def _(grad_out, pre, weight, scale, act):
     return grad_out.new_empty(*grad_out.shape[:-1], weight.shape[1])
 
 
-def dense_bwd_pairs(grad_pairs: Tensor, weight: Tensor, scale: float) -> Tensor:
+def dense_bwd_pairs(grad: Tensor, weight: Tensor, scale: float, rows_lo: Optional[Tensor] = None,
+                    rows_hi: Optional[Tensor] = None) -> Tensor:
     """Input gradient of a bias-free linear layer whose output rows are shared by pairs of
-    consumers: gx[p] = scale (g[2p] + g[2p + 1]) W for a pair-major (2P, m) gradient ``g``
-    (``tp_bwd`` with ``pair_slot``). One GEMM over the (P, 2m) view that adds the two halves of
-    each row as its operands are read (``fc_dense_fwd_pairsum``): the MFMA work of P rows."""
-    go = _lib.contig("grad_pairs", grad_pairs)
+    consumers: gx[p] = scale (g_lo[p] + g_hi[p]) W, with g_lo / g_hi rows rows_lo[p] / rows_hi[p]
+    of ``grad`` (an edge-order gradient and the pairs' edges), or rows 2p / 2p + 1 without them.
+    One GEMM that adds the two rows as its operands are read (``fc_dense_fwd_pairsum``): the
+    MFMA work of P rows."""
+    go = _lib.contig("grad", grad)
     w = _lib.contig("weight", weight)
     m, k = w.shape
-    if go.dim() != 2 or go.shape[1] != m or go.shape[0] % 2:
-        raise RuntimeError(f"grad_pairs must be (2P, {m}), got {tuple(go.shape)}.")
-    n_pairs = go.shape[0] // 2
+    gathered = rows_lo is not None
+    if go.dim() != 2 or go.shape[1] != m or (not gathered and go.shape[0] % 2):
+        raise RuntimeError(f"grad must be (E, {m}) (pair-major (2P, {m}) without row indices), got {tuple(go.shape)}.")
+    lo, hi = (_i32("rows_lo", rows_lo), _i32("rows_hi", rows_hi)) if gathered else (None, None)
+    n_pairs = lo.shape[0] if gathered else go.shape[0] // 2
     wt = w.t().contiguous()  # (k, m): the forward kernel's (N, K) weight
     gx = _lib.rows_empty(go, n_pairs, k)
     if m % 32 == 0 and k <= 64 and k % 4 == 0 and go.data_ptr() % 16 == 0:
-        _lib_call("fc_dense_fwd_pairsum", n_pairs, m, k, go.data_ptr(), wt.data_ptr(), float(scale), gx.data_ptr(),
-                  _lib.stream_of(go))
-    else:  # other widths: one GEMM over K = 2m with the stacked weight [W; W]
-        wt2 = torch.cat([wt, wt], dim=1)
-        _lib_call("fc_dense_fwd", n_pairs, 2 * m, k, go.data_ptr(), wt2.data_ptr(), float(scale), None, 0, None,
-                  gx.data_ptr(), _lib.stream_of(go))
+        _lib_call("fc_dense_fwd_pairsum", n_pairs, m, k, go.data_ptr(), _lib.ptr(lo), _lib.ptr(hi), wt.data_ptr(),
+                  float(scale), gx.data_ptr(), _lib.stream_of(go))
+        return gx
+    # other widths: the pair sum formed first, then the plain GEMM
+    s = go[lo.long()] + go[hi.long()] if gathered else go.view(n_pairs, 2, m).sum(1)
+    _lib_call("fc_dense_fwd", n_pairs, m, k, s.data_ptr(), wt.data_ptr(), float(scale), None, 0, None, gx.data_ptr(),
+              _lib.stream_of(go))
     return gx
 
 
@@ -1189,6 +1194,22 @@ def radial_mlp_fwd(x: Tensor, w0: Tensor, s0: float, w1: Tensor, s1: float, w2: 
 @radial_mlp_fwd.register_fake
 def _(x, w0, s0, w1, s1, w2, s2):
     return x.new_empty(*x.shape[:-1], w2.shape[0])
+
+
+def radial_mlp_bwd_pairsum(grad_h2: Tensor, x: Tensor, w0: Tensor, s0: float, w1: Tensor, s1: float) -> Tensor:
+    """``radial_mlp_bwd`` with dL/dh2 given as two rows per row of x (2n, 64), summed
+    (``fc_radial_mlp_bwd_pairsum``)."""
+    x = _lib.contig("x", x)
+    w0, w1 = _lib.contig("w0", w0), _lib.contig("w1", w1)
+    gh = _lib.contig("grad_h2", grad_h2)
+    n_in = _radial_mlp_check(x, w0, w1)
+    x2 = x.reshape(-1, n_in)
+    if gh.numel() != 2 * x2.shape[0] * 64:
+        raise RuntimeError(f"grad_h2 must hold {2 * x2.shape[0]} rows of 64, got {tuple(gh.shape)}.")
+    gx = _lib.rows_empty(x2, *x2.shape)
+    _lib_call("fc_radial_mlp_bwd_pairsum", x2.shape[0], n_in, x2.data_ptr(), w0.data_ptr(), float(s0), w1.data_ptr(),
+              float(s1), gh.data_ptr(), gx.data_ptr(), _lib.stream_of(x))
+    return gx.reshape(x.shape)
 
 
 @torch.library.custom_op("flashcart::radial_mlp_bwd", mutates_args=())

@@ -130,21 +130,22 @@ typedef struct fc_csr {
   int64_t n_sender_rows;       /* rows of in1 (senders may include ghost atoms) */
   const int32_t* pair_slot;    /* optional (NULL: edge e uses weight row e). Per-edge weights shared
                                   by the two edges of a pair (fc_edge_pairs): edge e reads weight row
-                                  pair_slot[e] / 2 and writes its weight gradient to row pair_slot[e],
-                                  so the gradient has 2 rows per pair. No counterpart in the reference,
-                                  which forms the weights of every edge (nn/layers.py:357-364). */
+                                  pair_slot[e] / 2; its weight gradient stays at row e. No counterpart
+                                  in the reference, which forms the weights of every edge
+                                  (nn/layers.py:357-364). */
 } fc_csr;
 
 /* Edge pairs of a full neighbour list (no counterpart in the reference): the reverse of
  * edge (i <- j, S) is the edge (j <- i, -S) of receiver j; shifts (n_edges, 3) may be NULL
  * (no periodic shifts). Writes pair_slot[e] = 2p for the lower edge of pair p and 2p + 1
  * for its reverse (-1: no unique mutual reverse), pair_edge[p] = the lower edge (pairs
- * numbered in its order, at most max_pairs written), counts[0] = edges without a reverse,
- * counts[1] = pairs. Index work only; workspace of fc_edge_pairs_workspace(n_edges) int32. */
+ * numbered in its order, at most max_pairs written), pair_upper[p] = its reverse (may be
+ * NULL), counts[0] = edges without a reverse, counts[1] = pairs. Index work only;
+ * workspace of fc_edge_pairs_workspace(n_edges) int32. */
 int64_t fc_edge_pairs_workspace(int64_t n_edges);
 int fc_edge_pairs(const fc_csr* graph, const int32_t* idx_i, const int32_t* shifts, int32_t* pair_slot,
-                  int32_t* pair_edge, int64_t max_pairs, int32_t* counts, int32_t* workspace,
-                  int64_t workspace_ints, void* stream);
+                  int32_t* pair_edge, int32_t* pair_upper, int64_t max_pairs, int32_t* counts,
+                  int32_t* workspace, int64_t workspace_ints, void* stream);
 
 /* Radial-MLP inputs of edge pairs (no counterpart in the reference, which forms
  * edge_feats * envelope for every edge, src/flashcart/nn/layers.py:350-356):
@@ -267,12 +268,13 @@ int fc_linear_dgrad(const fc_linear_desc* desc, int64_t n_rows, const float* gra
  * receives the value before the activation when non-NULL. */
 int fc_dense_fwd(int64_t n, int32_t k, int32_t m, const float* x, const float* w, float scale,
                  const float* bias, int32_t act, float* pre_act, float* out, void* stream);
-/* out (n, m) = scale * (x[:, 0:k] + x[:, k:2k]) @ W^T for x (n, 2k), W (m, k), m <= 64, k a
- * multiple of 32, x and W 16-byte aligned: a dense layer applied to the sum of two row halves
- * without forming it (no counterpart in the reference; the radial output layer's input gradient
- * over edge pairs, whose two edges' weight gradients sit side by side). */
-int fc_dense_fwd_pairsum(int64_t n, int32_t k, int32_t m, const float* x, const float* w, float scale,
-                         float* out, void* stream);
+/* out (n, m) = scale * (x_lo[p] + x_hi[p]) @ W^T, W (m, k), m <= 64, k a multiple of 32, x and W
+ * 16-byte aligned: a dense layer applied to the sum of two rows without forming it. rows_lo and
+ * rows_hi NULL: x is (n, 2k) and the halves are x[p, 0:k] and x[p, k:2k]; else x has rows of k
+ * floats and the halves are rows rows_lo[p] and rows_hi[p]. No counterpart in the reference;
+ * the radial output layer's input gradient over edge pairs (the two edges' weight gradients). */
+int fc_dense_fwd_pairsum(int64_t n, int32_t k, int32_t m, const float* x, const int32_t* rows_lo,
+                         const int32_t* rows_hi, const float* w, float scale, float* out, void* stream);
 /* grad_x (n, k) = (grad_out * act'(pre_act)) @ W * scale. */
 int fc_dense_dgrad(int64_t n, int32_t k, int32_t m, const float* grad_out, const float* pre_act,
                    const float* w, float scale, int32_t act, float* grad_x, void* stream);
@@ -292,6 +294,10 @@ int fc_radial_mlp_hidden_fwd(int64_t n, int32_t n_in, const float* x, const floa
  * hidden layers recomputed from x (replaces the two hidden fc_dense_dgrad calls). */
 int fc_radial_mlp_bwd(int64_t n, int32_t n_in, const float* x, const float* w0, float s0, const float* w1,
                       float s1, const float* grad_h2, float* grad_x, void* stream);
+/* The same with dL/dh2 given as two rows per input row (grad_h2 (2n, 64); row p takes rows 2p and
+ * 2p + 1 summed): the rows of an edge pair's two edges, no counterpart in the reference. */
+int fc_radial_mlp_bwd_pairsum(int64_t n, int32_t n_in, const float* x, const float* w0, float s0,
+                              const float* w1, float s1, const float* grad_h2, float* grad_x, void* stream);
 
 /* Weight gradients (training). Replaces the weight-gradient part of the reference's
  * linear_bwd and its linear_wgrad kernel (src/flashcart/o3/_linear.py:457-570), and the

@@ -141,7 +141,7 @@ def _tp(l1, l2, lo, c):
 @pytest.mark.parametrize("l1,c", [(2, 128), (0, 64), (1, 32)])
 def test_tp_with_pair_slot_equals_expanded_weights(l1, c):
     """Forward and backward with pair_slot are the per-edge computation with the pair's weight row,
-    bit for bit; the weight gradient comes back pair-major."""
+    bit for bit (the weight gradient per edge, in edge order)."""
     from flashcart_amd.o3 import _ops
     numbers, pos, cell, pbc = fcc_alloy(2, 2, 2, seed=3)
     g = AtomicGraph.from_arrays(numbers, pos, ["Cu", "Ni", "Fe", "Cr"], 5.0, cell=cell, pbc=pbc).to(DEV)
@@ -165,7 +165,7 @@ def test_tp_with_pair_slot_equals_expanded_weights(l1, c):
                                 pairs.slot)
     g1e, g2e, gwe = _ops.tp_bwd(go, x, y, w_edge, csr.idx_i, csr.idx_j, *args, True, True, True, *csr_args, 0.3)
     assert torch.equal(g1p, g1e) and torch.equal(g2p, g2e)
-    assert gwp.shape == gwe.shape and torch.equal(gwp[pairs.slot.long()], gwe)
+    assert gwp.shape == gwe.shape and torch.equal(gwp, gwe)
     # through autograd the pair-shared weights get the sum of both edges' gradients
     wq = wp.clone().requires_grad_(True)
     _ops.tp_fwd(x, y, wq, csr.idx_i, csr.idx_j, *args, *csr_args, 0.3, pairs.slot).backward(go)
@@ -345,13 +345,20 @@ def test_species_conv_matches_paired_conv():
 
 
 @pytest.mark.parametrize("m", [2176, 272])
-def test_dense_bwd_pairs(m):
-    """The pair-summed input gradient (fc_dense_fwd_pairsum, and the stacked-weight form for
-    widths that are not multiples of 32) against torch float64."""
+@pytest.mark.parametrize("gathered", [False, True])
+def test_dense_bwd_pairs(m, gathered):
+    """The pair-summed input gradient (fc_dense_fwd_pairsum with adjacent or gathered rows, and the
+    summed-then-multiplied form for widths that are not multiples of 32) against torch float64."""
     from flashcart_amd.o3 import _ops
     gen = torch.Generator(device=DEV).manual_seed(9)
     g = torch.randn(2 * 1001, m, device=DEV, generator=gen)
     w = torch.randn(m, 64, device=DEV, generator=gen)
-    got = _ops.dense_bwd_pairs(g, w, 0.37)
-    want = 0.37 * (g.double()[0::2] + g.double()[1::2]) @ w.double()
+    if gathered:
+        perm = torch.randperm(2 * 1001, device=DEV, generator=gen).to(torch.int32)
+        lo, hi = perm[:1001], perm[1001:]
+        got = _ops.dense_bwd_pairs(g, w, 0.37, lo, hi)
+        want = 0.37 * (g.double()[lo.long()] + g.double()[hi.long()]) @ w.double()
+    else:
+        got = _ops.dense_bwd_pairs(g, w, 0.37)
+        want = 0.37 * (g.double()[0::2] + g.double()[1::2]) @ w.double()
     assert_close(got, want, 1e-5, 1e-5 * float(want.abs().max()), "pair-summed input gradient")
