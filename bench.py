@@ -37,12 +37,13 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the dominant kernel from rocprofv3 memory-request counters of
-# `bench.py --kernel-only` (first step graph, E = 1,080,166): read bytes by request size
-# (TCC_EA0_RDREQ_32B/64B/128B), written bytes from TCC_EA0_WRREQ / WRREQ_64B; a 2 GiB copy reads
-# back 2.148 / 2.147 GB. See profiles/hbm_counter_method.md and profiles/tp_conv_l1_fcc25k_kernel_only.md.
-MEASURED_TRAFFIC_BYTES = 11.67e9
-# The same for the layer-1 backward op (tp_bwd_conv_kernel 27.220 GB + segment_rows_kernel 5.104 GB).
-MEASURED_TRAFFIC_BWD_BYTES = 32.32e9
+# `bench.py --kernel-only` (first step graph, E = 1,080,166, weight rows shared by edge pairs as the
+# step runs them): read bytes by request size (TCC_EA0_RDREQ_32B/64B/128B), written bytes from
+# TCC_EA0_WRREQ / WRREQ_64B; a 2 GiB copy reads back 2.148 / 2.147 GB. See
+# profiles/hbm_counter_method.md and profiles/tp_conv_l1_fcc25k_kernel_only.md.
+MEASURED_TRAFFIC_BYTES = 11.33e9
+# The same for the layer-1 backward op (tp_bwd_conv_kernel 27.037 GB + segment_rows_kernel 5.104 GB).
+MEASURED_TRAFFIC_BWD_BYTES = 32.14e9
 from flashcart_amd.data.synthetic import FCC25K_R_MAX as R_MAX  # noqa: E402
 from flashcart_amd.data.synthetic import FCC25K_SIGMA_STEP as SIGMA_STEP  # noqa: E402
 from flashcart_amd.data.synthetic import FCC25K_SKIN as SKIN  # noqa: E402
@@ -126,7 +127,9 @@ def calibration_kernels(dev, reps):
 def measure_dominant(model, graph, dev, reps=10, with_backward=False):
     """Average duration of the layer-1 TP convolution forward (the north star's TP kernel),
     timed with HIP events on the stream the op launches on (torch's current stream), and
-    with ``with_backward`` also of its backward op (the largest kernel of the step by time)."""
+    with ``with_backward`` also of its backward op (the largest kernel of the step by time).
+    As the step runs them: when the edge list pairs up, one weight row per edge pair read by
+    both edges (pair_slot)."""
     from flashcart_amd.o3 import _ops
     from flashcart_amd.o3._graph import build_graph
     inter = model.interactions[1]
@@ -134,12 +137,15 @@ def measure_dominant(model, graph, dev, reps=10, with_backward=False):
     n = graph.num_nodes
     csr = build_graph(graph.edge_index, n)
     E = csr.n_edges
+    pairs = csr.edge_pairs(graph.shifts if bool(getattr(graph, "use_shifts", True)) else None)
     g = torch.Generator(device=dev).manual_seed(0)
     in1 = torch.randn(n, tp.in1_dim, device=dev, generator=g)
     in2 = torch.randn(E, tp.in2_dim, device=dev, generator=g)
-    w = torch.randn(E, tp.n_total_paths * tp.in1_features, device=dev, generator=g)
+    w_rows = pairs.n_pairs if pairs is not None else E
+    w = torch.randn(w_rows, tp.n_total_paths * tp.in1_features, device=dev, generator=g)
     args = (in1, in2, w, csr.idx_i, csr.idx_j, tp.in1_l_max, tp.in2_l_max, tp.out_l_max, tp.in1_features,
-            tp.in2_features, False, False, *tp.op_meta, False, csr.rowptr, csr.sender_perm, csr.sender_ptr, 1.0)
+            tp.in2_features, False, False, *tp.op_meta, False, csr.rowptr, csr.sender_perm, csr.sender_ptr, 1.0,
+            pairs.slot if pairs is not None else None)
     for _ in range(2):
         _ops.tp_fwd(*args)
     stream = torch.cuda.current_stream(dev)
@@ -154,8 +160,11 @@ def measure_dominant(model, graph, dev, reps=10, with_backward=False):
     nout = tp.out_dim // tp.in1_features
     d1, d2, P, C = (tp.in1_l_max + 1) ** 2, (tp.in2_l_max + 1) ** 2, tp.n_total_paths, tp.in1_features
     byts = tp_conv_bytes(n, n, E, d1, d2, P, C, nout)
+    # bytes of distinct data: with pairs each weight row is read by two edges (the formula counts E)
+    uniq = byts - 4 * (E - w_rows) * P * C
+    info = {"weight_rows": w_rows, "edges": E, "distinct_bytes_fwd": uniq}
     if not with_backward:
-        return ms, byts
+        return ms, byts, info
     # The backward op as the energy+forces step runs it (gradients for in1, in2 and the
     # weights): the backward kernel, then the sender-ordered segmented sum of the per-edge
     # messages; achieved bandwidth on the compulsory bytes of the three gradients.
@@ -170,7 +179,9 @@ def measure_dominant(model, graph, dev, reps=10, with_backward=False):
     ev1.record(stream)
     torch.cuda.synchronize(dev)
     ms_b = ev0.elapsed_time(ev1) / reps
-    return ms, byts, ms_b, tp_conv_bwd_bytes(n, E, d1, d2, P, C, nout)
+    byts_b = tp_conv_bwd_bytes(n, E, d1, d2, P, C, nout)
+    info["distinct_bytes_bwd"] = byts_b - 4 * (E - w_rows) * P * C
+    return ms, byts, ms_b, byts_b, info
 
 
 def cpu_baseline(model, cfg, avg_neighbors, budget_s=20.0, cells=(8, 8, 8)):
@@ -375,7 +386,7 @@ def config_line(name, dev, steps, warmup, cpu):
         ms = ev0.elapsed_time(ev1) / steps
         if not bool(torch.isfinite(out["energy"]).all()):
             raise RuntimeError(f"{name}: non-finite energy")
-        f_ms, f_b, b_ms, b_b = measure_dominant(model, gdev, dev, with_backward=True)
+        f_ms, f_b, b_ms, b_b, _ = measure_dominant(model, gdev, dev, with_backward=True)
         res.update({"metric": "atom-steps/s (energy+forces)", "value": n_atoms / (ms * 1e-3), "unit": "atom-steps/s",
                     "ms_per_step": ms, "mode": "HIP graph replay of predict (use_compile=True)",
                     "eager": {"value": n_atoms * steps / dt_eager, "ms_per_step": 1e3 * dt_eager / steps},
@@ -594,7 +605,7 @@ def main():
         sg = StepGraphs(numbers, pos, cell, pbc, ["Cu", "Ni", "Fe", "Cr"], 1)
         model, _ = build_model(43.0)
         g = sg.graph(0, dev)
-        ms, byts, ms_b, byts_b = measure_dominant(model.to(dev), g, dev, reps=5, with_backward=True)
+        ms, byts, ms_b, byts_b, _ = measure_dominant(model.to(dev), g, dev, reps=5, with_backward=True)
         cal = calibration_kernels(dev, 5)
         print(json.dumps({"kernel_only": True, "avg_launch_ms": ms, "algorithmic_bytes": byts,
                           "avg_bwd_op_ms": ms_b, "algorithmic_bytes_bwd": byts_b, **cal}), flush=True)
@@ -627,7 +638,7 @@ def main():
     if not (np.isfinite(e) and np.isfinite(fmax)):
         raise RuntimeError("non-finite energy or forces")
     log(f"{args.steps} steps in {dt:.3f}s ({1e3 * dt / args.steps:.3f} ms/step); E={e:.6f} |F|max={fmax:.4f}")
-    ms, byts, ms_b, byts_b = measure_dominant(model, graphs[-1], dev, with_backward=True)
+    ms, byts, ms_b, byts_b, dom = measure_dominant(model, graphs[-1], dev, with_backward=True)
     gbs = byts / (ms * 1e-3) / 1e9
     gbs_b = byts_b / (ms_b * 1e-3) / 1e9
     log(f"tp_fwd conv (layer 1): {ms:.3f} ms/launch, {byts / 1e9:.3f} GB algorithmic, {gbs:.1f} GB/s; "
@@ -653,7 +664,12 @@ def main():
                      "traffic": MEASURED_TRAFFIC_BYTES, "traffic_launch": f"bench.py --kernel-only (E={TRAFFIC_E})",
                      "traffic_over_algorithmic": MEASURED_TRAFFIC_BYTES / TRAFFIC_ALG_FWD,
                      "algorithmic_bytes": byts, "avg_launch_ms": ms,
-                     "note": "the north star's TP kernel; by time the layer-1 backward dominates the step "
+                     "weight_rows": dom["weight_rows"], "edges": dom["edges"],
+                     "distinct_bytes": dom["distinct_bytes_fwd"],
+                     "distinct_frac": dom["distinct_bytes_fwd"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                     "note": "the north star's TP kernel as the step runs it: the two edges of a pair read one "
+                             "weight row; algorithmic_bytes count a row per edge (the survey's formula), "
+                             "distinct_bytes each row once. By time the layer-1 backward dominates the step "
                              "(roofline_tp_bwd)"},
         # the step's largest TP kernel by time: the layer-1 TP backward op (backward kernel + the
         # sender-ordered sum of its per-edge messages), on the compulsory bytes of its three gradients
@@ -662,7 +678,9 @@ def main():
                             "traffic": MEASURED_TRAFFIC_BWD_BYTES,
                             "traffic_launch": f"bench.py --kernel-only (E={TRAFFIC_E})",
                             "traffic_over_algorithmic": MEASURED_TRAFFIC_BWD_BYTES / TRAFFIC_ALG_BWD,
-                            "algorithmic_bytes": byts_b, "avg_launch_ms": ms_b},
+                            "algorithmic_bytes": byts_b, "avg_launch_ms": ms_b,
+                            "distinct_bytes": dom["distinct_bytes_bwd"],
+                            "distinct_frac": dom["distinct_bytes_bwd"] / (ms_b * 1e-3) / 1e9 / HBM_PEAK_GBS},
         "energy": e,
     }
     if not args.no_configs:
