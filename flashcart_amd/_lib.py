@@ -75,7 +75,8 @@ _SIGNATURES = {
     "fc_csr_from_sorted": (c_int, [c_i64, c_vp, c_i64, c_vp, c_vp]),
     "fc_edge_grad_to_nodes": (c_int, [ctypes.POINTER(CSR), c_vp, c_vp, c_vp]),
     "fc_edge_pairs_workspace": (c_i64, [c_i64]),
-    "fc_edge_pairs": (c_int, [ctypes.POINTER(CSR), c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp]),
+    "fc_edge_pairs": (c_int, [ctypes.POINTER(CSR), c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64,
+                              c_vp]),
     "fc_pair_inputs_fwd": (c_int, [c_i64, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "fc_pair_inputs_bwd": (c_int, [c_i64, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "fc_tp_num_paths": (c_int, [ctypes.POINTER(TPDesc)]),

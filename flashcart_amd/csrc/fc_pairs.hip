@@ -4,7 +4,8 @@
 // v = (pos[j] - pos[i]) + s is bitwise the same for the reverse edge whenever its shift
 // vector is the exact negation of s (IEEE rounding is symmetric under negation, and
 // x^2 + y^2 + z^2 does not see the sign). Both edges of a pair therefore get identical
-// per-edge weights, which are formed once per pair. This file finds the pairs:
+// per-edge weights, which are formed once per pair. This file finds the pairs (receiver rows
+// sorted by strictly increasing (sender, shift), as this library's neighbour lists are):
 //   pair_slot[e] = 2p (the edge with the lower index) or 2p + 1 (its reverse), pairs
 //   numbered in the order of their lower edge, pair_edge[p] = that lower edge and
 //   pair_upper[p] = its reverse;
@@ -19,27 +20,44 @@ constexpr int kPairBlock = 256;
 constexpr int kPairPerThread = 4;
 constexpr int kPairTile = kPairBlock * kPairPerThread;
 
-// Reverse of edge e: the edge of receiver j whose sender is i and whose shift is -S.
-// Senders outside the receiver rows (ghost atoms) have no reverse.
+// Reverse of edge e: the edge of receiver j whose sender is i and whose shift is -S. Rows must
+// be sorted by strictly increasing (sender, shift), as the neighbour lists of this library emit
+// them; the reverse is then found by bisection. An edge whose key does not exceed its
+// predecessor's in the row (unsorted row or duplicate edge) gets -2, so the pairing is refused.
+// Senders outside the receiver rows (ghost atoms) have no reverse (-1).
+__device__ __forceinline__ int edge_key_cmp(const int32_t* idx_j, const int32_t* shifts, int32_t k, int32_t i,
+                                            int32_t t0, int32_t t1, int32_t t2) {
+  const int32_t a = idx_j[k];
+  if (a != i) return a < i ? -1 : 1;
+  if (!shifts) return 0;
+  const int32_t b0 = shifts[3 * (int64_t)k], b1 = shifts[3 * (int64_t)k + 1], b2 = shifts[3 * (int64_t)k + 2];
+  if (b0 != t0) return b0 < t0 ? -1 : 1;
+  if (b1 != t1) return b1 < t1 ? -1 : 1;
+  if (b2 != t2) return b2 < t2 ? -1 : 1;
+  return 0;
+}
+
 __global__ void pair_find_kernel(int64_t n_edges, int64_t n_nodes, const int32_t* __restrict__ idx_i,
                                  const int32_t* __restrict__ idx_j, const int32_t* __restrict__ rowptr,
                                  const int32_t* __restrict__ shifts, int32_t* __restrict__ rev) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= n_edges) return;
   const int32_t i = idx_i[e], j = idx_j[e];
+  const int32_t s0 = shifts ? shifts[3 * e] : 0, s1 = shifts ? shifts[3 * e + 1] : 0, s2 = shifts ? shifts[3 * e + 2] : 0;
+  if (e > 0 && idx_i[e - 1] == i && edge_key_cmp(idx_j, shifts, (int32_t)(e - 1), j, s0, s1, s2) >= 0) {
+    rev[e] = -2;  // not strictly after its predecessor in the row
+    return;
+  }
   int32_t r = -1;
   if (i >= 0 && i < n_nodes && j >= 0 && j < n_nodes) {
-    const int32_t s0 = shifts ? shifts[3 * e] : 0, s1 = shifts ? shifts[3 * e + 1] : 0,
-                  s2 = shifts ? shifts[3 * e + 2] : 0;
     const int32_t k1 = rowptr[j + 1];
-    for (int32_t k = rowptr[j]; k < k1; ++k) {
-      if ((int64_t)k == e || idx_j[k] != i) continue;
-      if (shifts && (shifts[3 * (int64_t)k] != -s0 || shifts[3 * (int64_t)k + 1] != -s1 ||
-                     shifts[3 * (int64_t)k + 2] != -s2))
-        continue;
-      r = k;
-      break;
+    int32_t lo = rowptr[j], hi = k1;  // first entry >= (i, -S)
+    while (lo < hi) {
+      const int32_t mid = lo + ((hi - lo) >> 1);
+      if (edge_key_cmp(idx_j, shifts, mid, i, -s0, -s1, -s2) < 0) lo = mid + 1;
+      else hi = mid;
     }
+    if (lo < k1 && (int64_t)lo != e && edge_key_cmp(idx_j, shifts, lo, i, -s0, -s1, -s2) == 0) r = lo;
   }
   rev[e] = r;
 }
@@ -242,8 +260,8 @@ extern "C" int64_t fc_edge_pairs_workspace(int64_t n_edges) {
 }
 
 extern "C" int fc_edge_pairs(const fc_csr* gr, const int32_t* idx_i, const int32_t* shifts, int32_t* pair_slot,
-                             int32_t* pair_edge, int32_t* pair_upper, int64_t max_pairs, int32_t* counts,
-                             int32_t* workspace, int64_t workspace_ints, void* stream) {
+                             int32_t* pair_edge, int32_t* pair_upper, int32_t* reverse, int64_t max_pairs,
+                             int32_t* counts, int32_t* workspace, int64_t workspace_ints, void* stream) {
   if (!gr || !counts) return FC_ERR_NULL;
   const int64_t E = gr->n_edges;
   if (E < 0 || gr->n_nodes < 0 || max_pairs < 0) return FC_ERR_SHAPE;
@@ -253,7 +271,7 @@ extern "C" int fc_edge_pairs(const fc_csr* gr, const int32_t* idx_i, const int32
     return FC_ERR_NULL;
   hipStream_t s = (hipStream_t)stream;
   const int64_t tiles = (E + kPairTile - 1) / kPairTile;
-  int32_t* rev = workspace;
+  int32_t* rev = reverse ? reverse : workspace;
   int32_t* tile_pairs = workspace + E;
   int32_t* tile_bad = tile_pairs + tiles;
   if (E > 0) {

@@ -82,6 +82,7 @@ class _PredictReplay:
             with torch.cuda.graph(self.topology):
                 csr = build_graph(self.inputs["edge_index"], n_rows)
                 pend = launch_edge_pairs(csr, pair_shifts) if want_pairs else None
+                sorted_senders = csr.sort_senders()  # the sender order without a pairing
                 base["csr"] = csr
             self.topology.replay()  # capturing records the work without running it
             if pend is not None:
@@ -90,6 +91,11 @@ class _PredictReplay:
                 self.pair_counts = pend[1]
                 self.paired = pairs_complete(pend[1], csr.n_edges)
                 csr.set_edge_pairs(pair_shifts, pend[0] if self.paired else None)
+            # both sender orders are refreshed by every topology replay
+            if self.paired:
+                csr.set_senders(pend[0].reverse, csr.rowptr)
+            else:
+                csr.set_senders(*sorted_senders)
             self._src_edges = (tensors["edge_index"], tensors["edge_index"]._version)
 
         def run():

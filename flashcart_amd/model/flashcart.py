@@ -162,16 +162,27 @@ class FlashCartPotential(AtomisticModel):
             use_shifts = graph.get("use_shifts", True)
             if not isinstance(use_shifts, bool):
                 use_shifts = uses_periodic_shifts(use_shifts)
-            if not is_lammps and self.wants_edge_pairs(positions):
-                pairs = csr.edge_pairs(graph["shifts"] if use_shifts else None)
+            want_pairs = not is_lammps and self.wants_edge_pairs(positions)
+            pair_shifts = graph["shifts"] if use_shifts else None
+            # The pairing is launched first and its counters are read only after the edge geometry
+            # and the embedding are queued. Until then the geometry takes the sender order a
+            # complete pairing gives (the reverse edges, which its backward alone reads); an
+            # incomplete pairing re-runs it with the sorted sender order.
+            speculative = want_pairs and csr.request_edge_pairs(pair_shifts)
             sv = shift_vectors(graph["cell"], graph["shifts"], edge_index[0], batch,
-                               antisymmetric=pairs is not None) if use_shifts else None
+                               antisymmetric=want_pairs) if use_shifts else None
+            senders = speculative if speculative else (csr.sender_perm, csr.sender_ptr)
             edge_attrs, edge_feats, envelope = _ops.edge_geometry(
-                positions, sv, csr.idx_i, csr.idx_j, None, csr.rowptr, csr.sender_perm, csr.sender_ptr, *geo)
+                positions, sv, csr.idx_i, csr.idx_j, None, csr.rowptr, *senders, *geo)
         else:
             edge_attrs, edge_feats, envelope = _ops.edge_geometry(
                 None, None, csr.idx_i, csr.idx_j, vectors, csr.rowptr, csr.sender_perm, csr.sender_ptr, *geo)
         node_feats = self.embedding(atom_types)
+        if vectors is None and want_pairs:
+            pairs = csr.edge_pairs(pair_shifts)
+            if pairs is None and speculative:
+                edge_attrs, edge_feats, envelope = _ops.edge_geometry(
+                    positions, sv, csr.idx_i, csr.idx_j, None, csr.rowptr, csr.sender_perm, csr.sender_ptr, *geo)
         species = None
         if pairs is not None and not self.embedding.weight.requires_grad:
             # the first layer's sender features are embedding rows: species density (fused.species_conv)

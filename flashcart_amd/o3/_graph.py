@@ -30,43 +30,108 @@ class EdgePairs:
     slot: torch.Tensor   # int32 (E,): 2p for the lower edge of pair p, 2p + 1 for its reverse
     edge: torch.Tensor   # int32 (P,): the lower edge of each pair, in edge order
     upper: torch.Tensor  # int32 (P,): the other edge of each pair
+    reverse: torch.Tensor  # int32 (E,): the reverse of every edge
 
     @property
     def n_pairs(self) -> int:
         return int(self.edge.shape[0])
 
 
-@dataclass
 class GraphCSR:
-    n_nodes: int           # receiver rows
-    n_sender_rows: int     # rows of the sender features (>= n_nodes with ghosts)
-    idx_i: torch.Tensor    # int32 (E,) receivers, sorted
-    idx_j: torch.Tensor    # int32 (E,) senders
-    rowptr: torch.Tensor   # int32 (n_nodes + 1,)
-    sender_perm: torch.Tensor  # int32 (E,) edges ordered by sender (stable)
-    sender_ptr: torch.Tensor   # int32 (n_sender_rows + 1,)
+    """Receiver CSR of an edge list and a sender order of its edges.
+
+    n_nodes: receiver rows; n_sender_rows: rows of the sender features (>= n_nodes with ghosts);
+    idx_i / idx_j: int32 (E,) receivers (sorted) and senders; rowptr: int32 (n_nodes + 1,).
+    sender_perm / sender_ptr: the edges grouped by sender (int32 (E,)) and the group bounds
+    (int32 (n_sender_rows + 1,)), formed on first use: with a complete edge pairing the edges sent
+    by node n are the reverses of the edges it receives (``reverse[rowptr[n]:rowptr[n+1]]``, group
+    bounds = rowptr), otherwise a stable sort of idx_j.
+    """
+
+    def __init__(self, n_nodes: int, n_sender_rows: int, idx_i: torch.Tensor, idx_j: torch.Tensor,
+                 rowptr: torch.Tensor, sender_perm: Optional[torch.Tensor] = None,
+                 sender_ptr: Optional[torch.Tensor] = None):
+        self.n_nodes = int(n_nodes)
+        self.n_sender_rows = int(n_sender_rows)
+        self.idx_i, self.idx_j, self.rowptr = idx_i, idx_j, rowptr
+        self._sender_perm, self._sender_ptr = sender_perm, sender_ptr
 
     @property
     def n_edges(self) -> int:
         return int(self.idx_i.shape[0])
 
-    def struct(self) -> "_lib.CSR":
+    def _senders(self) -> None:
+        if self._sender_perm is not None:
+            return
+        pairs = next((p for p in self.__dict__.get("_pairs", {}).values() if p is not None), None)
+        if pairs is not None and self.n_sender_rows == self.n_nodes:
+            self._sender_perm, self._sender_ptr = pairs.reverse, self.rowptr
+            return
+        self._sender_perm, self._sender_ptr = self.sort_senders()
+
+    def sort_senders(self):
+        """(sender_perm, sender_ptr) by a stable sort of idx_j, whatever the pairing."""
+        perm = torch.argsort(self.idx_j, stable=True).to(torch.int32)
+        return perm, rowptr_from_sorted(self.idx_j[perm.long()].contiguous(), self.n_sender_rows)
+
+    def set_senders(self, sender_perm: torch.Tensor, sender_ptr: torch.Tensor) -> None:
+        self._sender_perm, self._sender_ptr = sender_perm, sender_ptr
+
+    @property
+    def sender_perm(self) -> torch.Tensor:
+        self._senders()
+        return self._sender_perm
+
+    @property
+    def sender_ptr(self) -> torch.Tensor:
+        self._senders()
+        return self._sender_ptr
+
+    def struct(self, senders: bool = True) -> "_lib.CSR":
+        if not senders:
+            return _lib.csr_struct(self.n_nodes, self.n_edges, self.idx_j, self.rowptr, None, None,
+                                   self.n_sender_rows)
         return _lib.csr_struct(self.n_nodes, self.n_edges, self.idx_j, self.rowptr, self.sender_perm,
                                self.sender_ptr, self.n_sender_rows)
 
+    def request_edge_pairs(self, shifts: Optional[torch.Tensor]):
+        """Launch the pairing of this edge list for ``shifts`` without waiting for it (the host
+        reads its counters in ``edge_pairs``, so work queued in between overlaps them). Returns
+        the sender order a complete pairing gives, (reverse, rowptr), when the pairing is still
+        pending (None when it is decided already or cannot apply): valid once ``edge_pairs``
+        confirms the pairing."""
+        cache = self.__dict__.setdefault("_pairs", {})
+        key = _shift_key(shifts)
+        pending = self.__dict__.setdefault("_pending", {})
+        if key in cache:
+            return None
+        if key not in pending:
+            if not pairable(self, shifts):
+                cache.clear()
+                cache[key] = None
+                return None
+            self._pending = pending = {key: launch_edge_pairs(self, shifts)}
+        if self.n_sender_rows != self.n_nodes:
+            return None
+        return pending[key][0].reverse, self.rowptr
+
     def edge_pairs(self, shifts: Optional[torch.Tensor]) -> Optional[EdgePairs]:
         """The pairing of this edge list (cached per shift tensor), or None when some edge has no
-        unique reverse (ghost senders, half lists, duplicate edges)."""
+        unique reverse (ghost senders, half lists, duplicate or unsorted edges)."""
         cache = self.__dict__.setdefault("_pairs", {})
         key = _shift_key(shifts)
         if key not in cache:
-            cache.clear()
-            cache[key] = find_edge_pairs(self, shifts)
+            self.request_edge_pairs(shifts)
+            if key not in cache:
+                pairs, counts = self._pending.pop(key)
+                cache.clear()
+                cache[key] = pairs if pairs_complete(counts, self.n_edges) else None
         return cache[key]
 
     def set_edge_pairs(self, shifts: Optional[torch.Tensor], pairs: Optional[EdgePairs]) -> None:
         """Record the pairing of this edge list for ``shifts`` (computed elsewhere, e.g. in a graph)."""
         self.__dict__["_pairs"] = {_shift_key(shifts): pairs}
+        self.__dict__["_pending"] = {}
 
 
 def _shift_key(shifts: Optional[torch.Tensor]):
@@ -96,14 +161,15 @@ def launch_edge_pairs(csr: GraphCSR, shifts: Optional[torch.Tensor]):
     slot = torch.empty(n_edges, dtype=torch.int32, device=dev)
     edge = torch.empty(n_edges // 2, dtype=torch.int32, device=dev)
     upper = torch.empty(n_edges // 2, dtype=torch.int32, device=dev)
+    reverse = torch.empty(n_edges, dtype=torch.int32, device=dev)
     counts = torch.empty(2, dtype=torch.int32, device=dev)
     ws = torch.empty(max(n_ws, 1), dtype=torch.int32, device=dev)
-    keep = csr.struct()
+    keep = csr.struct(senders=False)
     _lib.check(lib.fc_edge_pairs(keep, csr.idx_i.data_ptr(), _lib.ptr(sh), slot.data_ptr(), edge.data_ptr(),
-                                 upper.data_ptr(), n_edges // 2, counts.data_ptr(), ws.data_ptr(), n_ws,
-                                 _lib.stream_of(csr.idx_i)),
+                                 upper.data_ptr(), reverse.data_ptr(), n_edges // 2, counts.data_ptr(),
+                                 ws.data_ptr(), n_ws, _lib.stream_of(csr.idx_i)),
                "fc_edge_pairs")
-    return EdgePairs(slot, edge, upper), counts
+    return EdgePairs(slot, edge, upper, reverse), counts
 
 
 def pairs_complete(counts: torch.Tensor, n_edges: int) -> bool:
@@ -145,6 +211,4 @@ def build_graph(edge_index: torch.Tensor, n_nodes: int, n_sender_rows: Optional[
     if check_sorted and idx_i.numel() > 1:
         torch._assert_async((idx_i[1:] >= idx_i[:-1]).all(), "edge_index[0] (receivers) must be sorted.")
     rowptr = rowptr_from_sorted(idx_i, n_nodes)
-    sender_perm = torch.argsort(idx_j, stable=True).to(torch.int32)
-    sender_ptr = rowptr_from_sorted(idx_j[sender_perm.long()].contiguous(), n_send)
-    return GraphCSR(int(n_nodes), n_send, idx_i, idx_j, rowptr, sender_perm, sender_ptr)
+    return GraphCSR(int(n_nodes), n_send, idx_i, idx_j, rowptr)

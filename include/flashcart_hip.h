@@ -136,16 +136,20 @@ typedef struct fc_csr {
 } fc_csr;
 
 /* Edge pairs of a full neighbour list (no counterpart in the reference): the reverse of
- * edge (i <- j, S) is the edge (j <- i, -S) of receiver j; shifts (n_edges, 3) may be NULL
- * (no periodic shifts). Writes pair_slot[e] = 2p for the lower edge of pair p and 2p + 1
+ * edge (i <- j, S) is the edge (j <- i, -S) of receiver j, found by bisection; each receiver's
+ * edges must be sorted by strictly increasing (sender, shift) (fc_neighbor_list and
+ * fc_neighbor_list_device emit them so), an edge out of that order counts as unpaired. shifts
+ * (n_edges, 3) may be NULL (no periodic shifts). Writes pair_slot[e] = 2p for the lower edge of pair p and 2p + 1
  * for its reverse (-1: no unique mutual reverse), pair_edge[p] = the lower edge (pairs
- * numbered in its order, at most max_pairs written), pair_upper[p] = its reverse (may be
- * NULL), counts[0] = edges without a reverse, counts[1] = pairs. Index work only;
- * workspace of fc_edge_pairs_workspace(n_edges) int32. */
+ * numbered in its order, at most max_pairs written), pair_upper[p] = its reverse and
+ * reverse[e] = the reverse of every edge (-1: none; each may be NULL), counts[0] = edges
+ * without a reverse, counts[1] = pairs. With every edge paired, reverse[rowptr[n] ..
+ * rowptr[n+1]) lists the edges whose sender is n: a sender order with sender_ptr = rowptr.
+ * Index work only; workspace of fc_edge_pairs_workspace(n_edges) int32. */
 int64_t fc_edge_pairs_workspace(int64_t n_edges);
 int fc_edge_pairs(const fc_csr* graph, const int32_t* idx_i, const int32_t* shifts, int32_t* pair_slot,
-                  int32_t* pair_edge, int32_t* pair_upper, int64_t max_pairs, int32_t* counts,
-                  int32_t* workspace, int64_t workspace_ints, void* stream);
+                  int32_t* pair_edge, int32_t* pair_upper, int32_t* reverse, int64_t max_pairs,
+                  int32_t* counts, int32_t* workspace, int64_t workspace_ints, void* stream);
 
 /* Radial-MLP inputs of edge pairs (no counterpart in the reference, which forms
  * edge_feats * envelope for every edge, src/flashcart/nn/layers.py:350-356):

@@ -21,8 +21,10 @@ DEV = "cuda"
 
 
 def _np_pairs(ii, jj, shifts):
-    """Restatement of fc_edge_pairs: the reverse of edge e is the first edge of receiver jj[e]
-    with sender ii[e] and shift -S; pairs are mutual reverses, numbered by their lower edge."""
+    """Restatement of fc_edge_pairs on receiver rows sorted by strictly increasing (sender, shift):
+    the reverse of edge e is the edge of receiver jj[e] with sender ii[e] and shift -S; pairs are
+    mutual reverses, numbered by their lower edge. An edge whose (sender, shift) does not exceed
+    its predecessor's in the row has no reverse."""
     ii, jj = np.asarray(ii), np.asarray(jj)
     n_edges = ii.shape[0]
     s = np.zeros((n_edges, 3), np.int64) if shifts is None else np.asarray(shifts, np.int64)
@@ -31,6 +33,9 @@ def _np_pairs(ii, jj, shifts):
         starts.setdefault(int(ii[e]), []).append(e)
     rev = np.full(n_edges, -1, np.int64)
     for e in range(n_edges):
+        if e > 0 and ii[e - 1] == ii[e] and (int(jj[e - 1]), *s[e - 1]) >= (int(jj[e]), *s[e]):
+            rev[e] = -2
+            continue
         for k in starts.get(int(jj[e]), []):
             if k != e and jj[k] == ii[e] and (s[k] == -s[e]).all():
                 rev[e] = k
@@ -83,14 +88,32 @@ def test_pairs_match_restatement(name, graph):
 
 def test_incomplete_pairings_are_refused():
     from flashcart_amd.o3._graph import build_graph, find_edge_pairs, launch_edge_pairs
-    # random directed edges: most have no reverse
+    # random directed edges in unsorted rows: refused
     ei = random_csr_graph(40, [3, 5, 0, 8], seed=4)
+    csr = build_graph(ei.to(DEV), 40)
+    pairs, counts = launch_edge_pairs(csr, None)
+    assert counts.tolist()[0] > 0
+    assert find_edge_pairs(csr, None) is None
+    # the same edges with every row sorted: most still have no reverse
+    order = torch.argsort(ei[0] * 1000 + ei[1], stable=True)
+    ei = ei[:, order]
+    keep = torch.ones(ei.shape[1], dtype=torch.bool)
+    keep[1:] = (ei[:, 1:] != ei[:, :-1]).any(0)  # drop duplicate edges
+    ei = ei[:, keep]
     csr = build_graph(ei.to(DEV), 40)
     pairs, counts = launch_edge_pairs(csr, None)
     slot, edge, bad = _np_pairs(ei[0].numpy(), ei[1].numpy(), None)
     assert counts.tolist() == [bad, len(edge)] and bad > 0
     assert np.array_equal(pairs.slot.cpu().numpy(), slot)
     assert find_edge_pairs(csr, None) is None
+    # a symmetric list with one row out of order: refused
+    numbers, pos, cell, pbc = fcc_alloy(2, 2, 2, seed=3)
+    g = AtomicGraph.from_arrays(numbers, pos, ["Cu", "Ni", "Fe", "Cr"], 5.0, cell=cell, pbc=pbc)
+    ei, sh = g.edge_index.clone(), g.shifts.clone()
+    ei[:, [3, 4]] = ei[:, [4, 3]]
+    sh[[3, 4]] = sh[[4, 3]]
+    assert int(ei[0, 3]) == int(ei[0, 4])
+    assert find_edge_pairs(build_graph(ei.to(DEV), int(g.atom_types.shape[0])), sh.to(DEV)) is None
     # a symmetric list with one pair's shift broken
     numbers, pos, cell, pbc = fcc_alloy(2, 2, 2, seed=3)
     g = AtomicGraph.from_arrays(numbers, pos, ["Cu", "Ni", "Fe", "Cr"], 5.0, cell=cell, pbc=pbc)
