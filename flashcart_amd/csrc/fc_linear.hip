@@ -436,7 +436,7 @@ struct PipeTile {
 // radial output layer's input gradient over edge pairs, whose two edges share the layer's
 // output row).
 template <int BM, int BN, int WM, int WN, int MI, bool KB, bool PS = false>
-__global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 80 * 1024 ? 2 : 1) gemm_pipe_kernel(GemmBatch gb, int32_t tiles_per_xcd) {
+__global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 80 * 1024 ? 2 : 1) gemm_pipe_kernel(GemmBatch gb) {
   static_assert(WM * WN == 4, "four waves");
   static_assert(MI == 32 || MI == 16, "MFMA block: 32x32x2 or 16x16x4");
   constexpr int TM = BM / WM, TN = BN / WN;
@@ -459,19 +459,34 @@ __global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, h = lane >> 5;
   const int wm = wave / WN, wn = wave % WN;
   const int G = gridDim.x, b = blockIdx.x;
-  // tiles of this workgroup: an XCD (hardware block b runs on XCD b % 8) owns a contiguous
-  // range of tiles, dealt round-robin to its workgroups
-  int t_first, t_step, t_end;
-  if (G >= 8 && G % 8 == 0) {
-    const int x = b % 8;
-    t_first = x * tiles_per_xcd + b / 8;
-    t_step = G / 8;
-    t_end = min(gb.total_tiles, (x + 1) * tiles_per_xcd);
-  } else {
-    t_first = b;
-    t_step = G;
-    t_end = gb.total_tiles;
-  }
+  // Tiles of this workgroup: a contiguous range holding 1/G of the batch's K steps (ranks
+  // differ in K, so equal tile counts would not be equal work). Workgroups of one XCD
+  // (hardware block b runs on XCD b % 8) take neighbouring ranges, so an XCD's L2 serves
+  // one contiguous run of A rows.
+  const int v = (G >= 8 && G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
+  int64_t work = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    if (q < gb.n_ranks) work += (int64_t)gb.r[q].tiles_m * gb.r[q].tiles_n * (gb.r[q].K / 32);
+  // first tile whose first K step (counted over the whole batch) is at or after step s
+  auto tile_at = [&](int64_t s) -> int {
+    int64_t base = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (q >= gb.n_ranks) break;
+      const GemmRank& g = gb.r[q];
+      const int64_t ks = g.K / 32, n = (int64_t)g.tiles_m * g.tiles_n;
+      if (n > 0 && s <= base + (n - 1) * ks) {
+        const int64_t d = s - base;
+        return g.tile_base + (int)(d <= 0 ? 0 : (d + ks - 1) / ks);
+      }
+      base += n * ks;
+    }
+    return gb.total_tiles;
+  };
+  const int t_first = tile_at(((int64_t)v * work + G - 1) / G);
+  const int t_end = tile_at(((int64_t)(v + 1) * work + G - 1) / G);
+  constexpr int t_step = 1;
   auto decode = [&](int tile) -> PipeTile {
     int ri = 0;
 #pragma unroll
@@ -751,9 +766,8 @@ int launch_pipe_cfg(GemmBatch gb, int n_ranks, hipStream_t s) {
   int64_t grid = 2 * (int64_t)device_cu_count();
   if (grid > total) grid = total;
   if (grid >= 8) grid -= grid % 8;
-  const int32_t per_xcd = (int32_t)((total + 7) / 8);
-  if (gb.trans_b) hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WM, WN, MI, false, PS>), dim3((unsigned)grid), dim3(256), 0, s, gb, per_xcd);
-  else hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WM, WN, MI, true, PS>), dim3((unsigned)grid), dim3(256), 0, s, gb, per_xcd);
+  if (gb.trans_b) hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WM, WN, MI, false, PS>), dim3((unsigned)grid), dim3(256), 0, s, gb);
+  else hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, WM, WN, MI, true, PS>), dim3((unsigned)grid), dim3(256), 0, s, gb);
   FC_LAUNCH_CHECK();
   return FC_OK;
 }
