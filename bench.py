@@ -184,6 +184,101 @@ def measure_dominant(model, graph, dev, reps=10, with_backward=False):
     return ms, byts, ms_b, byts_b, info
 
 
+def _socket_power_sampler(samples, stop):
+    """Append (socket W, mean GFX clock MHz) read by ``amd-smi metric -p -c`` until ``stop``."""
+    import re
+    import subprocess
+    while not stop.is_set():
+        try:
+            txt = subprocess.run(["amd-smi", "metric", "-p", "-c"], capture_output=True, text=True,
+                                 timeout=10).stdout
+        except (OSError, subprocess.TimeoutExpired):
+            return
+        p = re.search(r"SOCKET_POWER: (\d+)", txt)
+        c = [int(v) for v in re.findall(r"GFX_\d+:\s*CLK: (\d+) MHz", txt)]
+        if p and c:
+            samples.append((int(p.group(1)), sum(c) / len(c)))
+
+
+def power_per_kernel(model, graphs, dev, seconds=4.0):
+    """Socket power while each of the step's heavy ops runs alone in a loop (and the whole
+    energy+forces step, cycling over ``graphs``), sampled by amd-smi over the last 3 s of each
+    loop. Returns {op: {"ms_per_call", "watts", "clock_mhz", "samples"}}."""
+    import ctypes
+    import threading
+    from flashcart_amd import _lib
+    from flashcart_amd.o3 import _ops
+    from flashcart_amd.o3._graph import build_graph
+    graph = graphs[0]
+    inter = model.interactions[1]
+    tp = inter.tp
+    n = graph.num_nodes
+    csr = build_graph(graph.edge_index, n)
+    pairs = csr.edge_pairs(graph.shifts)
+    g = torch.Generator(device=dev).manual_seed(0)
+    in1 = torch.randn(n, tp.in1_dim, device=dev, generator=g)
+    in2 = torch.randn(csr.n_edges, tp.in2_dim, device=dev, generator=g)
+    rows = pairs.n_pairs if pairs is not None else csr.n_edges
+    w = torch.randn(rows, tp.n_total_paths * tp.in1_features, device=dev, generator=g)
+    args = (in1, in2, w, csr.idx_i, csr.idx_j, tp.in1_l_max, tp.in2_l_max, tp.out_l_max, tp.in1_features,
+            tp.in2_features, False, False, *tp.op_meta, False, csr.rowptr, csr.sender_perm, csr.sender_ptr, 1.0,
+            pairs.slot if pairs is not None else None)
+    go = torch.randn(n, tp.out_dim, device=dev, generator=g)
+    bargs = (go,) + args[:17] + (False, True, True, True) + args[18:]
+    lin = model.products[0].product_linears[1]
+    x_lin = torch.randn(n, lin.in_dim, device=dev, generator=g)
+    mlp = inter.radial_mlp
+    x_mlp = torch.randn(rows, mlp[0].weight.shape[1], device=dev, generator=g)
+    src = torch.ones(2 ** 29, device=dev)
+    dst = torch.empty_like(src)
+    step_k = [0]
+
+    def step():
+        model.predict(graphs[step_k[0] % len(graphs)], compute_forces=True)
+        step_k[0] += 1
+
+    ops = {
+        "idle": None,
+        "copy_2GiB": lambda: torch.mul(src, 1.0, out=dst),
+        "gemm_product_linear_fwd": lambda: lin(x_lin),
+        "tp_conv_fwd_layer1": lambda: _ops.tp_fwd(*args),
+        "tp_conv_bwd_layer1": lambda: _ops.tp_bwd(*bargs),
+        "radial_mlp_fwd_layer1": lambda: _ops.radial_mlp_fwd(x_mlp, mlp[0].weight, mlp[0]._scale, mlp[2].weight,
+                                                             mlp[2]._scale, mlp[4].weight, mlp[4]._scale),
+        "energy_forces_step": step,
+    }
+    out = {}
+    for name, fn in ops.items():
+        if fn is not None and name != "energy_forces_step":
+            fn = torch.no_grad()(fn)
+        if fn is not None:
+            for _ in range(3):
+                fn()
+        torch.cuda.synchronize(dev)
+        samples, stop = [], threading.Event()
+        sampler = threading.Thread(target=_socket_power_sampler, args=(samples, stop), daemon=True)
+        calls, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds:
+            if fn is None:
+                time.sleep(0.05)
+            else:
+                for _ in range(5):
+                    fn()
+                calls += 5
+                torch.cuda.synchronize(dev)
+            if not sampler.is_alive() and not stop.is_set() and time.perf_counter() - t0 > seconds - 3.0:
+                sampler.start()
+        dt = time.perf_counter() - t0
+        stop.set()
+        sampler.join(timeout=15)
+        out[name] = {"ms_per_call": round(1e3 * dt / calls, 4) if calls else None,
+                     "watts": round(sum(p for p, _ in samples) / len(samples), 1) if samples else None,
+                     "clock_mhz": round(sum(c for _, c in samples) / len(samples)) if samples else None,
+                     "samples": len(samples)}
+        log(f"power {name}: {out[name]}")
+    return out
+
+
 def cpu_baseline(model, cfg, avg_neighbors, budget_s=20.0, cells=(8, 8, 8)):
     """Oracle (CPU PyTorch restatement of the reference path), float32, on a bounded sample of the
     same system: fcc 8x8x8 cells = 2,048 atoms of the same model, at least 3 calls after 1 warmup."""
@@ -575,6 +670,9 @@ def main():
     ap.add_argument("--profile-step", action="store_true",
                     help="two energy+forces steps on the first step graph, then the calibration kernels (2x), "
                          "for per-kernel counter runs")
+    ap.add_argument("--power", action="store_true",
+                    help="socket power (amd-smi) of the step's heavy ops, each looping alone for 4 s, and of "
+                         "the energy+forces step")
     ap.add_argument("--no-configs", action="store_true",
                     help="measure only the metric's configuration (no lines for the other BASELINE configurations)")
     args = ap.parse_args()
@@ -600,6 +698,12 @@ def main():
         cal = calibration_kernels(dev, 2)
         print(json.dumps({"profile_step": True, "n_atoms": len(numbers), "n_edges": int(g.edge_index.shape[1]),
                           **cal}), flush=True)
+        return
+    if args.power:
+        sg = StepGraphs(numbers, pos, cell, pbc, ["Cu", "Ni", "Fe", "Cr"], 8)
+        graphs = [sg.graph(k, dev) for k in range(8)]
+        model, _ = build_model(graphs[0].edge_index.shape[1] / len(numbers))
+        print(json.dumps({"power": power_per_kernel(model.to(dev), graphs, dev)}), flush=True)
         return
     if args.kernel_only:
         sg = StepGraphs(numbers, pos, cell, pbc, ["Cu", "Ni", "Fe", "Cr"], 1)

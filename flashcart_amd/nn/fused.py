@@ -289,24 +289,29 @@ def paired_conv(layer, in1: Tensor, in2: Tensor, x_pairs: Tensor, graph, pairs, 
     return _PairedConv.apply(in1, in2, x_pairs, layer, graph, pairs, alpha)
 
 
-def species_maps(layer, x_table: Tensor, alpha: float):
+def species_maps(layer, table: Tensor, alpha: float):
     """Matrices and scales of the first interaction layer's species density, with its
-    ``linear_second`` folded in: per rank l,
+    ``linear_second`` folded in: per rank l, with x_table = linear_first(table) (the sender
+    features of each species),
         M_l[o, Z * 64 + k] = sum_c Wsec_l[o, c] x_table[Z, c] W2[l C + c, k],
         scale_l = alpha s2 s_l,
     so that linear_second(TP(...))_l = scale_l dens_l @ M_l^T (the path (0, l, l) takes block l
-    of the radial output layer W2). Cached on the layer while the parameters, the table and
-    alpha are unchanged (recomputed under graph capture, which then replays the computation)."""
+    of the radial output layer W2). Cached on the layer while the table, the parameters that
+    enter (linear_first, W2, linear_second) and alpha are unchanged: keyed by their storage and
+    in-place version counters (recomputed under graph capture, which then replays the
+    computation)."""
     tp, lin, w2 = layer.tp, layer.linear_second, layer.radial_mlp[4].weight
     c = tp.in1_features
     lm = min(tp.in2_l_max, tp.out_l_max)
     common = min(lm, lin.out_l_max)
-    srcs = [x_table, w2, *lin.weight]
+    srcs = [table, w2, *lin.parameters(), *layer.linear_first.parameters()]
     key = tuple((t.data_ptr(), t._version) for t in srcs) + (float(alpha),)
     capturing = torch.cuda.is_current_stream_capturing()
     hit = layer.__dict__.get("_species_maps")
     if not capturing and hit is not None and hit[0] == key:
         return hit[1]
+    with torch.no_grad():
+        x_table = layer.linear_first(table)
     n_sp = x_table.shape[0]
     mats = []
     for l in range(common + 1):
@@ -336,16 +341,16 @@ class _SpeciesConv(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, y: Tensor, x_pairs: Tensor, layer, graph, pairs, edge_species: Tensor,
-                x_table: Tensor, alpha: float) -> Tensor:
+                table: Tensor, alpha: float) -> Tensor:
         from flashcart_amd import _lib
         tp = layer.tp
         l0, l1 = layer.radial_mlp[0], layer.radial_mlp[2]
-        n_sp = x_table.shape[0]
+        n_sp = table.shape[0]
         lm = min(tp.in2_l_max, tp.out_l_max)
         h = _ops.radial_mlp_hidden_fwd(x_pairs, l0.weight, l0._scale, l1.weight, l1._scale)
         csr = _lib.csr_struct(graph.n_nodes, graph.n_edges, graph.idx_j, graph.rowptr, pair_slot=pairs.slot)
         dens = _ops.species_density_fwd(csr, lm, tp.in2_l_max, n_sp, edge_species, h, y, graph.n_nodes)
-        mats, cfg = species_maps(layer, x_table, alpha)
+        mats, cfg = species_maps(layer, table, alpha)
         out = _ops.linear_fwd(dens, mats, *cfg)
         ctx.save_for_backward(y, x_pairs, h, edge_species, pairs.slot, *mats)
         ctx.layer, ctx.graph, ctx.cfg, ctx.n_sp = layer, graph, cfg, n_sp
@@ -393,5 +398,7 @@ def species_conv_applies(layer, node_feats: Tensor, n_species: int) -> bool:
 
 
 def species_conv(layer, edge_attrs: Tensor, x_pairs: Tensor, graph, pairs, edge_species: Tensor,
-                 x_table: Tensor, alpha: float) -> Tensor:
-    return _SpeciesConv.apply(edge_attrs, x_pairs, layer, graph, pairs, edge_species, x_table, alpha)
+                 table: Tensor, alpha: float) -> Tensor:
+    """``table``: the embedding rows of the species (the layer's sender features are
+    linear_first(table)[species])."""
+    return _SpeciesConv.apply(edge_attrs, x_pairs, layer, graph, pairs, edge_species, table, alpha)

@@ -207,7 +207,7 @@ class InteractionLayer(nn.Module):
             if species is not None and out_nodes is None and \
                     fused.species_conv_applies(self, node_feats, species[1].shape[0]):
                 mapped = fused.species_conv(self, edge_attrs, mlp_pairs, graph, edge_pairs, species[0],
-                                            self.linear_first(species[1]), self._inv_sqrt_avg())
+                                            species[1], self._inv_sqrt_avg())
                 return self._finish(mapped, residual_feats, out_nodes, mapped=True)
             else:
                 aggregated = fused.paired_conv(self, self.linear_first(node_feats), edge_attrs, mlp_pairs, graph,

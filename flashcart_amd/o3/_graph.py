@@ -169,12 +169,34 @@ def launch_edge_pairs(csr: GraphCSR, shifts: Optional[torch.Tensor]):
                                  upper.data_ptr(), reverse.data_ptr(), n_edges // 2, counts.data_ptr(),
                                  ws.data_ptr(), n_ws, _lib.stream_of(csr.idx_i)),
                "fc_edge_pairs")
+    if not torch.cuda.is_current_stream_capturing():
+        # the counters travel to pinned host memory behind the pairing kernels; reading them
+        # waits for that copy only, not for the work queued after it
+        host = torch.empty(2, dtype=torch.int32, pin_memory=True)
+        host.copy_(counts, non_blocking=True)
+        done = torch.cuda.Event()
+        done.record(torch.cuda.current_stream(dev))
+        while len(_READBACK) >= 16:  # launches whose counters were never checked
+            _READBACK.pop(next(iter(_READBACK)))
+        _READBACK[counts.data_ptr()] = (counts, host, done)
     return EdgePairs(slot, edge, upper, reverse), counts
 
 
+# device counters of launched pairings -> (counters, pinned host copy, event after the copy)
+_READBACK = {}
+
+
 def pairs_complete(counts: torch.Tensor, n_edges: int) -> bool:
-    """Host check of ``launch_edge_pairs``'s counters (one synchronisation)."""
-    unpaired, n_pairs = (int(v) for v in counts.tolist())
+    """Host check of ``launch_edge_pairs``'s counters: waits for the pinned copy queued behind
+    the pairing when there is one (work queued after it keeps the GPU busy), else reads the
+    device counters (a full synchronisation)."""
+    pending = _READBACK.pop(counts.data_ptr(), None)
+    if pending is not None and pending[0] is counts:
+        pending[2].synchronize()
+        values = pending[1].tolist()
+    else:
+        values = counts.tolist()
+    unpaired, n_pairs = (int(v) for v in values)
     return unpaired == 0 and 2 * n_pairs == n_edges
 
 

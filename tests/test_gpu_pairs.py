@@ -355,9 +355,9 @@ def test_species_conv_matches_paired_conv():
     alpha = layer._inv_sqrt_avg()
     node = model.embedding(g.atom_types)
     assert fused.species_conv_applies(layer, node, table.shape[0])
-    out_s = fused.species_conv(layer, y, xp, csr, pairs, zj, layer.linear_first(table), alpha)
+    out_s = fused.species_conv(layer, y, xp, csr, pairs, zj, table, alpha)
     out_p = layer.linear_second(fused.paired_conv(layer, layer.linear_first(node), y, xp, csr, pairs, alpha))
-    again = fused.species_conv(layer, y, xp, csr, pairs, zj, layer.linear_first(table), alpha)
+    again = fused.species_conv(layer, y, xp, csr, pairs, zj, table, alpha)
     assert torch.equal(out_s, again)
     assert_close(out_s, out_p, 1e-5, 1e-5 * float(out_p.abs().max()), "species vs paired output")
     go = torch.randn_like(out_p)
@@ -365,6 +365,15 @@ def test_species_conv_matches_paired_conv():
     gp = torch.autograd.grad(out_p, (y, xp), go)
     for a, b, what in zip(gs, gp, ("edge attributes", "radial inputs")):
         assert_close(a, b, 1e-5, 1e-5 * float(b.abs().max()), f"species vs paired gradient of {what}")
+    # the cached maps follow in-place changes of the table and of linear_first's weights
+    with torch.no_grad():
+        table.mul_(1.5)
+        layer.linear_first.weight[0].add_(0.25)
+    node = model.embedding(g.atom_types)
+    out_s = fused.species_conv(layer, y, xp, csr, pairs, zj, table, alpha)
+    out_p = layer.linear_second(fused.paired_conv(layer, layer.linear_first(node), y, xp, csr, pairs, alpha))
+    assert not torch.equal(out_s, again)
+    assert_close(out_s, out_p, 1e-5, 1e-5 * float(out_p.abs().max()), "species vs paired output after an update")
 
 
 @pytest.mark.parametrize("m", [2176, 272])
