@@ -14,9 +14,37 @@ __global__ void csr_from_sorted_kernel(int64_t n_edges, const int32_t* __restric
   for (int64_t n = lo; n <= hi && n <= n_nodes; ++n) rowptr[n] = (int32_t)e;
 }
 
-// Wide rows (width >= 64): one workgroup per segment, threads over columns (float4 when
-// the rows are 16-byte aligned), rows of the segment summed in order.
-__global__ void __launch_bounds__(256) segment_rows_kernel(int64_t width, const float* __restrict__ src,
+// Wide rows (width >= 64): one workgroup per segment (blockIdx.y splits rows wider than
+// 512 columns), threads over columns (float4 when the rows are 16-byte aligned). The rows of
+// a segment are summed in order; four are loaded before they are added, so each wave keeps
+// four row reads in flight.
+template <typename V>
+__device__ __forceinline__ void add_to(V& a, const V& b);
+template <>
+__device__ __forceinline__ void add_to<float4>(float4& a, const float4& b) {
+  a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+}
+template <>
+__device__ __forceinline__ void add_to<float>(float& a, const float& b) { a += b; }
+
+template <typename V>
+__device__ __forceinline__ void segment_cols(int64_t w, const V* __restrict__ src, const int32_t* __restrict__ perm,
+                                             int32_t k0, int32_t k1, V* __restrict__ dst) {
+  for (int64_t c = threadIdx.x + (int64_t)blockIdx.y * blockDim.x; c < w; c += (int64_t)gridDim.y * blockDim.x) {
+    V acc{};
+    auto row = [&](int32_t k) { return perm ? (int64_t)perm[k] : (int64_t)k; };
+    int32_t k = k0;
+    for (; k + 4 <= k1; k += 4) {
+      const V v0 = src[row(k) * w + c], v1 = src[row(k + 1) * w + c];
+      const V v2 = src[row(k + 2) * w + c], v3 = src[row(k + 3) * w + c];
+      add_to(acc, v0); add_to(acc, v1); add_to(acc, v2); add_to(acc, v3);
+    }
+    for (; k < k1; ++k) add_to(acc, src[row(k) * w + c]);
+    dst[c] = acc;
+  }
+}
+
+__global__ void __launch_bounds__(512) segment_rows_kernel(int64_t width, const float* __restrict__ src,
                                                            const int32_t* __restrict__ perm,
                                                            const int32_t* __restrict__ ptr, float* __restrict__ dst,
                                                            int vec4, int64_t n_seg) {
@@ -24,25 +52,10 @@ __global__ void __launch_bounds__(256) segment_rows_kernel(int64_t width, const 
   if (s >= n_seg) return;
   const int32_t k0 = ptr[s], k1 = ptr[s + 1];
   if (vec4) {
-    const int64_t w4 = width >> 2;
-    for (int64_t c = threadIdx.x + (int64_t)blockIdx.y * blockDim.x; c < w4; c += (int64_t)gridDim.y * blockDim.x) {
-      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-      for (int32_t k = k0; k < k1; ++k) {
-        const int64_t r = perm ? (int64_t)perm[k] : (int64_t)k;
-        const float4 v = reinterpret_cast<const float4*>(src + r * width)[c];
-        acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
-      }
-      reinterpret_cast<float4*>(dst + s * width)[c] = acc;
-    }
+    segment_cols<float4>(width >> 2, reinterpret_cast<const float4*>(src), perm, k0, k1,
+                         reinterpret_cast<float4*>(dst + s * width));
   } else {
-    for (int64_t c = threadIdx.x + (int64_t)blockIdx.y * blockDim.x; c < width; c += (int64_t)gridDim.y * blockDim.x) {
-      float acc = 0.f;
-      for (int32_t k = k0; k < k1; ++k) {
-        const int64_t r = perm ? (int64_t)perm[k] : (int64_t)k;
-        acc += src[r * width + c];
-      }
-      dst[s * width + c] = acc;
-    }
+    segment_cols<float>(width, src, perm, k0, k1, dst + s * width);
   }
 }
 
@@ -108,9 +121,12 @@ int segment_sum(int64_t n_seg, int64_t width, const float* src, const int32_t* p
   } else {
     const int vec4 = (width % 4 == 0) && (((uintptr_t)src & 15) == 0) && (((uintptr_t)dst & 15) == 0);
     const int64_t cols = vec4 ? width / 4 : width;
-    const unsigned gy = (unsigned)((cols + 255) / 256);
-    hipLaunchKernelGGL(segment_rows_kernel, dim3((unsigned)xcd_grid(n_seg), gy), dim3(256), 0, s, width, src, perm,
-                       ptr, dst, vec4, n_seg);
+    // whole waves covering the columns, at most 512 threads (one workgroup per segment for
+    // rows of up to 512 columns: 288 float4 at 9 x 128 take 320 threads)
+    const int64_t threads = cols >= 512 ? 512 : (cols + 63) / 64 * 64;
+    const unsigned gy = (unsigned)((cols + threads - 1) / threads);
+    hipLaunchKernelGGL(segment_rows_kernel, dim3((unsigned)xcd_grid(n_seg), gy), dim3((unsigned)threads), 0, s, width,
+                       src, perm, ptr, dst, vec4, n_seg);
   }
   FC_LAUNCH_CHECK();
   return FC_OK;
