@@ -996,11 +996,13 @@ __device__ __forceinline__ void wide_body(const float* As, float (*Bs)[WIDE_BN *
       rb[i] = *reinterpret_cast<const float4*>(w + (int64_t)col * WIDE_K + k4);
     }
   };
+  // the weight chunk goes to LDS scaled, out = x (W scale)^T (the order of F.linear(x, W * s))
   auto store_b = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int e = t + 256 * i;
-      put4(Bs[buf], e >> 4, (e & 15) * 4, rb[i]);
+      put4(Bs[buf], e >> 4, (e & 15) * 4,
+           make_float4(rb[i].x * scale, rb[i].y * scale, rb[i].z * scale, rb[i].w * scale));
     }
   };
   load_b(0);
@@ -1012,11 +1014,26 @@ __device__ __forceinline__ void wide_body(const float* As, float (*Bs)[WIDE_BN *
   const int nch = (m + WIDE_BN - 1) / WIDE_BN;
   // output rows of this lane: r0 + 32 wave + 8 (v/4) + 4 (lane/32) + v%4
   const int64_t rl = r0 + wave * 32 + 4 * (lane >> 5);
+  // Unguarded blocks: the element offset of row v (of this lane's 16) from the block's first
+  // element is fixed for the whole block, so a store is a wave-uniform base (the block and the
+  // chunk's column) plus a precomputed 32-bit offset, with no per-store address arithmetic.
+  // (The caller keeps 128 m 4 below 2^31.)
+  uint32_t voff[GUARD ? 1 : 16];  // bytes
+  if constexpr (!GUARD) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+      voff[v] = (uint32_t)((wave * 32 + 4 * (lane >> 5) + 8 * (v >> 2) + (v & 3)) * m + (lane & 31)) * 4u;
+  }
+  float* const blk = out + r0 * m;
   // results of output row v (of this lane's 16) and column block j of a chunk at column c0
   auto store_one = [&](const floatx16 (&res)[2], int c0, int v, int j) {
-    const int64_t row = rl + 8 * (v >> 2) + (v & 3);
-    const int col = c0 + j * 32 + (lane & 31);
-    if (!GUARD || (row < n && col < m)) out[row * m + col] = res[j][v] * scale;
+    if constexpr (GUARD) {
+      const int64_t row = rl + 8 * (v >> 2) + (v & 3);
+      const int col = c0 + j * 32 + (lane & 31);
+      if (row < n && col < m) out[row * m + col] = res[j][v];
+    } else {
+      *reinterpret_cast<float*>(reinterpret_cast<char*>(blk + c0 + j * 32) + voff[v]) = res[j][v];
+    }
   };
   // One chunk into `cur`; the previous chunk's results (`prv`, complete by now) are
   // stored in between this chunk's MFMAs, so the wave keeps the matrix core fed while
@@ -1335,7 +1352,8 @@ extern "C" int fc_dense_fwd(int64_t n, int32_t k, int32_t m, const float* x, con
   if (n > 0x7fffffff) return FC_ERR_SHAPE;
   if (k == WIDE_K && m >= 4 * WIDE_BN && !bias && act == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0) {
     const int64_t blocks = (n + WIDE_BM - 1) / WIDE_BM;
-    const int64_t full = m % WIDE_BN == 0 ? n / WIDE_BM : 0;
+    // unguarded blocks address their 128 rows with 32-bit byte offsets: 128 m 4 < 2^31
+    const int64_t full = (m % WIDE_BN == 0 && (int64_t)m < (int64_t(1) << 22)) ? n / WIDE_BM : 0;
     if (full > 0) {
       hipLaunchKernelGGL(gemm_wide_kernel<false>, dim3((unsigned)full), dim3(256), 0, (hipStream_t)stream, n, m, x,
                          w, scale, out, (int64_t)0);
@@ -1389,8 +1407,9 @@ extern "C" int fc_radial_mlp_fwd(int64_t n, int32_t n_in, const float* x, const 
   if (((uintptr_t)w2 & 15) != 0) return FC_ERR_SHAPE;  // weight chunks load as float4
   const int64_t blocks = (n + WIDE_BM - 1) / WIDE_BM;
   if (blocks > 0x7fffffff) return FC_ERR_SHAPE;
-  // one launch (the partial last row block is guarded inside it)
-  if (m % WIDE_BN == 0)
+  // one launch (the partial last row block is guarded inside it); unguarded blocks address their
+  // 128 rows with 32-bit byte offsets: 128 m 4 < 2^31
+  if (m % WIDE_BN == 0 && (int64_t)m < (int64_t(1) << 22))
     hipLaunchKernelGGL(radial_mlp_fwd_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, n,
                        (int)n_in, x, w0, s0, w1, s1, (int)m, w2, s2, out, (int64_t)0);
   else
