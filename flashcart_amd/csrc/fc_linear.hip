@@ -408,11 +408,31 @@ __device__ __forceinline__ int pipe_kswz(int k) {
 // indirect register indexing, no compiler-issued direct loads), so clobbering it is safe here.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void lds_dma16(const float* src, const float* lds_dst) {
-  const uint32_t off = __builtin_amdgcn_readfirstlane(
-      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float*)(lds_dst));
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(off)
+__device__ __forceinline__ void lds_dma16(const float* src, uint32_t lds_off) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_off)
                : "memory", "m0");
+}
+
+// The same with a wave-uniform 64-bit base in scalar registers and a 32-bit per-lane byte
+// offset (no per-lane 64-bit address arithmetic per load).
+__device__ __forceinline__ void lds_dma16_s(const float* base, uint32_t voff, uint32_t lds_off) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base),
+               "s"(lds_off)
+               : "memory", "m0");
+}
+
+// A pointer that is the same in every lane, moved to scalar registers (the asm operands of
+// lds_dma16_s must be scalar).
+__device__ __forceinline__ const float* uniform_ptr(const float* p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const float*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
+// LDS byte address of a __shared__ array (a compile-time constant for a named array)
+__device__ __forceinline__ uint32_t lds_addr(const float* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float*)(p);
 }
 #pragma clang diagnostic pop
 
@@ -484,8 +504,9 @@ __global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 
     }
     return gb.total_tiles;
   };
-  const int t_first = tile_at(((int64_t)v * work + G - 1) / G);
-  const int t_end = tile_at(((int64_t)(v + 1) * work + G - 1) / G);
+  // (uniform; kept in scalar registers so the tile loop's bookkeeping stays scalar)
+  const int t_first = __builtin_amdgcn_readfirstlane(tile_at(((int64_t)v * work + G - 1) / G));
+  const int t_end = __builtin_amdgcn_readfirstlane(tile_at(((int64_t)(v + 1) * work + G - 1) / G));
   constexpr int t_step = 1;
   auto decode = [&](int tile) -> PipeTile {
     int ri = 0;
@@ -499,15 +520,49 @@ __global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 
   };
 
   // ---- producer: direct loads of K steps in tile order
+  // Without pair sums every load of a tile addresses a uniform base (the tile's first A row,
+  // its first B column) plus a 32-bit lane offset fixed for the tile (pipe_ok bounds them);
+  // the pair-sum mode's gathered rows span the whole A, so it keeps 64-bit lane addresses.
+  constexpr bool SADDR = !PS;
   int p_tile = t_first, p_k = 0, n_issued = 0;
   PipeTile pt{0, 0, 0, 32};
-  const float* a_src[A_DMA];
+  const float* a_src[SADDR ? 1 : A_DMA];
   const float* a_src2[PS ? A_DMA : 1];  // second halves
-  const float* b_src[B_DMA];
+  const float* b_src[SADDR ? 1 : B_DMA];
+  const float* a_base = nullptr;
+  const float* b_base = nullptr;
+  uint32_t a_off[SADDR ? A_DMA : 1], b_off[SADDR ? B_DMA : 1];  // bytes
   auto p_setup = [&]() {
     if (p_tile >= t_end) return;
     pt = decode(p_tile);
     const GemmRank& g = gb.r[pt.ri];
+    if constexpr (SADDR) {
+      const int n0 = pt.r0 / g.comps;
+      a_base = uniform_ptr(g.A + (int64_t)n0 * g.a_row);
+      b_base = uniform_ptr(KB ? g.B : g.B + (int64_t)pt.c0 * g.K);
+#pragma unroll
+      for (int j = 0; j < A_DMA; ++j) {
+        const int s = (j * 4 + wave) * 64 + lane;
+        const int row = s >> 3, c = (s & 7) ^ pipe_swz(row);
+        const int grow = min(pt.r0 + row, g.M - 1);
+        const int n = grow / g.comps, cc = grow - n * g.comps;
+        a_off[j] = 4u * (uint32_t)((int64_t)(n - n0) * g.a_row + (int64_t)cc * g.a_comp + 4 * c);
+      }
+#pragma unroll
+      for (int j = 0; j < B_DMA; ++j) {
+        const int s = (j * 4 + wave) * 64 + lane;
+        if constexpr (KB) {
+          const int kk = s / BQ, p = (s % BQ) ^ pipe_kswz<MI>(kk);
+          const int col = min(pt.c0 + 4 * p, g.N - 4);
+          b_off[j] = 4u * (uint32_t)((int64_t)kk * g.N + col);
+        } else {
+          const int col = s >> 3, c = (s & 7) ^ pipe_swz(col);
+          const int gcol = min(pt.c0 + col, g.N - 1);
+          b_off[j] = 4u * (uint32_t)((int64_t)(gcol - pt.c0) * g.K + 4 * c);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < A_DMA; ++j) {
       const int s = (j * 4 + wave) * 64 + lane;
@@ -540,17 +595,29 @@ __global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 
       }
     }
   };
-  auto p_issue = [&](float* as, float* bs) {
+  // LDS byte addresses of the stage being filled (as, bs); this wave's 16-byte chunks of a
+  // direct load land at + 1024 (j * 4 + wave), kept in scalar registers
+  const uint32_t wave_lds = 1024u * (uint32_t)__builtin_amdgcn_readfirstlane(wave);
+  auto p_issue = [&](uint32_t as, uint32_t bs) {
     if (p_tile >= t_end) return;
     const int64_t bstep = KB ? (int64_t)p_k * gb.r[pt.ri].N : (int64_t)p_k;
+    if constexpr (SADDR) {
+      const float* sa = uniform_ptr(a_base + p_k);
+      const float* sb = uniform_ptr(b_base + bstep);
 #pragma unroll
-    for (int j = 0; j < A_DMA; ++j) lds_dma16(a_src[j] + p_k, as + (j * 4 + wave) * 256);
+      for (int j = 0; j < A_DMA; ++j) lds_dma16_s(sa, a_off[j], as + 4096u * j + wave_lds);
+#pragma unroll
+      for (int j = 0; j < B_DMA; ++j) lds_dma16_s(sb, b_off[j], bs + 4096u * j + wave_lds);
+    } else {
+#pragma unroll
+    for (int j = 0; j < A_DMA; ++j) lds_dma16(a_src[j] + p_k, as + 4096u * j + wave_lds);
     if constexpr (PS) {
 #pragma unroll
-      for (int j = 0; j < A_DMA; ++j) lds_dma16(a_src2[j] + p_k, as + BM * 32 + (j * 4 + wave) * 256);
+      for (int j = 0; j < A_DMA; ++j) lds_dma16(a_src2[j] + p_k, as + 4u * BM * 32 + 4096u * j + wave_lds);
     }
 #pragma unroll
-    for (int j = 0; j < B_DMA; ++j) lds_dma16(b_src[j] + bstep, bs + (j * 4 + wave) * 256);
+    for (int j = 0; j < B_DMA; ++j) lds_dma16(b_src[j] + bstep, bs + 4096u * j + wave_lds);
+    }
     ++n_issued;
     p_k += 32;
     if (p_k >= pt.K) {
@@ -697,7 +764,7 @@ __global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 
   // flight), barrier (every wave's loads have landed and every wave is done with the stage
   // the new loads overwrite), refill that stage, multiply, and finish the tile at its end.
   bool more = c_tile < t_end;
-  auto step = [&](const float* as, const float* bs, float* pas, float* pbs) {
+  auto step = [&](const float* as, const float* bs, uint32_t pas, uint32_t pbs) {
     if (n_issued - n_done >= 2) __builtin_amdgcn_s_waitcnt(FC_WAITCNT_IMM(L, 0));
     else __builtin_amdgcn_s_waitcnt(FC_WAITCNT_IMM(0, 0));
     pipe_barrier();
@@ -715,14 +782,14 @@ __global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 
   };
 
   p_setup();
-  p_issue(As0, Bs0);
-  p_issue(As1, Bs1);
+  p_issue(lds_addr(As0), lds_addr(Bs0));
+  p_issue(lds_addr(As1), lds_addr(Bs1));
   while (more) {
-    step(As0, Bs0, As2, Bs2);
+    step(As0, Bs0, lds_addr(As2), lds_addr(Bs2));
     if (!more) break;
-    step(As1, Bs1, As0, Bs0);
+    step(As1, Bs1, lds_addr(As0), lds_addr(Bs0));
     if (!more) break;
-    step(As2, Bs2, As1, Bs1);
+    step(As2, Bs2, lds_addr(As1), lds_addr(Bs1));
   }
 }
 
@@ -743,6 +810,9 @@ static bool pipe_ok(const GemmBatch& gb, int n_ranks) {
   for (int l = 0; l < n_ranks; ++l) {
     const GemmRank& g = gb.r[l];
     if (g.pre || g.P || g.K < 32 || (g.K & 31) || (g.a_row & 3) || (g.a_comp & 3)) return false;
+    // 32-bit byte offsets of a tile's loads from its first A row / B column (128-row tiles)
+    if ((int64_t)129 * g.a_row + (int64_t)g.comps * g.a_comp + g.K >= (int64_t(1) << 30)) return false;
+    if ((int64_t)128 * g.K >= (int64_t(1) << 30) || (int64_t)32 * g.N + g.N >= (int64_t(1) << 30)) return false;
     if (((uintptr_t)g.A & 15) || ((uintptr_t)g.B & 15)) return false;
     if (!gb.trans_b && (g.N & 3)) return false;
   }
