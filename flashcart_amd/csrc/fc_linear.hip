@@ -30,6 +30,7 @@
 // XCDs), so the A rows are fetched from HBM once and then hit that XCD's L2.
 // fp32 inputs, fp32 accumulation: no reduced-precision operands.
 #include "fc_common.h"
+#include <type_traits>  // std::true_type
 
 namespace fc {
 
@@ -430,6 +431,16 @@ __device__ __forceinline__ const float* uniform_ptr(const float* p) {
   return (const float*)(uintptr_t)(((uint64_t)hi << 32) | lo);
 }
 
+// The same as a global-address-space pointer (loads and stores through it stay global
+// instructions with a scalar base rather than flat ones).
+typedef __attribute__((address_space(1))) float gfloat;
+__device__ __forceinline__ gfloat* uniform_gptr(const float* p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (gfloat*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
 // LDS byte address of a __shared__ array (a compile-time constant for a named array)
 __device__ __forceinline__ uint32_t lds_addr(const float* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float*)(p);
@@ -644,7 +655,10 @@ __global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 
   // q of half s (2 halves). Either way a lane reads its four k values as one chunk.
   constexpr int NS = MI == 32 ? 4 : 2;
   const int kg = MI == 32 ? h : (lane >> 4);  // lane group along k
-  auto compute = [&](const float* as, const float* bs) {
+  // FIRST: the tile's first K step, whose first MFMA of each block starts from zero (the
+  // accumulators need no clearing between tiles)
+  auto compute = [&](const float* as, const float* bs, auto first_c) {
+    constexpr bool FIRST = decltype(first_c)::value;
 #pragma unroll
     for (int s4 = 0; s4 < NS; ++s4) {
       float4 a4[FM], b4[FN];
@@ -677,8 +691,9 @@ __global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 
           for (int j = 0; j < FN; ++j) {
             const float a = reinterpret_cast<const float*>(&a4[i])[q];
             const float b = reinterpret_cast<const float*>(&b4[j])[q];
-            if constexpr (MI == 32) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[i][j], 0, 0, 0);
-            else acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[i][j], 0, 0, 0);
+            const accv c = (FIRST && s4 == 0 && q == 0) ? accv{} : acc[i][j];
+            if constexpr (MI == 32) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+            else acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
           }
     }
   };
@@ -688,46 +703,60 @@ __global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 
   // including the direct loads of the next K steps.
   auto epilogue = [&]() {
     const GemmRank& g = gb.r[ct.ri];
-    float* const D = g.D;
-    const float* const R = g.R;
-    const int64_t d_row = g.d_row, d_comp = g.d_comp;
     const int M = g.M, N = g.N, comps = g.comps;
     const float scale = g.scale;
+    // Rows are addressed from the tile's first node (a uniform base) with 32-bit byte
+    // offsets (pipe_ok bounds them), columns j > 0 as immediate offsets: the stores and
+    // residual loads need no per-access 64-bit address arithmetic.
+    const int n0 = ct.r0 / comps, c00 = ct.r0 - n0 * comps;
+    const float inv_comps = 1.0f / (float)comps;
+    gfloat* const Dt = uniform_gptr(g.D + (int64_t)n0 * g.d_row);
+    const bool has_r = g.R != nullptr;
+    const gfloat* const Rt = uniform_gptr(has_r ? g.R + (int64_t)n0 * g.d_row : g.D);
+    const int col0 = ct.c0 + wn * TN + (lane & (MI - 1));  // this lane's column in block j = 0
+    const bool all_cols = ct.c0 + BN <= N;                  // uniform
     float bias_v[FN];
-    int cols[FN];
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      cols[j] = ct.c0 + wn * TN + j * MI + (lane & (MI - 1));
-      bias_v[j] = (gb.bias && cols[j] < N) ? gb.bias[cols[j]] : 0.f;
-    }
+    for (int j = 0; j < FN; ++j) bias_v[j] = (gb.bias && col0 + j * MI < N) ? gb.bias[col0 + j * MI] : 0.f;
     // block rows of acc value v = 4 vg + q: 8 vg + 4 (lane / 32) + q (32x32), 4 (lane / 16) + q (16x16)
-    int64_t offs[FM][NV];
+    uint32_t roff[FM][NV];
+    bool rok[FM][NV];
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
 #pragma unroll
       for (int vg = 0; vg < NV / 4; ++vg) {
-        const int r = ct.r0 + wm * TM + i * MI + (MI == 32 ? 8 * vg + 4 * h : 4 * (lane >> 4));
-        int n = r / comps, c = r - n * comps;
+        const int rl = wm * TM + i * MI + (MI == 32 ? 8 * vg + 4 * h : 4 * (lane >> 4));
+        // node and component of row r0 + rl, counted from node n0: y / comps for y < BM + comps
+        // (exact in float: (y + 1/2) / comps is at least 1 / (2 comps) from an integer)
+        const int y = c00 + rl;
+        int dn = (int)(((float)y + 0.5f) * inv_comps), c = y - dn * comps;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          offs[i][4 * vg + q] = (r + q < M) ? (int64_t)n * d_row + (int64_t)c * d_comp : -1;
+          rok[i][4 * vg + q] = ct.r0 + rl + q < M;
+          roff[i][4 * vg + q] = 4u * (uint32_t)(dn * (int)g.d_row + c * (int)g.d_comp + col0);
           if (++c == comps) {
             c = 0;
-            ++n;
+            ++dn;
           }
         }
       }
     }
+    typedef __attribute__((address_space(1))) char gchar;
+    auto d_at = [&](uint32_t off, int j) { return reinterpret_cast<gfloat*>(reinterpret_cast<gchar*>(Dt) + off) + j * MI; };
+    auto r_at = [&](uint32_t off, int j) {
+      return reinterpret_cast<const gfloat*>(reinterpret_cast<const gchar*>(Rt) + off) + j * MI;
+    };
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j)
 #pragma unroll
         for (int v = 0; v < NV; ++v) acc[i][j][v] = fmaf(acc[i][j][v], scale, bias_v[j]);
-    if (R) {
-      // every residual value is loaded (from a clamped, valid address) before the first store:
-      // a load into a register that a pending store still reads makes the compiler wait for
-      // all outstanding loads, the direct loads of the next K steps included
+    if (has_r) {
+      // every residual value is loaded (rows out of range read the tile's first row, columns
+      // out of range nothing) before the first store: a load into a register that a pending
+      // store still reads makes the compiler wait for all outstanding loads, the direct loads
+      // of the next K steps included
       float rv[FM][NV][FN];
 #pragma unroll
       for (int i = 0; i < FM; ++i)
@@ -735,7 +764,7 @@ __global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 
         for (int v = 0; v < NV; ++v)
 #pragma unroll
           for (int j = 0; j < FN; ++j)
-            rv[i][v][j] = R[(offs[i][v] < 0 ? 0 : offs[i][v]) + (cols[j] < N ? cols[j] : N - 1)];
+            rv[i][v][j] = (all_cols || col0 + j * MI < N) ? *r_at(rok[i][v] ? roff[i][v] : 0u, j) : 0.f;
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -747,17 +776,11 @@ __global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int v = 0; v < NV; ++v) {
-        if (offs[i][v] < 0) continue;
+        if (!rok[i][v]) continue;
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          if (cols[j] < N) D[offs[i][v] + cols[j]] = acc[i][j][v];
+          if (all_cols || col0 + j * MI < N) *d_at(roff[i][v], j) = acc[i][j][v];
       }
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-#pragma unroll
-        for (int v = 0; v < NV; ++v) acc[i][j][v] = 0.f;
   };
 
   // One K step: wait for this wave's loads of the step (the step issued after it may stay in
@@ -769,7 +792,8 @@ __global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 
     else __builtin_amdgcn_s_waitcnt(FC_WAITCNT_IMM(0, 0));
     pipe_barrier();
     p_issue(pas, pbs);
-    compute(as, bs);
+    if (c_k == 0) compute(as, bs, std::true_type{});
+    else compute(as, bs, std::false_type{});
     ++n_done;
     c_k += 32;
     if (c_k >= ct.K) {
@@ -813,6 +837,9 @@ static bool pipe_ok(const GemmBatch& gb, int n_ranks) {
     // 32-bit byte offsets of a tile's loads from its first A row / B column (128-row tiles)
     if ((int64_t)129 * g.a_row + (int64_t)g.comps * g.a_comp + g.K >= (int64_t(1) << 30)) return false;
     if ((int64_t)128 * g.K >= (int64_t(1) << 30) || (int64_t)32 * g.N + g.N >= (int64_t(1) << 30)) return false;
+    // and of the epilogue's stores from the tile's first output node
+    if ((int64_t)129 * g.d_row + (int64_t)g.comps * g.d_comp + g.N >= (int64_t(1) << 30)) return false;
+    if (g.d_row > 0x7fffffff || g.d_comp > 0x7fffffff) return false;
     if (((uintptr_t)g.A & 15) || ((uintptr_t)g.B & 15)) return false;
     if (!gb.trans_b && (g.N & 3)) return false;
   }
