@@ -527,6 +527,7 @@ __global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 
     ri = __builtin_amdgcn_readfirstlane(ri);  // uniform: keeps the rank's fields in scalar loads
     const GemmRank& g = gb.r[ri];
     const int local = tile - g.tile_base;
+    if (g.tiles_n == 1) return PipeTile{ri, local * BM, 0, g.K};  // uniform: no division
     return PipeTile{ri, (local / g.tiles_n) * BM, (local % g.tiles_n) * BN, g.K};
   };
 
@@ -548,7 +549,8 @@ __global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 
     pt = decode(p_tile);
     const GemmRank& g = gb.r[pt.ri];
     if constexpr (SADDR) {
-      const int n0 = pt.r0 / g.comps;
+      const int n0 = pt.r0 / g.comps, c00 = pt.r0 - n0 * g.comps;
+      const float inv_comps = 1.0f / (float)g.comps;
       a_base = uniform_ptr(g.A + (int64_t)n0 * g.a_row);
       b_base = uniform_ptr(KB ? g.B : g.B + (int64_t)pt.c0 * g.K);
 #pragma unroll
@@ -556,8 +558,11 @@ __global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 
         const int s = (j * 4 + wave) * 64 + lane;
         const int row = s >> 3, c = (s & 7) ^ pipe_swz(row);
         const int grow = min(pt.r0 + row, g.M - 1);
-        const int n = grow / g.comps, cc = grow - n * g.comps;
-        a_off[j] = 4u * (uint32_t)((int64_t)(n - n0) * g.a_row + (int64_t)cc * g.a_comp + 4 * c);
+        // node and component counted from node n0: y / comps for y < BM + comps (exact in
+        // float, as in the epilogue)
+        const int y = c00 + (grow - pt.r0);
+        const int dn = (int)(((float)y + 0.5f) * inv_comps), cc = y - dn * g.comps;
+        a_off[j] = 4u * (uint32_t)((int64_t)dn * g.a_row + (int64_t)cc * g.a_comp + 4 * c);
       }
 #pragma unroll
       for (int j = 0; j < B_DMA; ++j) {
