@@ -120,6 +120,17 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// A global pointer that is the same in every lane, moved to scalar registers and typed as
+// global memory: accesses through it plus a 32-bit lane byte offset can compile to global
+// loads and stores with a scalar base (no per-lane 64-bit address arithmetic), not flat ones.
+typedef __attribute__((address_space(1))) float gfloat;
+typedef __attribute__((address_space(1))) char gchar;
+__device__ __forceinline__ gfloat* uniform_gptr(const float* p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (gfloat*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
 }  // namespace fc
 
 #define FC_LAUNCH_CHECK()                                    \

@@ -431,16 +431,6 @@ __device__ __forceinline__ const float* uniform_ptr(const float* p) {
   return (const float*)(uintptr_t)(((uint64_t)hi << 32) | lo);
 }
 
-// The same as a global-address-space pointer (loads and stores through it stay global
-// instructions with a scalar base rather than flat ones).
-typedef __attribute__((address_space(1))) float gfloat;
-__device__ __forceinline__ gfloat* uniform_gptr(const float* p) {
-  const uint64_t v = (uint64_t)(uintptr_t)p;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-  return (gfloat*)(uintptr_t)(((uint64_t)hi << 32) | lo);
-}
-
 // LDS byte address of a __shared__ array (a compile-time constant for a named array)
 __device__ __forceinline__ uint32_t lds_addr(const float* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float*)(p);
@@ -746,7 +736,6 @@ __global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 
         }
       }
     }
-    typedef __attribute__((address_space(1))) char gchar;
     auto d_at = [&](uint32_t off, int j) { return reinterpret_cast<gfloat*>(reinterpret_cast<gchar*>(Dt) + off) + j * MI; };
     auto r_at = [&](uint32_t off, int j) {
       return reinterpret_cast<const gfloat*>(reinterpret_cast<const gchar*>(Rt) + off) + j * MI;
