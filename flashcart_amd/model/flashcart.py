@@ -188,6 +188,7 @@ class FlashCartPotential(AtomisticModel):
             # the first layer's sender features are embedding rows: species density (fused.species_conv)
             species = (torch.index_select(atom_types.to(torch.int32), 0, csr.idx_j), self.embedding.weight)
         outputs = []
+        shared = {}  # per-evaluation values the interaction layers share (their pair radial inputs)
         for k, interaction in enumerate(self.interactions):
             msg = node_feats
             if is_lammps and k > 0:
@@ -195,7 +196,8 @@ class FlashCartPotential(AtomisticModel):
                 msg = lammps_exchange_features(node_feats, nlocal, ntotal)
             feats = interaction(msg, edge_attrs, edge_feats, edge_index, envelope,
                                 atom_types=atom_types if not self.element_agnostic_interaction else None,
-                                out_nodes=nlocal, graph=csr, edge_pairs=pairs, species=species if k == 0 else None)
+                                out_nodes=nlocal, graph=csr, edge_pairs=pairs, species=species if k == 0 else None,
+                                shared=shared)
             if self.nonlinearity:
                 feats = self.nonlinearities[k](feats)
             if self.use_products:

@@ -193,17 +193,26 @@ class InteractionLayer(nn.Module):
                 edge_index: torch.Tensor, envelope: torch.Tensor, atom_types: Optional[torch.Tensor] = None,
                 out_nodes: Optional[int] = None, graph: Optional[GraphCSR] = None,
                 edge_pairs: Optional[EdgePairs] = None,
-                species: Optional[Tuple[torch.Tensor, torch.Tensor]] = None) -> torch.Tensor:
+                species: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
+                shared: Optional[dict] = None) -> torch.Tensor:
         """``edge_pairs`` (with ``graph``): the reverse-edge pairing of a full neighbour list whose
         edge lengths agree bitwise within each pair; the radial weights are then formed once per
         pair where ``fused.paired_conv_applies`` (same outputs, half the radial MLP work).
+        ``shared``: a dict the caller passes to every interaction layer of one evaluation; the
+        radial-MLP inputs per pair (the same for every layer without element embeddings) are
+        formed by the first layer that needs them and reused by the others.
         ``species = (edge_species, table)``: ``node_feats`` is ``table[atom_types]`` and
         ``edge_species[e]`` the sender's row of ``table``; with pairs the layer then runs as a
         species density where ``fused.species_conv_applies``."""
         idx_i, idx_j = edge_index[0], edge_index[1]
         residual_feats = node_feats if out_nodes is None else node_feats[:out_nodes]
         if edge_pairs is not None and graph is not None and fused.paired_conv_applies(self, node_feats):
-            mlp_pairs = _ops.pair_inputs(edge_feats, envelope, edge_pairs.edge, edge_pairs.slot)
+            key = ("pair_inputs", id(edge_feats), id(envelope), id(edge_pairs))
+            mlp_pairs = shared.get(key) if shared is not None else None
+            if mlp_pairs is None:
+                mlp_pairs = _ops.pair_inputs(edge_feats, envelope, edge_pairs.edge, edge_pairs.slot)
+                if shared is not None:
+                    shared[key] = mlp_pairs
             if species is not None and out_nodes is None and \
                     fused.species_conv_applies(self, node_feats, species[1].shape[0]):
                 mapped = fused.species_conv(self, edge_attrs, mlp_pairs, graph, edge_pairs, species[0],
