@@ -189,6 +189,8 @@ class FlashCartPotential(AtomisticModel):
             species = (torch.index_select(atom_types.to(torch.int32), 0, csr.idx_j), self.embedding.weight)
         outputs = []
         shared = {}  # per-evaluation values the interaction layers share (their pair radial inputs)
+        entry = None
+        n_layers = len(self.interactions)
         for k, interaction in enumerate(self.interactions):
             msg = node_feats
             if is_lammps and k > 0:
@@ -197,14 +199,23 @@ class FlashCartPotential(AtomisticModel):
             feats = interaction(msg, edge_attrs, edge_feats, edge_index, envelope,
                                 atom_types=atom_types if not self.element_agnostic_interaction else None,
                                 out_nodes=nlocal, graph=csr, edge_pairs=pairs, species=species if k == 0 else None,
-                                shared=shared)
+                                shared=shared, entry=entry)
+            entry = None
             if self.nonlinearity:
                 feats = self.nonlinearities[k](feats)
             if self.use_products:
                 node_feats = self.products[k](feats, None if self.element_agnostic_product else local_types)
             else:
                 node_feats = feats
-            outputs.append(node_feats[:, : self.n_hidden_feats])
+            nxt = self.interactions[k + 1] if k + 1 < n_layers else None
+            if nxt is not None and pairs is not None and not is_lammps and \
+                    fused.entry_maps_apply(nxt, node_feats, self.n_hidden_feats):
+                # the next layer's input maps and this layer's readout columns with one input gradient
+                h, r, readout = fused.entry_maps(nxt, node_feats, self.n_hidden_feats)
+                entry = (h, r)
+                outputs.append(readout)
+            else:
+                outputs.append(node_feats[:, : self.n_hidden_feats])
         return self.scale_shift(self.readout(outputs), local_types)
 
     def to_model_config(self) -> Dict[str, Any]:

@@ -285,6 +285,56 @@ def paired_conv_applies(layer, node_feats: Tensor) -> bool:
             and 1 <= l0.weight.shape[1] <= 64)
 
 
+class _EntryMaps(torch.autograd.Function):
+    """The two equivariant maps an interaction layer applies to its input rows (``linear_first``
+    and the skip projection) and the leading ``n_read`` columns the energy readout takes from the
+    same rows, as one Function: the skip projection's input gradient takes ``linear_first``'s as
+    its GEMM-epilogue residual and the readout's gradient is added into its columns in place,
+    instead of three full-width gradients summed by autograd (reference: the separate calls of
+    ``nn/layers.py:351-379`` and ``model/flashcart.py:298-311``)."""
+
+    @staticmethod
+    def forward(ctx, x: Tensor, layer, n_read: int):
+        h = layer.linear_first(x)
+        r = layer.skip_projection(x)
+        s = x[:, :n_read].contiguous()
+        ctx.layer, ctx.n_read = layer, n_read
+        return h, r, s
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, gh: Tensor, gr: Tensor, gs: Tensor):
+        layer = ctx.layer
+        g = layer.linear_first.input_grad(gh.contiguous()) if gh is not None else None
+        if gr is not None:
+            g = layer.skip_projection.input_grad(gr.contiguous(), residual=g)
+        if g is None:
+            return None, None, None
+        if gs is not None:
+            g[:, : ctx.n_read] += gs
+        return g, None, None
+
+
+def entry_maps_apply(layer, x: Tensor, n_read: int) -> bool:
+    """True when the interaction layer's input maps may run as ``entry_maps``: the paired
+    convolution applies, the skip projection is an equivariant map feeding ``linear_second``'s
+    epilogue, both maps are frozen, and the readout columns lie inside the rows."""
+    from flashcart_amd.o3.linear import LinearLayer as O3Linear
+    if not paired_conv_applies(layer, x) or not isinstance(layer.linear_first, O3Linear):
+        return False
+    sp = layer.skip_projection
+    if sp is None or layer.in1_l_max == 0 or not isinstance(sp, O3Linear):
+        return False
+    if any(p.requires_grad for p in layer.linear_first.parameters()) or any(p.requires_grad for p in sp.parameters()):
+        return False
+    return x.dim() == 2 and 0 < n_read <= x.shape[1]
+
+
+def entry_maps(layer, x: Tensor, n_read: int):
+    """(linear_first(x), skip_projection(x), x[:, :n_read]) with one input gradient."""
+    return _EntryMaps.apply(x, layer, n_read)
+
+
 def paired_conv(layer, in1: Tensor, in2: Tensor, x_pairs: Tensor, graph, pairs, alpha: float) -> Tensor:
     return _PairedConv.apply(in1, in2, x_pairs, layer, graph, pairs, alpha)
 

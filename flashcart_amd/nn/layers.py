@@ -194,13 +194,16 @@ class InteractionLayer(nn.Module):
                 out_nodes: Optional[int] = None, graph: Optional[GraphCSR] = None,
                 edge_pairs: Optional[EdgePairs] = None,
                 species: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
-                shared: Optional[dict] = None) -> torch.Tensor:
+                shared: Optional[dict] = None,
+                entry: Optional[Tuple[torch.Tensor, torch.Tensor]] = None) -> torch.Tensor:
         """``edge_pairs`` (with ``graph``): the reverse-edge pairing of a full neighbour list whose
         edge lengths agree bitwise within each pair; the radial weights are then formed once per
         pair where ``fused.paired_conv_applies`` (same outputs, half the radial MLP work).
         ``shared``: a dict the caller passes to every interaction layer of one evaluation; the
         radial-MLP inputs per pair (the same for every layer without element embeddings) are
         formed by the first layer that needs them and reused by the others.
+        ``entry = (linear_first(node_feats), skip_projection(node_feats))`` from
+        ``fused.entry_maps``, used on the paired path instead of evaluating both maps here.
         ``species = (edge_species, table)``: ``node_feats`` is ``table[atom_types]`` and
         ``edge_species[e]`` the sender's row of ``table``; with pairs the layer then runs as a
         species density where ``fused.species_conv_applies``."""
@@ -219,9 +222,10 @@ class InteractionLayer(nn.Module):
                                             species[1], self._inv_sqrt_avg())
                 return self._finish(mapped, residual_feats, out_nodes, mapped=True)
             else:
-                aggregated = fused.paired_conv(self, self.linear_first(node_feats), edge_attrs, mlp_pairs, graph,
-                                               edge_pairs, self._inv_sqrt_avg())
-            return self._finish(aggregated, residual_feats, out_nodes)
+                in1 = entry[0] if entry is not None else self.linear_first(node_feats)
+                aggregated = fused.paired_conv(self, in1, edge_attrs, mlp_pairs, graph, edge_pairs,
+                                               self._inv_sqrt_avg())
+            return self._finish(aggregated, residual_feats, out_nodes, skip=entry[1] if entry is not None else None)
         if self.emb_i is not None:
             if atom_types is None:
                 raise ValueError(f"atom_types required when n_elements is set. Provided: {atom_types}.")
@@ -239,14 +243,18 @@ class InteractionLayer(nn.Module):
         return self._finish(aggregated, residual_feats, out_nodes)
 
     def _finish(self, aggregated: torch.Tensor, residual_feats: torch.Tensor,
-                out_nodes: Optional[int], mapped: bool = False) -> torch.Tensor:
+                out_nodes: Optional[int], mapped: bool = False,
+                skip: Optional[torch.Tensor] = None) -> torch.Tensor:
         """linear_second, skip connection and norm; ``mapped``: ``aggregated`` is already the
-        output of linear_second (the species density folds it in)."""
+        output of linear_second (the species density folds it in); ``skip``: the skip projection
+        of ``residual_feats``, already formed."""
         if out_nodes is not None:
             aggregated = aggregated[:out_nodes]
         if self.skip_projection is not None and self.in1_l_max > 0 and not mapped:
             # the skip projection enters linear_second's GEMM epilogue as its residual
-            out = self.linear_second(aggregated, residual=self.skip_projection(residual_feats))
+            if skip is None:
+                skip = self.skip_projection(residual_feats)
+            out = self.linear_second(aggregated, residual=skip)
         elif mapped and self.skip_projection is not None and self.in1_l_max > 0:
             out = aggregated + self.skip_projection(residual_feats)
         else:
