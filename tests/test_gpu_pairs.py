@@ -15,6 +15,7 @@ from flashcart_amd.data import AtomicGraph, batch_graphs
 from flashcart_amd.data.synthetic import fcc_alloy, model_config, molecules, water_box
 from oracle import model as OM
 from tests.helpers import assert_close, random_csr_graph
+from flashcart_amd.nn import fused
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -230,6 +231,9 @@ def test_paired_potential_matches_oracle_and_unpaired(case):
     out = m.predict(gd, compute_forces=True)
     csr = gd.csr
     assert any(v is not None for v in csr.__dict__.get("_pairs", {}).values()), "the paired path was not taken"
+    # the second layer's input maps and the first readout's columns ran as one Function
+    nxt = m.interactions[1]
+    assert fused.entry_maps_apply(nxt, torch.empty(1, nxt.linear_first.in_dim, device=DEV), m.n_hidden_feats)
     assert_close(out["energy"], ref["energy"], 1e-5, 1e-6, "energy")
     assert_close(out["forces"], ref["forces"], 0.0, 1e-4, "forces")
     # the same potential with the radial MLP parameters trainable takes the per-edge path
@@ -337,7 +341,6 @@ def test_species_conv_matches_paired_conv():
     """The first interaction layer as a species density (linear_second folded in) against the same
     layer over edge pairs followed by linear_second: outputs and input gradients (edge attributes,
     radial inputs) at float32 round-off; a second call reuses the cached maps."""
-    from flashcart_amd.nn import fused
     from flashcart_amd.o3 import _ops
     numbers, pos, cell, pbc = fcc_alloy(3, 3, 3, seed=4)
     cfg = model_config(["Cu", "Ni", "Fe", "Cr"], 128, 3, avg_neighbors=42.0)
