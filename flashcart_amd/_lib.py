@@ -69,6 +69,7 @@ _SIGNATURES = {
     "fc_irreps_dbwd": (c_int, [c_i64, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "fc_radial_fwd": (c_int, [ctypes.POINTER(RadialDesc), c_i64, c_vp, c_vp, c_vp, c_vp]),
     "fc_radial_bwd": (c_int, [ctypes.POINTER(RadialDesc), c_i64, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "fc_shift_vectors": (c_int, [c_i64, c_i32, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp]),
     "fc_edge_geometry_fwd": (c_int, [ctypes.POINTER(EdgeDesc), c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "fc_edge_geometry_bwd": (c_int, [ctypes.POINTER(EdgeDesc), c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "fc_edge_geometry_dbwd": (c_int, [ctypes.POINTER(EdgeDesc), c_i64] + [c_vp] * 14),

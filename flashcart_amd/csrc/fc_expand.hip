@@ -519,6 +519,39 @@ int launch_edge_bwd(const RadialParams& p, int64_t n, const float* pos, const fl
   return FC_OK;
 }
 
+// x as an opaque value: the library builds with -ffp-contract=fast (pragmas ignored), and a
+// product passed through here cannot be fused into an FMA with the sum that takes it.
+__device__ __forceinline__ float rounded(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// Periodic translation of each edge, one thread per edge: out[e] = (S0 a + S1 b) + S2 c with
+// (a, b, c) the rows of the edge's cell, each product and sum rounded on its own (no contraction),
+// so the translation of -S is the exact negation of that of S. A structure index outside
+// [0, n_cells) or a receiver outside [0, n_nodes) gives NaN rows.
+__global__ void shift_vectors_kernel(int64_t n, int n_cells, const int64_t* __restrict__ shifts,
+                                     const float* __restrict__ cell, const int32_t* __restrict__ idx_i,
+                                     const int32_t* __restrict__ batch, int64_t n_nodes, float* __restrict__ out) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n) return;
+  int b = 0;
+  if (n_cells > 1) {
+    const int32_t i = idx_i[e];
+    b = (i >= 0 && i < n_nodes) ? batch[i] : -1;
+  }
+  const float s0 = (float)shifts[3 * e], s1 = (float)shifts[3 * e + 1], s2 = (float)shifts[3 * e + 2];
+  float* o = out + 3 * e;
+  if (b < 0 || b >= n_cells) {
+    o[0] = o[1] = o[2] = __builtin_nanf("");
+    return;
+  }
+  const float* c = cell + 9 * (int64_t)b;
+#pragma unroll
+  for (int k = 0; k < 3; ++k)
+    o[k] = (rounded(s0 * c[k]) + rounded(s1 * c[3 + k])) + rounded(s2 * c[6 + k]);
+}
+
 }  // namespace fc
 
 using namespace fc;
@@ -633,6 +666,20 @@ extern "C" int fc_edge_geometry_dbwd(const fc_edge_desc* desc, int64_t n, const 
     case 3: FC_EDGE_DBWD(3); break;
   }
 #undef FC_EDGE_DBWD
+  FC_LAUNCH_CHECK();
+  return FC_OK;
+}
+
+extern "C" int fc_shift_vectors(int64_t n_edges, int32_t n_cells, const int64_t* shifts, const float* cell,
+                                const int32_t* idx_i, const int32_t* batch, int64_t n_nodes, float* out,
+                                void* stream) {
+  if (n_edges < 0 || n_cells < 1 || n_nodes < 0) return FC_ERR_SHAPE;
+  if (n_edges == 0) return FC_OK;
+  if (!shifts || !cell || !out) return FC_ERR_NULL;
+  if (n_cells > 1 && (!idx_i || !batch)) return FC_ERR_NULL;
+  const int bs = 256;
+  hipLaunchKernelGGL(shift_vectors_kernel, dim3((unsigned)((n_edges + bs - 1) / bs)), dim3(bs), 0,
+                     (hipStream_t)stream, n_edges, n_cells, shifts, cell, idx_i, batch, n_nodes, out);
   FC_LAUNCH_CHECK();
   return FC_OK;
 }

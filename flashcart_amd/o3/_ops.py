@@ -275,6 +275,31 @@ def _edge_desc(l_max, basis, n_radial, r_min, r_max, poly_order):
     return _lib.EdgeDesc(int(l_max), _lib.radial_desc(basis, n_radial, r_min, r_max, poly_order))
 
 
+def shift_vectors(cell: Tensor, shifts: Tensor, idx_i: Optional[Tensor], batch: Optional[Tensor]) -> Tensor:
+    """Translation S . cell[batch[idx_i]] of every edge (``fc_shift_vectors``; reference
+    ``utils/geometry.py:52``): each product and sum rounded on its own, so -S gives exactly the
+    negated translation. No gradient: for a cell that is differentiated, form it with tensor ops.
+    ``idx_i`` and ``batch`` are read only for several cells."""
+    c = _lib.contig("cell", cell)
+    if c.dim() != 3 or tuple(c.shape[1:]) != (3, 3):
+        raise ValueError(f"cell must be (n_cells, 3, 3), got {tuple(c.shape)}.")
+    if not shifts.is_cuda or shifts.device != c.device:
+        raise RuntimeError(f"`shifts` must be on {c.device}, got {shifts.device}.")
+    if shifts.dim() != 2 or shifts.shape[1] != 3:
+        raise ValueError(f"shifts must be (n_edges, 3), got {tuple(shifts.shape)}.")
+    sh = shifts if shifts.dtype == torch.int64 else shifts.to(torch.int64)
+    sh = sh.contiguous()
+    n_cells = int(c.shape[0])
+    ii = _i32("idx_i", idx_i) if n_cells > 1 else None
+    bb = _i32("batch", batch) if n_cells > 1 else None
+    if n_cells > 1 and (ii is None or bb is None or ii.shape[0] != sh.shape[0]):
+        raise ValueError("several cells need idx_i (one per edge) and batch.")
+    out = torch.empty(sh.shape[0], 3, dtype=torch.float32, device=c.device)
+    _lib_call("fc_shift_vectors", sh.shape[0], n_cells, sh.data_ptr(), c.data_ptr(), _lib.ptr(ii),
+              _lib.ptr(bb), 0 if bb is None else bb.shape[0], out.data_ptr(), _lib.stream_of(c))
+    return out
+
+
 @torch.library.custom_op("flashcart::edge_geometry", mutates_args=())
 def edge_geometry(positions: Optional[Tensor], shift_vec: Optional[Tensor], idx_i: Tensor, idx_j: Tensor,
                   vectors: Optional[Tensor], rowptr: Optional[Tensor], sender_perm: Optional[Tensor],

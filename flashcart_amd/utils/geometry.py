@@ -24,11 +24,16 @@ def shift_vectors(cell: torch.Tensor, shifts: torch.Tensor, idx_i: torch.Tensor,
     ``antisymmetric``: the per-edge sums also for one structure, each element evaluated as
     (s0 c0 + s1 c1) + s2 c2 with one rounding per operation, so the translation of -S is the
     exact negation of that of S (a library matrix product does not promise one summation
-    order for all rows).
+    order for all rows). The per-edge sums run as one kernel (``fc_shift_vectors``) for a
+    float32 device cell that is not differentiated.
     """
-    s = shifts.to(cell.dtype)
     if cell.shape[0] == 1 and not antisymmetric:
-        return s @ cell[0]
+        return shifts.to(cell.dtype) @ cell[0]
+    if cell.is_cuda and cell.dtype == torch.float32 and not shifts.is_floating_point() and \
+            not (torch.is_grad_enabled() and cell.requires_grad):
+        from flashcart_amd.o3 import _ops
+        return _ops.shift_vectors(cell, shifts, idx_i, batch)  # the expression below in one kernel
+    s = shifts.to(cell.dtype)
     c = cell[0].unsqueeze(0) if cell.shape[0] == 1 else cell[batch[idx_i]]
     return s[:, 0:1] * c[:, 0] + s[:, 1:2] * c[:, 1] + s[:, 2:3] * c[:, 2]
 

@@ -96,6 +96,15 @@ typedef struct fc_edge_desc {
   fc_radial_desc radial;     /* basis and cutoff */
 } fc_edge_desc;
 
+/* Periodic translation of every edge (reference src/flashcart/utils/geometry.py:52,
+ * shifts @ cell[batch[idx_i]]): out[e, k] = (S0 cell[b][0][k] + S1 cell[b][1][k]) + S2 cell[b][2][k],
+ * b = 0 for one cell, else batch[idx_i[e]]; each product and sum rounded on its own, so the
+ * translation of -S is exactly the negation of that of S. shifts (n_edges, 3) int64, cell
+ * (n_cells, 3, 3) row-major, out (n_edges, 3). idx_i (n_edges) and batch (n_nodes) are read only
+ * when n_cells > 1; an index out of range gives a NaN row. */
+int fc_shift_vectors(int64_t n_edges, int32_t n_cells, const int64_t* shifts, const float* cell,
+                     const int32_t* idx_i, const int32_t* batch, int64_t n_nodes, float* out, void* stream);
+
 int fc_edge_geometry_fwd(const fc_edge_desc* desc, int64_t n_edges, const float* pos,
                          const float* shift_vec, const int32_t* idx_i, const int32_t* idx_j,
                          const float* vectors, float* attrs, float* feats, float* env,

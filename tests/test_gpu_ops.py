@@ -509,3 +509,41 @@ def test_irreps_dbwd_op():
         want_g, want_x = torch.autograd.grad((gx * v).sum(), [gd, ud], allow_unused=True)
         _close(d_g, want_g, f"irreps_dbwd d_grad_output l={l_max}")
         _close(d_x, torch.zeros_like(ud) if want_x is None else want_x, f"irreps_dbwd d_x l={l_max}")
+
+
+def test_shift_vectors_kernel():
+    """fc_shift_vectors against the tensor-op sums it replaces, bit for bit: one cell and several
+    cells; the translation of -S is the exact negation of that of S; a structure index out of range
+    gives NaN rows; a differentiated cell keeps the tensor ops (and its gradient)."""
+    from flashcart_amd.o3 import _ops
+    from flashcart_amd.utils.geometry import shift_vectors
+
+    def torch_sums(cell, shifts, idx_i, batch):
+        s = shifts.to(cell.dtype)
+        c = cell[0].unsqueeze(0) if cell.shape[0] == 1 else cell[batch[idx_i]]
+        return s[:, 0:1] * c[:, 0] + s[:, 1:2] * c[:, 1] + s[:, 2:3] * c[:, 2]
+
+    g = torch.Generator().manual_seed(11)
+    n_nodes, n_edges = 300, 5000
+    shifts = torch.randint(-3, 4, (n_edges, 3), generator=g)
+    idx_i = torch.randint(0, n_nodes, (n_edges,), generator=g)
+    batch = torch.sort(torch.randint(0, 4, (n_nodes,), generator=g)).values
+    for n_cells in (1, 4):
+        cell = (torch.randn(n_cells, 3, 3, generator=g) * 4.0 + 7.0 * torch.eye(3)).to(DEV)
+        args = (shifts.to(DEV), idx_i.to(DEV), batch.to(DEV))
+        print(f"shift vectors: {n_cells} cells, {n_edges} edges", flush=True)
+        got = _ops.shift_vectors(cell, args[0], args[1], args[2])
+        assert torch.equal(got, torch_sums(cell, *args))
+        assert torch.equal(shift_vectors(cell, args[0], args[1], args[2], antisymmetric=True), got)
+        assert torch.equal(_ops.shift_vectors(cell, -args[0], args[1], args[2]), -got)
+    bad = batch.clone()
+    bad[int(idx_i[7])] = 9
+    got = _ops.shift_vectors(cell, shifts.to(DEV), idx_i.to(DEV), bad.to(DEV))
+    rows = (bad[idx_i] == 9).to(DEV)
+    assert torch.isnan(got[rows]).all() and not torch.isnan(got[~rows]).any()
+    assert _ops.shift_vectors(cell[:1], shifts[:0].to(DEV), None, None).shape == (0, 3)
+    # a differentiated cell: tensor ops, with the cell gradient
+    cg = cell.clone().requires_grad_(True)
+    sv = shift_vectors(cg, shifts.to(DEV), idx_i.to(DEV), batch.to(DEV), antisymmetric=True)
+    assert sv.grad_fn is not None and torch.equal(sv.detach(), torch_sums(cell, shifts.to(DEV), idx_i.to(DEV),
+                                                                          batch.to(DEV)))
