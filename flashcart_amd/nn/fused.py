@@ -308,9 +308,9 @@ class _EntryMaps(torch.autograd.Function):
         g = layer.linear_first.input_grad(gh.contiguous()) if gh is not None else None
         if gr is not None:
             g = layer.skip_projection.input_grad(gr.contiguous(), residual=g)
-        if g is None:
-            return None, None, None
-        if gs is not None:
+        if g is None and gs is not None:
+            g = gs.new_zeros(gs.shape[0], layer.linear_first.in_dim)
+        if g is not None and gs is not None:
             g[:, : ctx.n_read] += gs
         return g, None, None
 
