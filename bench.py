@@ -76,8 +76,6 @@ def tp_conv_bwd_bytes(n_nodes, E, d1, d2, P, C, nout):
     return 4 * (n_nodes * nout * C + 2 * n_nodes * d1 * C + 2 * E * d2 + 2 * E * P * C) + 8 * E + 4 * (n_nodes + 1)
 
 
-TRAFFIC_ALG_FWD = tp_conv_bytes(25000, 25000, TRAFFIC_E, 9, 16, 17, 128, 71)
-TRAFFIC_ALG_BWD = tp_conv_bwd_bytes(25000, TRAFFIC_E, 9, 16, 17, 128, 71)
 
 
 def device_time_ms(fn, reps, dev, warmup=3):
@@ -355,11 +353,49 @@ def _cpu_rate(fn, units, budget_s=8.0):
     return units * calls / dt, cores, calls, dt
 
 
-def config_line(name, dev, steps, warmup, cpu):
+MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 MFMA
+
+
+def mfma_in_step(step, dev):
+    """In-step MFMA utilisation of the linear maps: ``step()`` (one energy+forces evaluation, run
+    eagerly) under ``_ops.mfma_timer``, which brackets every MFMA kernel launch of the step with HIP
+    events on its stream; achieved = the launches' algorithmic FLOPs (by formula from each call's
+    shapes) / the sum of their event durations, per family and overall, against the fp32 MFMA peak."""
+    from flashcart_amd.o3 import _ops
+    with _ops.mfma_timer() as rec:
+        step()
+    torch.cuda.synchronize(dev)
+    groups = {}
+    for name, group, flops, e0, e1 in rec:
+        ms = e0.elapsed_time(e1)
+        g = groups.setdefault(group, {"launches": 0, "flops": 0.0, "ms": 0.0})
+        g["launches"] += 1
+        g["flops"] += flops
+        g["ms"] += ms
+    tot_f = sum(g["flops"] for g in groups.values())
+    tot_ms = sum(g["ms"] for g in groups.values())
+    for g in groups.values():
+        g["tflops"] = g["flops"] / (g["ms"] * 1e-3) / 1e12
+        g["frac"] = g["tflops"] / MFMA_PEAK_TFLOPS
+    achieved = tot_f / (tot_ms * 1e-3) / 1e12 if tot_ms > 0 else 0.0
+    return {"bound": "mfma", "kernel": "every MFMA launch of one step (equivariant linear maps, dense layers, "
+                                       "radial MLP)",
+            "achieved": achieved, "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": achieved / MFMA_PEAK_TFLOPS,
+            "flops_per_step": tot_f, "ms_per_step": tot_ms, "launches": sum(g["launches"] for g in groups.values()),
+            "groups": groups,
+            "method": "HIP events around each MFMA launch inside one eager energy+forces step (the stream the "
+                      "kernels run on); FLOPs from each call's shapes: 2 n (2l+1) C_in paths_l C_out per rank for "
+                      "the equivariant maps, 2 n k m for dense layers, each layer for the radial MLP kernels"}
+
+
+def config_line(name, dev, steps, warmup, cpu, extras=True):
     """One BASELINE configuration other than the metric's: throughput from device time (HIP
     events around HIP-graph replays, so that host launch work is not counted), the roofline
     fraction of its tensor-product work on the compulsory bytes, and (``cpu``) the oracle on
-    the host cores on the same inputs or a stated sample."""
+    the host cores on the same inputs or a stated sample. ``extras=False`` (the kernel-trace
+    runs of the model configurations) times the replays only: no eager timing, no separate
+    launches of the dominant kernels, no MFMA event run, so that the trace holds exactly the
+    kernels of the timed path."""
     from flashcart_amd import o3
     from flashcart_amd.data import AtomicGraph, batch_graphs
     from flashcart_amd.data.synthetic import model_config, molecules, water_box
@@ -466,7 +502,7 @@ def config_line(name, dev, steps, warmup, cpu):
             q.requires_grad_(False)
         model = model.to(dev)
         gdev = graph.to(dev)
-        dt_eager, _ = _timed(lambda: model.predict(gdev, compute_forces=True), steps, warmup, dev)
+        dt_eager = _timed(lambda: model.predict(gdev, compute_forces=True), steps, warmup, dev)[0] if extras else None
         # fixed topology: the whole prediction replayed as one HIP graph (predict(use_compile=True))
         for _ in range(warmup):
             model.predict(gdev, compute_forces=True, use_compile=True)
@@ -481,19 +517,24 @@ def config_line(name, dev, steps, warmup, cpu):
         ms = ev0.elapsed_time(ev1) / steps
         if not bool(torch.isfinite(out["energy"]).all()):
             raise RuntimeError(f"{name}: non-finite energy")
-        f_ms, f_b, b_ms, b_b, _ = measure_dominant(model, gdev, dev, with_backward=True)
         res.update({"metric": "atom-steps/s (energy+forces)", "value": n_atoms / (ms * 1e-3), "unit": "atom-steps/s",
-                    "ms_per_step": ms, "mode": "HIP graph replay of predict (use_compile=True)",
-                    "eager": {"value": n_atoms * steps / dt_eager, "ms_per_step": 1e3 * dt_eager / steps},
+                    "ms_per_step": ms, "mode": "HIP graph replay of predict (use_compile=True), frozen parameters",
                     "config": {"n_atoms": n_atoms, "n_graphs": graph.num_graphs,
-                               "n_edges": int(graph.edge_index.shape[1]), "channels": C, "l_max_edge_attrs": L},
-                    "roofline": {"bound": "hbm", "kernel": "layer-1 TP convolution forward", "algorithmic_bytes": f_b,
-                                 "avg_launch_ms": f_ms, "achieved": f_b / (f_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS,
-                                 "unit": "GB/s", "frac": f_b / (f_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
-                    "roofline_tp_bwd": {"bound": "hbm", "kernel": "layer-1 TP convolution backward op",
-                                        "algorithmic_bytes": b_b, "avg_launch_ms": b_ms,
-                                        "achieved": b_b / (b_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                        "frac": b_b / (b_ms * 1e-3) / 1e9 / HBM_PEAK_GBS}})
+                               "n_edges": int(graph.edge_index.shape[1]), "channels": C, "l_max_edge_attrs": L}})
+        if extras:
+            f_ms, f_b, b_ms, b_b, _ = measure_dominant(model, gdev, dev, with_backward=True)
+            res.update({
+                "eager": {"value": n_atoms * steps / dt_eager, "ms_per_step": 1e3 * dt_eager / steps},
+                "roofline": {"bound": "hbm", "kernel": "layer-1 TP convolution backward op (tp_bwd_conv_kernel + "
+                                                       "segment_rows_kernel)",
+                             "algorithmic_bytes": b_b, "avg_launch_ms": b_ms,
+                             "achieved": b_b / (b_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": b_b / (b_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
+                "roofline_tp_fwd": {"bound": "hbm", "kernel": "layer-1 TP convolution forward", "algorithmic_bytes": f_b,
+                                    "avg_launch_ms": f_ms, "achieved": f_b / (f_ms * 1e-3) / 1e9,
+                                    "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                    "frac": f_b / (f_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
+                "roofline_linear": mfma_in_step(lambda: model.predict(gdev, compute_forces=True), dev)})
         if cpu:
             sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
             rate, cores, calls, cdt = _oracle_rate(sd, model.to_model_config(), oracle_graph.to_dict(),
@@ -515,7 +556,8 @@ def run_other_workload(name, args, dev):
     res = {"workload": name, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "dtype": "f32",
            "data": "synthetic (seeded)"}
     if name in CONFIG_LINES:
-        res.update(config_line(name, dev, args.steps, args.warmup, not args.no_cpu_baseline))
+        res.update(config_line(name, dev, args.steps, args.warmup, not args.no_cpu_baseline,
+                               extras=not args.trace_timed))
     elif name.startswith("train_"):
         run_training(name, args, dev, res)
     elif name == "lammps_fcc25k":
@@ -673,6 +715,10 @@ def main():
     ap.add_argument("--power", action="store_true",
                     help="socket power (amd-smi) of the step's heavy ops, each looping alone for 4 s, and of "
                          "the energy+forces step")
+    ap.add_argument("--trace-timed", action="store_true",
+                    help="with --workload cfg3_water_1536 / cfg5_molecules_512: time the graph replays only (no "
+                         "eager timing, no separate dominant-kernel launches, no MFMA event step), for kernel traces "
+                         "that hold exactly the timed path")
     ap.add_argument("--no-configs", action="store_true",
                     help="measure only the metric's configuration (no lines for the other BASELINE configurations)")
     args = ap.parse_args()
@@ -742,11 +788,16 @@ def main():
     if not (np.isfinite(e) and np.isfinite(fmax)):
         raise RuntimeError("non-finite energy or forces")
     log(f"{args.steps} steps in {dt:.3f}s ({1e3 * dt / args.steps:.3f} ms/step); E={e:.6f} |F|max={fmax:.4f}")
-    ms, byts, ms_b, byts_b, dom = measure_dominant(model, graphs[-1], dev, with_backward=True)
+    # the TP ops on the first step graph: the graph `bench.py --kernel-only` builds for the counter
+    # runs whose HBM bytes are the lines' `traffic` (same positions, same edge list)
+    ms, byts, ms_b, byts_b, dom = measure_dominant(model, graphs[0], dev, with_backward=True)
     gbs = byts / (ms * 1e-3) / 1e9
     gbs_b = byts_b / (ms_b * 1e-3) / 1e9
     log(f"tp_fwd conv (layer 1): {ms:.3f} ms/launch, {byts / 1e9:.3f} GB algorithmic, {gbs:.1f} GB/s; "
         f"backward op: {ms_b:.3f} ms, {byts_b / 1e9:.3f} GB, {gbs_b:.1f} GB/s")
+    mfma = mfma_in_step(lambda: model.predict(graphs[0], compute_forces=True), dev)
+    log(f"MFMA launches in one step: {mfma['launches']}, {mfma['flops_per_step'] / 1e9:.1f} GFLOP in "
+        f"{mfma['ms_per_step']:.3f} ms = {mfma['achieved']:.1f} TFLOP/s ({mfma['frac']:.3f} of peak)")
     result = {
         "metric": "atom-steps/s (energy+forces) at 25k atoms L_max=3",
         "value": n_atoms * args.steps / dt,
@@ -763,28 +814,34 @@ def main():
         "config": {"workload": "fcc_alloy_25k_L3_C128_energy_forces", "n_atoms": n_atoms,
                    "mean_edges": float(np.mean(n_edges)), "channels": 128, "l_max_edge_attrs": 3,
                    "l_max_hidden_feats": 2, "n_interactions": 2, "r_max": R_MAX, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": "tp_fwd_kernel<2,3,3> (conv, layer 1)", "achieved": gbs,
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
-                     "traffic": MEASURED_TRAFFIC_BYTES, "traffic_launch": f"bench.py --kernel-only (E={TRAFFIC_E})",
-                     "traffic_over_algorithmic": MEASURED_TRAFFIC_BYTES / TRAFFIC_ALG_FWD,
-                     "algorithmic_bytes": byts, "avg_launch_ms": ms,
-                     "weight_rows": dom["weight_rows"], "edges": dom["edges"],
-                     "distinct_bytes": dom["distinct_bytes_fwd"],
-                     "distinct_frac": dom["distinct_bytes_fwd"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                     "note": "the north star's TP kernel as the step runs it: the two edges of a pair read one "
-                             "weight row; algorithmic_bytes count a row per edge (the survey's formula), "
-                             "distinct_bytes each row once. By time the layer-1 backward dominates the step "
-                             "(roofline_tp_bwd)"},
-        # the step's largest TP kernel by time: the layer-1 TP backward op (backward kernel + the
+        # the step's largest kernel by time: the layer-1 TP backward op (the backward kernel + the
         # sender-ordered sum of its per-edge messages), on the compulsory bytes of its three gradients
-        "roofline_tp_bwd": {"bound": "hbm", "kernel": "tp_bwd_conv_kernel<2,3,3> + segment_rows_kernel (layer 1)",
-                            "achieved": gbs_b, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs_b / HBM_PEAK_GBS,
-                            "traffic": MEASURED_TRAFFIC_BWD_BYTES,
-                            "traffic_launch": f"bench.py --kernel-only (E={TRAFFIC_E})",
-                            "traffic_over_algorithmic": MEASURED_TRAFFIC_BWD_BYTES / TRAFFIC_ALG_BWD,
-                            "algorithmic_bytes": byts_b, "avg_launch_ms": ms_b,
-                            "distinct_bytes": dom["distinct_bytes_bwd"],
-                            "distinct_frac": dom["distinct_bytes_bwd"] / (ms_b * 1e-3) / 1e9 / HBM_PEAK_GBS},
+        "roofline": {"bound": "hbm", "kernel": "tp_bwd_conv_kernel<2,3,3> + segment_rows_kernel (layer-1 TP "
+                                                "convolution backward op)",
+                     "achieved": gbs_b, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs_b / HBM_PEAK_GBS,
+                     "traffic": MEASURED_TRAFFIC_BWD_BYTES,
+                     "traffic_graph": f"first step graph, E={dom['edges']} (measured on E={TRAFFIC_E} by "
+                                      "bench.py --kernel-only, which builds the same graph)",
+                     "traffic_over_algorithmic": MEASURED_TRAFFIC_BWD_BYTES / byts_b,
+                     "algorithmic_bytes": byts_b, "avg_launch_ms": ms_b, "edges": dom["edges"],
+                     "weight_rows": dom["weight_rows"],
+                     "distinct_bytes": dom["distinct_bytes_bwd"],
+                     "distinct_frac": dom["distinct_bytes_bwd"] / (ms_b * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                     "note": "the step's largest TP kernel by time; algorithmic_bytes = the survey's compulsory "
+                             "per-edge formula (weights read and their gradient written per edge); distinct_bytes "
+                             "count each pair's shared weight row once"},
+        # the north star's TP forward kernel as the step runs it (the two edges of a pair read one
+        # weight row)
+        "roofline_tp_fwd": {"bound": "hbm", "kernel": "tp_fwd_kernel<2,3,3> (conv, layer 1)", "achieved": gbs,
+                            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
+                            "traffic": MEASURED_TRAFFIC_BYTES,
+                            "traffic_graph": f"first step graph, E={dom['edges']} (measured on E={TRAFFIC_E})",
+                            "traffic_over_algorithmic": MEASURED_TRAFFIC_BYTES / byts,
+                            "algorithmic_bytes": byts, "avg_launch_ms": ms,
+                            "distinct_bytes": dom["distinct_bytes_fwd"],
+                            "distinct_frac": dom["distinct_bytes_fwd"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
+        # in-step MFMA utilisation of the equivariant linear maps, dense layers and radial MLP
+        "roofline_linear": mfma,
         "energy": e,
     }
     if not args.no_configs:

@@ -44,6 +44,7 @@ class TPDesc(ctypes.Structure):
         ("in1_l_max", c_i32), ("in2_l_max", c_i32), ("out_l_max", c_i32),
         ("in1_features", c_i32), ("in2_features", c_i32),
         ("symmetric_product", c_i32), ("shared_weights", c_i32), ("reduce_paths", c_i32),
+        ("alpha_div", c_vp),
     ]
 
 
@@ -207,9 +208,12 @@ def rows_empty(like: torch.Tensor, rows: int, *cols: int, dtype: Optional[torch.
     return like.new_empty((rounded_rows(rows), *cols), dtype=dtype)[:rows]
 
 
-def tp_desc(in1_l_max, in2_l_max, out_l_max, in1_features, in2_features, symmetric, shared, reduced) -> TPDesc:
+def tp_desc(in1_l_max, in2_l_max, out_l_max, in1_features, in2_features, symmetric, shared, reduced,
+            alpha_div: Optional[torch.Tensor] = None) -> TPDesc:
+    """``alpha_div``: optional one-element float32 device tensor s; the kernels then scale by
+    alpha / s, reading s on the device."""
     return TPDesc(int(in1_l_max), int(in2_l_max), int(out_l_max), int(in1_features), int(in2_features),
-                  int(bool(symmetric)), int(bool(shared)), int(bool(reduced)))
+                  int(bool(symmetric)), int(bool(shared)), int(bool(reduced)), ptr(alpha_div))
 
 
 def linear_desc(in_l_max: int, out_l_max: int, in_features: int, out_features: int,

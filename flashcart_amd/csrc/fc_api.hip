@@ -56,6 +56,7 @@ static TPArgs make_args(const fc_tp_desc* d, int64_t n_rows) {
   g.shared_w = d->shared_weights;
   g.reduced = d->reduce_paths;
   g.alpha = 1.0f;
+  g.alpha_div = d->alpha_div;
   return g;
 }
 

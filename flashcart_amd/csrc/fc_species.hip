@@ -60,7 +60,7 @@ __global__ void __launch_bounds__(256) species_density_fwd_kernel(int64_t n_rows
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       hk[u] = 0.f;
-      if ((z[u] & 3) == wave && z[u] < 4 * ZW) hk[u] = h[(int64_t)(sl[u] >> 1) * kHid + k];
+      if ((z[u] & 3) == wave && z[u] < 4 * ZW && sl[u] >= 0) hk[u] = h[(int64_t)(sl[u] >> 1) * kHid + k];
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -151,7 +151,7 @@ __global__ void __launch_bounds__(256) species_density_bwd_kernel(int64_t n_rows
       for (int c = 0; c < D; ++c) yv[u][c] = y[(int64_t)e * y_stride + c];
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) hk[u] = h[(int64_t)(sl[u] >> 1) * kHid + lane];
+    for (int u = 0; u < U; ++u) hk[u] = sl[u] >= 0 ? h[(int64_t)(sl[u] >> 1) * kHid + lane] : 0.f;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int32_t e = b + 4 * u;
@@ -168,7 +168,7 @@ __global__ void __launch_bounds__(256) species_density_bwd_kernel(int64_t n_rows
           gyv[c] = a * hk[u];
         }
       }
-      g_h[(int64_t)sl[u] * kHid + lane] = gh;
+      if (sl[u] >= 0) g_h[(int64_t)sl[u] * kHid + lane] = gh;  // an unpaired edge has no h row
       const float r = wave_reduce_n<R>(gyv, lane);
       const int v = lane >> SH;
       if ((lane & ((1 << SH) - 1)) == 0 && v < D) g_y[(int64_t)e * y_stride + v] = r;

@@ -36,6 +36,7 @@ struct TPArgs {
   int32_t F1, F2, C;       // in1 / in2 / output features (1 broadcasts)
   int32_t shared_w, reduced;
   float alpha;             // output scale (fwd) / its transpose (bwd)
+  const float* alpha_div;  // optional device scalar s: the scale is alpha / s
   // rows backward only: gradients added to grad_in1 / grad_in2 (leading res*_comps
   // components of each row, row width res*_comps * C; may alias the gradient)
   const float* res1;
@@ -53,7 +54,14 @@ struct TPConfig {
   static constexpr int NOUT_RED = PL::NOUT_RED;
 };
 
-// Weight row of edge e (the pair's row when edges share weights).
+// Output scale: alpha, divided by the device scalar *alpha_div when one is given (read once per
+// workgroup; the divisor's storage is the caller's, e.g. a module buffer).
+__device__ __forceinline__ float scale_of(const TPArgs& g) {
+  return g.alpha_div ? g.alpha / *g.alpha_div : g.alpha;
+}
+
+// Weight row of edge e (the pair's row when edges share weights); negative for an edge that a
+// pairing left without a partner (slot -1), whose weights then count as zero.
 __device__ __forceinline__ int64_t weight_row(const TPArgs& g, int64_t e) {
   return g.wslot ? (int64_t)(g.wslot[e] >> 1) : e;
 }
@@ -80,7 +88,13 @@ __device__ __forceinline__ void load_edge(const TPArgs& g, int64_t e, int f1, in
 #pragma unroll
     for (int u = 0; u < D2; ++u) o.y[u] = active ? g.in2[e * s2 + u * g.F2 + f2] : 0.f;
   }
-  const float* wr = g.shared_w ? g.w : g.w + weight_row(g, e) * (int64_t)NP * g.C;
+  const int64_t wrow = g.shared_w ? 0 : weight_row(g, e);
+  if (wrow < 0) {  // uniform over the workgroup
+#pragma unroll
+    for (int i = 0; i < NP; ++i) o.w[i] = 0.f;
+    return;
+  }
+  const float* wr = g.w + wrow * (int64_t)NP * g.C;
 #pragma unroll
   for (int i = 0; i < NP; ++i) o.w[i] = active ? wr[i * g.C + fw] : 0.f;
 }
@@ -171,8 +185,9 @@ __global__ void __launch_bounds__(256) tp_fwd_kernel(TPArgs g) {
   }
   if (!g.reduced) {
     float* o = g.out + row * (int64_t)NOUT * C + f;
+    const float alpha = scale_of(g);
 #pragma unroll
-    for (int k = 0; k < NOUT; ++k) o[(int64_t)k * C] = g.alpha * acc[k];
+    for (int k = 0; k < NOUT; ++k) o[(int64_t)k * C] = alpha * acc[k];
   } else {
     constexpr int NR = CF::NOUT_RED;
     float red[NR];
@@ -185,8 +200,9 @@ __global__ void __launch_bounds__(256) tp_fwd_kernel(TPArgs g) {
       for (int a = 0; a < 2 * P.lo + 1; ++a) red[PL::out_index_red(i, a)] += acc[PL::out_index(i, a)];
     });
     float* o = g.out + row * (int64_t)NR * C + f;
+    const float alpha = scale_of(g);
 #pragma unroll
-    for (int k = 0; k < NR; ++k) o[(int64_t)k * C] = g.alpha * red[k];
+    for (int k = 0; k < NR; ++k) o[(int64_t)k * C] = alpha * red[k];
   }
 }
 
@@ -265,18 +281,19 @@ __global__ void __launch_bounds__(256, 2) tp_bwd_kernel(TPArgs g) {
   // BC2 implies F2 == 1, so F1 == C there: in1 is never channel-reduced (compile-time,
   // which keeps the unused butterfly registers of gx out of the kernel).
   const bool red1 = !BC2 && need1 && g.F1 == 1 && C > 1, red2 = need2 && g.F2 == 1 && C > 1;
+  const float alpha = scale_of(g);
 
   float go[NOUT];
   if (!g.reduced) {
 #pragma unroll
     for (int k = 0; k < NOUT; ++k)
-      go[k] = active ? g.alpha * g.grad_out[row * (int64_t)NOUT * C + (int64_t)k * C + fa] : 0.f;
+      go[k] = active ? alpha * g.grad_out[row * (int64_t)NOUT * C + (int64_t)k * C + fa] : 0.f;
   } else {
     constexpr int NR = CF::NOUT_RED;
     float gr[NR];
 #pragma unroll
     for (int k = 0; k < NR; ++k)
-      gr[k] = active ? g.alpha * g.grad_out[row * (int64_t)NR * C + (int64_t)k * C + fa] : 0.f;
+      gr[k] = active ? alpha * g.grad_out[row * (int64_t)NR * C + (int64_t)k * C + fa] : 0.f;
     static_for<NP>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
       constexpr PathDesc P = PL::at(i);
@@ -431,16 +448,23 @@ __global__ void __launch_bounds__(C, 2) tp_bwd_conv_kernel(TPArgs g) {
   const int64_t e0 = g.rowptr[row], e1 = g.rowptr[row + 1];
   if (e0 >= e1) return;  // uniform over the workgroup: no barrier is skipped by a part of it
 
+  const float alpha = scale_of(g);
   float go[NOUT];
 #pragma unroll
-  for (int k = 0; k < NOUT; ++k) go[k] = g.alpha * g.grad_out[row * (int64_t)NOUT * C + (int64_t)k * C + f];
+  for (int k = 0; k < NOUT; ++k) go[k] = alpha * g.grad_out[row * (int64_t)NOUT * C + (int64_t)k * C + f];
 
   auto load = [&](int64_t e, EdgeOps<D1, D2, NP>& o) {
     const int64_t j = (int64_t)g.idx_j[e];
     const float* xr = g.in1 + j * S1 + f;
-    const float* wr = g.w + weight_row(g, e) * SW + f;
 #pragma unroll
     for (int u = 0; u < D1; ++u) o.x[u] = xr[u * C];
+    const int64_t wrow = weight_row(g, e);
+    if (wrow < 0) {  // uniform: an unpaired edge's weights count as zero
+#pragma unroll
+      for (int i = 0; i < NP; ++i) o.w[i] = 0.f;
+      return;
+    }
+    const float* wr = g.w + wrow * SW + f;
 #pragma unroll
     for (int i = 0; i < NP; ++i) o.w[i] = wr[i * C];
   };
@@ -537,6 +561,7 @@ __global__ void __launch_bounds__(256) tp_bwd_rows_kernel(TPArgs g) {
   const int C = g.C;
   if (f >= C || row >= g.n_rows) return;
   const bool need1 = g.grad_in1 != nullptr, need2 = g.grad_in2 != nullptr, needw = g.grad_w != nullptr;
+  const float alpha = scale_of(g);
   const float* gor = g.grad_out + row * (int64_t)NOUT * C + f;
   const float* wr = (g.shared_w ? g.w : g.w + row * (int64_t)NP * C) + f;
   float x[D1], y[D2], gx[D1], gy[D2];
@@ -551,7 +576,7 @@ __global__ void __launch_bounds__(256) tp_bwd_rows_kernel(TPArgs g) {
     const float* xp = x + P.r1 * P.r1;
     float go[T::NO];
 #pragma unroll
-    for (int a = 0; a < T::NO; ++a) go[a] = g.alpha * gor[(int64_t)PL::out_index(i, a) * C];
+    for (int a = 0; a < T::NO; ++a) go[a] = alpha * gor[(int64_t)PL::out_index(i, a) * C];
     const float w = wr[i * C];
     if (needw || need1) {  // v = A_p^T go_p: grad_w = <v, x>, gx += w v
       float A[T::NA], v[T::N1];

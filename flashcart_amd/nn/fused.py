@@ -19,6 +19,7 @@ again raises). Reference behaviour: ``nn/layers.py:538-652`` (gated update) and
 only the order of floating-point additions in the backward differs.
 """
 
+import collections
 import contextlib
 import threading
 from typing import List, Optional
@@ -30,6 +31,11 @@ from torch.autograd.function import once_differentiable
 from flashcart_amd.o3 import _ops
 
 _state = threading.local()
+
+# How often each fused path's forward ran (keys "paired", "species", "entry_maps", "product",
+# "gated"), for tests and diagnostics that must know which path an evaluation took; clear()
+# resets it. Under graph capture the count grows while capturing, not per replay.
+path_counts: "collections.Counter[str]" = collections.Counter()
 
 
 @contextlib.contextmanager
@@ -72,6 +78,7 @@ class _ProductBlock(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x: Tensor, layer) -> Tensor:
+        path_counts["product"] += 1
         K = layer.correlation
         out: Optional[Tensor] = None
         p = x
@@ -136,6 +143,7 @@ class _GatedBlock(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x: Tensor, layer) -> Tensor:
+        path_counts["gated"] += 1
         values = layer.value_linear(x)
         gl = layer.gate_linear
         act_gemm = 1 if layer.gate_activation_name == "silu" else 0
@@ -228,29 +236,30 @@ class _PairedConv(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, in1: Tensor, in2: Tensor, x: Tensor, layer, graph, pairs, alpha: float) -> Tensor:
+    def forward(ctx, in1: Tensor, in2: Tensor, x: Tensor, layer, graph, pairs, alpha_div: Tensor) -> Tensor:
+        path_counts["paired"] += 1
         slot = pairs.slot
         l0, l1, l2 = layer.radial_mlp[0], layer.radial_mlp[2], layer.radial_mlp[4]
         w = _ops.radial_mlp_fwd(x, l0.weight, l0._scale, l1.weight, l1._scale, l2.weight, l2._scale)
         tp = layer.tp
         out = _ops.tp_fwd(in1, in2, w, graph.idx_i, graph.idx_j, tp.in1_l_max, tp.in2_l_max, tp.out_l_max,
                           tp.in1_features, tp.in2_features, tp.symmetric_product, tp.shared_weights, *tp.op_meta,
-                          tp.reduce_paths, graph.rowptr, graph.sender_perm, graph.sender_ptr, float(alpha), slot)
-        ctx.save_for_backward(in1, in2, x, w, slot, pairs.edge, pairs.upper)
-        ctx.layer, ctx.graph, ctx.alpha = layer, graph, float(alpha)
+                          tp.reduce_paths, graph.rowptr, graph.sender_perm, graph.sender_ptr, 1.0, slot, alpha_div)
+        ctx.save_for_backward(in1, in2, x, w, slot, pairs.edge, pairs.upper, alpha_div)
+        ctx.layer, ctx.graph = layer, graph
         return out
 
     @staticmethod
     @once_differentiable
     def backward(ctx, g: Tensor):
-        in1, in2, x, w, slot, pairs_lo, pairs_hi = ctx.saved_tensors
+        in1, in2, x, w, slot, pairs_lo, pairs_hi, alpha_div = ctx.saved_tensors
         layer, graph = ctx.layer, ctx.graph
         n1, n2, nx = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[2]
         tp = layer.tp
         g1, g2, gw = _ops.tp_bwd(g.contiguous(), in1, in2, w, graph.idx_i, graph.idx_j, tp.in1_l_max, tp.in2_l_max,
                                  tp.out_l_max, tp.in1_features, tp.in2_features, tp.symmetric_product,
                                  tp.shared_weights, *tp.op_meta, tp.reduce_paths, bool(n1), bool(n2), bool(nx),
-                                 graph.rowptr, graph.sender_perm, graph.sender_ptr, ctx.alpha, slot)
+                                 graph.rowptr, graph.sender_perm, graph.sender_ptr, 1.0, slot, alpha_div)
         gx = None
         if nx:
             l0, l1, l2 = layer.radial_mlp[0], layer.radial_mlp[2], layer.radial_mlp[4]
@@ -295,6 +304,7 @@ class _EntryMaps(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x: Tensor, layer, n_read: int):
+        path_counts["entry_maps"] += 1
         h = layer.linear_first(x)
         r = layer.skip_projection(x)
         s = x[:, :n_read].contiguous()
@@ -335,33 +345,29 @@ def entry_maps(layer, x: Tensor, n_read: int):
     return _EntryMaps.apply(x, layer, n_read)
 
 
-def paired_conv(layer, in1: Tensor, in2: Tensor, x_pairs: Tensor, graph, pairs, alpha: float) -> Tensor:
-    return _PairedConv.apply(in1, in2, x_pairs, layer, graph, pairs, alpha)
+def paired_conv(layer, in1: Tensor, in2: Tensor, x_pairs: Tensor, graph, pairs, alpha_div: Tensor) -> Tensor:
+    """``alpha_div``: the one-element device tensor the convolution output is divided by (the
+    layer's ``sqrt_avg_neighbors``)."""
+    return _PairedConv.apply(in1, in2, x_pairs, layer, graph, pairs, alpha_div)
 
 
-def species_maps(layer, table: Tensor, alpha: float):
+def species_maps(layer, table: Tensor, alpha_div: Tensor):
     """Matrices and scales of the first interaction layer's species density, with its
-    ``linear_second`` folded in: per rank l, with x_table = linear_first(table) (the sender
-    features of each species),
+    ``linear_second`` folded in: per rank l, with x_table = linear_first(table) / s (the sender
+    features of each species, divided by the device scalar s = ``alpha_div``),
         M_l[o, Z * 64 + k] = sum_c Wsec_l[o, c] x_table[Z, c] W2[l C + c, k],
-        scale_l = alpha s2 s_l,
-    so that linear_second(TP(...))_l = scale_l dens_l @ M_l^T (the path (0, l, l) takes block l
-    of the radial output layer W2). Cached on the layer while the table, the parameters that
-    enter (linear_first, W2, linear_second) and alpha are unchanged: keyed by their storage and
-    in-place version counters (recomputed under graph capture, which then replays the
-    computation)."""
+        scale_l = s2 s_l,
+    so that linear_second(TP(...) / s)_l = scale_l dens_l @ M_l^T (the path (0, l, l) takes block l
+    of the radial output layer W2). Formed on the device at every call (a few small launches,
+    no host synchronisation) from the parameters as they are at that moment, so weights written
+    in place by any route (``param.data.copy_`` included, which no version counter records) are
+    always seen; under graph capture the computation is recorded and replayed."""
     tp, lin, w2 = layer.tp, layer.linear_second, layer.radial_mlp[4].weight
     c = tp.in1_features
     lm = min(tp.in2_l_max, tp.out_l_max)
     common = min(lm, lin.out_l_max)
-    srcs = [table, w2, *lin.parameters(), *layer.linear_first.parameters()]
-    key = tuple((t.data_ptr(), t._version) for t in srcs) + (float(alpha),)
-    capturing = torch.cuda.is_current_stream_capturing()
-    hit = layer.__dict__.get("_species_maps")
-    if not capturing and hit is not None and hit[0] == key:
-        return hit[1]
     with torch.no_grad():
-        x_table = layer.linear_first(table)
+        x_table = layer.linear_first(table) / alpha_div.detach().reshape(1, 1)
     n_sp = x_table.shape[0]
     mats = []
     for l in range(common + 1):
@@ -371,11 +377,8 @@ def species_maps(layer, table: Tensor, alpha: float):
         mats.append(m.contiguous())
     s2 = layer.radial_mlp[4]._scale
     cfg = (lm, lin.out_l_max, 64, lin.out_features, [n_sp] * (lm + 1),
-           [float(alpha) * s2 * lin._scale_list[l] for l in range(common + 1)])
-    out = (mats, cfg)
-    if not capturing:
-        layer.__dict__["_species_maps"] = (key, out)
-    return out
+           [s2 * lin._scale_list[l] for l in range(common + 1)])
+    return mats, cfg
 
 
 class _SpeciesConv(torch.autograd.Function):
@@ -391,7 +394,8 @@ class _SpeciesConv(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, y: Tensor, x_pairs: Tensor, layer, graph, pairs, edge_species: Tensor,
-                table: Tensor, alpha: float) -> Tensor:
+                table: Tensor, alpha_div: Tensor) -> Tensor:
+        path_counts["species"] += 1
         from flashcart_amd import _lib
         tp = layer.tp
         l0, l1 = layer.radial_mlp[0], layer.radial_mlp[2]
@@ -400,7 +404,7 @@ class _SpeciesConv(torch.autograd.Function):
         h = _ops.radial_mlp_hidden_fwd(x_pairs, l0.weight, l0._scale, l1.weight, l1._scale)
         csr = _lib.csr_struct(graph.n_nodes, graph.n_edges, graph.idx_j, graph.rowptr, pair_slot=pairs.slot)
         dens = _ops.species_density_fwd(csr, lm, tp.in2_l_max, n_sp, edge_species, h, y, graph.n_nodes)
-        mats, cfg = species_maps(layer, table, alpha)
+        mats, cfg = species_maps(layer, table, alpha_div)
         out = _ops.linear_fwd(dens, mats, *cfg)
         ctx.save_for_backward(y, x_pairs, h, edge_species, pairs.slot, *mats)
         ctx.layer, ctx.graph, ctx.cfg, ctx.n_sp = layer, graph, cfg, n_sp
@@ -448,7 +452,7 @@ def species_conv_applies(layer, node_feats: Tensor, n_species: int) -> bool:
 
 
 def species_conv(layer, edge_attrs: Tensor, x_pairs: Tensor, graph, pairs, edge_species: Tensor,
-                 table: Tensor, alpha: float) -> Tensor:
+                 table: Tensor, alpha_div: Tensor) -> Tensor:
     """``table``: the embedding rows of the species (the layer's sender features are
-    linear_first(table)[species])."""
-    return _SpeciesConv.apply(edge_attrs, x_pairs, layer, graph, pairs, edge_species, table, alpha)
+    linear_first(table)[species]); ``alpha_div``: the layer's ``sqrt_avg_neighbors``."""
+    return _SpeciesConv.apply(edge_attrs, x_pairs, layer, graph, pairs, edge_species, table, alpha_div)

@@ -137,8 +137,6 @@ class InteractionLayer(nn.Module):
             raise ValueError(f"avg_neighbors must be positive. Provided: {avg_neighbors}.")
         self.register_buffer("sqrt_avg_neighbors",
                              torch.tensor(float(avg_neighbors) ** 0.5, dtype=torch.get_default_dtype()))
-        self._alpha_key = None  # (storage, version) of the buffer that self._alpha was read from
-        self._alpha = 1.0
         self.out_dim = sum((2 * l + 1) * out_features for l in range(out_l_max + 1))
         out_paths, n_total_paths = o3.utils.count_output_paths(in1_l_max, in2_l_max, out_l_max)
         if n_elements is not None and element_features is None:
@@ -175,19 +173,9 @@ class InteractionLayer(nn.Module):
 
     @property
     def _sqrt_avg(self) -> float:
-        return 1.0 / self._inv_sqrt_avg()
-
-    def _inv_sqrt_avg(self) -> float:
-        """1 / sqrt_avg_neighbors for the TP kernel's output factor. The buffer is read again
-        (one device-to-host copy) only when it was replaced or written in place since the last
-        read: load_state_dict, set_avg_neighbors and the reference's broadcast_pre_fit_state
-        (``copy_``) all bump its version counter."""
-        buf = self.sqrt_avg_neighbors
-        key = (buf.data_ptr(), buf.device, buf._version)
-        if key != self._alpha_key:
-            self._alpha = 1.0 / float(buf.detach().float())
-            self._alpha_key = key
-        return self._alpha
+        """sqrt_avg_neighbors as a Python float (a host read; the kernels divide by the buffer on the
+        device, so the forward pass never needs this value)."""
+        return float(self.sqrt_avg_neighbors.detach().float())
 
     def forward(self, node_feats: torch.Tensor, edge_attrs: torch.Tensor, edge_feats: torch.Tensor,
                 edge_index: torch.Tensor, envelope: torch.Tensor, atom_types: Optional[torch.Tensor] = None,
@@ -219,12 +207,12 @@ class InteractionLayer(nn.Module):
             if species is not None and out_nodes is None and \
                     fused.species_conv_applies(self, node_feats, species[1].shape[0]):
                 mapped = fused.species_conv(self, edge_attrs, mlp_pairs, graph, edge_pairs, species[0],
-                                            species[1], self._inv_sqrt_avg())
+                                            species[1], self.sqrt_avg_neighbors)
                 return self._finish(mapped, residual_feats, out_nodes, mapped=True)
             else:
                 in1 = entry[0] if entry is not None else self.linear_first(node_feats)
                 aggregated = fused.paired_conv(self, in1, edge_attrs, mlp_pairs, graph, edge_pairs,
-                                               self._inv_sqrt_avg())
+                                               self.sqrt_avg_neighbors)
             return self._finish(aggregated, residual_feats, out_nodes, skip=entry[1] if entry is not None else None)
         if self.emb_i is not None:
             if atom_types is None:
@@ -239,7 +227,7 @@ class InteractionLayer(nn.Module):
         else:
             weights = run_mlp(self.radial_mlp, mlp_input)
         aggregated = self.tp(node_feats, edge_attrs, weights, idx_i, idx_j, graph=graph,
-                             alpha=self._inv_sqrt_avg())
+                             alpha_div=self.sqrt_avg_neighbors)
         return self._finish(aggregated, residual_feats, out_nodes)
 
     def _finish(self, aggregated: torch.Tensor, residual_feats: torch.Tensor,

@@ -14,6 +14,7 @@ raises otherwise; there is no CPU path.
 
 from __future__ import annotations
 
+import contextlib
 from typing import List, Optional, Tuple
 
 import torch
@@ -25,8 +26,59 @@ from flashcart_amd.o3 import _torch_math
 Tensor = torch.Tensor
 
 
+# MFMA entry points of the library and the algorithmic FLOPs of one call, from its arguments:
+# equivariant maps sum 2 n (2l+1) (C_in paths_l) C_out over the ranks both sides have; dense layers
+# 2 n k m; the pair-sum GEMM 2 P m k (after the pair sum); the radial MLP kernels count each layer
+# they run (the backward recomputes the two hidden layers, then multiplies back through both).
+def _linear_flops(args):
+    d, n = args[0], int(args[1])
+    lm = min(d.in_l_max, d.out_l_max)
+    return sum(2.0 * n * (2 * l + 1) * d.in_features * d.in_paths[l] * d.out_features for l in range(lm + 1))
+
+
+_MFMA_CALLS = {
+    "fc_linear_fwd": ("equivariant_linear", _linear_flops),
+    "fc_linear_dgrad": ("equivariant_linear", _linear_flops),
+    "fc_linear_wgrad": ("equivariant_linear", _linear_flops),
+    "fc_dense_fwd": ("dense", lambda a: 2.0 * a[0] * a[1] * a[2]),
+    "fc_dense_dgrad": ("dense", lambda a: 2.0 * a[0] * a[1] * a[2]),
+    "fc_dense_wgrad": ("dense", lambda a: 2.0 * a[0] * a[1] * a[2]),
+    "fc_dense_fwd_pairsum": ("dense", lambda a: 2.0 * a[0] * a[1] * a[2]),
+    "fc_radial_mlp_fwd": ("radial_mlp", lambda a: 2.0 * a[0] * (a[1] * 64 + 64 * 64 + 64 * a[7])),
+    "fc_radial_mlp_hidden_fwd": ("radial_mlp", lambda a: 2.0 * a[0] * (a[1] * 64 + 64 * 64)),
+    "fc_radial_mlp_bwd": ("radial_mlp", lambda a: 2.0 * a[0] * (2 * a[1] * 64 + 2 * 64 * 64)),
+    "fc_radial_mlp_bwd_pairsum": ("radial_mlp", lambda a: 2.0 * a[0] * (2 * a[1] * 64 + 2 * 64 * 64)),
+}
+_mfma_record: Optional[list] = None
+
+
+@contextlib.contextmanager
+def mfma_timer():
+    """Within the context, every launch of an MFMA kernel family of the library (equivariant
+    linear maps, dense layers, radial MLP) is bracketed by HIP events on the stream it runs on,
+    and (name, group, flops, start event, end event) is appended to the yielded list: the in-step
+    MFMA time and achieved FLOP/s of the linear maps (bench.py). Not during graph capture."""
+    global _mfma_record
+    prev, rec = _mfma_record, []
+    _mfma_record = rec
+    try:
+        yield rec
+    finally:
+        _mfma_record = prev
+
+
 def _lib_call(name: str, *args) -> None:
     lib = _lib.load()
+    rec = _mfma_record
+    if rec is not None and name in _MFMA_CALLS and not torch.cuda.is_current_stream_capturing():
+        group, flops = _MFMA_CALLS[name]
+        stream = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        _lib.check(getattr(lib, name)(*args), name)
+        e1.record(stream)
+        rec.append((name, group, float(flops(args)), e0, e1))
+        return
     _lib.check(getattr(lib, name)(*args), name)
 
 
@@ -416,6 +468,15 @@ _register_autograd(edge_geometry, _edge_backward, _edge_setup)
 # Tensor product
 # ---------------------------------------------------------------------------
 
+def _alpha_div(t: Optional[Tensor]) -> Optional[Tensor]:
+    """The divisor tensor of a tensor product: one float32 element on the device (contiguous)."""
+    if t is None:
+        return None
+    if t.numel() != 1:
+        raise ValueError(f"alpha_div must hold one element, got shape {tuple(t.shape)}.")
+    return _lib.contig("alpha_div", t.detach().reshape(1))
+
+
 def _tp_csr(in1: Tensor, idx_i: Tensor, idx_j: Tensor, rowptr: Optional[Tensor], sender_perm: Optional[Tensor],
             sender_ptr: Optional[Tensor], need_senders: bool, pair_slot: Optional[Tensor] = None):
     n = in1.shape[0]
@@ -467,11 +528,15 @@ def tp_fwd(in1: Tensor, in2: Tensor, weights: Tensor, idx_i: Optional[Tensor], i
            symmetric_product: bool, shared_weights: bool, in1_offs: List[int], in2_offs: List[int],
            out_sizes: List[int], n_paths_per_l: List[int], n_total_paths: int, reduce_paths: bool = False,
            rowptr: Optional[Tensor] = None, sender_perm: Optional[Tensor] = None,
-           sender_ptr: Optional[Tensor] = None, alpha: float = 1.0, pair_slot: Optional[Tensor] = None) -> Tensor:
+           sender_ptr: Optional[Tensor] = None, alpha: float = 1.0, pair_slot: Optional[Tensor] = None,
+           alpha_div: Optional[Tensor] = None) -> Tensor:
     """Reference schema (src/flashcart/o3/_tensor_product.py:332-352) plus optional CSR
     arrays (``rowptr``, ``sender_perm``, ``sender_ptr``, see ``o3._graph``), ``alpha``,
-    a scale applied to the output, and ``pair_slot`` (``o3._graph.EdgePairs.slot``): the two
-    edges of a pair read one weight row, so ``weights`` holds E / 2 rows."""
+    a scale applied to the output, ``pair_slot`` (``o3._graph.EdgePairs.slot``): the two
+    edges of a pair read one weight row, so ``weights`` holds E / 2 rows, and ``alpha_div``, a
+    one-element device tensor s: the output is then scaled by alpha / s, s read on the device
+    (the interaction layers' ``aggregated / sqrt_avg_neighbors``, reference
+    ``nn/layers.py:368``, without a host copy of the buffer)."""
     _check_tp_meta((in1_l_max, in2_l_max, out_l_max, in1_features, in2_features, symmetric_product, reduce_paths),
                    in1_offs, in2_offs, out_sizes, n_paths_per_l, n_total_paths)
     conv = _check_tp_inputs(in1, in2, weights, idx_i, idx_j, in1_l_max, in2_l_max, out_l_max, in1_features,
@@ -480,7 +545,7 @@ def tp_fwd(in1: Tensor, in2: Tensor, weights: Tensor, idx_i: Optional[Tensor], i
     in2 = _lib.contig("in2", in2)
     w = _lib.contig("weights", weights)
     desc = _lib.tp_desc(in1_l_max, in2_l_max, out_l_max, in1_features, in2_features, symmetric_product,
-                        shared_weights, reduce_paths)
+                        shared_weights, reduce_paths, _alpha_div(alpha_div))
     out = in1.new_empty(in1.shape[0], _tp_out_dim(in1_l_max, in2_l_max, out_l_max, in1_features, in2_features,
                                                   symmetric_product, reduce_paths))
     csr, keep = (None, None)
@@ -495,7 +560,8 @@ def tp_fwd(in1: Tensor, in2: Tensor, weights: Tensor, idx_i: Optional[Tensor], i
 @tp_fwd.register_fake
 def _(in1, in2, weights, idx_i, idx_j, in1_l_max, in2_l_max, out_l_max, in1_features, in2_features,
       symmetric_product, shared_weights, in1_offs, in2_offs, out_sizes, n_paths_per_l, n_total_paths,
-      reduce_paths=False, rowptr=None, sender_perm=None, sender_ptr=None, alpha=1.0, pair_slot=None):
+      reduce_paths=False, rowptr=None, sender_perm=None, sender_ptr=None, alpha=1.0, pair_slot=None,
+      alpha_div=None):
     return in1.new_empty(in1.shape[0], _tp_out_dim(in1_l_max, in2_l_max, out_l_max, in1_features, in2_features,
                                                    symmetric_product, reduce_paths))
 
@@ -508,11 +574,11 @@ def tp_bwd(grad_out: Tensor, in1: Tensor, in2: Tensor, weights: Tensor, idx_i: O
            reduce_paths: bool, need_grad_in1: bool, need_grad_in2: bool, need_grad_weights: bool,
            rowptr: Optional[Tensor] = None, sender_perm: Optional[Tensor] = None,
            sender_ptr: Optional[Tensor] = None, alpha: float = 1.0,
-           pair_slot: Optional[Tensor] = None) -> Tuple[Tensor, Tensor, Tensor]:
+           pair_slot: Optional[Tensor] = None, alpha_div: Optional[Tensor] = None) -> Tuple[Tensor, Tensor, Tensor]:
     """Gradients wrt (in1, in2, weights); unrequested ones are returned as empty (0,) tensors.
 
     Reference schema (src/flashcart/o3/_tensor_product.py:588-611) plus the optional
-    CSR arrays, ``alpha`` and ``pair_slot`` of ``tp_fwd``. With ``pair_slot`` the weight
+    CSR arrays, ``alpha``, ``pair_slot`` and ``alpha_div`` of ``tp_fwd``. With ``pair_slot`` the weight
     gradient has one row per edge (edge order); the sum of a pair's two rows is the gradient
     of the pair's weight row."""
     _check_tp_meta((in1_l_max, in2_l_max, out_l_max, in1_features, in2_features, symmetric_product, reduce_paths),
@@ -523,7 +589,7 @@ def tp_bwd(grad_out: Tensor, in1: Tensor, in2: Tensor, weights: Tensor, idx_i: O
     in2 = _lib.contig("in2", in2)
     w = _lib.contig("weights", weights)
     desc = _lib.tp_desc(in1_l_max, in2_l_max, out_l_max, in1_features, in2_features, symmetric_product,
-                        shared_weights, reduce_paths)
+                        shared_weights, reduce_paths, _alpha_div(alpha_div))
     csr, keep = (None, None)
     if conv:
         csr, keep = _tp_csr(in1, idx_i, idx_j, rowptr, sender_perm, sender_ptr, need_senders=need_grad_in1,
@@ -549,7 +615,7 @@ def tp_bwd(grad_out: Tensor, in1: Tensor, in2: Tensor, weights: Tensor, idx_i: O
 def _(grad_out, in1, in2, weights, idx_i, idx_j, in1_l_max, in2_l_max, out_l_max, in1_features, in2_features,
       symmetric_product, shared_weights, in1_offs, in2_offs, out_sizes, n_paths_per_l, n_total_paths,
       reduce_paths, need_grad_in1, need_grad_in2, need_grad_weights, rowptr=None, sender_perm=None,
-      sender_ptr=None, alpha=1.0, pair_slot=None):
+      sender_ptr=None, alpha=1.0, pair_slot=None, alpha_div=None):
     gw_rows = 2 * weights.shape[0] if pair_slot is not None else weights.shape[0]
     return (torch.empty_like(in1) if need_grad_in1 else in1.new_empty(0),
             torch.empty_like(in2) if need_grad_in2 else in2.new_empty(0),
@@ -558,21 +624,21 @@ def _(grad_out, in1, in2, weights, idx_i, idx_j, in1_l_max, in2_l_max, out_l_max
 
 def _tp_setup(ctx, inputs, output):
     (in1, in2, weights, idx_i, idx_j, l1, l2, lo, f1, f2, sym, shared, o1, o2, osz, npl, ntot, red,
-     rowptr, sperm, sptr, alpha, pair_slot) = inputs
-    ctx.save_for_backward(in1, in2, weights, idx_i, idx_j, rowptr, sperm, sptr, pair_slot)
+     rowptr, sperm, sptr, alpha, pair_slot, alpha_div) = inputs
+    ctx.save_for_backward(in1, in2, weights, idx_i, idx_j, rowptr, sperm, sptr, pair_slot, alpha_div)
     ctx.cfg = (int(l1), int(l2), int(lo), int(f1), int(f2), bool(sym), bool(shared), list(o1), list(o2),
                list(osz), list(npl), int(ntot), bool(red))
     ctx.alpha = float(alpha)
 
 
 def _tp_backward(ctx, grad):
-    in1, in2, weights, idx_i, idx_j, rowptr, sperm, sptr, pair_slot = ctx.saved_tensors
+    in1, in2, weights, idx_i, idx_j, rowptr, sperm, sptr, pair_slot, alpha_div = ctx.saved_tensors
     n1, n2, nw = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[2]
-    none_tail = (None,) * 20
+    none_tail = (None,) * 21
     if not (n1 or n2 or nw):
         return (None, None, None) + none_tail
     g1, g2, gw = tp_bwd(grad, in1, in2, weights, idx_i, idx_j, *ctx.cfg, bool(n1), bool(n2), bool(nw),
-                        rowptr, sperm, sptr, ctx.alpha, pair_slot)
+                        rowptr, sperm, sptr, ctx.alpha, pair_slot, alpha_div)
     if nw and pair_slot is not None:  # both edges of a pair read its weight row (two terms: order-free)
         gw = gw.new_zeros(weights.shape).index_add_(0, (pair_slot // 2).long(), gw)
     return (g1 if n1 else None, g2 if n2 else None, gw if nw else None) + none_tail

@@ -51,8 +51,8 @@ def _acc(*terms):
 
 def _tp_bwd_setup(ctx, inputs, output):
     (go, in1, in2, w, idx_i, idx_j, l1, l2, lo, f1, f2, sym, shared, o1, o2, osz, npl, ntot, red,
-     n1, n2, nw, rowptr, sperm, sptr, alpha, pair_slot) = inputs
-    ctx.save_for_backward(go, in1, in2, w, idx_i, idx_j, rowptr, sperm, sptr)
+     n1, n2, nw, rowptr, sperm, sptr, alpha, pair_slot, alpha_div) = inputs
+    ctx.save_for_backward(go, in1, in2, w, idx_i, idx_j, rowptr, sperm, sptr, alpha_div)
     ctx.paired = pair_slot is not None
     ctx.cfg = (int(l1), int(l2), int(lo), int(f1), int(f2), bool(sym), bool(shared), list(o1), list(o2),
                list(osz), list(npl), int(ntot), bool(red))
@@ -62,24 +62,25 @@ def _tp_bwd_setup(ctx, inputs, output):
 
 def _tp_dbwd(ctx, c1, c2, cw):
     """Backward of tp_bwd (reference tp_dbwd, src/flashcart/o3/_tensor_product.py:789-1093)."""
-    go, in1, in2, w, ii, jj, rp, sp, sq = ctx.saved_tensors
+    go, in1, in2, w, ii, jj, rp, sp, sq, adiv = ctx.saved_tensors
     need = ctx.needs_input_grad
     c1 = _live(c1) if ctx.computed[0] else None
     c2 = _live(c2) if ctx.computed[1] else None
     cw = _live(cw) if ctx.computed[2] else None
     cfg, alpha = ctx.cfg, ctx.alpha
-    tail = (None,) * 23
+    tail = (None,) * 24
     if ctx.paired:
         raise NotImplementedError("second derivatives of a tensor product with shared pair weights (pair_slot) "
                                   "are not implemented; run without edge pairs under create_graph.")
 
     def fwd(a, b, ww):
-        return _ops.tp_fwd(a, b, ww, ii, jj, *cfg, rp, sp, sq, alpha)
+        return _ops.tp_fwd(a, b, ww, ii, jj, *cfg, rp, sp, sq, alpha, None, adiv)
 
     def bwd(a, b, ww, n1, n2, nw):
         if not (n1 or n2 or nw):
             return None, None, None
-        g1, g2, gw = _ops.tp_bwd(go, a, b, ww, ii, jj, *cfg, bool(n1), bool(n2), bool(nw), rp, sp, sq, alpha)
+        g1, g2, gw = _ops.tp_bwd(go, a, b, ww, ii, jj, *cfg, bool(n1), bool(n2), bool(nw), rp, sp, sq, alpha,
+                                 None, adiv)
         return (g1 if n1 else None), (g2 if n2 else None), (gw if nw else None)
 
     d_go = None

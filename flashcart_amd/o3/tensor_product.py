@@ -24,7 +24,8 @@ class TensorProduct(nn.Module):
 
     ``forward`` additionally accepts ``graph`` (a :class:`GraphCSR` built once per
     neighbour list) so that the receiver CSR and sender ordering are not rebuilt by
-    every call, and ``alpha``, a scale folded into the kernel output.
+    every call, ``alpha``, a scale folded into the kernel output, and ``alpha_div``, a
+    one-element device tensor the output is divided by on the device.
     """
 
     def __init__(self, in1_l_max: int, in2_l_max: int, out_l_max: int, in1_features: int, in2_features: int,
@@ -70,7 +71,8 @@ class TensorProduct(nn.Module):
 
     def forward(self, in1: torch.Tensor, in2: torch.Tensor, weights: torch.Tensor,
                 idx_i: Optional[torch.Tensor] = None, idx_j: Optional[torch.Tensor] = None,
-                graph: Optional[GraphCSR] = None, alpha: float = 1.0) -> torch.Tensor:
+                graph: Optional[GraphCSR] = None, alpha: float = 1.0,
+                alpha_div: Optional[torch.Tensor] = None) -> torch.Tensor:
         if in1.shape[-1] != self.in1_dim:
             raise RuntimeError(f"Incorrect last dimension for in1. Expected {self.in1_dim}, got {in1.shape[-1]}.")
         if in2.shape[-1] != self.in2_dim:
@@ -86,7 +88,8 @@ class TensorProduct(nn.Module):
         return _ops.tp_fwd(in1, in2, _ops.param_alias(weights), idx_i, idx_j, self.in1_l_max, self.in2_l_max,
                            self.out_l_max,
                            self.in1_features, self.in2_features, self.symmetric_product, self.shared_weights,
-                           *self.op_meta, self.reduce_paths, rowptr, sender_perm, sender_ptr, float(alpha))
+                           *self.op_meta, self.reduce_paths, rowptr, sender_perm, sender_ptr, float(alpha), None,
+                           alpha_div)
 
     def __repr__(self) -> str:
         return (f"{self.__class__.__name__}({self.in1_l_max} x {self.in2_l_max} -> {self.out_l_max}, "

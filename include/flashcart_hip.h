@@ -139,7 +139,11 @@ typedef struct fc_csr {
   int64_t n_sender_rows;       /* rows of in1 (senders may include ghost atoms) */
   const int32_t* pair_slot;    /* optional (NULL: edge e uses weight row e). Per-edge weights shared
                                   by the two edges of a pair (fc_edge_pairs): edge e reads weight row
-                                  pair_slot[e] / 2; its weight gradient stays at row e. No counterpart
+                                  pair_slot[e] / 2; its weight gradient stays at row e. Must come
+                                  from a complete pairing (fc_edge_pairs with counts[0] == 0 and
+                                  counts[1] == n_edges / 2): an edge with a negative slot has no
+                                  weight row and contributes nothing (weights read as zero, its
+                                  density and h-gradient terms skipped). No counterpart
                                   in the reference, which forms the weights of every edge
                                   (nn/layers.py:357-364). */
 } fc_csr;
@@ -211,6 +215,11 @@ typedef struct fc_tp_desc {
   int32_t symmetric_product;               /* canonical pairs only (in1 == in2) */
   int32_t shared_weights;                  /* weights (n_paths*C,) instead of (items, n_paths*C) */
   int32_t reduce_paths;                    /* sum paths within each output rank */
+  const float* alpha_div;                  /* optional device scalar s (NULL: 1): the output (and the
+                                              gradient's transpose) is scaled by alpha / s, read on the
+                                              device at launch, so a divisor held in a device buffer
+                                              (the interaction layers' sqrt_avg_neighbors, reference
+                                              nn/layers.py:368) needs no host copy */
 } fc_tp_desc;
 
 /* Path count (the weight layout) of a configuration, or a negative fc_status. */
@@ -221,7 +230,7 @@ int64_t fc_tp_out_dim(const fc_tp_desc* desc);
 /* graph == NULL: independent rows (in1, in2, weights and out all have n_rows rows).
  * graph != NULL: convolution; in1 has graph->n_sender_rows rows, in2 and weights have
  * n_edges rows, out has graph->n_nodes rows (receiver-sorted segmented sum).
- * out = alpha * TP(...). */
+ * out = alpha / *desc->alpha_div * TP(...) (alpha * TP(...) when alpha_div is NULL). */
 int fc_tp_fwd(const fc_tp_desc* desc, const fc_csr* graph, int64_t n_rows, const float* in1,
               const float* in2, const float* weights, float alpha, float* out, void* stream);
 

@@ -168,3 +168,56 @@ def test_cfg5_molecules_512():
         single = model.predict(graphs[k].to(DEV), compute_forces=True)
         assert_close(out["energy"][k:k + 1], single["energy"], 1e-5, 1e-6, f"cfg5 batched vs single {k}")
         assert_close(out["forces"][starts[k]:starts[k + 1]], single["forces"], 0.0, 1e-4, f"cfg5 forces {k}")
+
+
+def _frozen_replay(model, gdev, what):
+    """``predict(use_compile=True)`` with frozen parameters, as bench.py times cfgs 3 and 5: the
+    capture call and one replay, bitwise equal; the fused paths the timed step takes (edge pairs,
+    the first layer as a species density, the shared input maps) must have run."""
+    from flashcart_amd.nn import fused
+    model.requires_grad_(False)
+    fused.path_counts.clear()
+    _log(f"{what}: frozen parameters, HIP graph capture")
+    out = model.predict(gdev, compute_forces=True, use_compile=True)
+    _log(f"{what}: replay")
+    again = model.predict(gdev, compute_forces=True, use_compile=True)
+    for key in ("species", "paired", "entry_maps", "product", "gated"):
+        assert fused.path_counts[key] > 0, f"{what}: the timed path did not take the {key} block"
+    assert torch.equal(out["energy"], again["energy"]) and torch.equal(out["forces"], again["forces"])
+    return again
+
+
+def test_cfg3_water_1536_timed_path():
+    """The whole 1,536-atom water box through the path bench.py times (frozen parameters, edge pairs,
+    species density, HIP graph replay) against the float64 oracle at the north-star bars."""
+    z, p, cell, pbc = water_box(512, seed=0)
+    g = AtomicGraph.from_arrays(z, p, ["H", "O"], 5.0, cell=cell, pbc=pbc)
+    avg = g.edge_index.shape[1] / g.num_nodes
+    model = _model(model_config(["H", "O"], 64, 2, avg_neighbors=avg), 31)
+    ref = OM.predict(model.state_dict(), model.to_model_config(), g.to_dict(), compute_forces=True)
+    out = _frozen_replay(model.to(DEV), g.to(DEV), "cfg3 water")
+    assert_close(out["energy"], ref["energy"], 1e-5, 1e-6, "cfg3 replay energy")
+    assert_close(out["forces"], ref["forces"], 0.0, 1e-4, "cfg3 replay forces")
+
+
+def test_cfg5_molecules_512_timed_path():
+    """The full 512-molecule batch through the timed path (frozen, pairs, species density, replay);
+    a sample of molecules against the float64 oracle, and every molecule's energy against the
+    eager per-edge evaluation of the same batch."""
+    mols = molecules(512, seed=0)
+    elements = ["H", "C", "N", "O"]
+    graphs = [AtomicGraph.from_arrays(zz, pp, elements, 5.0) for zz, pp in mols]
+    batch = batch_graphs(graphs)
+    avg = batch.edge_index.shape[1] / batch.num_nodes
+    model = _model(model_config(elements, 64, 2, avg_neighbors=avg), 41).to(DEV)
+    per_edge = model.predict(batch.to(DEV), compute_forces=True)  # trainable: the per-edge path
+    out = _frozen_replay(model, batch.to(DEV), "cfg5 molecules")
+    assert out["energy"].shape == (512,)
+    assert_close(out["energy"], per_edge["energy"], 1e-5, 1e-6, "cfg5 replay vs per-edge energies")
+    assert_close(out["forces"], per_edge["forces"], 0.0, 1e-4, "cfg5 replay vs per-edge forces")
+    starts = np.concatenate([[0], np.cumsum([g.num_nodes for g in graphs])])
+    sd, mcfg = model.state_dict(), model.to_model_config()
+    for k in (0, 3, 128, 300, 511):
+        ref = OM.predict(sd, mcfg, graphs[k].to_dict(), compute_forces=True)
+        assert_close(out["energy"][k:k + 1], ref["energy"], 1e-5, 1e-6, f"cfg5 replay energy mol {k}")
+        assert_close(out["forces"][starts[k]:starts[k + 1]], ref["forces"], 0.0, 1e-4, f"cfg5 replay forces mol {k}")

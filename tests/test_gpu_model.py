@@ -145,4 +145,6 @@ def test_predict_replay(frozen):
         assert_close(got["forces"], ref["forces"], 0.0, F_ABS, f"replay {it} forces vs oracle")
         assert_close(got["stress"], ref["stress"], 1e-5, 1e-5 * float(ref["stress"].abs().max()),
                      f"replay {it} stress vs oracle")
-    assert len(m._replay_cache) == 3  # one capture per avg_neighbors state
+    # the kernels divide by each interaction's sqrt_avg_neighbors buffer on the device, so the new
+    # values reach the captured graph without a re-capture
+    assert len(m._replay_cache) == 1

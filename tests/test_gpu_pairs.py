@@ -197,6 +197,62 @@ def test_tp_with_pair_slot_equals_expanded_weights(l1, c):
     assert_close(wq.grad, want, 1e-6, 1e-6, "pair weight gradient")
 
 
+def test_unpaired_slot_contributes_nothing():
+    """An edge whose pair slot is -1 (a pairing left it without a partner) has no weight row and no
+    h row: the kernels' guards read its weights and h as zero and skip its h-gradient row, so the
+    products equal the per-edge computation with that edge's weights (or h) zeroed, bit for bit for
+    the tensor product, and the species density matches its float64 definition."""
+    from flashcart_amd import _lib
+    from flashcart_amd.o3 import _ops
+    numbers, pos, cell, pbc = fcc_alloy(2, 2, 2, seed=3)
+    g = AtomicGraph.from_arrays(numbers, pos, ["Cu", "Ni", "Fe", "Cr"], 5.0, cell=cell, pbc=pbc).to(DEV)
+    csr = _csr(g)
+    pairs = csr.edge_pairs(g.shifts)
+    k = 7
+    slot = pairs.slot.clone()
+    slot[k] = -1
+    tp = _tp(2, 3, 3, 128)
+    n, e = csr.n_nodes, csr.n_edges
+    gen = torch.Generator(device=DEV).manual_seed(13)
+    x = torch.randn(n, tp.in1_dim, device=DEV, generator=gen)
+    y = torch.randn(e, 16, device=DEV, generator=gen)
+    wp = torch.randn(pairs.n_pairs, tp.n_total_paths * 128, device=DEV, generator=gen)
+    w_edge = wp[(pairs.slot // 2).long()].clone()
+    w_edge[k] = 0.0
+    args = (tp.in1_l_max, tp.in2_l_max, tp.out_l_max, tp.in1_features, tp.in2_features, False, False,
+            *tp.op_meta, False)
+    csr_args = (csr.rowptr, csr.sender_perm, csr.sender_ptr)
+    print("unpaired slot: tensor product", flush=True)
+    out_p = _ops.tp_fwd(x, y, wp, csr.idx_i, csr.idx_j, *args, *csr_args, 1.0, slot)
+    out_e = _ops.tp_fwd(x, y, w_edge, csr.idx_i, csr.idx_j, *args, *csr_args, 1.0)
+    assert torch.equal(out_p, out_e)
+    go = torch.randn_like(out_e)
+    gp = _ops.tp_bwd(go, x, y, wp, csr.idx_i, csr.idx_j, *args, True, True, True, *csr_args, 1.0, slot)
+    ge = _ops.tp_bwd(go, x, y, w_edge, csr.idx_i, csr.idx_j, *args, True, True, True, *csr_args, 1.0)
+    for a, b in zip(gp, ge):
+        assert torch.equal(a, b)
+    print("unpaired slot: species density", flush=True)
+    n_sp, d = 4, 16
+    zj = torch.randint(0, n_sp, (e,), device=DEV, generator=gen, dtype=torch.int32)
+    h = torch.randn(pairs.n_pairs, 64, device=DEV, generator=gen)
+    st = _lib.csr_struct(n, e, csr.idx_j, csr.rowptr, pair_slot=slot)
+    dens = _ops.species_density_fwd(st, 3, 3, n_sp, zj, h, y, n)
+    he = h.double()[(pairs.slot // 2).long()].clone()
+    he[k] = 0.0
+    onehot = torch.nn.functional.one_hot(zj.long(), n_sp).double()
+    per_edge = (he[:, None, :] * y.double()[:, :, None])[:, :, None, :] * onehot[:, None, :, None]
+    want = torch.zeros(n, d, n_sp, 64, dtype=torch.float64, device=DEV).index_add_(0, csr.idx_i.long(), per_edge)
+    assert_close(dens.view(n, d, n_sp, 64), want, 1e-5, 1e-5, "density with an unpaired edge")
+    gd = torch.randn(n, d * n_sp * 64, device=DEV, generator=gen)
+    g_h, g_y = _ops.species_density_bwd(st, 3, 3, n_sp, zj, h, y, gd)
+    gsel = (gd.double().view(n, d, n_sp, 64)[csr.idx_i.long()] * onehot[:, None, :, None]).sum(2)
+    want_h = (gsel * y.double()[:, :, None]).sum(1)
+    want_y = (gsel * he[:, None, :]).sum(2)
+    keep = torch.arange(e, device=DEV) != k
+    assert_close(g_h[pairs.slot.long()][keep], want_h[keep], 1e-5, 1e-5, "dL/dh of the paired edges")
+    assert_close(g_y, want_y, 1e-5, 1e-5, "dL/dy with an unpaired edge")
+
+
 def _model(cfg, seed=1234):
     from flashcart_amd.model import FlashCartPotential
     torch.manual_seed(seed)
@@ -340,7 +396,7 @@ def test_species_density_op(l_max, y_l_max):
 def test_species_conv_matches_paired_conv():
     """The first interaction layer as a species density (linear_second folded in) against the same
     layer over edge pairs followed by linear_second: outputs and input gradients (edge attributes,
-    radial inputs) at float32 round-off; a second call reuses the cached maps."""
+    radial inputs) at float32 round-off; a second call forms the same maps again."""
     from flashcart_amd.o3 import _ops
     numbers, pos, cell, pbc = fcc_alloy(3, 3, 3, seed=4)
     cfg = model_config(["Cu", "Ni", "Fe", "Cr"], 128, 3, avg_neighbors=42.0)
@@ -355,7 +411,7 @@ def test_species_conv_matches_paired_conv():
     xp = torch.rand(pairs.n_pairs, 8, device=DEV, generator=gen, requires_grad=True)
     table = model.embedding.weight
     zj = torch.index_select(g.atom_types.to(torch.int32), 0, csr.idx_j)
-    alpha = layer._inv_sqrt_avg()
+    alpha = layer.sqrt_avg_neighbors
     node = model.embedding(g.atom_types)
     assert fused.species_conv_applies(layer, node, table.shape[0])
     out_s = fused.species_conv(layer, y, xp, csr, pairs, zj, table, alpha)
@@ -368,7 +424,7 @@ def test_species_conv_matches_paired_conv():
     gp = torch.autograd.grad(out_p, (y, xp), go)
     for a, b, what in zip(gs, gp, ("edge attributes", "radial inputs")):
         assert_close(a, b, 1e-5, 1e-5 * float(b.abs().max()), f"species vs paired gradient of {what}")
-    # the cached maps follow in-place changes of the table and of linear_first's weights
+    # the maps follow in-place changes of the table and of linear_first's weights
     with torch.no_grad():
         table.mul_(1.5)
         layer.linear_first.weight[0].add_(0.25)
