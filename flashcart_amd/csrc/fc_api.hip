@@ -119,7 +119,7 @@ extern "C" int fc_tp_fwd(const fc_tp_desc* d, const fc_csr* graph, int64_t n_row
   if (conv && graph->pair_slot && d->shared_weights) return FC_ERR_BAD_DESC;
   TPArgs g = make_args(d, rows);
   g.in1 = in1; g.in2 = in2; g.w = w; g.out = out; g.alpha = alpha;
-  if (conv) { g.idx_j = graph->idx_j; g.rowptr = graph->rowptr; g.wslot = graph->pair_slot; }
+  if (conv) { g.idx_j = graph->idx_j; g.rowptr = graph->rowptr; g.wslot = graph->pair_slot; g.n_edges = graph->n_edges; }
   return dispatch(d, g, conv, false, (hipStream_t)stream);
 }
 
@@ -166,7 +166,7 @@ extern "C" int fc_tp_bwd(const fc_tp_desc* d, const fc_csr* graph, int64_t n_row
   g.grad_in1 = conv ? msg : gin1;
   g.grad_in2 = gin2;
   g.grad_w = (gw && d->shared_weights) ? wtmp : gw;
-  if (conv) { g.idx_j = graph->idx_j; g.rowptr = graph->rowptr; g.wslot = graph->pair_slot; }
+  if (conv) { g.idx_j = graph->idx_j; g.rowptr = graph->rowptr; g.wslot = graph->pair_slot; g.n_edges = graph->n_edges; }
   if (rows > 0) {
     st = dispatch(d, g, conv, true, s);
     if (st != FC_OK) return st;

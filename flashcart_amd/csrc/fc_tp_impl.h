@@ -33,6 +33,7 @@ struct TPArgs {
   float* grad_in2;
   float* grad_w;           // per-item weight gradient (item = edge or row)
   int64_t n_rows;
+  int64_t n_edges;         // conv: edges of the graph (launch shape only)
   int32_t F1, F2, C;       // in1 / in2 / output features (1 broadcasts)
   int32_t shared_w, reduced;
   float alpha;             // output scale (fwd) / its transpose (bwd)
@@ -146,7 +147,11 @@ __device__ __forceinline__ void fill_amat(const float* __restrict__ in2, int64_t
   });
 }
 
-template <int L1, int L2, int LO, bool SYM, bool CONV, bool BC2>
+// EG > 1 (convolution with C = 32 or 64 only): EG groups of C lanes share a receiver (block C * EG
+// threads), group g taking the edges e0 + g, e0 + g + EG, ...; the groups' partial sums are added in
+// LDS in group order (so results are reproducible run to run) and stored by group 0. This gives a
+// graph with few receivers and few channels enough waves to hide the gather latency.
+template <int L1, int L2, int LO, bool SYM, bool CONV, bool BC2, int EG = 1>
 __global__ void __launch_bounds__(256) tp_fwd_kernel(TPArgs g) {
   // The forward keeps the per-lane coupling matrices: it is bound by the gathered
   // operand stream, and staging the matrices in LDS (as the backward does) measured
@@ -154,10 +159,14 @@ __global__ void __launch_bounds__(256) tp_fwd_kernel(TPArgs g) {
   using CF = TPConfig<L1, L2, LO, SYM>;
   using PL = typename CF::PL;
   constexpr int D1 = CF::D1, D2 = CF::D2, NOUT = CF::NOUT, NP = CF::NP;
+  static_assert(EG == 1 || CONV, "edge groups split a receiver's edges");
+  extern __shared__ float part_lds[];  // EG > 1: (EG - 1) x NOUT x C partial sums
   const int64_t row = CONV ? xcd_row(g.n_rows) : (int64_t)blockIdx.x;
-  const int f = threadIdx.x;
   const int C = g.C;
-  if (f >= C || row >= g.n_rows) return;
+  const int grp = EG == 1 ? 0 : (int)threadIdx.x / C;
+  const int f = EG == 1 ? (int)threadIdx.x : (int)threadIdx.x % C;
+  if (row >= g.n_rows) return;  // uniform over the workgroup
+  if (EG == 1 && f >= C) return;
   const int f1 = g.F1 == 1 ? 0 : f;
   const int f2 = g.F2 == 1 ? 0 : f;
 
@@ -166,12 +175,12 @@ __global__ void __launch_bounds__(256) tp_fwd_kernel(TPArgs g) {
   for (int k = 0; k < NOUT; ++k) acc[k] = 0.f;
 
   int64_t e0 = row, e1 = row + 1;
-  if constexpr (CONV) { e0 = g.rowptr[row]; e1 = g.rowptr[row + 1]; }
+  if constexpr (CONV) { e0 = g.rowptr[row] + grp; e1 = g.rowptr[row + 1]; }
   EdgeOps<D1, D2, NP> cur, nxt;
   if (e0 < e1) load_edge<D1, D2, NP, CONV, BC2>(g, e0, f1, f2, f, true, nxt);
-  for (int64_t e = e0; e < e1; ++e) {
+  for (int64_t e = e0; e < e1; e += EG) {
     cur = nxt;
-    if (e + 1 < e1) load_edge<D1, D2, NP, CONV, BC2>(g, e + 1, f1, f2, f, true, nxt);
+    if (e + EG < e1) load_edge<D1, D2, NP, CONV, BC2>(g, e + EG, f1, f2, f, true, nxt);
     static_for<NP>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
       constexpr PathDesc P = PL::at(i);
@@ -182,6 +191,18 @@ __global__ void __launch_bounds__(256) tp_fwd_kernel(TPArgs g) {
 #pragma unroll
       for (int a = 0; a < T::NO; ++a) acc[PL::out_index(i, a)] = fmaf(cur.w[i], t[a], acc[PL::out_index(i, a)]);
     });
+  }
+  if constexpr (EG > 1) {
+    if (grp > 0) {
+#pragma unroll
+      for (int k = 0; k < NOUT; ++k) part_lds[((grp - 1) * NOUT + k) * C + f] = acc[k];
+    }
+    __syncthreads();
+    if (grp > 0) return;
+#pragma unroll
+    for (int q = 1; q < EG; ++q)
+#pragma unroll
+      for (int k = 0; k < NOUT; ++k) acc[k] += part_lds[((q - 1) * NOUT + k) * C + f];
   }
   if (!g.reduced) {
     float* o = g.out + row * (int64_t)NOUT * C + f;
@@ -218,14 +239,17 @@ __host__ __device__ constexpr int pow2_at_least(int n) {
 // halving butterfly: every exchange step keeps half of the values (N-1 + 6-log2 N
 // shuffles instead of 6 N). Afterwards every lane of group lane >> (6 - log2 N) == v
 // holds the total of value v.
-template <int N>
+// W = 32 reduces each half of the wave on its own: afterwards lane group (lane & 31) >> (5 - log2 N)
+// == v of each half holds that half's total of value v.
+template <int N, int W = 64>
 __device__ __forceinline__ float wave_reduce_halving(float (&v)[N], int lane) {
   constexpr int LOGN = log2_exact(N);
   static_assert((1 << LOGN) == N, "N must be a power of two");
+  static_assert((W == 32 || W == 64) && N <= W, "lane groups of 32 or 64");
   static_for<LOGN>([&](auto sc) {
     constexpr int s = decltype(sc)::value;
     constexpr int half = N >> (s + 1);
-    const int o = 32 >> s;
+    const int o = (W / 2) >> s;
     const bool lower = (lane & o) == 0;
 #pragma unroll
     for (int j = 0; j < half; ++j) {
@@ -236,7 +260,7 @@ __device__ __forceinline__ float wave_reduce_halving(float (&v)[N], int lane) {
   });
   float r = v[0];
 #pragma unroll
-  for (int o = 32 >> LOGN; o > 0; o >>= 1) r += __shfl_xor(r, o, 64);
+  for (int o = (W / 2) >> LOGN; o > 0; o >>= 1) r += __shfl_xor(r, o, 64);
   return r;
 }
 
@@ -415,36 +439,46 @@ __global__ void __launch_bounds__(256, 2) tp_bwd_kernel(TPArgs g) {
 }
 
 // Backward of the interaction-layer convolution (one in2 channel, unreduced outputs),
-// specialised at compile time: C channels = the block size (every lane active, operand
-// offsets are immediates), the weight and edge-attribute gradients always formed, the
-// per-edge in1 messages when NEED1. Same arithmetic, in the same order, as
-// tp_bwd_kernel<..., CONV, BC2>; without the run-time flags the path contractions are one
-// basic block, so loads, stores and LDS reads of neighbouring paths interleave with
-// their FMAs. The edge loop is unrolled by two with two operand sets (no register
-// copies between iterations): the operands of edge e+1 load while edge e is contracted.
+// specialised at compile time: C channels (every lane active, operand offsets are
+// immediates), the weight and edge-attribute gradients always formed, the per-edge in1
+// messages when NEED1. Same arithmetic, in the same order, as tp_bwd_kernel<..., CONV, BC2>;
+// without the run-time flags the path contractions are one basic block, so loads, stores and
+// LDS reads of neighbouring paths interleave with their FMAs. The edge loop is unrolled by
+// two with two operand sets (no register copies between iterations): the operands of the
+// next edge load while the current one is contracted.
+// EG edge groups of C lanes share a receiver (block C * EG threads): group g takes the edges
+// e0 + g, e0 + g + EG, ..., so a receiver with few channels (C = 32: two groups per wave; C = 64:
+// one wave per group) still gives the GPU enough waves when the graph has few receivers. Every
+// per-edge output is written by one group, so the groups need no combining step.
 template <int L1, int L2, int LO, bool SYM>
 __host__ __device__ constexpr int bwd_conv_chunk() {
   return AmatLayout<L1, L2, LO, SYM>::chunk >= 2 ? (AmatLayout<L1, L2, LO, SYM>::chunk & ~1) : 2;
 }
 
-template <int L1, int L2, int LO, bool SYM, int C, bool NEED1>
-__global__ void __launch_bounds__(C, 2) tp_bwd_conv_kernel(TPArgs g) {
+template <int L1, int L2, int LO, bool SYM, int C, int EG, bool NEED1>
+__global__ void __launch_bounds__(C * EG, 2) tp_bwd_conv_kernel(TPArgs g) {
   using CF = TPConfig<L1, L2, LO, SYM>;
   using PL = typename CF::PL;
   using AL = AmatLayout<L1, L2, LO, SYM>;
   constexpr int D1 = CF::D1, D2 = CF::D2, NOUT = CF::NOUT, NP = CF::NP;
-  constexpr int R2 = pow2_at_least(D2), SH2 = 6 - log2_exact(R2);
+  constexpr int T = C * EG;                          // threads
+  constexpr int NW = T / 64;                         // waves
+  constexpr int GW = C >= 64 ? 64 : C;               // lanes of a group within one wave
+  constexpr int NWG = C >= 64 ? C / 64 : 1;          // waves per group
+  constexpr int R2 = pow2_at_least(D2), SH2 = log2_exact(GW) - log2_exact(R2);
   constexpr int CH = bwd_conv_chunk<L1, L2, LO, SYM>();
-  constexpr int NW = C / 64;
-  static_assert(C % 64 == 0 && C <= 256, "one lane per channel, whole waves");
+  static_assert((C == 32 || C % 64 == 0) && C <= 256 && T % 64 == 0 && T <= 256, "whole waves of whole groups");
+  static_assert(CH % (2 * EG) == 0, "every full chunk gives each group an even number of edges");
   static_assert(2 * CH * AL::total * 4 <= 65536, "coupling-matrix chunks exceed the LDS budget");
   constexpr int64_t SW = (int64_t)NP * C, S1 = (int64_t)D1 * C;
   __shared__ __align__(16) float a_lds[2 * CH * AL::total];
-  __shared__ float red_lds[CH * NW * D2];
+  __shared__ float red_lds[CH * NWG * D2];
 
   const int64_t row = xcd_row(g.n_rows);
   if (row >= g.n_rows) return;
-  const int f = threadIdx.x, wave = f >> 6, lane = f & 63;
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const int grp = EG == 1 ? 0 : t / C, f = EG == 1 ? t : t % C;
+  const int wig = C >= 64 ? f >> 6 : 0;  // wave within the group
   const int64_t e0 = g.rowptr[row], e1 = g.rowptr[row + 1];
   if (e0 >= e1) return;  // uniform over the workgroup: no barrier is skipped by a part of it
 
@@ -459,7 +493,7 @@ __global__ void __launch_bounds__(C, 2) tp_bwd_conv_kernel(TPArgs g) {
 #pragma unroll
     for (int u = 0; u < D1; ++u) o.x[u] = xr[u * C];
     const int64_t wrow = weight_row(g, e);
-    if (wrow < 0) {  // uniform: an unpaired edge's weights count as zero
+    if (wrow < 0) {  // an unpaired edge's weights count as zero
 #pragma unroll
       for (int i = 0; i < NP; ++i) o.w[i] = 0.f;
       return;
@@ -479,31 +513,31 @@ __global__ void __launch_bounds__(C, 2) tp_bwd_conv_kernel(TPArgs g) {
     static_for<NP>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
       constexpr PathDesc P = PL::at(i);
-      using T = TPPath<P.r1, P.r2, P.lo>;
+      using TP = TPPath<P.r1, P.r2, P.lo>;
       const float* xp = cur.x + P.r1 * P.r1;
-      float gop[T::NO];
+      float gop[TP::NO];
 #pragma unroll
-      for (int a = 0; a < T::NO; ++a) gop[a] = go[PL::out_index(i, a)];
-      float v[T::N1];
+      for (int a = 0; a < TP::NO; ++a) gop[a] = go[PL::out_index(i, a)];
+      float v[TP::N1];
 #pragma unroll
-      for (int b = 0; b < T::N1; ++b) v[b] = 0.f;
-      T::apply_t(ae + AL::template off<i>(), gop, v);
+      for (int b = 0; b < TP::N1; ++b) v[b] = 0.f;
+      TP::apply_t(ae + AL::template off<i>(), gop, v);
       float s = 0.f;
 #pragma unroll
-      for (int b = 0; b < T::N1; ++b) s = fmaf(v[b], xp[b], s);
+      for (int b = 0; b < TP::N1; ++b) s = fmaf(v[b], xp[b], s);
       gwr[i * C] = s;
       if constexpr (NEED1) {
 #pragma unroll
-        for (int b = 0; b < T::N1; ++b) gx[P.r1 * P.r1 + b] = fmaf(cur.w[i], v[b], gx[P.r1 * P.r1 + b]);
+        for (int b = 0; b < TP::N1; ++b) gx[P.r1 * P.r1 + b] = fmaf(cur.w[i], v[b], gx[P.r1 * P.r1 + b]);
       }
-      float xw[T::N1];
+      float xw[TP::N1];
 #pragma unroll
-      for (int b = 0; b < T::N1; ++b) xw[b] = cur.w[i] * xp[b];
-      T::vjp2(gop, xw, gy + P.r2 * P.r2);
+      for (int b = 0; b < TP::N1; ++b) xw[b] = cur.w[i] * xp[b];
+      TP::vjp2(gop, xw, gy + P.r2 * P.r2);
     });
-    const float s = wave_reduce_halving<R2>(gy, lane);
-    const int v = lane >> SH2;
-    if ((lane & ((1 << SH2) - 1)) == 0 && v < D2) red_lds[(slot * NW + wave) * D2 + v] = s;
+    const float s = wave_reduce_halving<R2, GW>(gy, lane);
+    const int v = (lane & (GW - 1)) >> SH2;
+    if ((lane & ((1 << SH2) - 1)) == 0 && v < D2) red_lds[(slot * NWG + wig) * D2 + v] = s;
     if constexpr (NEED1) {
       float* mr = g.grad_in1 + e * S1 + f;
 #pragma unroll
@@ -512,33 +546,34 @@ __global__ void __launch_bounds__(C, 2) tp_bwd_conv_kernel(TPArgs g) {
   };
 
   EdgeOps<D1, D2, NP> opa, opb;
-  load(e0, opa);
+  if (EG == 1 || e0 + grp < e1) load(e0 + grp, opa);
   fill_amat<L1, L2, LO, SYM>(g.in2, e0, e1 - e0 < CH ? (int)(e1 - e0) : CH, a_lds, lane, wave, NW);
   __syncthreads();
   int buf = 0;
-  // Every chunk but the last holds CH (even) edges, so each chunk starts on operand set a.
+  // Every chunk but the last holds CH edges, an even number per group, so each chunk starts on
+  // operand set a; group grp takes the chunk's slots grp, grp + EG, ...
   for (int64_t c0 = e0; c0 < e1; c0 += CH) {
     const int64_t c1 = c0 + CH < e1 ? c0 + CH : e1;
+    const int n = (int)(c1 - c0);
     const int n_next = e1 - c1 < CH ? (int)(e1 - c1) : CH;
     const float* ab = a_lds + buf * CH * AL::total;
-    for (int64_t e = c0; e < c1; e += 2) {
+    for (int64_t e = c0 + grp; e < c1; e += 2 * EG) {
       const int slot = (int)(e - c0);
-      if (e + 1 < e1) load(e + 1, opb);
+      if (e + EG < e1) load(e + EG, opb);
       step(e, opa, ab + slot * AL::total, slot);
-      if (e + 1 < c1) {
-        if (e + 2 < e1) load(e + 2, opa);
-        step(e + 1, opb, ab + (slot + 1) * AL::total, slot + 1);
+      if (e + EG < c1) {
+        if (e + 2 * EG < e1) load(e + 2 * EG, opa);
+        step(e + EG, opb, ab + (slot + EG) * AL::total, slot + EG);
       }
     }
     // the other buffer was last read in the previous chunk, before that chunk's barriers
     if (n_next > 0) fill_amat<L1, L2, LO, SYM>(g.in2, c1, n_next, a_lds + (buf ^ 1) * CH * AL::total, lane, wave, NW);
     __syncthreads();
-    const int n = (int)(c1 - c0);
-    for (int k = f; k < n * D2; k += C) {
+    for (int k = t; k < n * D2; k += T) {
       const int slot = k / D2, u = k % D2;
       float s = 0.f;
 #pragma unroll
-      for (int w = 0; w < NW; ++w) s += red_lds[(slot * NW + w) * D2 + u];
+      for (int w = 0; w < NWG; ++w) s += red_lds[(slot * NWG + w) * D2 + u];
       g.grad_in2[(c0 + slot) * D2 + u] = s;
     }
     __syncthreads();
@@ -623,6 +658,39 @@ __global__ void __launch_bounds__(256) tp_bwd_rows_kernel(TPArgs g) {
   }
 }
 
+// Edge groups per receiver of the convolution kernels with C <= 64 channels: enough waves to
+// occupy the GPU (about four per SIMD, 4,096) when the graph has few receivers, at most 256
+// threads per workgroup and at most half the mean in-degree per group.
+inline int conv_edge_groups(int64_t n_rows, int64_t n_edges, int C) {
+  // 512 receivers x 8 edges with 32 channels: 29.0 us per forward + backward with four groups,
+  // 32.4 us with eight (measured on the standalone product of the benchmark's first configuration)
+  const int max_eg = C == 32 || C == 64 ? 4 : 1;
+  int eg = C == 32 ? 2 : 1;
+  const double deg = n_rows > 0 ? (double)n_edges / (double)n_rows : 0.0;
+  while (eg < max_eg && (double)n_rows * eg * C / 64.0 < 4096.0 && 2.0 * eg <= deg) eg *= 2;
+  return eg;
+}
+
+// The specialised convolution backward with C channels and EG edge groups; false (nothing
+// launched) when a full coupling-matrix chunk would not split evenly over the groups.
+template <int L1, int L2, int LO, bool SYM, int C, int EG>
+bool launch_bwd_conv(const TPArgs& g, dim3 grid, hipStream_t stream) {
+  if constexpr (bwd_conv_chunk<L1, L2, LO, SYM>() % (2 * EG) != 0) {
+    return false;
+  } else {
+    if (g.grad_in1) hipLaunchKernelGGL((tp_bwd_conv_kernel<L1, L2, LO, SYM, C, EG, true>), grid, dim3(C * EG), 0, stream, g);
+    else hipLaunchKernelGGL((tp_bwd_conv_kernel<L1, L2, LO, SYM, C, EG, false>), grid, dim3(C * EG), 0, stream, g);
+    return true;
+  }
+}
+
+template <int L1, int L2, int LO, bool SYM, int EG>
+void launch_fwd_groups(const TPArgs& g, dim3 grid, hipStream_t stream) {
+  using CF = TPConfig<L1, L2, LO, SYM>;
+  const size_t lds = sizeof(float) * (size_t)(EG - 1) * CF::NOUT * g.C;
+  hipLaunchKernelGGL((tp_fwd_kernel<L1, L2, LO, SYM, true, true, EG>), grid, dim3(g.C * EG), lds, stream, g);
+}
+
 // Host-side launcher for one configuration.
 template <int L1, int L2, int LO, bool SYM>
 int launch_tp(const TPArgs& g, bool conv, bool bwd, hipStream_t stream) {
@@ -631,23 +699,30 @@ int launch_tp(const TPArgs& g, bool conv, bool bwd, hipStream_t stream) {
   if (threads > 256) return FC_ERR_SHAPE;
   dim3 grid((unsigned)(conv ? xcd_grid(g.n_rows) : g.n_rows)), block(threads);
   const bool bc2 = conv && g.F2 == 1;
+  // edge groups for few-channel convolutions (one in2 channel, full-width in1)
+  const int eg0 = (bc2 && g.F1 == g.C && (g.C == 32 || g.C == 64)) ? conv_edge_groups(g.n_rows, g.n_edges, g.C) : 1;
   if (bwd) {
     const bool reduce = (g.grad_in1 && g.F1 == 1 && g.C > 1) || (g.grad_in2 && g.F2 == 1 && g.C > 1);
     const size_t per_edge = reduce ? sizeof(float) * (threads / 64) * (ncomp(L1) + ncomp(L2)) : 0;
     if constexpr (!SYM && L2 >= 1) {
       // interaction-layer shape: the compile-time specialisation
-      if (conv && bc2 && !g.reduced && !g.shared_w && g.grad_w && g.grad_in2 && g.F1 == g.C && threads == g.C &&
-          (g.C == 64 || g.C == 128)) {  // per-edge weights: the kernel reads w[e] rows
-        const bool n1 = g.grad_in1 != nullptr;
+      if (conv && bc2 && !g.reduced && !g.shared_w && g.grad_w && g.grad_in2 && g.F1 == g.C &&
+          (g.C == 32 || g.C == 64 || g.C == 128)) {  // per-edge weights: the kernel reads w[e] rows
+        bool done = false;
         if (g.C == 128) {
-          if (n1) hipLaunchKernelGGL((tp_bwd_conv_kernel<L1, L2, LO, SYM, 128, true>), grid, block, 0, stream, g);
-          else hipLaunchKernelGGL((tp_bwd_conv_kernel<L1, L2, LO, SYM, 128, false>), grid, block, 0, stream, g);
+          done = launch_bwd_conv<L1, L2, LO, SYM, 128, 1>(g, grid, stream);
+        } else if (g.C == 64) {
+          done = (eg0 >= 4 && launch_bwd_conv<L1, L2, LO, SYM, 64, 4>(g, grid, stream)) ||
+                 (eg0 >= 2 && launch_bwd_conv<L1, L2, LO, SYM, 64, 2>(g, grid, stream)) ||
+                 launch_bwd_conv<L1, L2, LO, SYM, 64, 1>(g, grid, stream);
         } else {
-          if (n1) hipLaunchKernelGGL((tp_bwd_conv_kernel<L1, L2, LO, SYM, 64, true>), grid, block, 0, stream, g);
-          else hipLaunchKernelGGL((tp_bwd_conv_kernel<L1, L2, LO, SYM, 64, false>), grid, block, 0, stream, g);
+          done = (eg0 >= 4 && launch_bwd_conv<L1, L2, LO, SYM, 32, 4>(g, grid, stream)) ||
+                 launch_bwd_conv<L1, L2, LO, SYM, 32, 2>(g, grid, stream);
         }
-        FC_LAUNCH_CHECK();
-        return FC_OK;
+        if (done) {
+          FC_LAUNCH_CHECK();
+          return FC_OK;
+        }
       }
     }
     if (conv) {
@@ -664,8 +739,14 @@ int launch_tp(const TPArgs& g, bool conv, bool bwd, hipStream_t stream) {
                          (per_edge * bwd_chunk<L1, L2, LO, SYM, false, false>()), stream, g);
     }
   } else {
+    // the forward's groups add their partial sums at the end: half as many groups measured as fast
+    // with 64 channels (water box, 1,536 receivers: 52 us with one group per receiver, 48 with two,
+    // 51 with four), as many as the backward with 32
+    const int eg = g.C == 64 ? (eg0 + 1) / 2 : eg0;
     if (conv) {
-      if (bc2) hipLaunchKernelGGL((tp_fwd_kernel<L1, L2, LO, SYM, true, true>), grid, block, 0, stream, g);
+      if (bc2 && eg >= 4) launch_fwd_groups<L1, L2, LO, SYM, 4>(g, grid, stream);
+      else if (bc2 && eg >= 2) launch_fwd_groups<L1, L2, LO, SYM, 2>(g, grid, stream);
+      else if (bc2) hipLaunchKernelGGL((tp_fwd_kernel<L1, L2, LO, SYM, true, true>), grid, block, 0, stream, g);
       else hipLaunchKernelGGL((tp_fwd_kernel<L1, L2, LO, SYM, true, false>), grid, block, 0, stream, g);
     } else {
       hipLaunchKernelGGL((tp_fwd_kernel<L1, L2, LO, SYM, false, false>), grid, block, 0, stream, g);
