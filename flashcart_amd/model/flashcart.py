@@ -178,15 +178,22 @@ class FlashCartPotential(AtomisticModel):
             edge_attrs, edge_feats, envelope = _ops.edge_geometry(
                 None, None, csr.idx_i, csr.idx_j, vectors, csr.rowptr, csr.sender_perm, csr.sender_ptr, *geo)
         node_feats = self.embedding(atom_types)
+        species = None
+        if vectors is None and want_pairs and not self.embedding.weight.requires_grad and self.interactions and \
+                fused.species_conv_applies(self.interactions[0], node_feats, self.embedding.weight.shape[0]):
+            # the first layer's sender features are embedding rows: species density (fused.species_conv).
+            # Its sender species and maps are queued before the pairing counters are read, so the GPU
+            # has them at hand when that read returns
+            first = self.interactions[0]
+            species = (torch.index_select(atom_types.to(torch.int32), 0, csr.idx_j), self.embedding.weight,
+                       fused.species_maps(first, self.embedding.weight, first.sqrt_avg_neighbors))
         if vectors is None and want_pairs:
             pairs = csr.edge_pairs(pair_shifts)
             if pairs is None and speculative:
                 edge_attrs, edge_feats, envelope = _ops.edge_geometry(
                     positions, sv, csr.idx_i, csr.idx_j, None, csr.rowptr, csr.sender_perm, csr.sender_ptr, *geo)
-        species = None
-        if pairs is not None and not self.embedding.weight.requires_grad:
-            # the first layer's sender features are embedding rows: species density (fused.species_conv)
-            species = (torch.index_select(atom_types.to(torch.int32), 0, csr.idx_j), self.embedding.weight)
+        if pairs is None:
+            species = None
         outputs = []
         shared = {}  # per-evaluation values the interaction layers share (their pair radial inputs)
         entry = None

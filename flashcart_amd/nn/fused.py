@@ -394,7 +394,7 @@ class _SpeciesConv(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, y: Tensor, x_pairs: Tensor, layer, graph, pairs, edge_species: Tensor,
-                table: Tensor, alpha_div: Tensor) -> Tensor:
+                table: Tensor, alpha_div: Tensor, maps=None) -> Tensor:
         path_counts["species"] += 1
         from flashcart_amd import _lib
         tp = layer.tp
@@ -404,7 +404,7 @@ class _SpeciesConv(torch.autograd.Function):
         h = _ops.radial_mlp_hidden_fwd(x_pairs, l0.weight, l0._scale, l1.weight, l1._scale)
         csr = _lib.csr_struct(graph.n_nodes, graph.n_edges, graph.idx_j, graph.rowptr, pair_slot=pairs.slot)
         dens = _ops.species_density_fwd(csr, lm, tp.in2_l_max, n_sp, edge_species, h, y, graph.n_nodes)
-        mats, cfg = species_maps(layer, table, alpha_div)
+        mats, cfg = maps if maps is not None else species_maps(layer, table, alpha_div)
         out = _ops.linear_fwd(dens, mats, *cfg)
         ctx.save_for_backward(y, x_pairs, h, edge_species, pairs.slot, *mats)
         ctx.layer, ctx.graph, ctx.cfg, ctx.n_sp = layer, graph, cfg, n_sp
@@ -417,7 +417,7 @@ class _SpeciesConv(torch.autograd.Function):
         y, x_pairs, h, edge_species, slot, *mats = ctx.saved_tensors
         layer, graph, cfg = ctx.layer, ctx.graph, ctx.cfg
         if not (ctx.needs_input_grad[0] or ctx.needs_input_grad[1]):
-            return (None,) * 8
+            return (None,) * 9
         g_dens = _ops.linear_bwd(g.contiguous(), mats, *cfg)
         csr = _lib.csr_struct(graph.n_nodes, graph.n_edges, graph.idx_j, graph.rowptr, pair_slot=slot)
         g_h, g_y = _ops.species_density_bwd(csr, cfg[0], layer.tp.in2_l_max, ctx.n_sp, edge_species, h, y, g_dens)
@@ -427,7 +427,7 @@ class _SpeciesConv(torch.autograd.Function):
             l0, l1 = layer.radial_mlp[0], layer.radial_mlp[2]
             # both edges of a pair read its h row: rows 2p and 2p + 1 of g_h summed in the kernel
             gx = _ops.radial_mlp_bwd_pairsum(g_h, x_pairs, l0.weight, l0._scale, l1.weight, l1._scale)
-        return (g_y if ctx.needs_input_grad[0] else None), gx, None, None, None, None, None, None
+        return (g_y if ctx.needs_input_grad[0] else None), gx, None, None, None, None, None, None, None
 
 
 MAX_DENSITY_SPECIES = 8
@@ -452,7 +452,8 @@ def species_conv_applies(layer, node_feats: Tensor, n_species: int) -> bool:
 
 
 def species_conv(layer, edge_attrs: Tensor, x_pairs: Tensor, graph, pairs, edge_species: Tensor,
-                 table: Tensor, alpha_div: Tensor) -> Tensor:
+                 table: Tensor, alpha_div: Tensor, maps=None) -> Tensor:
     """``table``: the embedding rows of the species (the layer's sender features are
-    linear_first(table)[species]); ``alpha_div``: the layer's ``sqrt_avg_neighbors``."""
-    return _SpeciesConv.apply(edge_attrs, x_pairs, layer, graph, pairs, edge_species, table, alpha_div)
+    linear_first(table)[species]); ``alpha_div``: the layer's ``sqrt_avg_neighbors``; ``maps``:
+    ``species_maps(layer, table, alpha_div)`` when the caller formed them already."""
+    return _SpeciesConv.apply(edge_attrs, x_pairs, layer, graph, pairs, edge_species, table, alpha_div, maps)

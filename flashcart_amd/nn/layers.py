@@ -192,9 +192,10 @@ class InteractionLayer(nn.Module):
         formed by the first layer that needs them and reused by the others.
         ``entry = (linear_first(node_feats), skip_projection(node_feats))`` from
         ``fused.entry_maps``, used on the paired path instead of evaluating both maps here.
-        ``species = (edge_species, table)``: ``node_feats`` is ``table[atom_types]`` and
-        ``edge_species[e]`` the sender's row of ``table``; with pairs the layer then runs as a
-        species density where ``fused.species_conv_applies``."""
+        ``species = (edge_species, table)`` or ``(edge_species, table, maps)``: ``node_feats`` is
+        ``table[atom_types]`` and ``edge_species[e]`` the sender's row of ``table``; with pairs the
+        layer then runs as a species density where ``fused.species_conv_applies`` (``maps``: its
+        ``fused.species_maps``, formed by the caller)."""
         idx_i, idx_j = edge_index[0], edge_index[1]
         residual_feats = node_feats if out_nodes is None else node_feats[:out_nodes]
         if edge_pairs is not None and graph is not None and fused.paired_conv_applies(self, node_feats):
@@ -207,7 +208,8 @@ class InteractionLayer(nn.Module):
             if species is not None and out_nodes is None and \
                     fused.species_conv_applies(self, node_feats, species[1].shape[0]):
                 mapped = fused.species_conv(self, edge_attrs, mlp_pairs, graph, edge_pairs, species[0],
-                                            species[1], self.sqrt_avg_neighbors)
+                                            species[1], self.sqrt_avg_neighbors,
+                                            species[2] if len(species) > 2 else None)
                 return self._finish(mapped, residual_feats, out_nodes, mapped=True)
             else:
                 in1 = entry[0] if entry is not None else self.linear_first(node_feats)
