@@ -356,7 +356,7 @@ def _cpu_rate(fn, units, budget_s=8.0):
 MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 MFMA
 
 
-def mfma_in_step(step, dev):
+def mfma_in_step(step, dev, launches=None):
     """In-step MFMA utilisation of the linear maps: ``step()`` (one energy+forces evaluation, run
     eagerly) under ``_ops.mfma_timer``, which brackets every MFMA kernel launch of the step with HIP
     events on its stream; achieved = the launches' algorithmic FLOPs (by formula from each call's
@@ -366,8 +366,11 @@ def mfma_in_step(step, dev):
         step()
     torch.cuda.synchronize(dev)
     groups = {}
-    for name, group, flops, e0, e1 in rec:
+    for name, group, flops, e0, e1, shape in rec:
         ms = e0.elapsed_time(e1)
+        if launches is not None:
+            launches.append({"entry_point": name, "family": group, "shape": shape, "gflop": flops / 1e9,
+                             "us": ms * 1e3, "tflops": flops / (ms * 1e-3) / 1e12})
         g = groups.setdefault(group, {"launches": 0, "flops": 0.0, "ms": 0.0})
         g["launches"] += 1
         g["flops"] += flops
@@ -719,6 +722,9 @@ def main():
                     help="with --workload cfg3_water_1536 / cfg5_molecules_512: time the graph replays only (no "
                          "eager timing, no separate dominant-kernel launches, no MFMA event step), for kernel traces "
                          "that hold exactly the timed path")
+    ap.add_argument("--mfma-launches", action="store_true",
+                    help="one energy+forces step on the first step graph with HIP events around every MFMA launch: "
+                         "prints each launch (entry point, shape, GFLOP, microseconds, TFLOP/s) as JSON lines")
     ap.add_argument("--no-configs", action="store_true",
                     help="measure only the metric's configuration (no lines for the other BASELINE configurations)")
     args = ap.parse_args()
@@ -750,6 +756,19 @@ def main():
         graphs = [sg.graph(k, dev) for k in range(8)]
         model, _ = build_model(graphs[0].edge_index.shape[1] / len(numbers))
         print(json.dumps({"power": power_per_kernel(model.to(dev), graphs, dev)}), flush=True)
+        return
+    if args.mfma_launches:
+        sg = StepGraphs(numbers, pos, cell, pbc, ["Cu", "Ni", "Fe", "Cr"], 1)
+        g = sg.graph(0, dev)
+        model, _ = build_model(g.edge_index.shape[1] / len(numbers))
+        model = model.to(dev)
+        for _ in range(3):
+            model.predict(g, compute_forces=True)
+        rows = []
+        summary = mfma_in_step(lambda: model.predict(g, compute_forces=True), dev, rows)
+        for r in rows:
+            print(json.dumps(r), flush=True)
+        print(json.dumps({"summary": {k: v for k, v in summary.items() if k != "method"}}), flush=True)
         return
     if args.kernel_only:
         sg = StepGraphs(numbers, pos, cell, pbc, ["Cu", "Ni", "Fe", "Cr"], 1)

@@ -36,18 +36,34 @@ def _linear_flops(args):
     return sum(2.0 * n * (2 * l + 1) * d.in_features * d.in_paths[l] * d.out_features for l in range(lm + 1))
 
 
+def _linear_shape(args):
+    d, n = args[0], int(args[1])
+    lm = min(d.in_l_max, d.out_l_max)
+    ks = [d.in_features * d.in_paths[l] for l in range(lm + 1)]
+    return f"rows n(2l+1), n={n}, l<={lm}, K per rank={ks}, N={d.out_features}"
+
+
+def _dense_shape(a):
+    return f"M={int(a[0])}, K={int(a[1])}, N={int(a[2])}"
+
+
 _MFMA_CALLS = {
-    "fc_linear_fwd": ("equivariant_linear", _linear_flops),
-    "fc_linear_dgrad": ("equivariant_linear", _linear_flops),
-    "fc_linear_wgrad": ("equivariant_linear", _linear_flops),
-    "fc_dense_fwd": ("dense", lambda a: 2.0 * a[0] * a[1] * a[2]),
-    "fc_dense_dgrad": ("dense", lambda a: 2.0 * a[0] * a[1] * a[2]),
-    "fc_dense_wgrad": ("dense", lambda a: 2.0 * a[0] * a[1] * a[2]),
-    "fc_dense_fwd_pairsum": ("dense", lambda a: 2.0 * a[0] * a[1] * a[2]),
-    "fc_radial_mlp_fwd": ("radial_mlp", lambda a: 2.0 * a[0] * (a[1] * 64 + 64 * 64 + 64 * a[7])),
-    "fc_radial_mlp_hidden_fwd": ("radial_mlp", lambda a: 2.0 * a[0] * (a[1] * 64 + 64 * 64)),
-    "fc_radial_mlp_bwd": ("radial_mlp", lambda a: 2.0 * a[0] * (2 * a[1] * 64 + 2 * 64 * 64)),
-    "fc_radial_mlp_bwd_pairsum": ("radial_mlp", lambda a: 2.0 * a[0] * (2 * a[1] * 64 + 2 * 64 * 64)),
+    "fc_linear_fwd": ("equivariant_linear", _linear_flops, _linear_shape),
+    "fc_linear_dgrad": ("equivariant_linear", _linear_flops, _linear_shape),
+    "fc_linear_wgrad": ("equivariant_linear", _linear_flops, _linear_shape),
+    "fc_dense_fwd": ("dense", lambda a: 2.0 * a[0] * a[1] * a[2], _dense_shape),
+    "fc_dense_dgrad": ("dense", lambda a: 2.0 * a[0] * a[1] * a[2], _dense_shape),
+    "fc_dense_wgrad": ("dense", lambda a: 2.0 * a[0] * a[1] * a[2], _dense_shape),
+    "fc_dense_fwd_pairsum": ("dense", lambda a: 2.0 * a[0] * a[1] * a[2],
+                             lambda a: f"pairs={int(a[0])}, K={int(a[1])} (summed row pair), N={int(a[2])}"),
+    "fc_radial_mlp_fwd": ("radial_mlp", lambda a: 2.0 * a[0] * (a[1] * 64 + 64 * 64 + 64 * a[7]),
+                          lambda a: f"rows={int(a[0])}, {int(a[1])}->64->64->{int(a[7])}"),
+    "fc_radial_mlp_hidden_fwd": ("radial_mlp", lambda a: 2.0 * a[0] * (a[1] * 64 + 64 * 64),
+                                 lambda a: f"rows={int(a[0])}, {int(a[1])}->64->64"),
+    "fc_radial_mlp_bwd": ("radial_mlp", lambda a: 2.0 * a[0] * (2 * a[1] * 64 + 2 * 64 * 64),
+                          lambda a: f"rows={int(a[0])}, 64->64->{int(a[1])} (hidden layers recomputed)"),
+    "fc_radial_mlp_bwd_pairsum": ("radial_mlp", lambda a: 2.0 * a[0] * (2 * a[1] * 64 + 2 * 64 * 64),
+                                  lambda a: f"pairs={int(a[0])}, 64->64->{int(a[1])} (hidden layers recomputed)"),
 }
 _mfma_record: Optional[list] = None
 
@@ -56,8 +72,8 @@ _mfma_record: Optional[list] = None
 def mfma_timer():
     """Within the context, every launch of an MFMA kernel family of the library (equivariant
     linear maps, dense layers, radial MLP) is bracketed by HIP events on the stream it runs on,
-    and (name, group, flops, start event, end event) is appended to the yielded list: the in-step
-    MFMA time and achieved FLOP/s of the linear maps (bench.py). Not during graph capture."""
+    and (name, group, flops, start event, end event, shape) is appended to the yielded list: the
+    in-step MFMA time and achieved FLOP/s of the linear maps (bench.py). Not during graph capture."""
     global _mfma_record
     prev, rec = _mfma_record, []
     _mfma_record = rec
@@ -71,13 +87,13 @@ def _lib_call(name: str, *args) -> None:
     lib = _lib.load()
     rec = _mfma_record
     if rec is not None and name in _MFMA_CALLS and not torch.cuda.is_current_stream_capturing():
-        group, flops = _MFMA_CALLS[name]
+        group, flops, shape = _MFMA_CALLS[name]
         stream = torch.cuda.current_stream()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         _lib.check(getattr(lib, name)(*args), name)
         e1.record(stream)
-        rec.append((name, group, float(flops(args)), e0, e1))
+        rec.append((name, group, float(flops(args)), e0, e1, shape(args)))
         return
     _lib.check(getattr(lib, name)(*args), name)
 
