@@ -20,6 +20,7 @@ c_int = ctypes.c_int
 c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64
 c_f32 = ctypes.c_float
+c_f64 = ctypes.c_double
 c_vp = ctypes.c_void_p
 c_cp = ctypes.c_char_p
 
@@ -52,6 +53,13 @@ class LinearDesc(ctypes.Structure):
     _fields_ = [
         ("in_l_max", c_i32), ("out_l_max", c_i32), ("in_features", c_i32), ("out_features", c_i32),
         ("in_paths", c_i32 * 4), ("weight", c_vp * 4), ("scale", c_f32 * 4),
+    ]
+
+
+class LinearDescF64(ctypes.Structure):
+    _fields_ = [
+        ("in_l_max", c_i32), ("out_l_max", c_i32), ("in_features", c_i32), ("out_features", c_i32),
+        ("in_paths", c_i32 * 4), ("weight", c_vp * 4), ("scale", c_f64 * 4),
     ]
 
 
@@ -104,6 +112,11 @@ _SIGNATURES = {
     "fc_linear_wgrad_workspace": (c_i64, [ctypes.POINTER(LinearDesc), c_i64, ctypes.POINTER(c_vp)]),
     "fc_linear_wgrad": (c_int, [ctypes.POINTER(LinearDesc), c_i64, c_vp, c_vp, c_f32, ctypes.POINTER(c_vp), c_vp,
                                 c_i64, c_vp]),
+    "fc_linear_fwd_f64": (c_int, [ctypes.POINTER(LinearDescF64), c_i64, c_vp, c_f64, c_vp, c_vp, c_vp]),
+    "fc_linear_dgrad_f64": (c_int, [ctypes.POINTER(LinearDescF64), c_i64, c_vp, c_f64, c_vp, c_vp, c_vp]),
+    "fc_linear_wgrad_f64_workspace": (c_i64, [ctypes.POINTER(LinearDescF64), c_i64, ctypes.POINTER(c_vp)]),
+    "fc_linear_wgrad_f64": (c_int, [ctypes.POINTER(LinearDescF64), c_i64, c_vp, c_vp, c_f64, ctypes.POINTER(c_vp),
+                                    c_vp, c_i64, c_vp]),
     "fc_dense_wgrad_workspace": (c_i64, [c_i64, c_i32, c_i32, c_i32]),
     "fc_dense_wgrad": (c_int, [c_i64, c_i32, c_i32, c_vp, c_vp, c_i32, c_vp, c_f32, c_vp, c_vp, c_vp, c_i64, c_vp]),
     "fc_segment_sum": (c_int, [c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp]),
@@ -217,8 +230,11 @@ def tp_desc(in1_l_max, in2_l_max, out_l_max, in1_features, in2_features, symmetr
 
 
 def linear_desc(in_l_max: int, out_l_max: int, in_features: int, out_features: int,
-                in_paths: Sequence[int], weights: Sequence[torch.Tensor], scale: Sequence[float]) -> LinearDesc:
-    d = LinearDesc()
+                in_paths: Sequence[int], weights: Sequence[torch.Tensor], scale: Sequence[float]):
+    """The descriptor of an equivariant linear map: ``LinearDescF64`` when the weights are float64
+    (the ``fc_linear_*_f64`` entry points), else ``LinearDesc``."""
+    f64 = len(weights) > 0 and weights[0].dtype == torch.float64
+    d = LinearDescF64() if f64 else LinearDesc()
     d.in_l_max, d.out_l_max, d.in_features, d.out_features = int(in_l_max), int(out_l_max), int(in_features), int(out_features)
     for l in range(4):
         d.in_paths[l] = int(in_paths[l]) if l < len(in_paths) else 1

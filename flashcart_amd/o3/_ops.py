@@ -713,6 +713,16 @@ def _wlist(w0, w1, w2, w3) -> List[Tensor]:
     return [w for w in (w0, w1, w2, w3) if w is not None]
 
 
+def _lin_dtype(t: Tensor) -> torch.dtype:
+    """Arithmetic type of a linear-map call: float64 tensors take the ``fc_linear_*_f64`` entry
+    points (float64 accumulation, as the reference's use_fp64), every other dtype must be float32."""
+    return torch.float64 if t.dtype == torch.float64 else torch.float32
+
+
+def _lin_name(name: str, dt: torch.dtype) -> str:
+    return name + "_f64" if dt == torch.float64 else name
+
+
 def _pad4(weights):
     ws = list(weights) + [None] * (4 - len(weights))
     if len(ws) != 4:
@@ -729,12 +739,13 @@ def linear_fwd_op(x: Tensor, w0: Tensor, w1: Optional[Tensor], w2: Optional[Tens
     in_dim, out_dim = _linear_dims(in_l_max, out_l_max, in_features, out_features, in_paths)
     if x.shape[-1] != in_dim:
         raise RuntimeError(f"Incorrect last dimension for x. Expected {in_dim}, got {x.shape[-1]}.")
-    x = _lib.contig("x", x)
-    ws = [_lib.contig(f"weight[{l}]", w) for l, w in enumerate(_wlist(w0, w1, w2, w3))]
+    dt = _lin_dtype(x)
+    x = _lib.contig("x", x, dt)
+    ws = [_lib.contig(f"weight[{l}]", w, dt) for l, w in enumerate(_wlist(w0, w1, w2, w3))]
     out = x.new_empty(x.shape[0], out_dim)
     r = _check_residual(residual, out)
     desc = _lib.linear_desc(in_l_max, out_l_max, in_features, out_features, in_paths, ws, scale)
-    _lib_call("fc_linear_fwd", desc, x.shape[0], x.data_ptr(), float(alpha), _lib.ptr(r), out.data_ptr(),
+    _lib_call(_lin_name("fc_linear_fwd", dt), desc, x.shape[0], x.data_ptr(), float(alpha), _lib.ptr(r), out.data_ptr(),
               _lib.stream_of(x))
     return out
 
@@ -752,12 +763,13 @@ def linear_bwd_op(grad_out: Tensor, w0: Tensor, w1: Optional[Tensor], w2: Option
                   scale: List[float], alpha: float = 1.0, residual: Optional[Tensor] = None) -> Tensor:
     """Input gradient of linear_fwd (the MFMA dgrad), plus ``residual`` when given."""
     in_dim, _ = _linear_dims(in_l_max, out_l_max, in_features, out_features, in_paths)
-    go = _lib.contig("grad_out", grad_out)
-    ws = [_lib.contig(f"weight[{l}]", w) for l, w in enumerate(_wlist(w0, w1, w2, w3))]
+    dt = _lin_dtype(grad_out)
+    go = _lib.contig("grad_out", grad_out, dt)
+    ws = [_lib.contig(f"weight[{l}]", w, dt) for l, w in enumerate(_wlist(w0, w1, w2, w3))]
     gx = go.new_empty(go.shape[0], in_dim)
     r = _check_residual(residual, gx)
     desc = _lib.linear_desc(in_l_max, out_l_max, in_features, out_features, in_paths, ws, scale)
-    _lib_call("fc_linear_dgrad", desc, go.shape[0], go.data_ptr(), float(alpha), _lib.ptr(r), gx.data_ptr(),
+    _lib_call(_lin_name("fc_linear_dgrad", dt), desc, go.shape[0], go.data_ptr(), float(alpha), _lib.ptr(r), gx.data_ptr(),
               _lib.stream_of(go))
     return gx
 
@@ -790,7 +802,7 @@ def _check_residual(residual: Optional[Tensor], out: Tensor) -> Optional[Tensor]
         return None
     if residual.shape != out.shape:
         raise RuntimeError(f"residual shape {tuple(residual.shape)} != output shape {tuple(out.shape)}.")
-    return _lib.contig("residual", residual)
+    return _lib.contig("residual", residual, out.dtype)
 
 
 def _linear_setup(ctx, inputs, output):
@@ -846,19 +858,21 @@ def linear_wgrad(grad_out: Tensor, x: Tensor, weights: List[Tensor], in_l_max: i
             in_off += m * k
             out_off += m * out_features
         return outs
-    go = _lib.contig("grad_out", grad_out)
-    xx = _lib.contig("x", x)
-    ws = [_lib.contig(f"weight[{l}]", w) for l, w in enumerate(weights)]
+    dt = _lin_dtype(grad_out)
+    go = _lib.contig("grad_out", grad_out, dt)
+    xx = _lib.contig("x", x, dt)
+    ws = [_lib.contig(f"weight[{l}]", w, dt) for l, w in enumerate(weights)]
     outs = [torch.empty_like(ws[l]) if (l <= common and need[l]) else None for l in range(len(ws))]
     desc = _lib.linear_desc(in_l_max, out_l_max, in_features, out_features, in_paths, ws, scale)
     lib = _lib.load()
     n = go.shape[0]
     ptrs = (_lib.c_vp * 4)(*([o.data_ptr() if o is not None else None for o in outs] + [None] * (4 - len(outs))))
-    n_ws = lib.fc_linear_wgrad_workspace(desc, n, ptrs)
+    ws_name = "fc_linear_wgrad_f64_workspace" if dt == torch.float64 else "fc_linear_wgrad_workspace"
+    n_ws = getattr(lib, ws_name)(desc, n, ptrs)
     if n_ws < 0:
-        _lib.check(-n_ws, "fc_linear_wgrad_workspace")
+        _lib.check(-n_ws, ws_name)
     buf = go.new_empty(max(int(n_ws), 1))
-    _lib_call("fc_linear_wgrad", desc, n, go.data_ptr(), xx.data_ptr(), float(alpha), ptrs, buf.data_ptr(),
+    _lib_call(_lin_name("fc_linear_wgrad", dt), desc, n, go.data_ptr(), xx.data_ptr(), float(alpha), ptrs, buf.data_ptr(),
               int(n_ws), _lib.stream_of(go))
     return outs
 
@@ -883,8 +897,6 @@ def _ref_linear_layout(x: Tensor, weights: List[Tensor], use_fp64: bool, dot_inp
     """The descriptor of the reference's metadata lists (make_linear_metadata, _linear.py:113-166):
     rank l of n active ranks has 2l+1 components, f_in_values[l] input columns (channels x paths)
     and f_out_values[l] = out_features outputs; returns (n, in_active_end, out_l_max, desc args)."""
-    if use_fp64:
-        raise NotImplementedError("flashcart_amd's linear kernels compute in float32 (use_fp64=False).")
     if dot_input_precision not in _PRECISIONS:
         raise ValueError(f"dot_input_precision must be one of {_PRECISIONS}. Provided: {dot_input_precision!r}.")
     n = len(in_offsets)
@@ -916,6 +928,22 @@ def _ref_linear_layout(x: Tensor, weights: List[Tensor], use_fp64: bool, dot_inp
     return n, i_off, out_l_max, fout
 
 
+def _widen(use_fp64: bool, *tensors):
+    """use_fp64 with float32 tensors (float64 accumulation, the reference's USE_FP64 kernels):
+    the tensors (lists of tensors too) as float64 copies, the map runs in float64 and its results
+    are rounded back to the inputs' dtype; otherwise the tensors unchanged."""
+    if not use_fp64:
+        return tensors
+    return tuple([t.double() for t in v] if isinstance(v, (list, tuple)) else
+                 (v.double() if v.dtype == torch.float32 else v) for v in tensors)
+
+
+def _narrow(t, dtype):
+    if isinstance(t, (list, tuple)):
+        return [v.to(dtype) for v in t]
+    return t.to(dtype)
+
+
 def _ref_desc(n, out_l_max, fout, f_in_values, weights, scale):
     return _lib.linear_desc(n - 1, out_l_max, 1, fout, [int(v) for v in f_in_values[:n]], weights[:n],
                             _scale_values(scale, n))
@@ -928,19 +956,22 @@ def linear_fwd_ref(x: Tensor, weights: List[Tensor], meta: Tensor, out_size: int
                    f_out_values: List[int], scale: Tensor) -> Tensor:
     """out_l = scale_l * x_l @ W_l^T for the active ranks, zeros above (the reference's op;
     ``meta`` holds the same columns as the lists and is not read)."""
+    dt0 = x.dtype
+    x, weights = _widen(use_fp64, x, weights)
     n, in_end, out_l_max, fout = _ref_linear_layout(x, weights, use_fp64, dot_input_precision, in_offsets,
                                                     out_offsets, weight_offsets, m_values, f_in_values,
                                                     f_out_values, out_size)
-    x = _lib.contig("x", x)
+    dt = _lin_dtype(x)
+    x = _lib.contig("x", x, dt)
     if n == 0:
-        return x.new_zeros(x.shape[0], int(out_size))
+        return x.new_zeros(x.shape[0], int(out_size), dtype=dt0)
     if x.shape[1] != in_end:  # input ranks above the output's: not read
         x = x[:, :in_end].contiguous()
-    ws = [_lib.contig(f"weight[{l}]", w) for l, w in enumerate(weights[:n])]
+    ws = [_lib.contig(f"weight[{l}]", w, dt) for l, w in enumerate(weights[:n])]
     out = x.new_empty(x.shape[0], int(out_size))
-    _lib_call("fc_linear_fwd", _ref_desc(n, out_l_max, fout, f_in_values, ws, scale), x.shape[0], x.data_ptr(),
-              1.0, None, out.data_ptr(), _lib.stream_of(x))
-    return out
+    _lib_call(_lin_name("fc_linear_fwd", dt), _ref_desc(n, out_l_max, fout, f_in_values, ws, scale), x.shape[0],
+              x.data_ptr(), 1.0, None, out.data_ptr(), _lib.stream_of(x))
+    return _narrow(out, dt0)
 
 
 @linear_fwd_ref.register_fake
@@ -951,10 +982,11 @@ def _(x, weights, meta, out_size, use_fp64, dot_input_precision, in_offsets, out
 
 def _ref_grad_x(grad_out, x, ws, n, in_end, fout, f_in_values, scale):
     """scale_l * go_l @ W_l into the active input columns, zeros beyond."""
-    go = _lib.contig("grad_out", grad_out)
+    dt = _lin_dtype(grad_out)
+    go = _lib.contig("grad_out", grad_out, dt)
     out_l_max = int(round((go.shape[1] / fout) ** 0.5)) - 1
     gx = go.new_empty(go.shape[0], in_end)
-    _lib_call("fc_linear_dgrad", _ref_desc(n, out_l_max, fout, f_in_values, ws, scale), go.shape[0],
+    _lib_call(_lin_name("fc_linear_dgrad", dt), _ref_desc(n, out_l_max, fout, f_in_values, ws, scale), go.shape[0],
               go.data_ptr(), 1.0, None, gx.data_ptr(), _lib.stream_of(go))
     if x.shape[1] != in_end:
         gx = torch.cat([gx, gx.new_zeros(gx.shape[0], x.shape[1] - in_end)], dim=1)
@@ -963,7 +995,7 @@ def _ref_grad_x(grad_out, x, ws, n, in_end, fout, f_in_values, scale):
 
 def _ref_grad_w(grad_out, b, ws, n, in_end, fout, f_in_values, scale):
     """scale_l * sum over rows of go_l^T b_l for every active rank (split-K MFMA)."""
-    b = _lib.contig("x", b)
+    b = _lib.contig("x", b, _lin_dtype(b))
     if b.shape[1] != in_end:
         b = b[:, :in_end].contiguous()
     out_l_max = int(round((grad_out.shape[1] / fout) ** 0.5)) - 1
@@ -978,13 +1010,24 @@ def linear_bwd_ref(grad_out: Tensor, x: Tensor, weights: List[Tensor], need_x: b
                    weight_offsets: List[int], m_values: List[int], f_in_values: List[int],
                    f_out_values: List[int], scale: Tensor) -> Tuple[Tensor, List[Tensor]]:
     """(grad_x, grad_weights) of linear_fwd, empty (0,) tensors for the unrequested ones."""
+    if use_fp64 and x.dtype != torch.float64:
+        gx, gws = linear_bwd_ref_impl(*_widen(True, grad_out, x, weights), need_x, need_weight, True,
+                                      dot_input_precision, in_offsets, out_offsets, weight_offsets, m_values,
+                                      f_in_values, f_out_values, scale)
+        return _narrow(gx, x.dtype), [g.to(w.dtype) for g, w in zip(gws, weights)]
+    return linear_bwd_ref_impl(grad_out, x, weights, need_x, need_weight, use_fp64, dot_input_precision, in_offsets,
+                               out_offsets, weight_offsets, m_values, f_in_values, f_out_values, scale)
+
+
+def linear_bwd_ref_impl(grad_out, x, weights, need_x, need_weight, use_fp64, dot_input_precision, in_offsets,
+                        out_offsets, weight_offsets, m_values, f_in_values, f_out_values, scale):
     n, in_end, _, fout = _ref_linear_layout(x, weights, use_fp64, dot_input_precision, in_offsets, out_offsets,
                                             weight_offsets, m_values, f_in_values, f_out_values)
     if n == 0 or not (need_x or need_weight):
         gx = torch.zeros_like(x) if need_x else x.new_empty((0,))
         gws = [torch.zeros_like(w) for w in weights] if need_weight else [w.new_empty(0) for w in weights]
         return gx, gws
-    ws = [_lib.contig(f"weight[{l}]", w) for l, w in enumerate(weights[:n])]
+    ws = [_lib.contig(f"weight[{l}]", w, _lin_dtype(x)) for l, w in enumerate(weights[:n])]
     gx = _ref_grad_x(grad_out, x, ws, n, in_end, fout, f_in_values, scale) if need_x else x.new_empty((0,))
     if need_weight:
         gws = _ref_grad_w(grad_out, x, ws, n, in_end, fout, f_in_values, scale)
@@ -1010,21 +1053,34 @@ def linear_dbwd_ref(grad_out: Tensor, x: Tensor, weights: List[Tensor], v_grad_x
                     scale: Tensor) -> Tuple[Tensor, Tensor, List[Tensor]]:
     """Backward of linear_bwd along cotangents (v_grad_x, v_grad_weight):
     d grad_out_l = s_l (v_gx_l W_l^T + x_l v_gW_l^T), d x_l = s_l go_l v_gW_l, d W_l = s_l go_l^T v_gx_l."""
+    args = (need_d_grad_out, need_d_x, need_d_weight, has_v_grad_x, has_v_grad_weight, in_offsets, out_offsets,
+            weight_offsets, m_values, f_in_values, f_out_values, scale)
+    if use_fp64 and x.dtype != torch.float64:
+        go64, x64, w64, vgx64, vgw64 = _widen(True, grad_out, x, weights, v_grad_x, v_grad_weight)
+        d_go, d_x, d_ws = linear_dbwd_ref_impl(go64, x64, w64, vgx64, vgw64, True, dot_input_precision, *args)
+        return _narrow(d_go, grad_out.dtype), _narrow(d_x, x.dtype), [d.to(w.dtype) for d, w in zip(d_ws, weights)]
+    return linear_dbwd_ref_impl(grad_out, x, weights, v_grad_x, v_grad_weight, use_fp64, dot_input_precision, *args)
+
+
+def linear_dbwd_ref_impl(grad_out, x, weights, v_grad_x, v_grad_weight, use_fp64, dot_input_precision,
+                         need_d_grad_out, need_d_x, need_d_weight, has_v_grad_x, has_v_grad_weight, in_offsets,
+                         out_offsets, weight_offsets, m_values, f_in_values, f_out_values, scale):
     n, in_end, _, fout = _ref_linear_layout(x, weights, use_fp64, dot_input_precision, in_offsets, out_offsets,
                                             weight_offsets, m_values, f_in_values, f_out_values)
-    go = _lib.contig("grad_out", grad_out)
-    ws = [_lib.contig(f"weight[{l}]", w) for l, w in enumerate(weights[:n])]
-    vws = [_lib.contig(f"v_grad_weight[{l}]", v) for l, v in enumerate(v_grad_weight[:n])] if has_v_grad_weight \
-        else []
+    dt = _lin_dtype(x)
+    go = _lib.contig("grad_out", grad_out, dt)
+    ws = [_lib.contig(f"weight[{l}]", w, dt) for l, w in enumerate(weights[:n])]
+    vws = [_lib.contig(f"v_grad_weight[{l}]", v, dt) for l, v in enumerate(v_grad_weight[:n])] \
+        if has_v_grad_weight else []
     out_l_max = int(round((go.shape[1] / max(fout, 1)) ** 0.5)) - 1
 
     def fwd(inp, mats, residual=None):
-        a = _lib.contig("input", inp)
+        a = _lib.contig("input", inp, dt)
         if a.shape[1] != in_end:
             a = a[:, :in_end].contiguous()
         out = a.new_empty(a.shape[0], go.shape[1])
-        _lib_call("fc_linear_fwd", _ref_desc(n, out_l_max, fout, f_in_values, mats, scale), a.shape[0],
-                  a.data_ptr(), 1.0, _lib.ptr(residual), out.data_ptr(), _lib.stream_of(a))
+        _lib_call(_lin_name("fc_linear_fwd", dt), _ref_desc(n, out_l_max, fout, f_in_values, mats, scale),
+                  a.shape[0], a.data_ptr(), 1.0, _lib.ptr(residual), out.data_ptr(), _lib.stream_of(a))
         return out
 
     if not need_d_grad_out:

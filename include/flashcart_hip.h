@@ -334,6 +334,29 @@ int64_t fc_linear_wgrad_workspace(const fc_linear_desc* desc, int64_t n_rows, fl
 int fc_linear_wgrad(const fc_linear_desc* desc, int64_t n_rows, const float* grad_out, const float* x,
                     float alpha, float* const* grad_w, float* workspace, int64_t workspace_floats,
                     void* stream);
+/* Float64 equivariant linear map: replaces the reference's linear_fwd / linear_bwd called with
+ * float64 tensors (use_fp64 = True, float64 accumulation: src/flashcart/o3/_linear.py:328-343,
+ * :382, :457-538, selected by dtype in src/flashcart/o3/utils.py:36-50). Same layout, residual
+ * and zero-fill rules as the float32 entry points above, with float64 weights, scales and
+ * data. fc_linear_wgrad_f64 splits the row reduction over workgroups when
+ * fc_linear_wgrad_f64_workspace() > 0 doubles (partial sums added in a fixed order). */
+typedef struct fc_linear_desc_f64 {
+  int32_t in_l_max, out_l_max;
+  int32_t in_features, out_features;
+  int32_t in_paths[4];
+  const double* weight[4];   /* W_l, row-major (out_features, in_features*in_paths[l]) */
+  double scale[4];
+} fc_linear_desc_f64;
+
+int fc_linear_fwd_f64(const fc_linear_desc_f64* desc, int64_t n_rows, const double* x, double alpha,
+                      const double* residual, double* out, void* stream);
+int fc_linear_dgrad_f64(const fc_linear_desc_f64* desc, int64_t n_rows, const double* grad_out, double alpha,
+                        const double* residual, double* grad_x, void* stream);
+int64_t fc_linear_wgrad_f64_workspace(const fc_linear_desc_f64* desc, int64_t n_rows, double* const* grad_w);
+int fc_linear_wgrad_f64(const fc_linear_desc_f64* desc, int64_t n_rows, const double* grad_out, const double* x,
+                        double alpha, double* const* grad_w, double* workspace, int64_t workspace_doubles,
+                        void* stream);
+
 /* grad_w (m, k) = scale * g^T x and grad_b (m, may be NULL) = column sums of g, with
  * g = grad_out * act'(pre_act) (act 1) or grad_out (act 0). */
 int64_t fc_dense_wgrad_workspace(int64_t n, int32_t k, int32_t m, int32_t with_bias);

@@ -483,8 +483,6 @@ def test_reference_linear_ops(lin, lout, fin, fout, in_paths):
     for k, (a, b) in enumerate(zip(got2, want2)):
         b = torch.zeros_like(a).double().cpu() if b is None else b
         _close(torch.zeros_like(b) if a is None else a, b, f"linear_dbwd input {k}")
-    with pytest.raises(NotImplementedError):
-        torch.ops.flashcart.linear_fwd(x, ws, lay.meta, lay.out_dim, True, "ieee", *lay.meta_lists, lay.scale)
     with pytest.raises(ValueError, match="dot_input_precision"):
         torch.ops.flashcart.linear_fwd(x, ws, lay.meta, lay.out_dim, False, "bf16", *lay.meta_lists, lay.scale)
 
