@@ -107,6 +107,8 @@ _SIGNATURES = {
     "fc_species_density_fwd": (c_int, [ctypes.POINTER(CSR), c_i32, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "fc_species_density_bwd": (c_int, [ctypes.POINTER(CSR), c_i32, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                        c_vp]),
+    "fc_species_maps": (c_int, [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp, c_f32, c_vp, ctypes.POINTER(c_vp),
+                                c_vp, ctypes.POINTER(c_vp), c_vp]),
     "fc_radial_mlp_bwd_pairsum": (c_int, [c_i64, c_i32, c_vp, c_vp, c_f32, c_vp, c_f32, c_vp, c_vp, c_vp]),
     "fc_radial_mlp_bwd": (c_int, [c_i64, c_i32, c_vp, c_vp, c_f32, c_vp, c_f32, c_vp, c_vp, c_vp]),
     "fc_linear_wgrad_workspace": (c_i64, [ctypes.POINTER(LinearDesc), c_i64, ctypes.POINTER(c_vp)]),

@@ -204,9 +204,122 @@ static int dispatch_species(int l_max, bool bwd, int64_t n_rows, int n_species, 
   return FC_ERR_UNSUPPORTED_L;
 }
 
+// The matrices of the species density's layer map, all ranks in one launch (they are formed
+// from the parameters at every evaluation, so a replayed graph sees weights written in place):
+//   x[Z, c] = s_first / *alpha_div * sum_j table[Z, j] w_first[c, j]
+//   maps[l][o, Z * nh + k] = sum_c w_second[l][o, c] x[Z, c] w_radial[(l * c_mid + c) * nh + k]
+// Workgroup (o block of 16, Z, l). x[Z, :] goes to LDS (four threads per row of w_first, each a
+// quarter of the row); per chunk of 128 c, the chunk's w_radial rows and the block's w_second
+// columns are staged in LDS by all threads at once (the first chunk together with the table row),
+// and each thread forms four outputs (o = o0 + t / 16, k = t % 16 + 16 j) from LDS. A few global
+// round trips in all: the kernel is latency-bound (tens of workgroups).
+struct SpeciesMapsArgs {
+  const float* table;
+  const float* w_first;
+  const float* alpha_div;
+  const float* w_second[4];
+  const float* w_radial;
+  float* maps[4];
+  float s_first;
+  int c_in, c_mid, c_out, nh, n_species;
+};
+
+constexpr int kMapsMaxMid = 1024, kMapsMaxIn = 1024, kMapsChunk = 128;
+
+__global__ void __launch_bounds__(256) species_maps_kernel(SpeciesMapsArgs a) {
+  __shared__ float xs[kMapsMaxMid];
+  __shared__ float tb[kMapsMaxIn];
+  __shared__ float w2s[kMapsChunk * 64];
+  __shared__ float wss[16 * kMapsChunk];
+  const int t = threadIdx.x, Z = blockIdx.y, l = blockIdx.z;
+  const int ol = t >> 4, o = blockIdx.x * 16 + ol;
+  const float* w2 = a.w_radial + (int64_t)l * a.c_mid * a.nh;
+  const float* ws = a.w_second[l];
+  // chunk c0 of w_radial's rows and of the block's w_second columns into LDS
+  auto stage = [&](int c0, int cn) {
+    for (int i = t; i < cn * a.nh; i += 256) w2s[i] = w2[(int64_t)c0 * a.nh + i];
+    for (int i = t; i < 16 * cn; i += 256) {
+      const int r = i / cn, cc = i - r * cn, oo = blockIdx.x * 16 + r;
+      wss[r * kMapsChunk + cc] = oo < a.c_out ? ws[(int64_t)oo * a.c_mid + c0 + cc] : 0.f;
+    }
+  };
+  // the first chunk loads together with the table row (neither depends on x)
+  for (int j = t; j < a.c_in; j += 256) tb[j] = a.table[(int64_t)Z * a.c_in + j];
+  stage(0, a.c_mid < kMapsChunk ? a.c_mid : kMapsChunk);
+  const float div = *a.alpha_div;
+  __syncthreads();
+  // x: four threads per row of w_first, thread q of a row taking the row's quarter q
+  const int q = t & 3, qn = (a.c_in + 3) / 4, j0 = q * qn, j1 = j0 + qn < a.c_in ? j0 + qn : a.c_in;
+  for (int c0 = 0; c0 < a.c_mid; c0 += 64) {
+    const int c = c0 + (t >> 2);
+    float d = 0.f;
+    if (c < a.c_mid) {
+      const float* wr = a.w_first + (int64_t)c * a.c_in;
+      for (int j = j0; j < j1; ++j) d = fmaf(tb[j], wr[j], d);
+    }
+    d += __shfl_xor(d, 1, 64);
+    d += __shfl_xor(d, 2, 64);
+    if (q == 0 && c < a.c_mid) xs[c] = d * a.s_first / div;
+  }
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int c0 = 0; c0 < a.c_mid; c0 += kMapsChunk) {
+    const int cn = a.c_mid - c0 < kMapsChunk ? a.c_mid - c0 : kMapsChunk;
+    if (c0 > 0) {
+      __syncthreads();  // the previous chunk consumed
+      stage(c0, cn);
+    }
+    __syncthreads();  // x and this chunk in LDS
+    for (int cc = 0; cc < cn; ++cc) {
+      const float wx = wss[ol * kMapsChunk + cc] * xs[c0 + cc];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int k = (t & 15) + 16 * j;
+        if (k < a.nh) acc[j] = fmaf(wx, w2s[cc * a.nh + k], acc[j]);
+      }
+    }
+  }
+  if (o >= a.c_out) return;
+  float* mr = a.maps[l] + (int64_t)o * a.n_species * a.nh + (int64_t)Z * a.nh;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int k = (t & 15) + 16 * j;
+    if (k < a.nh) mr[k] = acc[j];
+  }
+}
+
 }  // namespace fc
 
 using namespace fc;
+
+extern "C" int fc_species_maps(int32_t n_species, int32_t c_in, int32_t c_mid, int32_t c_out, int32_t n_hidden,
+                               int32_t n_ranks, const float* table, const float* w_first, float s_first,
+                               const float* alpha_div, const float* const* w_second, const float* w_radial,
+                               float* const* maps, void* stream) {
+  if (n_species < 1 || n_species > kSpeciesMax || c_in < 1 || c_out < 1 || n_hidden < 1) return FC_ERR_SHAPE;
+  if (c_mid < 1 || c_mid > kMapsMaxMid || c_in > kMapsMaxIn || n_hidden > 64) return FC_ERR_SHAPE;
+  if (n_ranks < 1 || n_ranks > 4) return FC_ERR_UNSUPPORTED_L;
+  if (!table || !w_first || !alpha_div || !w_second || !w_radial || !maps) return FC_ERR_NULL;
+  SpeciesMapsArgs a{};
+  for (int l = 0; l < n_ranks; ++l) {
+    if (!w_second[l] || !maps[l]) return FC_ERR_NULL;
+    a.w_second[l] = w_second[l];
+    a.maps[l] = maps[l];
+  }
+  a.table = table;
+  a.w_first = w_first;
+  a.alpha_div = alpha_div;
+  a.w_radial = w_radial;
+  a.s_first = s_first;
+  a.c_in = c_in;
+  a.c_mid = c_mid;
+  a.c_out = c_out;
+  a.nh = n_hidden;
+  a.n_species = n_species;
+  hipLaunchKernelGGL(species_maps_kernel, dim3((unsigned)((c_out + 15) / 16), (unsigned)n_species, (unsigned)n_ranks),
+                     dim3(256), 0, (hipStream_t)stream, a);
+  FC_LAUNCH_CHECK();
+  return FC_OK;
+}
 
 static int check_species(const fc_csr* gr, int32_t l_max, int32_t y_l_max, int32_t n_species) {
   if (!gr) return FC_ERR_NULL;

@@ -358,23 +358,17 @@ def species_maps(layer, table: Tensor, alpha_div: Tensor):
         M_l[o, Z * 64 + k] = sum_c Wsec_l[o, c] x_table[Z, c] W2[l C + c, k],
         scale_l = s2 s_l,
     so that linear_second(TP(...) / s)_l = scale_l dens_l @ M_l^T (the path (0, l, l) takes block l
-    of the radial output layer W2). Formed on the device at every call (a few small launches,
-    no host synchronisation) from the parameters as they are at that moment, so weights written
-    in place by any route (``param.data.copy_`` included, which no version counter records) are
-    always seen; under graph capture the computation is recorded and replayed."""
-    tp, lin, w2 = layer.tp, layer.linear_second, layer.radial_mlp[4].weight
-    c = tp.in1_features
+    of the radial output layer W2). Formed on the device at every call (one launch of
+    ``fc_species_maps``, no host synchronisation) from the parameters as they are at that moment, so
+    weights written in place by any route (``param.data.copy_`` included, which no version counter
+    records) are always seen; under graph capture the launch is recorded and replayed."""
+    tp, lin, first = layer.tp, layer.linear_second, layer.linear_first
     lm = min(tp.in2_l_max, tp.out_l_max)
     common = min(lm, lin.out_l_max)
-    with torch.no_grad():
-        x_table = layer.linear_first(table) / alpha_div.detach().reshape(1, 1)
-    n_sp = x_table.shape[0]
-    mats = []
-    for l in range(common + 1):
-        # Bt[(Z, k), c] = x_table[Z, c] W2[l C + c, k]; M_l = Wsec_l @ Bt^T on the MFMA dense kernel
-        bt = (x_table.unsqueeze(1) * w2[l * c:(l + 1) * c].t().unsqueeze(0)).reshape(n_sp * 64, c).contiguous()
-        m, _ = _ops.dense_fwd(lin.weight[l].detach(), bt, None, 1.0, 0)
-        mats.append(m.contiguous())
+    n_sp = table.shape[0]
+    mats = _ops.species_maps(table.detach(), first.weight[0].detach(), first._scale_list[0], alpha_div,
+                             [lin.weight[l].detach() for l in range(common + 1)],
+                             layer.radial_mlp[4].weight.detach())
     s2 = layer.radial_mlp[4]._scale
     cfg = (lm, lin.out_l_max, 64, lin.out_features, [n_sp] * (lm + 1),
            [s2 * lin._scale_list[l] for l in range(common + 1)])

@@ -1434,6 +1434,27 @@ def species_density_bwd(csr, l_max: int, y_l_max: int, n_species: int, edge_spec
     return g_h, g_y
 
 
+def species_maps(table: Tensor, w_first: Tensor, s_first: float, alpha_div: Tensor, w_second: List[Tensor],
+                 w_radial: Tensor) -> List[Tensor]:
+    """Per rank l < len(w_second): maps[l][o, Z * nh + k] = sum_c w_second[l][o, c] x[Z, c]
+    w_radial[l * c_mid + c, k] with x = s_first * table @ w_first^T / alpha_div (``fc_species_maps``,
+    one launch; alpha_div a one-element device tensor)."""
+    tb, wf, wr = _lib.contig("table", table), _lib.contig("w_first", w_first), _lib.contig("w_radial", w_radial)
+    ws = [_lib.contig(f"w_second[{l}]", w) for l, w in enumerate(w_second)]
+    div = _lib.contig("alpha_div", alpha_div.detach().reshape(-1)[:1])
+    n_sp, c_in = tb.shape
+    c_mid, nh, c_out, n = wf.shape[0], wr.shape[1], ws[0].shape[0], len(ws)
+    if wf.shape[1] != c_in or wr.shape[0] < n * c_mid or any(tuple(w.shape) != (c_out, c_mid) for w in ws):
+        raise RuntimeError("species_maps: inconsistent shapes.")
+    out = tb.new_empty(n, c_out, n_sp * nh)
+    mats = [out[l] for l in range(n)]
+    wp = (_lib.c_vp * 4)(*([w.data_ptr() for w in ws] + [None] * (4 - n)))
+    mp = (_lib.c_vp * 4)(*([m.data_ptr() for m in mats] + [None] * (4 - n)))
+    _lib_call("fc_species_maps", int(n_sp), int(c_in), int(c_mid), int(c_out), int(nh), int(n), tb.data_ptr(),
+              wf.data_ptr(), float(s_first), div.data_ptr(), wp, wr.data_ptr(), mp, _lib.stream_of(tb))
+    return mats
+
+
 def dense_wgrad(grad_out: Tensor, pre: Optional[Tensor], act: int, x: Tensor, scale: float, need_weight: bool,
                 need_bias: bool) -> Tuple[Optional[Tensor], Optional[Tensor]]:
     """(scale * g^T x, column sums of g) with g = grad_out * act'(pre) (act 1) or grad_out

@@ -192,6 +192,19 @@ int fc_species_density_fwd(const fc_csr* graph, int32_t l_max, int32_t y_l_max, 
 int fc_species_density_bwd(const fc_csr* graph, int32_t l_max, int32_t y_l_max, int32_t n_species,
                            const int32_t* edge_species, const float* h, const float* y, const float* g_dens,
                            float* g_h, float* g_y, void* stream);
+/* The matrices of that layer map, one launch for all ranks l < n_ranks (no counterpart in the
+ * reference; they fold the first layer's linear_first, radial output layer and linear_second,
+ * reference nn/layers.py:351-369, into one matrix per rank):
+ *   x[Z, c] = s_first / *alpha_div * sum_j table[Z, j] w_first[c, j]
+ *   maps[l][o, Z * n_hidden + k] = sum_c w_second[l][o, c] x[Z, c] w_radial[(l * c_mid + c) * n_hidden + k]
+ * table (n_species, c_in) the species' sender features, w_first (c_mid, c_in), w_second[l] (c_out, c_mid),
+ * w_radial (n_ranks * c_mid, n_hidden) the radial output layer's rows of paths (0, l, l), maps[l]
+ * (c_out, n_species * n_hidden); alpha_div a device scalar (the layer's sqrt_avg_neighbors).
+ * Limits: n_species <= 8, c_in and c_mid <= 1024, n_hidden <= 64, n_ranks <= 4. */
+int fc_species_maps(int32_t n_species, int32_t c_in, int32_t c_mid, int32_t c_out, int32_t n_hidden,
+                    int32_t n_ranks, const float* table, const float* w_first, float s_first,
+                    const float* alpha_div, const float* const* w_second, const float* w_radial,
+                    float* const* maps, void* stream);
 
 /* rowptr[n] = first edge with idx_sorted[e] >= n, for n in [0, n_nodes]. */
 int fc_csr_from_sorted(int64_t n_edges, const int32_t* idx_sorted, int64_t n_nodes,

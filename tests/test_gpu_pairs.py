@@ -393,6 +393,28 @@ def test_species_density_op(l_max, y_l_max):
     assert_close(g_y, want_y, 1e-5, 1e-5, "dL/dy")
 
 
+@pytest.mark.parametrize("n_sp,c_in,c_mid,c_out,nh,n_ranks", [(4, 128, 128, 128, 64, 4), (2, 64, 64, 64, 64, 3),
+                                                              (3, 20, 40, 24, 48, 1), (8, 16, 100, 17, 64, 2)])
+def test_species_maps_op(n_sp, c_in, c_mid, c_out, nh, n_ranks):
+    """fc_species_maps (every rank in one launch) against its definition in float64: the species'
+    sender features s table W_first^T / alpha_div, then per rank sum_c W_second[o, c] x[Z, c] W2[l c_mid + c, k];
+    partial o blocks and hidden widths below 64 included."""
+    from flashcart_amd.o3 import _ops
+    gen = torch.Generator(device=DEV).manual_seed(n_sp + c_mid)
+    table = torch.randn(n_sp, c_in, device=DEV, generator=gen)
+    wf = torch.randn(c_mid, c_in, device=DEV, generator=gen)
+    ws = [torch.randn(c_out, c_mid, device=DEV, generator=gen) for _ in range(n_ranks)]
+    w2 = torch.randn(n_ranks * c_mid + 5, nh, device=DEV, generator=gen)
+    div = torch.tensor([6.5], device=DEV)
+    mats = _ops.species_maps(table, wf, 0.125, div, ws, w2)
+    x = 0.125 * table.double() @ wf.double().t() / 6.5                       # (Z, c)
+    for l in range(n_ranks):
+        blk = w2.double()[l * c_mid:(l + 1) * c_mid]                          # (c, k)
+        want = torch.einsum("oc,zc,ck->ozk", ws[l].double(), x, blk).reshape(c_out, n_sp * nh)
+        assert mats[l].shape == (c_out, n_sp * nh)
+        assert_close(mats[l], want, 1e-5, 1e-5 * float(want.abs().max()), f"species map rank {l}")
+
+
 def test_species_conv_matches_paired_conv():
     """The first interaction layer as a species density (linear_second folded in) against the same
     layer over edge pairs followed by linear_second: outputs and input gradients (edge attributes,
