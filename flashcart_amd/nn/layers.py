@@ -171,12 +171,6 @@ class InteractionLayer(nn.Module):
             self.emb_i = None
             self.emb_j = None
 
-    @property
-    def _sqrt_avg(self) -> float:
-        """sqrt_avg_neighbors as a Python float (a host read; the kernels divide by the buffer on the
-        device, so the forward pass never needs this value)."""
-        return float(self.sqrt_avg_neighbors.detach().float())
-
     def forward(self, node_feats: torch.Tensor, edge_attrs: torch.Tensor, edge_feats: torch.Tensor,
                 edge_index: torch.Tensor, envelope: torch.Tensor, atom_types: Optional[torch.Tensor] = None,
                 out_nodes: Optional[int] = None, graph: Optional[GraphCSR] = None,

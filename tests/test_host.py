@@ -202,7 +202,7 @@ def test_checkpoint_round_trip(tmp_path):
     m2 = FlashCartPotential.from_checkpoint(tmp_path)
     for (k, a), (k2, b) in zip(m.state_dict().items(), m2.state_dict().items()):
         assert k == k2 and torch.equal(a, b)
-    assert m2.interactions[0]._sqrt_avg == m.interactions[0]._sqrt_avg
+    assert torch.equal(m2.interactions[0].sqrt_avg_neighbors, m.interactions[0].sqrt_avg_neighbors)
 
 
 def test_device_neighbor_list_host_fallback_decision():
