@@ -766,6 +766,8 @@ __global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 
 #pragma unroll
           for (int j = 0; j < FN; ++j) acc[i][j][v] += rv[i][v][j];
     }
+    // nontemporal stores: the output streams to HBM without displacing the operands the next
+    // tiles read from L2 (K = 128 maps 77 -> 81 TFLOP/s alone; 25k-atom step 26.31 -> 26.14 ms)
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -773,7 +775,7 @@ __global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 
         if (!rok[i][v]) continue;
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          if (all_cols || col0 + j * MI < N) *d_at(roff[i][v], j) = acc[i][j][v];
+          if (all_cols || col0 + j * MI < N) __builtin_nontemporal_store(acc[i][j][v], d_at(roff[i][v], j));
       }
   };
 
