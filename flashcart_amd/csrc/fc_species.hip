@@ -222,21 +222,38 @@ struct SpeciesMapsArgs {
   float* maps[4];
   float s_first;
   int c_in, c_mid, c_out, nh, n_species;
+  bool x_vec;   // c_in a multiple of 16 and w_first 16-byte aligned: rows read as float4
+  bool st_vec;  // c_mid and nh multiples of 4, w_radial and w_second 16-byte aligned: staged as float4
 };
 
 constexpr int kMapsMaxMid = 1024, kMapsMaxIn = 1024, kMapsChunk = 128;
 
 __global__ void __launch_bounds__(256) species_maps_kernel(SpeciesMapsArgs a) {
   __shared__ float xs[kMapsMaxMid];
-  __shared__ float tb[kMapsMaxIn];
-  __shared__ float w2s[kMapsChunk * 64];
-  __shared__ float wss[16 * kMapsChunk];
+  __shared__ __attribute__((aligned(16))) float tb[kMapsMaxIn];
+  __shared__ __attribute__((aligned(16))) float w2s[kMapsChunk * 64];
+  __shared__ __attribute__((aligned(16))) float wss[16 * kMapsChunk];
   const int t = threadIdx.x, Z = blockIdx.y, l = blockIdx.z;
   const int ol = t >> 4, o = blockIdx.x * 16 + ol;
   const float* w2 = a.w_radial + (int64_t)l * a.c_mid * a.nh;
   const float* ws = a.w_second[l];
   // chunk c0 of w_radial's rows and of the block's w_second columns into LDS
   auto stage = [&](int c0, int cn) {
+    if (a.st_vec) {  // float4 loads, eight in flight per thread
+      const float4* src = reinterpret_cast<const float4*>(w2 + (int64_t)c0 * a.nh);
+      float4* dst = reinterpret_cast<float4*>(w2s);
+      const int n4 = cn * a.nh / 4;
+#pragma unroll 8
+      for (int i = t; i < n4; i += 256) dst[i] = src[i];
+      const int q4 = cn / 4;
+      for (int i = t; i < 16 * q4; i += 256) {
+        const int r = i / q4, cc = 4 * (i - r * q4), oo = blockIdx.x * 16 + r;
+        *reinterpret_cast<float4*>(wss + r * kMapsChunk + cc) =
+            oo < a.c_out ? *reinterpret_cast<const float4*>(ws + (int64_t)oo * a.c_mid + c0 + cc)
+                         : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+      return;
+    }
     for (int i = t; i < cn * a.nh; i += 256) w2s[i] = w2[(int64_t)c0 * a.nh + i];
     for (int i = t; i < 16 * cn; i += 256) {
       const int r = i / cn, cc = i - r * cn, oo = blockIdx.x * 16 + r;
@@ -248,14 +265,28 @@ __global__ void __launch_bounds__(256) species_maps_kernel(SpeciesMapsArgs a) {
   stage(0, a.c_mid < kMapsChunk ? a.c_mid : kMapsChunk);
   const float div = *a.alpha_div;
   __syncthreads();
-  // x: four threads per row of w_first, thread q of a row taking the row's quarter q
+  // x: four threads per row of w_first, thread q of a row taking the row's quarter q (as float4
+  // loads issued eight at a time when the rows allow it: the loads, not the FMAs, set the time)
   const int q = t & 3, qn = (a.c_in + 3) / 4, j0 = q * qn, j1 = j0 + qn < a.c_in ? j0 + qn : a.c_in;
   for (int c0 = 0; c0 < a.c_mid; c0 += 64) {
     const int c = c0 + (t >> 2);
     float d = 0.f;
     if (c < a.c_mid) {
       const float* wr = a.w_first + (int64_t)c * a.c_in;
-      for (int j = j0; j < j1; ++j) d = fmaf(tb[j], wr[j], d);
+      if (a.x_vec) {
+        const float4* w4 = reinterpret_cast<const float4*>(wr + j0);
+        const float4* t4 = reinterpret_cast<const float4*>(tb + j0);
+#pragma unroll 8
+        for (int j = 0; j < qn / 4; ++j) {
+          const float4 w = w4[j], x = t4[j];
+          d = fmaf(x.x, w.x, d);
+          d = fmaf(x.y, w.y, d);
+          d = fmaf(x.z, w.z, d);
+          d = fmaf(x.w, w.w, d);
+        }
+      } else {
+        for (int j = j0; j < j1; ++j) d = fmaf(tb[j], wr[j], d);
+      }
     }
     d += __shfl_xor(d, 1, 64);
     d += __shfl_xor(d, 2, 64);
@@ -315,6 +346,9 @@ extern "C" int fc_species_maps(int32_t n_species, int32_t c_in, int32_t c_mid, i
   a.c_out = c_out;
   a.nh = n_hidden;
   a.n_species = n_species;
+  a.x_vec = (c_in % 16) == 0 && ((uintptr_t)w_first & 15) == 0;
+  a.st_vec = (c_mid % 4) == 0 && (n_hidden % 4) == 0 && ((uintptr_t)w_radial & 15) == 0;
+  for (int l = 0; l < n_ranks; ++l) a.st_vec = a.st_vec && ((uintptr_t)w_second[l] & 15) == 0;
   hipLaunchKernelGGL(species_maps_kernel, dim3((unsigned)((c_out + 15) / 16), (unsigned)n_species, (unsigned)n_ranks),
                      dim3(256), 0, (hipStream_t)stream, a);
   FC_LAUNCH_CHECK();
