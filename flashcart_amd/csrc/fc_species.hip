@@ -26,8 +26,10 @@ constexpr int kHid = 64;        // hidden width of the radial MLP
 
 // One workgroup (256 threads) per receiver: wave w accumulates the senders of species w and
 // w + 4 (lane k: hidden index k, all components in registers), so each edge costs FMAs in one
-// wave only; every output element is written once. Edges are taken U at a time, the batch's
-// species, pair slots, h values and edge attributes loaded before any is used.
+// wave only; every output element is written once. The receiver's edges are taken 64 at a
+// time: their species, pair slots and edge attributes go to LDS with one vector load per
+// thread (no chain of per-edge scalar loads), then each wave loads the h rows of its edges U
+// at a time, all before the first FMA waits for them.
 template <int D>
 __global__ void __launch_bounds__(256) species_density_fwd_kernel(int64_t n_rows, int n_species, int y_stride,
                                                                   const int32_t* __restrict__ rowptr,
@@ -36,40 +38,52 @@ __global__ void __launch_bounds__(256) species_density_fwd_kernel(int64_t n_rows
                                                                   const float* __restrict__ h,
                                                                   const float* __restrict__ y, float* __restrict__ dens) {
   constexpr int U = 16, ZW = kSpeciesMax / 4;  // species per wave
+  constexpr int B = 64;                        // edges staged per block
+  __shared__ int zs[B], ss[B];
+  __shared__ float ys[B * D];
   const int64_t row = xcd_row(n_rows);
   if (row >= n_rows) return;
-  const int k = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int t = threadIdx.x, k = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   float acc[ZW][D];
 #pragma unroll
   for (int q = 0; q < ZW; ++q)
 #pragma unroll
     for (int c = 0; c < D; ++c) acc[q][c] = 0.f;
   const int32_t e0 = rowptr[row], e1 = rowptr[row + 1];
-  for (int32_t b = e0; b < e1; b += U) {
-    int z[U], sl[U];
-    float hk[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int32_t e = b + u < e1 ? b + u : e1 - 1;  // clamped; the duplicate is skipped below
-      z[u] = b + u < e1 ? zj[e] : -1;
-      sl[u] = pair_slot[e];
+  for (int32_t b0 = e0; b0 < e1; b0 += B) {
+    const int n = e1 - b0 < B ? e1 - b0 : B;
+    if (b0 > e0) __syncthreads();  // the previous block's LDS reads are done
+    if (t < B) {
+      zs[t] = t < n ? zj[b0 + t] : -1;
+      ss[t] = t < n ? pair_slot[b0 + t] : -1;
     }
-    // h only where this wave takes the edge (uniform branches; the loads are all issued before
-    // the first FMA waits for them)
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      hk[u] = 0.f;
-      if ((z[u] & 3) == wave && z[u] < 4 * ZW && sl[u] >= 0) hk[u] = h[(int64_t)(sl[u] >> 1) * kHid + k];
+    for (int i = t; i < n * D; i += 256) {
+      const int u = i / D, c = i - u * D;
+      ys[i] = y[(int64_t)(b0 + u) * y_stride + c];
     }
+    __syncthreads();
+    for (int u0 = 0; u0 < n; u0 += U) {
+      int z[U];
+      float hk[U];
+      // h only where this wave takes the edge (uniform branches; the loads are all issued before
+      // the first FMA waits for them)
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
+      for (int u = 0; u < U; ++u) {
+        z[u] = u0 + u < n ? __builtin_amdgcn_readfirstlane(zs[u0 + u]) : -1;
+        const int sl = u0 + u < n ? __builtin_amdgcn_readfirstlane(ss[u0 + u]) : -1;
+        hk[u] = 0.f;
+        if ((z[u] & 3) == wave && z[u] >= 0 && z[u] < 4 * ZW && sl >= 0) hk[u] = h[(int64_t)(sl >> 1) * kHid + k];
+      }
 #pragma unroll
-      for (int q = 0; q < ZW; ++q) {
-        if (z[u] != wave + 4 * q) continue;  // uniform branch
-        const float* yr = y + (int64_t)(b + u) * y_stride;
+      for (int u = 0; u < U; ++u) {
 #pragma unroll
-        for (int c = 0; c < D; ++c) acc[q][c] = fmaf(hk[u], yr[c], acc[q][c]);
+        for (int q = 0; q < ZW; ++q) {
+          if (z[u] != wave + 4 * q) continue;  // uniform branch
+          const float* yr = ys + (u0 + u) * D;
+#pragma unroll
+          for (int c = 0; c < D; ++c) acc[q][c] = fmaf(hk[u], yr[c], acc[q][c]);
+        }
       }
     }
   }
