@@ -1248,6 +1248,45 @@ __device__ __forceinline__ void mfma_k64(const float* as, const float* bs, float
   }
 }
 
+// The same product with B stored the other way round: bt = W + (lane & 31) + half * WIDE_P for a
+// weight square W[k][j] (k-major rows), so lane j of block jb reads W[k][jb * 32 + j] for its four
+// k values (four scalar LDS reads, the same bytes as one float4): the input gradients multiply by
+// the weight matrices the forward staged, without staging their transposes.
+template <int NJ>
+__device__ __forceinline__ void mfma_k64_t(const float* as, const float* bt, floatx16 (&acc)[2]) {
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[j][v] = 0.f;
+  auto read_b = [&](int s4, float4 (&b)[NJ]) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const float* p = bt + 4 * s4 * WIDE_P + j * 32;
+      b[j] = make_float4(p[0], p[WIDE_P], p[2 * WIDE_P], p[3 * WIDE_P]);
+    }
+  };
+  float4 a4n = *reinterpret_cast<const float4*>(as), b4n[NJ];
+  read_b(0, b4n);
+#pragma unroll
+  for (int s4 = 0; s4 < 8; ++s4) {
+    const float4 a4 = a4n;
+    float4 b4[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) b4[j] = b4n[j];
+    if (s4 + 1 < 8) {
+      a4n = *reinterpret_cast<const float4*>(as + 4 * (s4 + 1));
+      read_b(s4 + 1, b4n);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep those reads ahead of this group's MFMAs
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(reinterpret_cast<const float*>(&a4)[q],
+                                                      reinterpret_cast<const float*>(&b4[j])[q], acc[j], 0, 0, 0);
+  }
+}
+
 // Row (within the wave's 32 rows) of accumulator element v of this lane.
 __device__ __forceinline__ int acc_row(int v, int lane) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); }
 
@@ -1259,25 +1298,32 @@ __device__ __forceinline__ float silu_r_grad(float z) {
 
 // x block (rows r0 .. r0 + 127 that exist; they are contiguous in x) -> As, zero-padded to 64
 // columns; rows past n stay zero (never stored). W0 (64 x n_in) -> B0 and W1 (64 x 64) -> B1 as
-// weight rows (zero-padded k); with trans, W1^T -> B0 and W0^T -> B1 instead. Every thread
-// issues all of its global loads before its first LDS store, so the load latency is paid once.
+// weight rows (zero-padded k). Every thread issues all of its global loads before its first LDS
+// store, so the load latency is paid once.
 __device__ __forceinline__ void mlp_stage_x(float* As, int64_t n, int n_in, const float* __restrict__ x, int64_t r0) {
   const int t = threadIdx.x;
   const int rows = n - r0 < WIDE_BM ? (int)(n - r0) : WIDE_BM;
   const int cnt = rows * n_in;
   const float* xb = x + r0 * n_in;
-  float v[WIDE_K / 2];  // 128 x 64 / 256 threads at most
+  // row of element e: e / n_in, exact in float for e < 2^13 ((e + 1/2) / n_in is at least
+  // 1 / (2 n_in) from an integer), without an integer division per element
+  const float inv_in = 1.0f / (float)n_in;
+  // in chunks of eight values per thread (one chunk for up to 16 inputs), so few registers stay
+  // reserved for the staging
+  for (int base = 0; base < WIDE_BM * n_in; base += 8 * 256) {
+    float v[8];
 #pragma unroll
-  for (int i = 0; i < WIDE_K / 2; ++i) {
-    const int e = t + 256 * i;
-    v[i] = e < cnt ? xb[e] : 0.f;
-  }
+    for (int i = 0; i < 8; ++i) {
+      const int e = base + t + 256 * i;
+      v[i] = e < cnt ? xb[e] : 0.f;
+    }
 #pragma unroll
-  for (int i = 0; i < WIDE_K / 2; ++i) {
-    const int e = t + 256 * i;
-    if (e < WIDE_BM * n_in) {
-      const int q = e / n_in;
-      As[q * WIDE_P + (e - q * n_in)] = v[i];
+    for (int i = 0; i < 8; ++i) {
+      const int e = base + t + 256 * i;
+      if (e < WIDE_BM * n_in) {
+        const int q = (int)(((float)e + 0.5f) * inv_in);
+        As[q * WIDE_P + (e - q * n_in)] = v[i];
+      }
     }
   }
   for (int e = t; e < WIDE_BM * (WIDE_K - n_in); e += 256) {
@@ -1287,7 +1333,7 @@ __device__ __forceinline__ void mlp_stage_x(float* As, int64_t n, int n_in, cons
 }
 
 __device__ __forceinline__ void mlp_stage_weights(float* B0, float* B1, int n_in, const float* __restrict__ w0,
-                                                  const float* __restrict__ w1, bool trans) {
+                                                  const float* __restrict__ w1) {
   const int t = threadIdx.x;
   float a[16], b[16];
 #pragma unroll
@@ -1299,13 +1345,8 @@ __device__ __forceinline__ void mlp_stage_weights(float* B0, float* B1, int n_in
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int e = t + 256 * i, r = e >> 6, c = e & 63;
-    if (!trans) {
-      B0[r * WIDE_P + c] = b[i];  // W0 row r (output), k = c
-      B1[r * WIDE_P + c] = a[i];  // W1 row r, k = c
-    } else {
-      B0[c * WIDE_P + r] = a[i];  // W1^T: row c (input of W1), k = r (output)
-      B1[c * WIDE_P + r] = b[i];  // W0^T: row c (input feature, zero past n_in), k = r
-    }
+    B0[r * WIDE_P + c] = b[i];  // W0 row r (output), k = c
+    B1[r * WIDE_P + c] = a[i];  // W1 row r, k = c
   }
 }
 
@@ -1332,7 +1373,7 @@ __global__ void __launch_bounds__(256, 2) radial_mlp_fwd_kernel(int64_t n, int n
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int64_t r0 = (first_block + blockIdx.x) * WIDE_BM;
   mlp_stage_x(As, n, n_in, x, r0);
-  mlp_stage_weights(Bs[0], Bs[1], n_in, w0, w1, false);
+  mlp_stage_weights(Bs[0], Bs[1], n_in, w0, w1);
   __syncthreads();
   const int half = (lane >> 5) * (WIDE_K / 2);
   const float* as = As + (wave * 32 + (lane & 31)) * WIDE_P + half;
@@ -1373,66 +1414,84 @@ __global__ void __launch_bounds__(256, 2) radial_mlp_bwd_kernel(int64_t n, int n
   __shared__ __attribute__((aligned(16))) float B0[WIDE_BN * WIDE_P];
   __shared__ __attribute__((aligned(16))) float B1[WIDE_BN * WIDE_P];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int64_t r0 = (int64_t)blockIdx.x * WIDE_BM;
-  // this lane's dL/dh2 values (accumulator layout), loaded first so that their latency
-  // overlaps the staging and the two recomputed layers; rows past n contribute nothing
+  // Persistent: workgroup b takes row blocks b, b + G, ...; the weights are staged once, and the
+  // next block's dL/dh2 loads while the current block's last two products run.
+  const int64_t nblk = (n + WIDE_BM - 1) / WIDE_BM;
+  int64_t blk = blockIdx.x;
+  if (blk >= nblk) return;  // uniform
+  // this lane's dL/dh2 values of block b (accumulator layout); rows past n contribute nothing
+  auto load_g2 = [&](int64_t b, float (&g)[2][16]) {
+    const int64_t rb = b * WIDE_BM;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t row = rb + wave * 32 + acc_row(v, lane);
+        if constexpr (PAIRS)
+          g[j][v] = row < n ? gh2[2 * row * 64 + j * 32 + (lane & 31)] + gh2[(2 * row + 1) * 64 + j * 32 + (lane & 31)]
+                            : 0.f;
+        else
+          g[j][v] = row < n ? gh2[row * 64 + j * 32 + (lane & 31)] : 0.f;
+      }
+  };
   float g2[2][16];
-#pragma unroll
-  for (int j = 0; j < 2; ++j)
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int64_t row = r0 + wave * 32 + acc_row(v, lane);
-      if constexpr (PAIRS)
-        g2[j][v] = row < n ? gh2[2 * row * 64 + j * 32 + (lane & 31)] + gh2[(2 * row + 1) * 64 + j * 32 + (lane & 31)]
-                           : 0.f;
-      else
-        g2[j][v] = row < n ? gh2[row * 64 + j * 32 + (lane & 31)] : 0.f;
-    }
-  mlp_stage_x(As, n, n_in, x, r0);
-  mlp_stage_weights(B0, B1, n_in, w0, w1, false);
-  __syncthreads();
+  load_g2(blk, g2);
+  mlp_stage_weights(B0, B1, n_in, w0, w1);
   const int half = (lane >> 5) * (WIDE_K / 2);
   const float* as = As + (wave * 32 + (lane & 31)) * WIDE_P + half;
-  floatx16 acc[2], d1[2];
+  // dh1 = dpre2 W1 and dx = dpre1 W0 read the weight rows staged for the forward layers
+  const float* w1t = B1 + (lane & 31) + half * WIDE_P;
+  const float* w0t = B0 + (lane & 31) + half * WIDE_P;
   const int ns4_in = n_in <= 32 ? (n_in + 3) / 4 : 8;
-  mfma_k64<2>(as, B0 + (lane & 31) * WIDE_P + half, acc, ns4_in);
+  const int nj = n_in <= 32 ? 1 : 2;  // dx has n_in columns: one 32-column block when n_in <= 32
+  for (; blk < nblk; blk += gridDim.x) {
+    const int64_t r0 = blk * WIDE_BM;
+    mlp_stage_x(As, n, n_in, x, r0);
+    __syncthreads();  // x rows (and, the first time, the weights) staged
+    floatx16 acc[2], d1[2];
+    mfma_k64<2>(as, B0 + (lane & 31) * WIDE_P + half, acc, ns4_in);
+    // one sigmoid per pre-activation serves both silu'(pre1) (kept) and h1 = silu(pre1) (to LDS)
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) d1[j][v] = silu_r_grad(acc[j][v] * s0);
-  __syncthreads();
-  acc_to_rows(acc, As, wave, lane, [&](float a) { return silu_r(a * s0); });
-  __syncthreads();
-  mfma_k64<2>(as, B1 + (lane & 31) * WIDE_P + half, acc);
-  // dpre2 = gh2 * silu'(pre2)
+      for (int v = 0; v < 16; ++v) {
+        const float z = acc[j][v] * s0, sg = sigmoidf_(z);
+        d1[j][v] = kSiluScale * sg * (1.0f + z * (1.0f - sg));
+        acc[j][v] = kSiluScale * z * sg;
+      }
+    __syncthreads();
+    acc_to_rows(acc, As, wave, lane, [](float a) { return a; });
+    __syncthreads();
+    mfma_k64<2>(as, B1 + (lane & 31) * WIDE_P + half, acc);
+    // dpre2 = gh2 * silu'(pre2)
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) acc[j][v] = g2[j][v] * silu_r_grad(acc[j][v] * s1);
-  __syncthreads();  // reads of h1, W0 and W1 done: stage dpre2, W1^T and W0^T
-  acc_to_rows(acc, As, wave, lane, [](float a) { return a; });
-  mlp_stage_weights(B0, B1, n_in, w0, w1, true);
-  __syncthreads();
-  mfma_k64<2>(as, B0 + (lane & 31) * WIDE_P + half, acc);
+      for (int v = 0; v < 16; ++v) acc[j][v] = g2[j][v] * silu_r_grad(acc[j][v] * s1);
+    if (blk + gridDim.x < nblk) load_g2(blk + gridDim.x, g2);  // in flight during the rest of this block
+    __syncthreads();  // reads of h1 done: stage dpre2
+    acc_to_rows(acc, As, wave, lane, [](float a) { return a; });
+    __syncthreads();
+    mfma_k64_t<2>(as, w1t, acc);
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) acc[j][v] = acc[j][v] * s1 * d1[j][v];
-  __syncthreads();
-  acc_to_rows(acc, As, wave, lane, [](float a) { return a; });
-  __syncthreads();
-  // dx has n_in columns: one 32-column block when n_in <= 32
-  const int nj = n_in <= 32 ? 1 : 2;
-  if (nj == 1) mfma_k64<1>(as, B1 + (lane & 31) * WIDE_P + half, acc);
-  else mfma_k64<2>(as, B1 + (lane & 31) * WIDE_P + half, acc);
+      for (int v = 0; v < 16; ++v) acc[j][v] = acc[j][v] * s1 * d1[j][v];
+    __syncthreads();
+    acc_to_rows(acc, As, wave, lane, [](float a) { return a; });
+    __syncthreads();
+    if (nj == 1) mfma_k64_t<1>(as, w0t, acc);
+    else mfma_k64_t<2>(as, w0t, acc);
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int64_t row = r0 + wave * 32 + acc_row(v, lane);
-      const int col = j * 32 + (lane & 31);
-      if (j < nj && row < n && col < n_in) gx[row * n_in + col] = acc[j][v] * s0;
-    }
+      for (int v = 0; v < 16; ++v) {
+        const int64_t row = r0 + wave * 32 + acc_row(v, lane);
+        const int col = j * 32 + (lane & 31);
+        if (j < nj && row < n && col < n_in) gx[row * n_in + col] = acc[j][v] * s0;
+      }
+    __syncthreads();  // every wave's reads of this block's rows done before the next block's x
+  }
 }
 
 }  // namespace fc
@@ -1525,6 +1584,12 @@ extern "C" int fc_radial_mlp_hidden_fwd(int64_t n, int32_t n_in, const float* x,
   return FC_OK;
 }
 
+// persistent workgroups of the radial MLP backward: two per CU (their LDS), at most one per block
+static int64_t mlp_bwd_grid(int64_t blocks) {
+  const int64_t g = 2 * (int64_t)device_cu_count();
+  return blocks < g ? blocks : g;
+}
+
 extern "C" int fc_radial_mlp_bwd(int64_t n, int32_t n_in, const float* x, const float* w0, float s0,
                                  const float* w1, float s1, const float* grad_h2, float* grad_x, void* stream) {
   if (n < 0 || n_in < 1 || n_in > WIDE_K) return FC_ERR_BAD_DESC;
@@ -1532,8 +1597,8 @@ extern "C" int fc_radial_mlp_bwd(int64_t n, int32_t n_in, const float* x, const 
   if (!x || !w0 || !w1 || !grad_h2 || !grad_x) return FC_ERR_NULL;
   const int64_t blocks = (n + WIDE_BM - 1) / WIDE_BM;
   if (blocks > 0x7fffffff) return FC_ERR_SHAPE;
-  hipLaunchKernelGGL(radial_mlp_bwd_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, n,
-                     (int)n_in, x, w0, s0, w1, s1, grad_h2, grad_x);
+  hipLaunchKernelGGL(radial_mlp_bwd_kernel<false>, dim3((unsigned)mlp_bwd_grid(blocks)), dim3(256), 0,
+                     (hipStream_t)stream, n, (int)n_in, x, w0, s0, w1, s1, grad_h2, grad_x);
   FC_LAUNCH_CHECK();
   return FC_OK;
 }
@@ -1546,8 +1611,8 @@ extern "C" int fc_radial_mlp_bwd_pairsum(int64_t n, int32_t n_in, const float* x
   if (!x || !w0 || !w1 || !grad_h2 || !grad_x) return FC_ERR_NULL;
   const int64_t blocks = (n + WIDE_BM - 1) / WIDE_BM;
   if (blocks > 0x7fffffff) return FC_ERR_SHAPE;
-  hipLaunchKernelGGL(radial_mlp_bwd_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, n,
-                     (int)n_in, x, w0, s0, w1, s1, grad_h2, grad_x);
+  hipLaunchKernelGGL(radial_mlp_bwd_kernel<true>, dim3((unsigned)mlp_bwd_grid(blocks)), dim3(256), 0,
+                     (hipStream_t)stream, n, (int)n_in, x, w0, s0, w1, s1, grad_h2, grad_x);
   FC_LAUNCH_CHECK();
   return FC_OK;
 }
