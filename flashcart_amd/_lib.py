@@ -121,6 +121,7 @@ _SIGNATURES = {
                                     c_vp, c_i64, c_vp]),
     "fc_dense_wgrad_workspace": (c_i64, [c_i64, c_i32, c_i32, c_i32]),
     "fc_dense_wgrad": (c_int, [c_i64, c_i32, c_i32, c_vp, c_vp, c_i32, c_vp, c_f32, c_vp, c_vp, c_vp, c_i64, c_vp]),
+    "fc_silu_grad_mix": (c_int, [c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "fc_segment_sum": (c_int, [c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "fc_gate_fwd": (c_int, [c_i64, c_int, c_int, c_vp, c_vp, c_int, c_vp, c_vp]),
     "fc_gate_bwd": (c_int, [c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_int, c_vp, c_vp, c_vp]),

@@ -1637,6 +1637,70 @@ extern "C" int fc_dense_dgrad(int64_t n, int32_t k, int32_t m, const float* go, 
 
 namespace fc {
 
+// ---- Elementwise products with the rescaled SiLU's derivatives (second-order backward of the
+// dense layers): out1 = a f'(pre) + add, out2 = a b f''(pre), with f(x) = kSiluScale x sigmoid(x),
+//   f'(x)  = kSiluScale s (1 + x (1 - s)),   f''(x) = kSiluScale s (1 - s) (2 + x (1 - 2 s)),
+// s = sigmoid(x). One pass over the operands for both products (one sigmoid per element).
+__device__ __forceinline__ void silu_mix_one(float a, float b, float p, float add, bool w1, bool w2, float* o1,
+                                             float* o2) {
+  const float s = sigmoidf_(p);
+  if (w1) *o1 = fmaf(a, kSiluScale * s * (1.0f + p * (1.0f - s)), add);
+  if (w2) *o2 = a * b * (kSiluScale * s * (1.0f - s) * (2.0f + p * (1.0f - 2.0f * s)));
+}
+
+__global__ void __launch_bounds__(256) silu_grad_mix_kernel(int64_t n, const float* __restrict__ a,
+                                                            const float* __restrict__ b,
+                                                            const float* __restrict__ pre,
+                                                            const float* __restrict__ add, float* __restrict__ out1,
+                                                            float* __restrict__ out2, bool vec) {
+  const bool w1 = out1 != nullptr, w2 = out2 != nullptr;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (vec) {  // n % 4 == 0 and every pointer 16-byte aligned
+    for (int64_t q = t0; q < n / 4; q += stride) {
+      const float4 av = reinterpret_cast<const float4*>(a)[q];
+      const float4 pv = reinterpret_cast<const float4*>(pre)[q];
+      const float4 bv = w2 ? reinterpret_cast<const float4*>(b)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 dv = (w1 && add) ? reinterpret_cast<const float4*>(add)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+      float4 r1, r2;
+      silu_mix_one(av.x, bv.x, pv.x, dv.x, w1, w2, &r1.x, &r2.x);
+      silu_mix_one(av.y, bv.y, pv.y, dv.y, w1, w2, &r1.y, &r2.y);
+      silu_mix_one(av.z, bv.z, pv.z, dv.z, w1, w2, &r1.z, &r2.z);
+      silu_mix_one(av.w, bv.w, pv.w, dv.w, w1, w2, &r1.w, &r2.w);
+      if (w1) reinterpret_cast<float4*>(out1)[q] = r1;
+      if (w2) reinterpret_cast<float4*>(out2)[q] = r2;
+    }
+    return;
+  }
+  for (int64_t i = t0; i < n; i += stride) {
+    float r1, r2;
+    silu_mix_one(a[i], w2 ? b[i] : 0.f, pre[i], (w1 && add) ? add[i] : 0.f, w1, w2, &r1, &r2);
+    if (w1) out1[i] = r1;
+    if (w2) out2[i] = r2;
+  }
+}
+
+}  // namespace fc
+
+extern "C" int fc_silu_grad_mix(int64_t n, const float* a, const float* b, const float* pre, const float* add,
+                                float* out1, float* out2, void* stream) {
+  using namespace fc;
+  if (n < 0) return FC_ERR_BAD_DESC;
+  if (n == 0 || (!out1 && !out2)) return FC_OK;
+  if (!a || !pre || (out2 && !b)) return FC_ERR_NULL;
+  auto al = [](const void* p) { return p == nullptr || ((uintptr_t)p & 15) == 0; };
+  const bool vec = (n & 3) == 0 && al(a) && al(b) && al(pre) && al(add) && al(out1) && al(out2);
+  const int64_t work = vec ? n / 4 : n;
+  const int64_t cap = (int64_t)device_cu_count() * 8;
+  const int64_t blocks = (work + 255) / 256 < cap ? (work + 255) / 256 : cap;
+  hipLaunchKernelGGL(silu_grad_mix_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, n, a, b, pre,
+                     add, out1, out2, vec);
+  FC_LAUNCH_CHECK();
+  return FC_OK;
+}
+
+namespace fc {
+
 // ---- Weight gradients (training): dW[o, j] = scale * sum_r A'[r, o] * B[r, j] over every row
 // r = (node, component) of a rank, with A = grad_out (A' = A * act'(pre) for a dense layer
 // with the fused SiLU) and B = the layer input; optionally db[o] = sum_r A'[r, o].

@@ -1317,7 +1317,12 @@ def _dense_backward(ctx, grad, grad_pre):
         if grad_pre is None:  # act'(pre) is applied inside the weight-gradient kernel
             g, act = grad, ctx.act
         else:
-            g = grad * _torch_math.silu_grad(pre) + grad_pre if grad is not None else grad_pre
+            if grad is None:
+                g = grad_pre
+            elif torch.is_grad_enabled():
+                g = grad * _torch_math.silu_grad(pre) + grad_pre
+            else:
+                g, _ = silu_grad_mix(grad, pre, add=grad_pre)
             act = 0
         gw, gb = dense_wgrad(g, pre, act, x, ctx.scale, bool(ctx.needs_input_grad[1]),
                              bool(ctx.has_bias and ctx.needs_input_grad[2]))
@@ -1455,6 +1460,25 @@ def species_maps(table: Tensor, w_first: Tensor, s_first: float, alpha_div: Tens
     return mats
 
 
+def silu_grad_mix(a: Tensor, pre: Tensor, add: Optional[Tensor] = None, b: Optional[Tensor] = None,
+                  need1: bool = True, need2: bool = False) -> Tuple[Optional[Tensor], Optional[Tensor]]:
+    """(a * f'(pre) + add, a * b * f''(pre)) for the rescaled SiLU f, the requested ones, in one
+    elementwise pass (``fc_silu_grad_mix``). Not differentiable: callers use it outside grad mode
+    (the torch statements in ``_torch_math`` otherwise)."""
+    ac = _lib.contig("a", a)
+    pc = _lib.contig("pre", pre)
+    dc = _lib.contig("add", add) if add is not None else None
+    bc = _lib.contig("b", b) if need2 else None
+    for name, t in (("pre", pc), ("add", dc), ("b", bc)):
+        if t is not None and t.shape != ac.shape:
+            raise RuntimeError(f"silu_grad_mix: {name} {tuple(t.shape)} does not match a {tuple(ac.shape)}.")
+    o1 = torch.empty_like(ac) if need1 else None
+    o2 = torch.empty_like(ac) if need2 else None
+    _lib_call("fc_silu_grad_mix", ac.numel(), ac.data_ptr(), _lib.ptr(bc), pc.data_ptr(), _lib.ptr(dc), _lib.ptr(o1),
+              _lib.ptr(o2), _lib.stream_of(ac))
+    return o1, o2
+
+
 def dense_wgrad(grad_out: Tensor, pre: Optional[Tensor], act: int, x: Tensor, scale: float, need_weight: bool,
                 need_bias: bool) -> Tuple[Optional[Tensor], Optional[Tensor]]:
     """(scale * g^T x, column sums of g) with g = grad_out * act'(pre) (act 1) or grad_out
@@ -1585,8 +1609,10 @@ def _rms_backward(ctx, grad_out, grad_scale):
     gw = None
     if ctx.needs_input_grad[1]:  # d/dg_l[c] = sum_{n,a} grad_out * x * s (parameter training only)
         n, C = x.shape[0], weight.shape[-1]
-        prod = (grad_out * x * scale.unsqueeze(-1)).view(n, -1, C)
-        gw = torch.stack([prod[:, l * l:(l + 1) ** 2].sum(dim=(0, 1)) for l in range(ctx.l_max + 1)])
+        # node sum first, over the contiguous rows (a strided per-rank slice summed over nodes
+        # and components is a slow reduction), then the components of each rank
+        per_comp = (grad_out * x * scale.unsqueeze(-1)).view(n, -1).sum(0).view(-1, C)
+        gw = torch.stack([per_comp[l * l:(l + 1) ** 2].sum(0) for l in range(ctx.l_max + 1)])
     return gx, gw, None, None
 
 

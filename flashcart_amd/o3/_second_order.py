@@ -60,6 +60,16 @@ def _tp_bwd_setup(ctx, inputs, output):
     ctx.computed = (bool(n1), bool(n2), bool(nw))
 
 
+def _conv_bwd_specialised(cfg, conv: bool) -> bool:
+    """Whether fc_tp_bwd runs a convolution of this configuration on its compile-time
+    specialised kernel when the weight and in2 gradients are both requested: per-edge
+    weights, one in2 channel, unreduced outputs, 32, 64 or 128 in1 channels, in2 rank >= 1,
+    no symmetric product (the launcher's conditions in csrc/fc_tp_impl.h)."""
+    l1, l2, lo, f1, f2, sym, shared = cfg[:7]
+    red = cfg[12]
+    return conv and not shared and not red and not sym and f2 == 1 and f1 in (32, 64, 128) and l2 >= 1
+
+
 def _tp_dbwd(ctx, c1, c2, cw):
     """Backward of tp_bwd (reference tp_dbwd, src/flashcart/o3/_tensor_product.py:789-1093)."""
     go, in1, in2, w, ii, jj, rp, sp, sq, adiv = ctx.saved_tensors
@@ -85,11 +95,15 @@ def _tp_dbwd(ctx, c1, c2, cw):
 
     d_go = None
     if need[0]:
-        d_go = _acc(fwd(c1, in2, w) if c1 is not None else None,
-                    fwd(in1, c2, w) if c2 is not None else None,
-                    fwd(in1, in2, cw) if cw is not None else None)
+        terms = [t for t in ((c1, in2, w), (in1, c2, w), (in1, in2, cw)) if t[0] is not None and t[1] is not None
+                 and t[2] is not None]
+        d_go = _acc(*[fwd(*t) for t in terms]) if terms else None
     a = bwd(c1, in2, w, False, need[2], need[3]) if c1 is not None else (None,) * 3
-    b = bwd(in1, c2, w, need[1], False, need[3]) if c2 is not None else (None,) * 3
+    # the in2 gradient of the second product is not needed; asking for it anyway lets an
+    # interaction-layer convolution take the kernel specialised for (in1, in2, weight) gradients
+    b = bwd(in1, c2, w, need[1], _conv_bwd_specialised(cfg, ii is not None) and bool(need[3]), need[3]) \
+        if c2 is not None else (None,) * 3
+    b = (b[0], None, b[2])
     c = bwd(in1, in2, cw, need[1], need[2], False) if cw is not None else (None,) * 3
     d_in1 = _acc(b[0], c[0]) if need[1] else None
     d_in2 = _acc(a[1], c[1]) if need[2] else None
@@ -158,10 +172,15 @@ def _dense_dbwd(ctx, c):
         dh, _ = _ops.dense_fwd(c2, w, None, ctx.scale, 0)
     if ctx.act:
         p2 = pre.reshape(-1, m)
-        if need[0]:
-            d_go = (dh * M.silu_grad(p2)).reshape(go.shape)
-        if need[1]:
-            d_pre = (dh * go2 * M.silu_grad2(p2)).reshape(pre.shape)
+        if not torch.is_grad_enabled() and (need[0] or need[1]):  # one elementwise pass for both
+            d_go, d_pre = _ops.silu_grad_mix(dh, p2, b=go2, need1=bool(need[0]), need2=bool(need[1]))
+            d_go = d_go.reshape(go.shape) if d_go is not None else None
+            d_pre = d_pre.reshape(pre.shape) if d_pre is not None else None
+        else:
+            if need[0]:
+                d_go = (dh * M.silu_grad(p2)).reshape(go.shape)
+            if need[1]:
+                d_pre = (dh * go2 * M.silu_grad2(p2)).reshape(pre.shape)
     elif need[0]:
         d_go = dh.reshape(go.shape)
     if need[2]:  # s * h^T c with h = go * act'(pre)

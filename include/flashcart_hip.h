@@ -377,6 +377,14 @@ int fc_dense_wgrad(int64_t n, int32_t k, int32_t m, const float* grad_out, const
                    const float* x, float scale, float* grad_w, float* grad_b, float* workspace,
                    int64_t workspace_floats, void* stream);
 
+/* Elementwise products with the derivatives of the rescaled SiLU f(x) = 1.6765 x sigmoid(x)
+ * (RescaledSiLULayer, reference src/flashcart/nn/layers.py:12-45), for the second-order
+ * backward of the dense layers that the reference leaves to PyTorch autograd over that layer:
+ *   out1 = a * f'(pre) + add   (add may be NULL),   out2 = a * b * f''(pre),
+ * each formed when its pointer is non-NULL; n elements of each operand. */
+int fc_silu_grad_mix(int64_t n, const float* a, const float* b, const float* pre, const float* add,
+                     float* out1, float* out2, void* stream);
+
 /* ------------------------------------------------------------------------- */
 /* Invariant RMS normalisation: replaces RMSLayerNorm.forward (reference        */
 /* src/flashcart/nn/layers.py:494-528; no centering) and its autograd in one    */

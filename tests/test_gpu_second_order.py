@@ -161,6 +161,29 @@ def test_dense_chain_second_order():
     _compare(gpu, ref, [x, w1, w2], seed=2)
 
 
+@pytest.mark.parametrize("n,offset", [(4096, 0), (1001, 0), (4096, 1)])
+def test_silu_grad_mix(n, offset):
+    """fc_silu_grad_mix against the float64 derivatives of the rescaled SiLU, obtained by
+    differentiating O.silu with torch.autograd (vector path, scalar tail, unaligned operands)."""
+    from flashcart_amd.o3 import _ops
+    g = torch.Generator().manual_seed(n + offset)
+    a, b, p, d = (4 * torch.randn(n + offset, generator=g, dtype=torch.float64) for _ in range(4))
+    pp = p.clone().requires_grad_(True)
+    (f1,) = torch.autograd.grad(O.silu(pp).sum(), pp, create_graph=True)
+    (f2,) = torch.autograd.grad(f1.sum(), pp)
+    want1, want2 = (a * f1 + d).detach()[offset:], (a * b * f2)[offset:]
+    ga, gb, gp, gd = (t.to(DEV, torch.float32)[offset:] for t in (a, b, p, d))
+    o1, o2 = _ops.silu_grad_mix(ga, gp, add=gd, b=gb, need1=True, need2=True)
+    # float32 inputs and sigmoid: 1e-5 relative, plus 2e-6 of the largest magnitude where
+    # 1 - sigmoid(pre) cancels (large pre)
+    assert_close(o1, want1, 1e-5, 2e-6 * float(want1.abs().max()), "a f'(pre) + add")
+    assert_close(o2, want2, 1e-5, 2e-6 * float(want2.abs().max()), "a b f''(pre)")
+    o1n, none = _ops.silu_grad_mix(ga, gp)
+    assert none is None
+    w1 = (a * f1).detach()[offset:]
+    assert_close(o1n, w1, 1e-5, 2e-6 * float(w1.abs().max()), "a f'(pre)")
+
+
 @pytest.mark.parametrize("l_max", [1, 2, 3])
 def test_irreps_second_order(l_max):
     from flashcart_amd.o3 import _ops
