@@ -92,6 +92,45 @@ __device__ __forceinline__ void radial_eval(const RadialParams& p, float d, floa
   }
 }
 
+// Values only (the forward kernels). The Bessel functions take sin(pi u) from sinpif: the same
+// quantity as sinf(pi * u) without a general range reduction (the product pi * u, up to n_radial pi,
+// sends sinf down its large-argument path).
+// NR > 0: n_radial == NR at compile time (the loop unrolls, the values stay in registers).
+template <int NR = 0>
+__device__ __forceinline__ void radial_feats(const RadialParams& p, float d, float* feats) {
+  const int n = NR > 0 ? NR : p.n_radial;
+  if (p.basis != FC_BASIS_BESSEL) {  // Chebyshev T_k of x(t): the recurrence of radial_eval
+    const float t = (d - p.r_min) / (p.r_max - p.r_min);
+    const float x = p.basis == FC_BASIS_CHEBYSHEV_COSINE ? cosf(t * (float)M_PI) : 2.0f * t - 1.0f;
+    float tm2 = 1.0f, tm1 = x;
+    feats[0] = 1.0f;
+    if (n > 1) feats[1] = x;
+#pragma unroll
+    for (int k = 2; k < n; ++k) {
+      const float tk = 2.0f * x * tm1 - tm2;
+      feats[k] = tk;
+      tm2 = tm1;
+      tm1 = tk;
+    }
+    return;
+  }
+  const float pre = sqrtf(2.0f / p.r_max);
+#pragma unroll
+  for (int k = 0; k < n; ++k) {
+    const float w = (float)M_PI / p.r_max * (float)(k + 1);
+    const float u = d * w / (float)M_PI;  // argument of torch.sinc
+    const float pu = (float)M_PI * u;
+    float sc;
+    if (fabsf(pu) < 0.05f) {
+      const float t2 = pu * pu;
+      sc = 1.0f - t2 * (1.0f / 6.0f) * (1.0f - t2 * (1.0f / 20.0f));
+    } else {
+      sc = sinpif(u) / pu;
+    }
+    feats[k] = pre * w * sc;
+  }
+}
+
 __device__ __forceinline__ float envelope_eval(const RadialParams& p, float d, float* denv) {
   // clamp(d, 0); t = d / r_max; f(t) = 1 - c1 t^p + c2 t^(p+1) - c3 t^(p+2); * [d < r_max]; clamp [0, 1].
   // f has a triple root at t = 1 and is evaluated in the exactly equal factored form
@@ -157,7 +196,7 @@ __global__ void radial_fwd_kernel(RadialParams p, int64_t n, const float* __rest
   const float di = d[i];
   if (feats && p.basis != FC_BASIS_NONE) {
     float f[kMaxRadial];
-    radial_eval(p, di, f, nullptr);
+    radial_feats(p, di, f);
     for (int k = 0; k < p.n_radial; ++k) feats[i * p.n_radial + k] = f[k];
   }
   if (env) env[i] = envelope_eval(p, di, nullptr);
@@ -198,29 +237,66 @@ __device__ __forceinline__ void edge_vector(int64_t e, const float* pos, const f
   }
 }
 
-template <int L>
-__global__ void edge_fwd_kernel(RadialParams p, int64_t n, const float* __restrict__ pos,
-                                const float* __restrict__ shift, const int32_t* __restrict__ ii,
-                                const int32_t* __restrict__ jj, const float* __restrict__ vectors,
-                                float* __restrict__ attrs, float* __restrict__ feats, float* __restrict__ env) {
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= n) return;
-  float v[3];
-  edge_vector(e, pos, shift, ii, jj, vectors, v);
+// Rows of W floats per edge (the block's edges e0 .. e0 + nb - 1) written through LDS: each thread
+// puts its row at stride W + 1 (odd: the row writes hit distinct banks), then the block stores the
+// nb * W floats as one contiguous run, consecutive lanes on consecutive floats. A row per thread
+// written straight to memory would be W stores whose lanes sit W floats apart.
+constexpr int kEdgeBlock = 256;
+
+// W <= MAXW; the row is a register array, read at compile-time indices only.
+template <int MAXW>
+__device__ __forceinline__ void block_store_rows(float* st, const float (&row)[MAXW], int W, bool active, int64_t e0,
+                                                 int nb, float* __restrict__ out) {
+  const int t = threadIdx.x;
+  if (active) {
+#pragma unroll
+    for (int k = 0; k < MAXW; ++k)
+      if (k < W) st[t * (W + 1) + k] = row[k];
+  }
+  __syncthreads();
+  float* o = out + e0 * W;
+  for (int idx = t; idx < nb * W; idx += kEdgeBlock) {
+    const int r = idx / W;
+    o[idx] = st[r * (W + 1) + (idx - r * W)];
+  }
+  __syncthreads();  // the buffer is reused by the next call
+}
+
+// NR > 0: exactly NR radial functions (the loops over them unroll); NR == 0: any count.
+template <int L, int NR>
+__global__ void __launch_bounds__(kEdgeBlock) edge_fwd_kernel(RadialParams p, int64_t n, const float* __restrict__ pos,
+                                                            const float* __restrict__ shift,
+                                                            const int32_t* __restrict__ ii,
+                                                            const int32_t* __restrict__ jj,
+                                                            const float* __restrict__ vectors,
+                                                            float* __restrict__ attrs, float* __restrict__ feats,
+                                                            float* __restrict__ env) {
+  extern __shared__ float st[];  // kEdgeBlock x (widest row + 1) floats, sized at launch
+  const int64_t e0 = (int64_t)blockIdx.x * kEdgeBlock;
+  const int64_t e = e0 + threadIdx.x;
+  const bool active = e < n;  // no early return: every thread takes part in the block stores
+  const int nb = n - e0 < kEdgeBlock ? (int)(n - e0) : kEdgeBlock;
+  float v[3] = {1.f, 0.f, 0.f};
+  if (active) edge_vector(e, pos, shift, ii, jj, vectors, v);
   const float d = sqrtf(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
   const float inv = 1.0f / fmaxf(d, kMinEdgeLength);
   if (attrs) {
     float o[ncomp(L)];
     expand_all<L>(v[0] * inv, v[1] * inv, v[2] * inv, o);
-#pragma unroll
-    for (int k = 0; k < ncomp(L); ++k) attrs[e * ncomp(L) + k] = o[k];
+    block_store_rows(st, o, ncomp(L), active, e0, nb, attrs);
   }
   if (feats && p.basis != FC_BASIS_NONE) {
-    float f[kMaxRadial];
-    radial_eval(p, d, f, nullptr);
-    for (int k = 0; k < p.n_radial; ++k) feats[e * p.n_radial + k] = f[k];
+    if constexpr (NR > 0) {
+      float f[NR];
+      radial_feats<NR>(p, d, f);
+      block_store_rows(st, f, NR, active, e0, nb, feats);
+    } else {
+      float f[kMaxRadial];
+      radial_feats(p, d, f);
+      block_store_rows(st, f, p.n_radial, active, e0, nb, feats);
+    }
   }
-  if (env) env[e] = p.poly_order > 0 ? envelope_eval(p, d, nullptr) : 1.0f;
+  if (env && active) env[e] = p.poly_order > 0 ? envelope_eval(p, d, nullptr) : 1.0f;
 }
 
 template <int L>
@@ -501,9 +577,16 @@ static int check_radial(const fc_radial_desc* d) {
 template <int L>
 int launch_edge_fwd(const RadialParams& p, int64_t n, const float* pos, const float* shift, const int32_t* ii,
                     const int32_t* jj, const float* vec, float* attrs, float* feats, float* env, hipStream_t s) {
-  const int bs = 256;
-  hipLaunchKernelGGL(edge_fwd_kernel<L>, dim3((unsigned)((n + bs - 1) / bs)), dim3(bs), 0, s, p, n, pos, shift,
-                     ii, jj, vec, attrs, feats, env);
+  const int bs = kEdgeBlock;
+  int w = attrs ? ncomp(L) : 0;
+  if (feats && p.basis != FC_BASIS_NONE && p.n_radial > w) w = p.n_radial;
+  const size_t lds = sizeof(float) * (size_t)kEdgeBlock * (size_t)(w + 1);
+  if (p.basis != FC_BASIS_NONE && p.n_radial == 8)  // the packaged default count
+    hipLaunchKernelGGL((edge_fwd_kernel<L, 8>), dim3((unsigned)((n + bs - 1) / bs)), dim3(bs), lds, s, p, n, pos,
+                       shift, ii, jj, vec, attrs, feats, env);
+  else
+    hipLaunchKernelGGL((edge_fwd_kernel<L, 0>), dim3((unsigned)((n + bs - 1) / bs)), dim3(bs), lds, s, p, n, pos,
+                       shift, ii, jj, vec, attrs, feats, env);
   FC_LAUNCH_CHECK();
   return FC_OK;
 }

@@ -83,19 +83,35 @@ __global__ void __launch_bounds__(256) segment_narrow_kernel(int64_t width, cons
   }
 }
 
-// grad_pos[n] = sum_{sender segment} g[perm[k]] - sum_{receiver segment} g[k]
-__global__ void edge_grad_to_nodes_kernel(int64_t n_nodes, int64_t n_recv, int64_t n_send, const float* __restrict__ g,
-                                          const int32_t* __restrict__ rowptr, const int32_t* __restrict__ sperm,
-                                          const int32_t* __restrict__ sptr, float* __restrict__ gpos) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= n_nodes * 3) return;
-  const int64_t n = t / 3, c = t % 3;
-  float acc = 0.f;
+// grad_pos[n] = sum_{sender segment} g[perm[k]] - sum_{receiver segment} g[k], one wave per node:
+// lane l takes the segments' edges l, l + 64, ... (its sender edges, then minus its receiver
+// edges) and the wave adds the 64 partial sums by a fixed butterfly, so the result does not
+// depend on scheduling. (A thread per node component walking its ~50 edges one after another
+// left a small graph with a few dozen waves of dependent gathers.)
+__global__ void __launch_bounds__(256) edge_grad_to_nodes_kernel(int64_t n_nodes, int64_t n_recv, int64_t n_send,
+                                                               const float* __restrict__ g,
+                                                               const int32_t* __restrict__ rowptr,
+                                                               const int32_t* __restrict__ sperm,
+                                                               const int32_t* __restrict__ sptr,
+                                                               float* __restrict__ gpos) {
+  const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (n >= n_nodes) return;  // uniform over the wave
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f;
   if (n < n_send)
-    for (int32_t k = sptr[n]; k < sptr[n + 1]; ++k) acc += g[(int64_t)sperm[k] * 3 + c];
+    for (int32_t k = sptr[n] + lane; k < sptr[n + 1]; k += 64) {
+      const float* r = g + (int64_t)sperm[k] * 3;
+      a0 += r[0]; a1 += r[1]; a2 += r[2];
+    }
   if (n < n_recv)
-    for (int32_t k = rowptr[n]; k < rowptr[n + 1]; ++k) acc -= g[(int64_t)k * 3 + c];
-  gpos[t] = acc;
+    for (int32_t k = rowptr[n] + lane; k < rowptr[n + 1]; k += 64) {
+      const float* r = g + (int64_t)k * 3;
+      a0 -= r[0]; a1 -= r[1]; a2 -= r[2];
+    }
+  a0 = wave_sum(a0);
+  a1 = wave_sum(a1);
+  a2 = wave_sum(a2);
+  if (lane < 3) gpos[n * 3 + lane] = lane == 0 ? a0 : (lane == 1 ? a1 : a2);
 }
 
 // Column sums dst[c] = sum_r src[r, c] in a fixed order (one block per column tile).
@@ -169,8 +185,7 @@ extern "C" int fc_edge_grad_to_nodes(const fc_csr* gr, const float* g, float* gp
   if (gr->n_edges > 0 && !g) return FC_ERR_NULL;
   const int64_t rows = gr->n_sender_rows > gr->n_nodes ? gr->n_sender_rows : gr->n_nodes;
   if (rows == 0) return FC_OK;
-  const int bs = 256;
-  hipLaunchKernelGGL(edge_grad_to_nodes_kernel, dim3((unsigned)((rows * 3 + bs - 1) / bs)), dim3(bs), 0,
+  hipLaunchKernelGGL(edge_grad_to_nodes_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
                      (hipStream_t)stream, rows, gr->n_nodes, gr->n_sender_rows, g, gr->rowptr, gr->sender_perm, gr->sender_ptr,
                      gpos);
   FC_LAUNCH_CHECK();

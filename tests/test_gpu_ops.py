@@ -256,14 +256,16 @@ def test_radial_mlp_fused(n, n_in, m):
     assert_close(gx, ref_gx, 1e-5, 2e-5 * float(ref_gx.abs().max()), "radial mlp input grad")
 
 
-def test_edge_geometry_positions_grad():
+@pytest.mark.parametrize("n,degrees", [(64, (3, 7, 12)), (300, (1, 90, 200))])
+def test_edge_geometry_positions_grad(n, degrees):
+    """Edge geometry forward (rows staged through LDS per 256 edges, a partial last block) and
+    the position gradient's segmented sums (one wave per node; segments above 64 edges)."""
     ops = _ops()
     from flashcart_amd import _lib
     from flashcart_amd.o3._graph import build_graph
     torch.manual_seed(11)
-    n = 64
     pos64 = (torch.rand(n, 3) * 8.0).double().requires_grad_(True)
-    ei = random_csr_graph(n, (3, 7, 12), seed=2)
+    ei = random_csr_graph(n, degrees, seed=2)
     E = ei.shape[1]
     shift = torch.randint(-1, 2, (E, 3)).double() * 8.0
     v = pos64[ei[1]] - pos64[ei[0]] + shift
