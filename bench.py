@@ -41,8 +41,8 @@ HBM_PEAK_GBS = 8000.0
 # step runs them): read bytes by request size (TCC_EA0_RDREQ_32B/64B/128B), written bytes from
 # TCC_EA0_WRREQ / WRREQ_64B; a 2 GiB copy reads back 2.148 / 2.147 GB. See
 # profiles/hbm_counter_method.md and profiles/tp_conv_l1_fcc25k_kernel_only.md.
-MEASURED_TRAFFIC_BYTES = 11.34e9
-# The same for the layer-1 backward op (tp_bwd_conv_kernel 26.970 GB + segment_rows_kernel 5.098 GB).
+MEASURED_TRAFFIC_BYTES = 11.33e9
+# The same for the layer-1 backward op (tp_bwd_conv_kernel + segment_rows_kernel).
 MEASURED_TRAFFIC_BWD_BYTES = 32.07e9
 from flashcart_amd.data.synthetic import FCC25K_R_MAX as R_MAX  # noqa: E402
 from flashcart_amd.data.synthetic import FCC25K_SIGMA_STEP as SIGMA_STEP  # noqa: E402
