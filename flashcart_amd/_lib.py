@@ -14,7 +14,22 @@ from typing import Optional, Sequence
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libflashcart_hip.so")
+# Rank slots of the descriptors (FC_MAX_RANKS of include/flashcart_hip.h).
+MAX_RANKS = 5
+_ENV_L_MAX = "FLASHCART_KERNEL_L_MAX"
+
+
+def library_path(l_max: Optional[int] = None) -> str:
+    """The library for the requested rank limit (default: ``FLASHCART_KERNEL_L_MAX``, else 3):
+    ``libflashcart_hip.so`` holds the kernels of ranks 0..3, ``libflashcart_hip_l4.so`` (built with
+    ``FLASHCART_KERNEL_L_MAX=4 python -m flashcart_amd.build``) those of ranks 0..4, as the
+    reference generates its kernels for the limit that variable sets."""
+    if l_max is None:
+        l_max = int(os.environ.get(_ENV_L_MAX, "3"))
+    return os.path.join(_HERE, "libflashcart_hip_l4.so" if l_max >= 4 else "libflashcart_hip.so")
+
+
+LIB_PATH = library_path()
 
 c_int = ctypes.c_int
 c_i32 = ctypes.c_int32
@@ -52,14 +67,14 @@ class TPDesc(ctypes.Structure):
 class LinearDesc(ctypes.Structure):
     _fields_ = [
         ("in_l_max", c_i32), ("out_l_max", c_i32), ("in_features", c_i32), ("out_features", c_i32),
-        ("in_paths", c_i32 * 4), ("weight", c_vp * 4), ("scale", c_f32 * 4),
+        ("in_paths", c_i32 * MAX_RANKS), ("weight", c_vp * MAX_RANKS), ("scale", c_f32 * MAX_RANKS),
     ]
 
 
 class LinearDescF64(ctypes.Structure):
     _fields_ = [
         ("in_l_max", c_i32), ("out_l_max", c_i32), ("in_features", c_i32), ("out_features", c_i32),
-        ("in_paths", c_i32 * 4), ("weight", c_vp * 4), ("scale", c_f64 * 4),
+        ("in_paths", c_i32 * MAX_RANKS), ("weight", c_vp * MAX_RANKS), ("scale", c_f64 * MAX_RANKS),
     ]
 
 
@@ -153,9 +168,10 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     if _lib is not None:
         return _lib
     if not os.path.exists(path):
+        l4 = os.path.basename(path) == "libflashcart_hip_l4.so"
         raise HipLibraryError(
-            f"{path} is missing: build it with `python -m flashcart_amd.build` "
-            "(flashcart_amd has no CPU implementation of its kernels)."
+            f"{path} is missing: build it with `{'FLASHCART_KERNEL_L_MAX=4 ' if l4 else ''}python -m "
+            "flashcart_amd.build` (flashcart_amd has no CPU implementation of its kernels)."
         )
     lib = ctypes.CDLL(path)
     for name, (res, args) in _SIGNATURES.items():
@@ -239,7 +255,7 @@ def linear_desc(in_l_max: int, out_l_max: int, in_features: int, out_features: i
     f64 = len(weights) > 0 and weights[0].dtype == torch.float64
     d = LinearDescF64() if f64 else LinearDesc()
     d.in_l_max, d.out_l_max, d.in_features, d.out_features = int(in_l_max), int(out_l_max), int(in_features), int(out_features)
-    for l in range(4):
+    for l in range(MAX_RANKS):
         d.in_paths[l] = int(in_paths[l]) if l < len(in_paths) else 1
         d.weight[l] = weights[l].data_ptr() if l < len(weights) else None
         d.scale[l] = float(scale[l]) if l < len(scale) else 0.0

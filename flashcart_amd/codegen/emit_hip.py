@@ -195,6 +195,7 @@ def emit_expand_header(l_max: int = KERNEL_L_MAX) -> str:
         "// Generated by flashcart_amd/codegen/emit_hip.py -- do not edit.",
         "// Eq. (1) stored components of ranks 0..L and their polynomial gradients.",
         "#pragma once",
+        f"#define FC_KERNEL_L_MAX {l_max}",
         "namespace fc {",
         "template <int L> struct Expand;",
     ]
@@ -243,10 +244,12 @@ def emit_expand_header(l_max: int = KERNEL_L_MAX) -> str:
     return "\n".join(L) + "\n"
 
 
-def write_all(out_dir: str) -> List[str]:
+def write_all(out_dir: str, l_max: int = KERNEL_L_MAX) -> List[str]:
+    """Write both headers for ranks 0..l_max (3: the default library; 4: the library built with
+    FLASHCART_KERNEL_L_MAX=4), rewriting a file only when its text changes."""
     os.makedirs(out_dir, exist_ok=True)
     written = []
-    for name, text in (("fc_tp_paths.h", emit_tp_header()), ("fc_expand_poly.h", emit_expand_header())):
+    for name, text in (("fc_tp_paths.h", emit_tp_header(l_max)), ("fc_expand_poly.h", emit_expand_header(l_max))):
         path = os.path.join(out_dir, name)
         old = open(path).read() if os.path.exists(path) else None
         if old != text:
@@ -259,5 +262,5 @@ def write_all(out_dir: str) -> List[str]:
 
 if __name__ == "__main__":
     out = sys.argv[1] if len(sys.argv) > 1 else os.path.join(os.path.dirname(__file__), "..", "csrc", "generated")
-    for p in write_all(out):
+    for p in write_all(out, int(sys.argv[2]) if len(sys.argv) > 2 else KERNEL_L_MAX):
         print(p)

@@ -38,7 +38,7 @@ static int check_tp(const fc_tp_desc* d) {
 }
 
 static int64_t out_width(const fc_tp_desc* d) {
-  int per[4] = {0, 0, 0, 0};
+  int per[FC_MAX_RANKS] = {0};
   count_paths(d->in1_l_max, d->in2_l_max, d->out_l_max, d->symmetric_product != 0, per);
   const int64_t C = d->in1_features > d->in2_features ? d->in1_features : d->in2_features;
   int64_t w = 0;
@@ -67,6 +67,9 @@ static int dispatch(const fc_tp_desc* d, const TPArgs& g, bool conv, bool bwd, h
     case 1: return dispatch_tp_l1(d->in2_l_max, d->out_l_max, sym, g, conv, bwd, s);
     case 2: return dispatch_tp_l2(d->in2_l_max, d->out_l_max, sym, g, conv, bwd, s);
     case 3: return dispatch_tp_l3(d->in2_l_max, d->out_l_max, sym, g, conv, bwd, s);
+#if FC_KERNEL_L_MAX >= 4
+    case 4: return dispatch_tp_l4(d->in2_l_max, d->out_l_max, sym, g, conv, bwd, s);
+#endif
   }
   return FC_ERR_UNSUPPORTED_L;
 }

@@ -6,7 +6,7 @@
 // (and their intermediates) of the reference forward (src/flashcart/model/
 // flashcart.py:268-284) and the matching autograd chain in the backward.
 #include "fc_common.h"
-#include "generated/fc_expand_poly.h"
+#include "fc_expand_poly.h"  // Expand<0..FC_KERNEL_L_MAX>, generated for the build's rank limit
 
 namespace fc {
 
@@ -555,6 +555,9 @@ int launch_by_l(int l, int64_t n, hipStream_t s, Args... args) {
     case 1: hipLaunchKernelGGL(K<1>::fn, grid, block, 0, s, n, args...); break;
     case 2: hipLaunchKernelGGL(K<2>::fn, grid, block, 0, s, n, args...); break;
     case 3: hipLaunchKernelGGL(K<3>::fn, grid, block, 0, s, n, args...); break;
+#if FC_KERNEL_L_MAX >= 4
+    case 4: hipLaunchKernelGGL(K<4>::fn, grid, block, 0, s, n, args...); break;
+#endif
     default: return FC_ERR_UNSUPPORTED_L;
   }
   FC_LAUNCH_CHECK();
@@ -702,6 +705,9 @@ extern "C" int fc_edge_geometry_fwd(const fc_edge_desc* desc, int64_t n, const f
     case 1: return launch_edge_fwd<1>(p, n, pos, shift, ii, jj, vectors, attrs, feats, env, s);
     case 2: return launch_edge_fwd<2>(p, n, pos, shift, ii, jj, vectors, attrs, feats, env, s);
     case 3: return launch_edge_fwd<3>(p, n, pos, shift, ii, jj, vectors, attrs, feats, env, s);
+#if FC_KERNEL_L_MAX >= 4
+    case 4: return launch_edge_fwd<4>(p, n, pos, shift, ii, jj, vectors, attrs, feats, env, s);
+#endif
   }
   return FC_ERR_UNSUPPORTED_L;
 }
@@ -722,6 +728,9 @@ extern "C" int fc_edge_geometry_bwd(const fc_edge_desc* desc, int64_t n, const f
     case 1: return launch_edge_bwd<1>(p, n, pos, shift, ii, jj, vectors, ga, gf, ge, gvec, s);
     case 2: return launch_edge_bwd<2>(p, n, pos, shift, ii, jj, vectors, ga, gf, ge, gvec, s);
     case 3: return launch_edge_bwd<3>(p, n, pos, shift, ii, jj, vectors, ga, gf, ge, gvec, s);
+#if FC_KERNEL_L_MAX >= 4
+    case 4: return launch_edge_bwd<4>(p, n, pos, shift, ii, jj, vectors, ga, gf, ge, gvec, s);
+#endif
   }
   return FC_ERR_UNSUPPORTED_L;
 }
@@ -733,7 +742,7 @@ extern "C" int fc_edge_geometry_dbwd(const fc_edge_desc* desc, int64_t n, const 
   if (!desc) return FC_ERR_NULL;
   int st = check_radial(&desc->radial);
   if (st != FC_OK) return st;
-  if (desc->l_max < 0 || desc->l_max > 3) return FC_ERR_UNSUPPORTED_L;
+  if (desc->l_max < 0 || desc->l_max > FC_KERNEL_L_MAX) return FC_ERR_UNSUPPORTED_L;
   if (n == 0) return FC_OK;
   if (!cot_vec || (pos ? (!ii || !jj) : !vectors)) return FC_ERR_NULL;
   const RadialParams p = radial_params(desc->radial);
@@ -747,6 +756,9 @@ extern "C" int fc_edge_geometry_dbwd(const fc_edge_desc* desc, int64_t n, const 
     case 1: FC_EDGE_DBWD(1); break;
     case 2: FC_EDGE_DBWD(2); break;
     case 3: FC_EDGE_DBWD(3); break;
+#if FC_KERNEL_L_MAX >= 4
+    case 4: FC_EDGE_DBWD(4); break;
+#endif
   }
 #undef FC_EDGE_DBWD
   FC_LAUNCH_CHECK();

@@ -8,7 +8,7 @@
 //   grad_pre[n, l, c]      = act'(pre) * sum_a grad_out[n,(l,a),c] * values[n,(l,a),c]
 // Thread per (node, channel); ranks and components in registers.
 #include "fc_common.h"
-#include "generated/fc_tp_paths.h"  // FC_KERNEL_L_MAX
+#include "fc_tp_paths.h"  // FC_KERNEL_L_MAX
 
 namespace fc {
 

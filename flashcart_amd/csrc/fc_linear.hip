@@ -55,7 +55,7 @@ struct GemmRank {
 };
 
 struct GemmBatch {
-  GemmRank r[4];
+  GemmRank r[FC_MAX_RANKS];
   int32_t n_ranks, total_tiles;
   const float* bias;  // dense fwd only
   int32_t trans_b;    // 1: B(k, o) = W[o*K + k] (forward); 0: B(k, o) = W[k*N + o] (input gradient)
@@ -94,7 +94,7 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmBatch gb) {
   if (tile >= gb.total_tiles) return;
   int ri = 0;
 #pragma unroll
-  for (int q = 1; q < 4; ++q)
+  for (int q = 1; q < FC_MAX_RANKS; ++q)
     if (q < gb.n_ranks && tile >= gb.r[q].tile_base) ri = q;
   const GemmRank& g = gb.r[ri];
   const int local = tile - g.tile_base;
@@ -487,13 +487,13 @@ __global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 
   const int v = (G >= 8 && G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
   int64_t work = 0;
 #pragma unroll
-  for (int q = 0; q < 4; ++q)
+  for (int q = 0; q < FC_MAX_RANKS; ++q)
     if (q < gb.n_ranks) work += (int64_t)gb.r[q].tiles_m * gb.r[q].tiles_n * (gb.r[q].K / 32);
   // first tile whose first K step (counted over the whole batch) is at or after step s
   auto tile_at = [&](int64_t s) -> int {
     int64_t base = 0;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < FC_MAX_RANKS; ++q) {
       if (q >= gb.n_ranks) break;
       const GemmRank& g = gb.r[q];
       const int64_t ks = g.K / 32, n = (int64_t)g.tiles_m * g.tiles_n;
@@ -512,7 +512,7 @@ __global__ void __launch_bounds__(256, ((PS ? 2 : 1) * BM + BN) * 32 * 4 * 3 <= 
   auto decode = [&](int tile) -> PipeTile {
     int ri = 0;
 #pragma unroll
-    for (int q = 1; q < 4; ++q)
+    for (int q = 1; q < FC_MAX_RANKS; ++q)
       if (q < gb.n_ranks && tile >= gb.r[q].tile_base) ri = q;
     ri = __builtin_amdgcn_readfirstlane(ri);  // uniform: keeps the rank's fields in scalar loads
     const GemmRank& g = gb.r[ri];
@@ -947,7 +947,7 @@ int fill_columns(int64_t rows, int64_t row_stride, int64_t off, int64_t width, c
 static int check_linear(const fc_linear_desc* d) {
   if (!d) return FC_ERR_NULL;
   if (d->in_l_max < 0 || d->out_l_max < 0) return FC_ERR_BAD_DESC;
-  if (d->in_l_max > 3 || d->out_l_max > 3) return FC_ERR_UNSUPPORTED_L;
+  if (d->in_l_max >= FC_MAX_RANKS || d->out_l_max >= FC_MAX_RANKS) return FC_ERR_UNSUPPORTED_L;
   if (d->in_features < 1 || d->out_features < 1) return FC_ERR_BAD_DESC;
   const int common = d->in_l_max < d->out_l_max ? d->in_l_max : d->out_l_max;
   for (int l = 0; l <= d->in_l_max; ++l)
@@ -958,7 +958,7 @@ static int check_linear(const fc_linear_desc* d) {
 }
 
 struct LinearLayout {
-  int64_t in_dim, out_dim, in_off[4], out_off[4];
+  int64_t in_dim, out_dim, in_off[FC_MAX_RANKS], out_off[FC_MAX_RANKS];
   int common;
 };
 
@@ -990,7 +990,7 @@ extern "C" int fc_linear_fwd(const fc_linear_desc* d, int64_t n, const float* x,
   if (st != FC_OK) return st;
   if (n == 0) return FC_OK;
   if (!x || !out) return FC_ERR_NULL;
-  if (n * 7 > 0x7fffffff) return FC_ERR_SHAPE;
+  if (n * (2 * FC_MAX_RANKS - 1) > 0x7fffffff) return FC_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   const LinearLayout L = linear_layout(d);
   GemmBatch gb{};
@@ -1026,7 +1026,7 @@ extern "C" int fc_linear_dgrad(const fc_linear_desc* d, int64_t n, const float* 
   if (st != FC_OK) return st;
   if (n == 0) return FC_OK;
   if (!go || !gx) return FC_ERR_NULL;
-  if (n * 7 > 0x7fffffff) return FC_ERR_SHAPE;
+  if (n * (2 * FC_MAX_RANKS - 1) > 0x7fffffff) return FC_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   const LinearLayout L = linear_layout(d);
   GemmBatch gb{};
@@ -1736,8 +1736,8 @@ struct WgradSection {
 };
 
 struct WgradBatch {
-  WgradProblem p[4];
-  WgradSection sec[8];
+  WgradProblem p[FC_MAX_RANKS];
+  WgradSection sec[2 * FC_MAX_RANKS];
   int32_t n, total_wg, n_sec;
   int64_t total_elems;
   float* part;
@@ -1784,7 +1784,7 @@ __global__ void __launch_bounds__(256) wgrad_kernel(WgradBatch wb) {
   if (b >= wb.total_wg) return;
   int pi = 0;
 #pragma unroll
-  for (int q = 1; q < 4; ++q)
+  for (int q = 1; q < FC_MAX_RANKS; ++q)
     if (q < wb.n && b >= wb.p[q].wg_base) pi = q;
   const WgradProblem& g = wb.p[pi];
   const int local = b - g.wg_base;
@@ -2040,8 +2040,8 @@ extern "C" int64_t fc_linear_wgrad_workspace(const fc_linear_desc* d, int64_t n,
   if (st != FC_OK) return -st;
   if (n < 0) return -FC_ERR_SHAPE;
   // only which entries are non-NULL matters here (NULL array: every rank)
-  float* all[4] = {reinterpret_cast<float*>(16), reinterpret_cast<float*>(16), reinterpret_cast<float*>(16),
-                   reinterpret_cast<float*>(16)};
+  float* all[FC_MAX_RANKS];
+  for (int l = 0; l < FC_MAX_RANKS; ++l) all[l] = reinterpret_cast<float*>(16);
   WgradBatch wb;
   linear_wgrad_batch(d, n, nullptr, nullptr, 1.f, grad_w ? grad_w : all, wb);
   int TO, TJ;
@@ -2054,7 +2054,7 @@ extern "C" int fc_linear_wgrad(const fc_linear_desc* d, int64_t n, const float* 
   if (st != FC_OK) return st;
   if (n < 0) return FC_ERR_SHAPE;
   if (!grad_w) return FC_ERR_NULL;
-  if (n * 7 > 0x7fffffff) return FC_ERR_SHAPE;
+  if (n * (2 * FC_MAX_RANKS - 1) > 0x7fffffff) return FC_ERR_SHAPE;
   const int common = d->in_l_max < d->out_l_max ? d->in_l_max : d->out_l_max;
   if (n == 0) {  // no rows: zero gradients (a fill kernel, so the call can be graph-captured)
     for (int l = 0; l <= common; ++l)

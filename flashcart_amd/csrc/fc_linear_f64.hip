@@ -16,7 +16,7 @@ namespace {
 
 constexpr int F64_T = 64;      // output tile edge
 constexpr int F64_KS = 16;     // reduction step
-constexpr int F64_MAXB = 16;   // (rank, component) blocks: sum over l <= 3 of 2l + 1
+constexpr int F64_MAXB = FC_MAX_RANKS * FC_MAX_RANKS;  // (rank, component) blocks: sum over l of 2l + 1
 constexpr int F64_MAXPARTS = 256;
 
 // One (rank l, component c) block of the forward or the input gradient:
@@ -113,7 +113,7 @@ struct F64WRank {
 };
 
 struct F64WBatch {
-  F64WRank r[4];
+  F64WRank r[FC_MAX_RANKS];
   int32_t n_ranks, parts;
   int64_t n, g_ld, x_ld;
 };
@@ -211,7 +211,7 @@ int fill_f64(int64_t rows, int64_t row_stride, int64_t off, int64_t width, const
 int check_f64(const fc_linear_desc_f64* d) {
   if (!d) return FC_ERR_NULL;
   if (d->in_l_max < 0 || d->out_l_max < 0) return FC_ERR_BAD_DESC;
-  if (d->in_l_max > 3 || d->out_l_max > 3) return FC_ERR_UNSUPPORTED_L;
+  if (d->in_l_max >= FC_MAX_RANKS || d->out_l_max >= FC_MAX_RANKS) return FC_ERR_UNSUPPORTED_L;
   if (d->in_features < 1 || d->out_features < 1) return FC_ERR_BAD_DESC;
   const int common = d->in_l_max < d->out_l_max ? d->in_l_max : d->out_l_max;
   for (int l = 0; l <= d->in_l_max; ++l)
@@ -222,7 +222,7 @@ int check_f64(const fc_linear_desc_f64* d) {
 }
 
 struct F64Layout {
-  int64_t in_dim, out_dim, in_off[4], out_off[4];
+  int64_t in_dim, out_dim, in_off[FC_MAX_RANKS], out_off[FC_MAX_RANKS];
   int common;
 };
 
@@ -345,8 +345,8 @@ extern "C" int64_t fc_linear_wgrad_f64_workspace(const fc_linear_desc_f64* d, in
   if (st != FC_OK) return -st;
   if (n < 0) return -FC_ERR_SHAPE;
   // only which entries are non-NULL matters here (NULL array: every rank)
-  double* all[4] = {reinterpret_cast<double*>(16), reinterpret_cast<double*>(16), reinterpret_cast<double*>(16),
-                    reinterpret_cast<double*>(16)};
+  double* all[FC_MAX_RANKS];
+  for (int l = 0; l < FC_MAX_RANKS; ++l) all[l] = reinterpret_cast<double*>(16);
   F64WBatch wb;
   return plan_wgrad_f64(d, n, grad_w ? grad_w : all, wb);
 }

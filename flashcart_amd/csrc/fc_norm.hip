@@ -9,7 +9,7 @@
 // One workgroup per node, one lane per channel; the channel sum is a wave butterfly
 // plus a fixed-order sum over the waves, so results are deterministic.
 #include "fc_common.h"
-#include "generated/fc_tp_paths.h"
+#include "fc_tp_paths.h"
 
 namespace fc {
 
@@ -219,6 +219,9 @@ static int rms_dispatch(bool bwd, int64_t n, int l_max, int C, const float* go, 
     case 1: return launch_rms<1>(bwd, n, C, go, x, g, eps, out, scale, s);
     case 2: return launch_rms<2>(bwd, n, C, go, x, g, eps, out, scale, s);
     case 3: return launch_rms<3>(bwd, n, C, go, x, g, eps, out, scale, s);
+#if FC_KERNEL_L_MAX >= 4
+    case 4: return launch_rms<4>(bwd, n, C, go, x, g, eps, out, scale, s);
+#endif
   }
   return FC_ERR_UNSUPPORTED_L;
 }
@@ -255,6 +258,9 @@ extern "C" int fc_rms_norm_dbwd(int64_t n, int32_t l_max, int32_t C, const float
     case 1: return launch_rms_dbwd<1>(n, C, grad_out, x, weight, scale, cot, d_grad_out, d_x, d_weight_part, s);
     case 2: return launch_rms_dbwd<2>(n, C, grad_out, x, weight, scale, cot, d_grad_out, d_x, d_weight_part, s);
     case 3: return launch_rms_dbwd<3>(n, C, grad_out, x, weight, scale, cot, d_grad_out, d_x, d_weight_part, s);
+#if FC_KERNEL_L_MAX >= 4
+    case 4: return launch_rms_dbwd<4>(n, C, grad_out, x, weight, scale, cot, d_grad_out, d_x, d_weight_part, s);
+#endif
   }
   return FC_ERR_UNSUPPORTED_L;
 }

@@ -101,8 +101,8 @@ __global__ void __launch_bounds__(256) species_density_fwd_kernel(int64_t n_rows
 // lane >> (6 - log2 N) == v holds the total of value v.
 template <int N>
 __device__ __forceinline__ float wave_reduce_n(float (&v)[N], int lane) {
-  constexpr int LOGN = N == 1 ? 0 : N == 2 ? 1 : N == 4 ? 2 : N == 8 ? 3 : 4;
-  static_assert((1 << LOGN) == N, "power of two up to 16");
+  constexpr int LOGN = N == 1 ? 0 : N == 2 ? 1 : N == 4 ? 2 : N == 8 ? 3 : N == 16 ? 4 : 5;
+  static_assert((1 << LOGN) == N, "power of two up to 32");
 #pragma unroll
   for (int s = 0; s < LOGN; ++s) {
     const int half = N >> (s + 1);
@@ -139,8 +139,9 @@ __global__ void __launch_bounds__(256) species_density_bwd_kernel(int64_t n_rows
                                                                   const float* __restrict__ y,
                                                                   const float* __restrict__ g_dens,
                                                                   float* __restrict__ g_h, float* __restrict__ g_y) {
-  constexpr int R = D <= 1 ? 1 : D <= 2 ? 2 : D <= 4 ? 4 : D <= 8 ? 8 : 16;
-  constexpr int SH = R == 1 ? 6 : R == 2 ? 5 : R == 4 ? 4 : R == 8 ? 3 : 2;
+  constexpr int R = D <= 1 ? 1 : D <= 2 ? 2 : D <= 4 ? 4 : D <= 8 ? 8 : D <= 16 ? 16 : 32;  // >= D
+  constexpr int SH = R == 1 ? 6 : R == 2 ? 5 : R == 4 ? 4 : R == 8 ? 3 : R == 16 ? 2 : 1;
+  static_assert(R >= D, "one reduction slot per component");
   constexpr int U = 4;
   extern __shared__ float ga[];
   const int64_t row = xcd_row(n_rows);
@@ -214,6 +215,7 @@ static int dispatch_species(int l_max, bool bwd, int64_t n_rows, int n_species, 
     case 1: return launch_species<4>(bwd, n_rows, n_species, y_stride, rowptr, slot, zj, h, y, g, g_h, out, s);
     case 2: return launch_species<9>(bwd, n_rows, n_species, y_stride, rowptr, slot, zj, h, y, g, g_h, out, s);
     case 3: return launch_species<16>(bwd, n_rows, n_species, y_stride, rowptr, slot, zj, h, y, g, g_h, out, s);
+    case 4: return launch_species<25>(bwd, n_rows, n_species, y_stride, rowptr, slot, zj, h, y, g, g_h, out, s);
   }
   return FC_ERR_UNSUPPORTED_L;
 }
@@ -231,9 +233,9 @@ struct SpeciesMapsArgs {
   const float* table;
   const float* w_first;
   const float* alpha_div;
-  const float* w_second[4];
+  const float* w_second[FC_MAX_RANKS];
   const float* w_radial;
-  float* maps[4];
+  float* maps[FC_MAX_RANKS];
   float s_first;
   int c_in, c_mid, c_out, nh, n_species;
   bool x_vec;   // c_in a multiple of 16 and w_first 16-byte aligned: rows read as float4
@@ -342,7 +344,7 @@ extern "C" int fc_species_maps(int32_t n_species, int32_t c_in, int32_t c_mid, i
                                float* const* maps, void* stream) {
   if (n_species < 1 || n_species > kSpeciesMax || c_in < 1 || c_out < 1 || n_hidden < 1) return FC_ERR_SHAPE;
   if (c_mid < 1 || c_mid > kMapsMaxMid || c_in > kMapsMaxIn || n_hidden > 64) return FC_ERR_SHAPE;
-  if (n_ranks < 1 || n_ranks > 4) return FC_ERR_UNSUPPORTED_L;
+  if (n_ranks < 1 || n_ranks > FC_MAX_RANKS) return FC_ERR_UNSUPPORTED_L;
   if (!table || !w_first || !alpha_div || !w_second || !w_radial || !maps) return FC_ERR_NULL;
   SpeciesMapsArgs a{};
   for (int l = 0; l < n_ranks; ++l) {
@@ -371,7 +373,7 @@ extern "C" int fc_species_maps(int32_t n_species, int32_t c_in, int32_t c_mid, i
 
 static int check_species(const fc_csr* gr, int32_t l_max, int32_t y_l_max, int32_t n_species) {
   if (!gr) return FC_ERR_NULL;
-  if (l_max > 3 || y_l_max > 3) return FC_ERR_UNSUPPORTED_L;
+  if (l_max >= FC_MAX_RANKS || y_l_max >= FC_MAX_RANKS) return FC_ERR_UNSUPPORTED_L;
   if (l_max < 0 || l_max > y_l_max) return FC_ERR_BAD_DESC;
   if (n_species < 1 || n_species > kSpeciesMax) return FC_ERR_SHAPE;
   if (gr->n_nodes < 0 || gr->n_edges < 0) return FC_ERR_SHAPE;

@@ -15,7 +15,7 @@
 // is contracted, so the HBM latency of the gathered rows is hidden at 2-3 waves/SIMD.
 #pragma once
 #include "fc_common.h"
-#include "generated/fc_tp_paths.h"
+#include "fc_tp_paths.h"  // generated for the build's rank limit
 
 namespace fc {
 
@@ -761,6 +761,9 @@ int dispatch_tp_l0(int l2, int lo, bool sym, const TPArgs& g, bool conv, bool bw
 int dispatch_tp_l1(int l2, int lo, bool sym, const TPArgs& g, bool conv, bool bwd, hipStream_t s);
 int dispatch_tp_l2(int l2, int lo, bool sym, const TPArgs& g, bool conv, bool bwd, hipStream_t s);
 int dispatch_tp_l3(int l2, int lo, bool sym, const TPArgs& g, bool conv, bool bwd, hipStream_t s);
+#if FC_KERNEL_L_MAX >= 4
+int dispatch_tp_l4(int l2, int lo, bool sym, const TPArgs& g, bool conv, bool bwd, hipStream_t s);
+#endif
 
 template <int L1>
 int dispatch_tp_for(int l2, int lo, bool sym, const TPArgs& g, bool conv, bool bwd, hipStream_t s) {
@@ -776,6 +779,10 @@ int dispatch_tp_for(int l2, int lo, bool sym, const TPArgs& g, bool conv, bool b
   FC_TP_CASE(1, 0) FC_TP_CASE(1, 1) FC_TP_CASE(1, 2) FC_TP_CASE(1, 3)
   FC_TP_CASE(2, 0) FC_TP_CASE(2, 1) FC_TP_CASE(2, 2) FC_TP_CASE(2, 3)
   FC_TP_CASE(3, 0) FC_TP_CASE(3, 1) FC_TP_CASE(3, 2) FC_TP_CASE(3, 3)
+#if FC_KERNEL_L_MAX >= 4
+  FC_TP_CASE(0, 4) FC_TP_CASE(1, 4) FC_TP_CASE(2, 4) FC_TP_CASE(3, 4)
+  FC_TP_CASE(4, 0) FC_TP_CASE(4, 1) FC_TP_CASE(4, 2) FC_TP_CASE(4, 3) FC_TP_CASE(4, 4)
+#endif
 #undef FC_TP_CASE
   return FC_ERR_UNSUPPORTED_L;
 }

@@ -709,8 +709,8 @@ def _linear_dims(in_l_max, out_l_max, in_features, out_features, in_paths):
     return in_dim, out_dim
 
 
-def _wlist(w0, w1, w2, w3) -> List[Tensor]:
-    return [w for w in (w0, w1, w2, w3) if w is not None]
+def _wlist(w0, w1, w2, w3, w4) -> List[Tensor]:
+    return [w for w in (w0, w1, w2, w3, w4) if w is not None]
 
 
 def _lin_dtype(t: Tensor) -> torch.dtype:
@@ -723,16 +723,17 @@ def _lin_name(name: str, dt: torch.dtype) -> str:
     return name + "_f64" if dt == torch.float64 else name
 
 
-def _pad4(weights):
-    ws = list(weights) + [None] * (4 - len(weights))
-    if len(ws) != 4:
-        raise ValueError("at most 4 rank blocks (l <= 3) are supported.")
+def _pad_ranks(weights):
+    """The weights in the ops' MAX_RANKS slots (ranks 0..4), None past the last rank."""
+    ws = list(weights) + [None] * (_lib.MAX_RANKS - len(weights))
+    if len(ws) != _lib.MAX_RANKS:
+        raise ValueError(f"at most {_lib.MAX_RANKS} rank blocks (l <= {_lib.MAX_RANKS - 1}) are supported.")
     return ws
 
 
 @torch.library.custom_op("flashcart::equiv_linear_fwd", mutates_args=())
 def linear_fwd_op(x: Tensor, w0: Tensor, w1: Optional[Tensor], w2: Optional[Tensor], w3: Optional[Tensor],
-                  in_l_max: int, out_l_max: int, in_features: int, out_features: int, in_paths: List[int],
+                  w4: Optional[Tensor], in_l_max: int, out_l_max: int, in_features: int, out_features: int, in_paths: List[int],
                   scale: List[float], alpha: float = 1.0, residual: Optional[Tensor] = None) -> Tensor:
     """out = linear(x) (+ residual, a tensor of the output's shape added in the GEMM epilogue): the
     build's own layers call this op (the reference-schema ``flashcart::linear_fwd`` is below)."""
@@ -741,7 +742,7 @@ def linear_fwd_op(x: Tensor, w0: Tensor, w1: Optional[Tensor], w2: Optional[Tens
         raise RuntimeError(f"Incorrect last dimension for x. Expected {in_dim}, got {x.shape[-1]}.")
     dt = _lin_dtype(x)
     x = _lib.contig("x", x, dt)
-    ws = [_lib.contig(f"weight[{l}]", w, dt) for l, w in enumerate(_wlist(w0, w1, w2, w3))]
+    ws = [_lib.contig(f"weight[{l}]", w, dt) for l, w in enumerate(_wlist(w0, w1, w2, w3, w4))]
     out = x.new_empty(x.shape[0], out_dim)
     r = _check_residual(residual, out)
     desc = _lib.linear_desc(in_l_max, out_l_max, in_features, out_features, in_paths, ws, scale)
@@ -751,7 +752,7 @@ def linear_fwd_op(x: Tensor, w0: Tensor, w1: Optional[Tensor], w2: Optional[Tens
 
 
 @linear_fwd_op.register_fake
-def _(x, w0, w1, w2, w3, in_l_max, out_l_max, in_features, out_features, in_paths, scale, alpha=1.0,
+def _(x, w0, w1, w2, w3, w4, in_l_max, out_l_max, in_features, out_features, in_paths, scale, alpha=1.0,
       residual=None):
     _, out_dim = _linear_dims(in_l_max, out_l_max, in_features, out_features, in_paths)
     return x.new_empty(x.shape[0], out_dim)
@@ -759,13 +760,13 @@ def _(x, w0, w1, w2, w3, in_l_max, out_l_max, in_features, out_features, in_path
 
 @torch.library.custom_op("flashcart::equiv_linear_dgrad", mutates_args=())
 def linear_bwd_op(grad_out: Tensor, w0: Tensor, w1: Optional[Tensor], w2: Optional[Tensor], w3: Optional[Tensor],
-                  in_l_max: int, out_l_max: int, in_features: int, out_features: int, in_paths: List[int],
+                  w4: Optional[Tensor], in_l_max: int, out_l_max: int, in_features: int, out_features: int, in_paths: List[int],
                   scale: List[float], alpha: float = 1.0, residual: Optional[Tensor] = None) -> Tensor:
     """Input gradient of linear_fwd (the MFMA dgrad), plus ``residual`` when given."""
     in_dim, _ = _linear_dims(in_l_max, out_l_max, in_features, out_features, in_paths)
     dt = _lin_dtype(grad_out)
     go = _lib.contig("grad_out", grad_out, dt)
-    ws = [_lib.contig(f"weight[{l}]", w, dt) for l, w in enumerate(_wlist(w0, w1, w2, w3))]
+    ws = [_lib.contig(f"weight[{l}]", w, dt) for l, w in enumerate(_wlist(w0, w1, w2, w3, w4))]
     gx = go.new_empty(go.shape[0], in_dim)
     r = _check_residual(residual, gx)
     desc = _lib.linear_desc(in_l_max, out_l_max, in_features, out_features, in_paths, ws, scale)
@@ -775,7 +776,7 @@ def linear_bwd_op(grad_out: Tensor, w0: Tensor, w1: Optional[Tensor], w2: Option
 
 
 @linear_bwd_op.register_fake
-def _(grad_out, w0, w1, w2, w3, in_l_max, out_l_max, in_features, out_features, in_paths, scale, alpha=1.0,
+def _(grad_out, w0, w1, w2, w3, w4, in_l_max, out_l_max, in_features, out_features, in_paths, scale, alpha=1.0,
       residual=None):
     in_dim, _ = _linear_dims(in_l_max, out_l_max, in_features, out_features, in_paths)
     return grad_out.new_empty(grad_out.shape[0], in_dim)
@@ -786,14 +787,14 @@ def linear_fwd(x: Tensor, weights: List[Tensor], in_l_max: int, out_l_max: int, 
                residual: Optional[Tensor] = None) -> Tensor:
     """out_l = alpha * scale_l * x_l @ W_l^T for every shared rank (torch.ops.flashcart.equiv_linear_fwd),
     plus ``residual`` (same shape as the output) when given."""
-    return linear_fwd_op(x, *_pad4(weights), in_l_max, out_l_max, in_features, out_features, list(in_paths),
+    return linear_fwd_op(x, *_pad_ranks(weights), in_l_max, out_l_max, in_features, out_features, list(in_paths),
                          [float(s) for s in scale], float(alpha), residual)
 
 
 def linear_bwd(grad_out: Tensor, weights: List[Tensor], in_l_max: int, out_l_max: int, in_features: int,
                out_features: int, in_paths: List[int], scale: List[float], alpha: float = 1.0,
                residual: Optional[Tensor] = None) -> Tensor:
-    return linear_bwd_op(grad_out, *_pad4(weights), in_l_max, out_l_max, in_features, out_features,
+    return linear_bwd_op(grad_out, *_pad_ranks(weights), in_l_max, out_l_max, in_features, out_features,
                          list(in_paths), [float(s) for s in scale], float(alpha), residual)
 
 
@@ -806,8 +807,8 @@ def _check_residual(residual: Optional[Tensor], out: Tensor) -> Optional[Tensor]
 
 
 def _linear_setup(ctx, inputs, output):
-    x, w0, w1, w2, w3, in_l_max, out_l_max, in_features, out_features, in_paths, scale, alpha, residual = inputs
-    ws = _wlist(w0, w1, w2, w3)
+    x, w0, w1, w2, w3, w4, in_l_max, out_l_max, in_features, out_features, in_paths, scale, alpha, residual = inputs
+    ws = _wlist(w0, w1, w2, w3, w4)
     ctx.save_for_backward(x, *ws)
     ctx.cfg = (int(in_l_max), int(out_l_max), int(in_features), int(out_features), list(in_paths), list(scale))
     ctx.alpha = float(alpha)
@@ -820,13 +821,14 @@ def _linear_backward(ctx, grad):
     gx = None
     if need[0]:
         gx = linear_bwd(grad, weights, in_l_max, out_l_max, fin, fout, in_paths, scale, ctx.alpha)
-    gws = [None, None, None, None]
-    if any(need[1:5]):  # parameter gradients (training)
+    gws = [None] * _lib.MAX_RANKS
+    if any(need[1:1 + _lib.MAX_RANKS]):  # parameter gradients (training)
         gws = linear_wgrad(grad, x, weights, in_l_max, out_l_max, fin, fout, in_paths, scale, ctx.alpha,
                            [bool(need[1 + l]) for l in range(len(weights))])
-        gws = gws + [None] * (4 - len(gws))
+        gws = gws + [None] * (_lib.MAX_RANKS - len(gws))
     # trailing arguments left at their defaults are not part of needs_input_grad
-    g_res = grad if len(need) > 12 and need[12] else None
+    i_res = 8 + _lib.MAX_RANKS  # x, the weight slots, 7 configuration arguments, residual
+    g_res = grad if len(need) > i_res and need[i_res] else None
     return (gx, *gws) + (None,) * 7 + (g_res,)
 
 
@@ -866,7 +868,8 @@ def linear_wgrad(grad_out: Tensor, x: Tensor, weights: List[Tensor], in_l_max: i
     desc = _lib.linear_desc(in_l_max, out_l_max, in_features, out_features, in_paths, ws, scale)
     lib = _lib.load()
     n = go.shape[0]
-    ptrs = (_lib.c_vp * 4)(*([o.data_ptr() if o is not None else None for o in outs] + [None] * (4 - len(outs))))
+    ptrs = (_lib.c_vp * _lib.MAX_RANKS)(*([o.data_ptr() if o is not None else None for o in outs] +
+                                          [None] * (_lib.MAX_RANKS - len(outs))))
     ws_name = "fc_linear_wgrad_f64_workspace" if dt == torch.float64 else "fc_linear_wgrad_workspace"
     n_ws = getattr(lib, ws_name)(desc, n, ptrs)
     if n_ws < 0:
@@ -901,8 +904,8 @@ def _ref_linear_layout(x: Tensor, weights: List[Tensor], use_fp64: bool, dot_inp
         raise ValueError(f"dot_input_precision must be one of {_PRECISIONS}. Provided: {dot_input_precision!r}.")
     n = len(in_offsets)
     lists = (out_offsets, weight_offsets, m_values, f_in_values, f_out_values)
-    if any(len(v) != n for v in lists) or n > 4:
-        raise RuntimeError("linear metadata lists must have one entry per active rank (at most 4).")
+    if any(len(v) != n for v in lists) or n > _lib.MAX_RANKS:
+        raise RuntimeError(f"linear metadata lists must have one entry per active rank (at most {_lib.MAX_RANKS}).")
     if len(weights) < n:
         raise RuntimeError(f"Expected at least {n} weight tensors, got {len(weights)}.")
     fout = int(f_out_values[0]) if n else 1
@@ -1453,8 +1456,8 @@ def species_maps(table: Tensor, w_first: Tensor, s_first: float, alpha_div: Tens
         raise RuntimeError("species_maps: inconsistent shapes.")
     out = tb.new_empty(n, c_out, n_sp * nh)
     mats = [out[l] for l in range(n)]
-    wp = (_lib.c_vp * 4)(*([w.data_ptr() for w in ws] + [None] * (4 - n)))
-    mp = (_lib.c_vp * 4)(*([m.data_ptr() for m in mats] + [None] * (4 - n)))
+    wp = (_lib.c_vp * _lib.MAX_RANKS)(*([w.data_ptr() for w in ws] + [None] * (_lib.MAX_RANKS - n)))
+    mp = (_lib.c_vp * _lib.MAX_RANKS)(*([m.data_ptr() for m in mats] + [None] * (_lib.MAX_RANKS - n)))
     _lib_call("fc_species_maps", int(n_sp), int(c_in), int(c_mid), int(c_out), int(nh), int(n), tb.data_ptr(),
               wf.data_ptr(), float(s_first), div.data_ptr(), wp, wr.data_ptr(), mp, _lib.stream_of(tb))
     return mats

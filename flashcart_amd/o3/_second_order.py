@@ -119,8 +119,8 @@ _ops._register_autograd(_ops.tp_bwd, _tp_dbwd, _tp_bwd_setup)
 # ---------------------------------------------------------------------------
 
 def _linear_bwd_setup(ctx, inputs, output):
-    go, w0, w1, w2, w3, in_l_max, out_l_max, fin, fout, in_paths, scale, alpha, residual = inputs
-    ws = _ops._wlist(w0, w1, w2, w3)
+    go, w0, w1, w2, w3, w4, in_l_max, out_l_max, fin, fout, in_paths, scale, alpha, residual = inputs
+    ws = _ops._wlist(w0, w1, w2, w3, w4)
     ctx.save_for_backward(go, *ws)
     ctx.cfg = (int(in_l_max), int(out_l_max), int(fin), int(fout), list(in_paths), list(scale))
     ctx.alpha = float(alpha)
@@ -135,12 +135,13 @@ def _linear_dbwd(ctx, c):
     d_go = None
     if need[0]:
         d_go = _ops.linear_fwd(c, weights, in_l_max, out_l_max, fin, fout, in_paths, scale, ctx.alpha)
-    d_ws = [None, None, None, None]
-    if any(need[1:5]):
+    d_ws = [None] * _ops._lib.MAX_RANKS
+    if any(need[1:1 + _ops._lib.MAX_RANKS]):
         d_ws = _ops.linear_wgrad(go, c, weights, in_l_max, out_l_max, fin, fout, in_paths, scale, ctx.alpha,
                                  [bool(need[1 + l]) for l in range(len(weights))])
-        d_ws = d_ws + [None] * (4 - len(d_ws))
-    d_res = c if len(need) > 12 and need[12] else None
+        d_ws = d_ws + [None] * (_ops._lib.MAX_RANKS - len(d_ws))
+    i_res = 8 + _ops._lib.MAX_RANKS
+    d_res = c if len(need) > i_res and need[i_res] else None
     return (d_go, *d_ws) + (None,) * 7 + (d_res,)
 
 

@@ -22,10 +22,15 @@
 extern "C" {
 #endif
 
+/* Rank slots of the descriptors (ranks 0..4). A library compiled for ranks <= 3 (the default,
+ * as the reference's FLASHCART_KERNEL_L_MAX) rejects rank 4 with FC_ERR_UNSUPPORTED_L; callers
+ * fill the slots above their ranks with zeros / NULL. */
+#define FC_MAX_RANKS 5
+
 typedef enum fc_status {
   FC_OK = 0,
   FC_ERR_BAD_DESC = 1,       /* inconsistent descriptor (feature counts, flags) */
-  FC_ERR_UNSUPPORTED_L = 2,  /* a rank above FC_KERNEL_L_MAX (3) */
+  FC_ERR_UNSUPPORTED_L = 2,  /* a rank above fc_kernel_l_max() (3; 4 for a FLASHCART_KERNEL_L_MAX=4 build) */
   FC_ERR_LAUNCH = 3,         /* hipGetLastError() reported a launch failure */
   FC_ERR_SHAPE = 4,          /* sizes the kernels do not support (e.g. > 1024 channels) */
   FC_ERR_NULL = 5,           /* a required pointer is NULL */
@@ -200,7 +205,7 @@ int fc_species_density_bwd(const fc_csr* graph, int32_t l_max, int32_t y_l_max, 
  * table (n_species, c_in) the species' sender features, w_first (c_mid, c_in), w_second[l] (c_out, c_mid),
  * w_radial (n_ranks * c_mid, n_hidden) the radial output layer's rows of paths (0, l, l), maps[l]
  * (c_out, n_species * n_hidden); alpha_div a device scalar (the layer's sqrt_avg_neighbors).
- * Limits: n_species <= 8, c_in and c_mid <= 1024, n_hidden <= 64, n_ranks <= 4. */
+ * Limits: n_species <= 8, c_in and c_mid <= 1024, n_hidden <= 64, n_ranks <= FC_MAX_RANKS. */
 int fc_species_maps(int32_t n_species, int32_t c_in, int32_t c_mid, int32_t c_out, int32_t n_hidden,
                     int32_t n_ranks, const float* table, const float* w_first, float s_first,
                     const float* alpha_div, const float* const* w_second, const float* w_radial,
@@ -285,9 +290,9 @@ int fc_tp_bwd_rows_acc(const fc_tp_desc* desc, int64_t n_rows, const float* grad
 typedef struct fc_linear_desc {
   int32_t in_l_max, out_l_max;
   int32_t in_features, out_features;
-  int32_t in_paths[4];       /* paths per input rank (1 for plain features) */
-  const float* weight[4];    /* W_l, row-major (out_features, in_features*in_paths[l]) */
-  float scale[4];            /* s_l */
+  int32_t in_paths[FC_MAX_RANKS];     /* paths per input rank (1 for plain features) */
+  const float* weight[FC_MAX_RANKS];  /* W_l, row-major (out_features, in_features*in_paths[l]) */
+  float scale[FC_MAX_RANKS];          /* s_l */
 } fc_linear_desc;
 
 /* residual (may be NULL, may equal out / grad_x): a tensor of the output's layout added to
@@ -356,9 +361,9 @@ int fc_linear_wgrad(const fc_linear_desc* desc, int64_t n_rows, const float* gra
 typedef struct fc_linear_desc_f64 {
   int32_t in_l_max, out_l_max;
   int32_t in_features, out_features;
-  int32_t in_paths[4];
-  const double* weight[4];   /* W_l, row-major (out_features, in_features*in_paths[l]) */
-  double scale[4];
+  int32_t in_paths[FC_MAX_RANKS];
+  const double* weight[FC_MAX_RANKS];  /* W_l, row-major (out_features, in_features*in_paths[l]) */
+  double scale[FC_MAX_RANKS];
 } fc_linear_desc_f64;
 
 int fc_linear_fwd_f64(const fc_linear_desc_f64* desc, int64_t n_rows, const double* x, double alpha,

@@ -35,12 +35,14 @@ from typing import Dict, List, Tuple
 import numpy as np
 
 # Stored components (count_x, count_y, count_z), reference
-# src/flashcart/o3/_codegen_common.py:37-73 (layout contract).
+# src/flashcart/o3/_codegen_common.py:37-73 (layout contract): explicit orders for ranks 0..3;
+# from rank 4 on, the components with no z by descending x count, then those with one z.
 STORED = {
     0: [(0, 0, 0)],
     1: [(1, 0, 0), (0, 1, 0), (0, 0, 1)],
     2: [(2, 0, 0), (0, 2, 0), (1, 1, 0), (1, 0, 1), (0, 1, 1)],
     3: [(3, 0, 0), (2, 1, 0), (2, 0, 1), (1, 2, 0), (1, 1, 1), (0, 2, 1), (0, 3, 0)],
+    4: [(a, 4 - a, 0) for a in range(4, -1, -1)] + [(a, 3 - a, 1) for a in range(3, -1, -1)],
 }
 
 

@@ -31,6 +31,48 @@ def test_library_exports_every_declared_symbol():
     assert lib.fc_kernel_l_max() == 3 and lib.fc_version() >= 100
 
 
+def test_rank_limit_selects_the_library(monkeypatch):
+    """FLASHCART_KERNEL_L_MAX (read at import, as by the reference) picks the rank-3 or the rank-4
+    library and the limit the modules enforce; above 4 is refused."""
+    import importlib
+
+    from flashcart_amd import _lib
+    from flashcart_amd.o3 import kernel_config
+    assert _lib.library_path(3).endswith("libflashcart_hip.so")
+    assert _lib.library_path(2).endswith("libflashcart_hip.so")
+    assert _lib.library_path(4).endswith("libflashcart_hip_l4.so")
+    try:
+        monkeypatch.setenv("FLASHCART_KERNEL_L_MAX", "4")
+        assert importlib.reload(kernel_config).KERNEL_L_MAX == 4
+        monkeypatch.setenv("FLASHCART_KERNEL_L_MAX", "5")
+        with pytest.raises(RuntimeError):
+            importlib.reload(kernel_config)
+        monkeypatch.delenv("FLASHCART_KERNEL_L_MAX")
+        assert importlib.reload(kernel_config).KERNEL_L_MAX == 3
+    finally:
+        monkeypatch.delenv("FLASHCART_KERNEL_L_MAX", raising=False)
+        importlib.reload(kernel_config)
+
+
+@pytest.mark.skipif(not (ROOT / "flashcart_amd" / "libflashcart_hip_l4.so").exists(),
+                    reason="libflashcart_hip_l4.so not built (FLASHCART_KERNEL_L_MAX=4 python -m flashcart_amd.build)")
+def test_rank4_library_exports_and_metadata():
+    """The rank-4 build exports the same symbols with the same descriptor layout and accepts rank 4
+    (42 paths of 4 x 4 -> 4, the reference's count)."""
+    from flashcart_amd import _lib
+    lib = ctypes.CDLL(str(ROOT / "flashcart_amd" / "libflashcart_hip_l4.so"))
+    for name in _declared_symbols():
+        assert hasattr(lib, name), name
+    lib.fc_kernel_l_max.restype = ctypes.c_int
+    assert lib.fc_kernel_l_max() == 4
+    lib.fc_tp_num_paths.argtypes = [ctypes.POINTER(_lib.TPDesc)]
+    lib.fc_tp_out_dim.argtypes = [ctypes.POINTER(_lib.TPDesc)]
+    lib.fc_tp_out_dim.restype = ctypes.c_int64
+    d = _lib.tp_desc(4, 4, 4, 8, 1, False, False, False)
+    assert lib.fc_tp_num_paths(ctypes.byref(d)) == 42
+    assert lib.fc_tp_num_paths(ctypes.byref(_lib.tp_desc(5, 4, 4, 8, 1, False, False, False))) == -2
+
+
 def test_abi_metadata_calls_without_gpu():
     from flashcart_amd import _lib
     lib = _lib.load()

@@ -131,9 +131,12 @@ def _rotate(l, stored, R):
 
 
 ALL_PATHS = [(a, b, c) for a in range(4) for b in range(a + 1) for c in range(4) if OC.allowed(a, b, c)]
+# rank-4 paths (the kernels of a FLASHCART_KERNEL_L_MAX=4 build): every canonical path with a rank 4
+RANK4_PATHS = [(a, b, c) for a in range(5) for b in range(a + 1) for c in range(5)
+               if OC.allowed(a, b, c) and 4 in (a, b, c)]
 
 
-@pytest.mark.parametrize("path", ALL_PATHS, ids=lambda p: f"{p[0]}{p[1]}{p[2]}")
+@pytest.mark.parametrize("path", ALL_PATHS + RANK4_PATHS, ids=lambda p: f"{p[0]}{p[1]}{p[2]}")
 def test_tp_path_rotation_equivariant_and_traceless(path):
     l1, l2, lo = path
     R = _random_rotation(7)
@@ -183,7 +186,37 @@ def test_expansion_closed_forms():
     assert torch.allclose(got, want, atol=1e-14)
 
 
-@pytest.mark.parametrize("l", [1, 2, 3])
+@pytest.mark.parametrize("path", RANK4_PATHS, ids=lambda p: f"{p[0]}{p[1]}{p[2]}")
+def test_rank4_paths_match_exact_derivation(path):
+    """The oracle's numeric path tensors (SVD projectors over the 3^l spaces) against the exact
+    rational coefficients of the HIP code generator (flashcart_amd/codegen/cartesian.py): two
+    independent routes to the same Eq. (2) coefficients, at the ranks no golden vector covers."""
+    from flashcart_amd.codegen.cartesian import tp_coefficients
+    l1, l2, lo = path
+    B = OC.path_tensor(l1, l2, lo)
+    exact = np.zeros_like(B)
+    for (a, b, c), v in tp_coefficients(l1, l2, lo).items():
+        exact[a, b, c] = float(v)
+    assert np.abs(B - exact).max() <= 1e-12 * max(1.0, np.abs(exact).max())
+
+
+def test_rank4_expansion_legendre_components():
+    """On unit vectors the all-x and all-y components of Eq. (1) are Legendre polynomials:
+    P_4(x) = (35 x^4 - 30 x^2 + 3) / 8 (as 1.5 x^2 - 0.5 and 2.5 x^3 - 1.5 x are P_2, P_3 above);
+    stored order of rank 4: (4,0,0) first, (0,4,0) fifth."""
+    g = torch.Generator().manual_seed(4)
+    r = torch.randn(40, 3, dtype=DT, generator=g)
+    r = r / r.norm(dim=1, keepdim=True)
+    T4 = O.irreps(r, 4)[:, 16:25]
+
+    def p4(t):
+        return (35 * t ** 4 - 30 * t ** 2 + 3) / 8
+
+    assert torch.allclose(T4[:, 0], p4(r[:, 0]), atol=1e-13)
+    assert torch.allclose(T4[:, 4], p4(r[:, 1]), atol=1e-13)
+
+
+@pytest.mark.parametrize("l", [1, 2, 3, 4])
 def test_expansion_normalised_and_traceless_on_sphere(l):
     g = torch.Generator().manual_seed(l)
     r = torch.randn(50, 3, dtype=DT, generator=g)
