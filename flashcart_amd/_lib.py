@@ -52,6 +52,7 @@ class CSR(ctypes.Structure):
     _fields_ = [
         ("n_nodes", c_i64), ("n_edges", c_i64), ("idx_j", c_vp), ("rowptr", c_vp),
         ("sender_perm", c_vp), ("sender_ptr", c_vp), ("n_sender_rows", c_i64), ("pair_slot", c_vp),
+        ("idx_i", c_vp),
     ]
 
 
@@ -267,6 +268,6 @@ def radial_desc(basis: int, n_radial: int, r_min: float, r_max: float, poly_orde
 
 
 def csr_struct(n_nodes: int, n_edges: int, idx_j, rowptr, sender_perm=None, sender_ptr=None,
-               n_sender_rows: Optional[int] = None, pair_slot=None) -> CSR:
+               n_sender_rows: Optional[int] = None, pair_slot=None, idx_i=None) -> CSR:
     return CSR(int(n_nodes), int(n_edges), ptr(idx_j), ptr(rowptr), ptr(sender_perm), ptr(sender_ptr),
-               int(n_nodes if n_sender_rows is None else n_sender_rows), ptr(pair_slot))
+               int(n_nodes if n_sender_rows is None else n_sender_rows), ptr(pair_slot), ptr(idx_i))

@@ -160,6 +160,18 @@ extern "C" int fc_tp_bwd(const fc_tp_desc* d, const fc_csr* graph, int64_t n_row
 
   TPArgs g = make_args(d, rows);
   g.in1 = in1; g.in2 = in2; g.w = w; g.grad_out = go; g.alpha = alpha;
+  // all three gradients of an interaction-layer convolution with few channels: in sender order
+  // (no per-edge messages, no segmented sum) when the configuration has a sender-order kernel
+  if (conv && gin1 && gin2 && gw && graph->idx_i && !d->shared_weights && graph->n_sender_rows > 0) {
+    TPArgs gs = g;
+    gs.n_rows = graph->n_sender_rows;
+    gs.grad_in1 = gin1; gs.grad_in2 = gin2; gs.grad_w = gw;
+    gs.idx_j = graph->idx_j; gs.rowptr = graph->rowptr; gs.wslot = graph->pair_slot; gs.n_edges = graph->n_edges;
+    gs.idx_i = graph->idx_i; gs.sperm = graph->sender_perm; gs.sptr = graph->sender_ptr;
+    gs.sender_major = 1;
+    st = dispatch(d, gs, true, true, s);
+    if (st != kSendNotApplicable) return st;
+  }
   const int np = count_paths(d->in1_l_max, d->in2_l_max, d->out_l_max, d->symmetric_product != 0, nullptr);
   float* msg = nullptr;
   float* wtmp = nullptr;

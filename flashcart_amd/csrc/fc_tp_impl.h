@@ -43,6 +43,12 @@ struct TPArgs {
   const float* res1;
   const float* res2;
   int32_t res1_comps, res2_comps;
+  // convolution backward in sender order (tp_bwd_send_kernel): receiver of each edge and the
+  // sender CSR; n_rows counts senders; grad_in1 receives the input gradient rows directly
+  const int32_t* idx_i;
+  const int32_t* sperm;
+  const int32_t* sptr;
+  int32_t sender_major;
 };
 
 template <int L1, int L2, int LO, bool SYM>
@@ -581,6 +587,178 @@ __global__ void __launch_bounds__(C * EG, 2) tp_bwd_conv_kernel(TPArgs g) {
   }
 }
 
+// The convolution backward in sender order, for C = 64 channels and at most
+// kSendMaxOut unreduced output rows (the interaction layers of the 64-channel models): one
+// workgroup per sender j walks j's out-edges (sender_perm), gathers each receiver's output
+// gradient row and keeps j's in1 row resident, so the in1 gradient of j is summed in registers
+// and written once, with no per-edge messages and no separate segmented sum. Per edge it forms
+// the weight gradient and the edge-attribute gradient as the receiver-order kernel does (same
+// products; the in1 gradient sums in sender order). EG edge groups share a sender as there;
+// their in1-gradient partial sums are added in LDS in group order (reproducible).
+constexpr int kSendMaxOut = 40;
+
+// Coupling matrices of a chunk of edges given by position in sender_perm.
+template <int L1, int L2, int LO, bool SYM>
+__device__ __forceinline__ void fill_amat_perm(const float* __restrict__ in2, const int32_t* __restrict__ sperm,
+                                               int64_t c0, int n, float* a, int lane, int wave, int nw) {
+  using PL = PathList<L1, L2, LO, SYM>;
+  using AL = AmatLayout<L1, L2, LO, SYM>;
+  constexpr int D2 = ncomp(L2);
+  if (lane >= n) return;
+  const int64_t e = sperm[c0 + lane];
+  float y[D2];
+#pragma unroll
+  for (int u = 0; u < D2; ++u) y[u] = in2[e * D2 + u];
+  float* ae = a + lane * AL::total;
+  const int p0 = wave * PL::NP / nw, p1 = (wave + 1) * PL::NP / nw;
+  static_for<PL::NP>([&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    if (i >= p0 && i < p1) {
+      constexpr PathDesc P = PL::at(i);
+      TPPath<P.r1, P.r2, P.lo>::amat(y + P.r2 * P.r2, ae + AL::template off<i>());
+    }
+  });
+}
+
+template <int NOUT, int NP>
+struct SendOps {
+  float go[NOUT], w[NP];
+};
+
+template <int L1, int L2, int LO, bool SYM, int C, int EG>
+__global__ void __launch_bounds__(C * EG, 2) tp_bwd_send_kernel(TPArgs g) {
+  using CF = TPConfig<L1, L2, LO, SYM>;
+  using PL = typename CF::PL;
+  using AL = AmatLayout<L1, L2, LO, SYM>;
+  constexpr int D1 = CF::D1, D2 = CF::D2, NOUT = CF::NOUT, NP = CF::NP;
+  constexpr int T = C * EG, NW = T / 64;
+  constexpr int GW = C >= 64 ? 64 : C, NWG = C >= 64 ? C / 64 : 1;
+  constexpr int R2 = pow2_at_least(D2), SH2 = log2_exact(GW) - log2_exact(R2);
+  constexpr int CH = bwd_conv_chunk<L1, L2, LO, SYM>();
+  static_assert(C == 64 && T % 64 == 0 && T <= 256, "whole waves of whole groups");
+  static_assert(NOUT <= kSendMaxOut, "the gathered output-gradient rows stay in registers");
+  static_assert(CH % (2 * EG) == 0, "every full chunk gives each group an even number of edges");
+  constexpr int64_t SW = (int64_t)NP * C, S1 = (int64_t)D1 * C, SO = (int64_t)NOUT * C;
+  __shared__ __align__(16) float a_lds[2 * CH * AL::total];
+  __shared__ float red_lds[CH * NWG * D2];
+  __shared__ float gx_lds[(EG > 1 ? EG - 1 : 1) * D1 * C];
+
+  const int64_t row = xcd_row(g.n_rows);  // the sender
+  if (row >= g.n_rows) return;
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const int grp = EG == 1 ? 0 : t / C, f = EG == 1 ? t : t % C;
+  const int wig = C >= 64 ? f >> 6 : 0;
+  const int64_t k0 = g.sptr[row], k1 = g.sptr[row + 1];
+  const float alpha = scale_of(g);
+  float x[D1], gx[D1];
+#pragma unroll
+  for (int u = 0; u < D1; ++u) {
+    x[u] = g.in1[row * S1 + (int64_t)u * C + f];
+    gx[u] = 0.f;
+  }
+
+  auto load = [&](int64_t k, SendOps<NOUT, NP>& o) {
+    const int64_t e = g.sperm[k];
+    const int64_t i = g.idx_i[e];
+    const float* gr = g.grad_out + i * SO + f;
+#pragma unroll
+    for (int a = 0; a < NOUT; ++a) o.go[a] = alpha * gr[(int64_t)a * C];
+    const int64_t wrow = weight_row(g, e);
+    if (wrow < 0) {
+#pragma unroll
+      for (int p = 0; p < NP; ++p) o.w[p] = 0.f;
+      return;
+    }
+    const float* wr = g.w + wrow * SW + f;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) o.w[p] = wr[p * C];
+  };
+
+  auto step = [&](int64_t k, const SendOps<NOUT, NP>& cur, const float* ae, int slot) {
+    const int64_t e = g.sperm[k];
+    float gy[R2];
+#pragma unroll
+    for (int u = 0; u < R2; ++u) gy[u] = 0.f;
+    float* gwr = g.grad_w + e * SW + f;
+    static_for<NP>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      constexpr PathDesc P = PL::at(i);
+      using TP = TPPath<P.r1, P.r2, P.lo>;
+      const float* xp = x + P.r1 * P.r1;
+      float gop[TP::NO];
+#pragma unroll
+      for (int a = 0; a < TP::NO; ++a) gop[a] = cur.go[PL::out_index(i, a)];
+      float v[TP::N1];
+#pragma unroll
+      for (int b = 0; b < TP::N1; ++b) v[b] = 0.f;
+      TP::apply_t(ae + AL::template off<i>(), gop, v);
+      float sw = 0.f;
+#pragma unroll
+      for (int b = 0; b < TP::N1; ++b) sw = fmaf(v[b], xp[b], sw);
+      gwr[i * C] = sw;
+#pragma unroll
+      for (int b = 0; b < TP::N1; ++b) gx[P.r1 * P.r1 + b] = fmaf(cur.w[i], v[b], gx[P.r1 * P.r1 + b]);
+      float xw[TP::N1];
+#pragma unroll
+      for (int b = 0; b < TP::N1; ++b) xw[b] = cur.w[i] * xp[b];
+      TP::vjp2(gop, xw, gy + P.r2 * P.r2);
+    });
+    const float s = wave_reduce_halving<R2, GW>(gy, lane);
+    const int v = (lane & (GW - 1)) >> SH2;
+    if ((lane & ((1 << SH2) - 1)) == 0 && v < D2) red_lds[(slot * NWG + wig) * D2 + v] = s;
+  };
+
+  if (k0 < k1) {  // uniform over the workgroup
+    SendOps<NOUT, NP> opa, opb;
+    if (EG == 1 || k0 + grp < k1) load(k0 + grp, opa);
+    fill_amat_perm<L1, L2, LO, SYM>(g.in2, g.sperm, k0, k1 - k0 < CH ? (int)(k1 - k0) : CH, a_lds, lane, wave, NW);
+    __syncthreads();
+    int buf = 0;
+    for (int64_t c0 = k0; c0 < k1; c0 += CH) {
+      const int64_t c1 = c0 + CH < k1 ? c0 + CH : k1;
+      const int n = (int)(c1 - c0);
+      const int n_next = k1 - c1 < CH ? (int)(k1 - c1) : CH;
+      const float* ab = a_lds + buf * CH * AL::total;
+      for (int64_t k = c0 + grp; k < c1; k += 2 * EG) {
+        const int slot = (int)(k - c0);
+        if (k + EG < k1) load(k + EG, opb);
+        step(k, opa, ab + slot * AL::total, slot);
+        if (k + EG < c1) {
+          if (k + 2 * EG < k1) load(k + 2 * EG, opa);
+          step(k + EG, opb, ab + (slot + EG) * AL::total, slot + EG);
+        }
+      }
+      if (n_next > 0)
+        fill_amat_perm<L1, L2, LO, SYM>(g.in2, g.sperm, c1, n_next, a_lds + (buf ^ 1) * CH * AL::total, lane, wave, NW);
+      __syncthreads();
+      for (int q = t; q < n * D2; q += T) {
+        const int slot = q / D2, u = q % D2;
+        float sum = 0.f;
+#pragma unroll
+        for (int w = 0; w < NWG; ++w) sum += red_lds[(slot * NWG + w) * D2 + u];
+        g.grad_in2[(int64_t)g.sperm[c0 + slot] * D2 + u] = sum;
+      }
+      __syncthreads();
+      buf ^= 1;
+    }
+  }
+  // the groups' in1 gradients, added in group order
+  if constexpr (EG > 1) {
+    if (grp > 0) {
+#pragma unroll
+      for (int u = 0; u < D1; ++u) gx_lds[((grp - 1) * D1 + u) * C + f] = gx[u];
+    }
+    __syncthreads();
+    if (grp > 0) return;
+#pragma unroll
+    for (int q = 1; q < EG; ++q)
+#pragma unroll
+      for (int u = 0; u < D1; ++u) gx[u] += gx_lds[((q - 1) * D1 + u) * C + f];
+  }
+#pragma unroll
+  for (int u = 0; u < D1; ++u) g.grad_in1[row * S1 + (int64_t)u * C + f] = gx[u];
+}
+
 // Backward of the node-wise (rows) product with full-width inputs (F1 == F2 == C) and
 // per-path outputs: no channel reduction, so no LDS or barriers. The output gradient
 // of a path is read when the path is processed (the node-wise kernels have no edge
@@ -684,6 +862,21 @@ bool launch_bwd_conv(const TPArgs& g, dim3 grid, hipStream_t stream) {
   }
 }
 
+// Sender-order backward with C channels and EG edge groups; false when a full chunk would not
+// split evenly over the groups.
+template <int L1, int L2, int LO, bool SYM, int C, int EG>
+bool launch_bwd_send(const TPArgs& g, dim3 grid, hipStream_t stream) {
+  if constexpr (bwd_conv_chunk<L1, L2, LO, SYM>() % (2 * EG) != 0) {
+    return false;
+  } else {
+    hipLaunchKernelGGL((tp_bwd_send_kernel<L1, L2, LO, SYM, C, EG>), grid, dim3(C * EG), 0, stream, g);
+    return true;
+  }
+}
+
+// launch_tp's answer when a sender-order backward was asked for a configuration it does not cover
+constexpr int kSendNotApplicable = -100;
+
 template <int L1, int L2, int LO, bool SYM, int EG>
 void launch_fwd_groups(const TPArgs& g, dim3 grid, hipStream_t stream) {
   using CF = TPConfig<L1, L2, LO, SYM>;
@@ -704,6 +897,25 @@ int launch_tp(const TPArgs& g, bool conv, bool bwd, hipStream_t stream) {
   if (bwd) {
     const bool reduce = (g.grad_in1 && g.F1 == 1 && g.C > 1) || (g.grad_in2 && g.F2 == 1 && g.C > 1);
     const size_t per_edge = reduce ? sizeof(float) * (threads / 64) * (ncomp(L1) + ncomp(L2)) : 0;
+    if (g.sender_major) {  // only launched here; the caller falls back to messages otherwise
+      if constexpr (!SYM && L2 >= 1 && TPConfig<L1, L2, LO, SYM>::NOUT <= kSendMaxOut) {
+        // 64 channels only: with 32 (the standalone 2x2->2 product, 512 senders) the sender order
+        // measured 7% slower per call than messages plus their gather
+        if (conv && bc2 && !g.reduced && !g.shared_w && g.grad_w && g.grad_in2 && g.grad_in1 && g.F1 == g.C &&
+            g.C == 64) {
+          const int eg = conv_edge_groups(g.n_rows, g.n_edges, g.C);
+          const dim3 sgrid((unsigned)xcd_grid(g.n_rows));
+          const bool done = (eg >= 4 && launch_bwd_send<L1, L2, LO, SYM, 64, 4>(g, sgrid, stream)) ||
+                            (eg >= 2 && launch_bwd_send<L1, L2, LO, SYM, 64, 2>(g, sgrid, stream)) ||
+                            launch_bwd_send<L1, L2, LO, SYM, 64, 1>(g, sgrid, stream);
+          if (done) {
+            FC_LAUNCH_CHECK();
+            return FC_OK;
+          }
+        }
+      }
+      return kSendNotApplicable;
+    }
     if constexpr (!SYM && L2 >= 1) {
       // interaction-layer shape: the compile-time specialisation
       if (conv && bc2 && !g.reduced && !g.shared_w && g.grad_w && g.grad_in2 && g.F1 == g.C &&

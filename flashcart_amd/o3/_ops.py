@@ -494,7 +494,10 @@ def _alpha_div(t: Optional[Tensor]) -> Optional[Tensor]:
 
 
 def _tp_csr(in1: Tensor, idx_i: Tensor, idx_j: Tensor, rowptr: Optional[Tensor], sender_perm: Optional[Tensor],
-            sender_ptr: Optional[Tensor], need_senders: bool, pair_slot: Optional[Tensor] = None):
+            sender_ptr: Optional[Tensor], need_senders: bool, pair_slot: Optional[Tensor] = None,
+            receivers: bool = False):
+    """``receivers``: also pass each edge's receiver (``fc_csr.idx_i``), which lets the backward of a
+    64-channel convolution run in sender order."""
     n = in1.shape[0]
     jj = _i32("idx_j", idx_j)
     if rowptr is None or (need_senders and (sender_perm is None or sender_ptr is None)):
@@ -509,8 +512,9 @@ def _tp_csr(in1: Tensor, idx_i: Tensor, idx_j: Tensor, rowptr: Optional[Tensor],
     ps = _i32("pair_slot", pair_slot)
     if ps is not None and ps.shape[0] != jj.shape[0]:
         raise ValueError(f"pair_slot must have one entry per edge ({jj.shape[0]}), got {ps.shape[0]}.")
-    keep = (jj, rp, sp, sq, ps)
-    return _lib.csr_struct(n, jj.shape[0], jj, rp, sp, sq, n, ps), keep
+    ii = _i32("idx_i", idx_i) if receivers else None
+    keep = (jj, rp, sp, sq, ps, ii)
+    return _lib.csr_struct(n, jj.shape[0], jj, rp, sp, sq, n, ps, ii), keep
 
 
 def _check_tp_inputs(in1, in2, weights, idx_i, idx_j, in1_l_max, in2_l_max, out_l_max, in1_features,
@@ -608,8 +612,10 @@ def tp_bwd(grad_out: Tensor, in1: Tensor, in2: Tensor, weights: Tensor, idx_i: O
                         shared_weights, reduce_paths, _alpha_div(alpha_div))
     csr, keep = (None, None)
     if conv:
+        sender_order = (need_grad_in1 and need_grad_in2 and need_grad_weights and not shared_weights
+                        and in2_features == 1 and in1_features == 64)
         csr, keep = _tp_csr(in1, idx_i, idx_j, rowptr, sender_perm, sender_ptr, need_senders=need_grad_in1,
-                            pair_slot=pair_slot)
+                            pair_slot=pair_slot, receivers=sender_order)
     elif pair_slot is not None:
         raise ValueError("pair_slot needs a convolution (idx_i, idx_j).")
     g1 = _lib.rows_empty(in1, *in1.shape) if need_grad_in1 else in1.new_empty(0)

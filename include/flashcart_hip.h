@@ -151,6 +151,10 @@ typedef struct fc_csr {
                                   density and h-gradient terms skipped). No counterpart
                                   in the reference, which forms the weights of every edge
                                   (nn/layers.py:357-364). */
+  const int32_t* idx_i;        /* optional: receiver of each edge. With it, fc_tp_bwd computes the three
+                                  gradients of a 64-channel interaction-layer convolution (at most 40
+                                  unreduced output rows) in sender order (no per-edge messages); NULL
+                                  keeps receiver order. No counterpart in the reference. */
 } fc_csr;
 
 /* Edge pairs of a full neighbour list (no counterpart in the reference): the reverse of
@@ -258,7 +262,9 @@ int64_t fc_tp_bwd_workspace(const fc_tp_desc* desc, const fc_csr* graph, int64_t
 
 /* Vector-Jacobian product of fc_tp_fwd (with the same alpha). NULL gradient pointers
  * are not computed. In convolution mode the in1 gradient is gathered to the senders
- * through graph->sender_perm / sender_ptr (segmented sum, no atomics). */
+ * through graph->sender_perm / sender_ptr (segmented sum, no atomics), or, with
+ * graph->idx_i for a 64-channel interaction layer, summed per sender in one pass over
+ * each sender's edges (then the workspace goes unused). */
 int fc_tp_bwd(const fc_tp_desc* desc, const fc_csr* graph, int64_t n_rows, const float* grad_out,
               const float* in1, const float* in2, const float* weights, float alpha,
               float* grad_in1, float* grad_in2, float* grad_weights, float* workspace,

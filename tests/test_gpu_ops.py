@@ -109,6 +109,8 @@ def _tp_case(l1, l2, lo, f1, f2, sym=False, shared=False, reduced=False, conv=Tr
 CONV_CASES = [
     (0, 3, 3, 16, 1), (2, 3, 3, 16, 1), (1, 2, 2, 8, 1), (2, 2, 2, 8, 1), (3, 3, 3, 4, 1), (0, 2, 2, 64, 1),
     (2, 3, 3, 128, 1), (1, 1, 2, 8, 8), (2, 1, 1, 1, 8),
+    # 64 channels with at most 40 output rows: the backward in sender order
+    (2, 2, 2, 32, 1), (2, 2, 2, 64, 1), (1, 2, 2, 64, 1), (2, 1, 2, 64, 1),
 ]
 
 
