@@ -528,8 +528,8 @@ def config_line(name, dev, steps, warmup, cpu, extras=True):
             f_ms, f_b, b_ms, b_b, _ = measure_dominant(model, gdev, dev, with_backward=True)
             res.update({
                 "eager": {"value": n_atoms * steps / dt_eager, "ms_per_step": 1e3 * dt_eager / steps},
-                "roofline": {"bound": "hbm", "kernel": "layer-1 TP convolution backward op (tp_bwd_conv_kernel + "
-                                                       "segment_rows_kernel)",
+                "roofline": {"bound": "hbm", "kernel": "layer-1 TP convolution backward op (64 channels: "
+                                                       "tp_bwd_send_kernel, in sender order)",
                              "algorithmic_bytes": b_b, "avg_launch_ms": b_ms,
                              "achieved": b_b / (b_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                              "frac": b_b / (b_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
