@@ -119,6 +119,33 @@ def test_tp_conv(case):
     _tp_case(*case, conv=True)
 
 
+@pytest.mark.parametrize("need", [(True, True, False), (True, False, True), (False, True, True)])
+def test_tp_conv_bwd_gradient_subsets(need):
+    """The interaction-layer backward asked for a subset of its gradients (the second derivative
+    asks for (in1, in2) without the weights): the general kernel that then runs forms each requested
+    gradient exactly as the specialised all-gradients kernel does, bit for bit."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(7)
+    l1, l2, lo, C = 2, 3, 3, 128
+    ei = random_csr_graph(40, (3, 9, 17), seed=4)
+    E = ei.shape[1]
+    from oracle.cartesian import enumerate_paths
+    P = len(enumerate_paths(l1, l2, lo, False))
+    in1 = torch.randn(40, 9 * C, generator=g).to(DEV)
+    in2 = torch.randn(E, 16, generator=g).to(DEV)
+    w = torch.randn(E, P * C, generator=g).to(DEV)
+    meta = ops.tp_meta(l1, l2, lo, C, 1, False, False)
+    go = torch.randn(40, ops._tp_out_dim(l1, l2, lo, C, 1, False, False), generator=g).to(DEV)
+    args = (go, in1, in2, w, ei[0].to(DEV), ei[1].to(DEV), l1, l2, lo, C, 1, False, False, *meta, False)
+    full = ops.tp_bwd(*args, True, True, True)
+    part = ops.tp_bwd(*args, *need)
+    for k in range(3):
+        if need[k]:
+            assert torch.equal(part[k], full[k]), f"gradient {k}"
+        else:
+            assert part[k].numel() == 0
+
+
 def test_tp_conv_reduced_shared():
     _tp_case(2, 2, 2, 8, 1, shared=True, reduced=True, conv=True, seed=3)
 
