@@ -51,6 +51,20 @@ struct TPArgs {
   int32_t sender_major;
 };
 
+// s_waitcnt immediate (gfx9 encoding) that waits until at most vm vector-memory operations of the
+// wave are outstanding (no LDS/scalar or export wait). The empty asm before it keeps the compiler
+// from moving memory accesses across the wait, so the operations counted are the ones in program
+// order before it.
+#define FC_VMCNT_IMM(vm) (((vm) & 0xF) | ((((vm) >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8))
+__device__ __forceinline__ void vm_wait_barrier() { asm volatile("" ::: "memory"); }
+
+// Zeros read in place of the weight row of an edge that a pairing left without a partner (slot
+// -1): the backward kernels then issue the same loads on every path and need no select on the
+// loaded values (which the compiler would place where it waits for them). Device globals start
+// zeroed and nothing writes this one.
+constexpr int kZeroRowFloats = 96 * 256;
+__device__ float zero_weight_row[kZeroRowFloats];
+
 template <int L1, int L2, int LO, bool SYM>
 struct TPConfig {
   using PL = PathList<L1, L2, LO, SYM>;
@@ -479,6 +493,7 @@ __global__ void __launch_bounds__(C * EG, 2) tp_bwd_conv_kernel(TPArgs g) {
   constexpr int64_t SW = (int64_t)NP * C, S1 = (int64_t)D1 * C;
   __shared__ __align__(16) float a_lds[2 * CH * AL::total];
   __shared__ float red_lds[CH * NWG * D2];
+  __shared__ int32_t ix_lds[3 * 2 * CH];  // sender and weight row of the edges of three chunks
 
   const int64_t row = xcd_row(g.n_rows);
   if (row >= g.n_rows) return;
@@ -488,25 +503,54 @@ __global__ void __launch_bounds__(C * EG, 2) tp_bwd_conv_kernel(TPArgs g) {
   const int64_t e0 = g.rowptr[row], e1 = g.rowptr[row + 1];
   if (e0 >= e1) return;  // uniform over the workgroup: no barrier is skipped by a part of it
 
+  // The edge loop reads each edge's sender and weight row from LDS, where they are staged two
+  // chunks ahead (chunk q in slot q % 3), filled at a chunk boundary with the coupling matrices.
+  // Read from global memory in the loop, they are vector loads whose waits (vector-memory
+  // operations of a wave complete in issue order) also wait for the prefetched operands and the
+  // stores issued before them.
+  auto fill_idx = [&](int64_t q0, int q) {
+    const int64_t n = e1 - q0 < CH ? e1 - q0 : CH;
+    if (t < n) {
+      const int64_t e = q0 + t;
+      ix_lds[(q % 3) * 2 * CH + t] = g.idx_j[e];
+      ix_lds[(q % 3) * 2 * CH + CH + t] = g.wslot ? (g.wslot[e] >> 1) : 0;
+    }
+  };
+
   const float alpha = scale_of(g);
   float go[NOUT];
 #pragma unroll
   for (int k = 0; k < NOUT; ++k) go[k] = alpha * g.grad_out[row * (int64_t)NOUT * C + (int64_t)k * C + f];
 
-  auto load = [&](int64_t e, EdgeOps<D1, D2, NP>& o) {
-    const int64_t j = (int64_t)g.idx_j[e];
+  // Operands of an edge given its sender j and weight row: exactly LD vector loads on every path
+  // (an unpaired edge's weights, row -1, are read from the zero row).
+  static_assert(SW <= kZeroRowFloats, "zero row");
+  auto load_rows = [&](int64_t j, int64_t wrow, EdgeOps<D1, D2, NP>& o) {
     const float* xr = g.in1 + j * S1 + f;
 #pragma unroll
     for (int u = 0; u < D1; ++u) o.x[u] = xr[u * C];
-    const int64_t wrow = weight_row(g, e);
-    if (wrow < 0) {  // an unpaired edge's weights count as zero
-#pragma unroll
-      for (int i = 0; i < NP; ++i) o.w[i] = 0.f;
-      return;
-    }
-    const float* wr = g.w + wrow * SW + f;
+    const float* wr = (wrow < 0 ? zero_weight_row : g.w + wrow * SW) + f;
 #pragma unroll
     for (int i = 0; i < NP; ++i) o.w[i] = wr[i * C];
+  };
+  // operands of edge e = (chunk q's first edge) + s, s < CH, from the staged indices
+  auto load = [&](int64_t e, int q, int s, EdgeOps<D1, D2, NP>& o) {
+    const int* ix = ix_lds + (q % 3) * 2 * CH;
+    load_rows(ix[s], g.wslot ? (int64_t)ix[CH + s] : e, o);
+  };
+  // Before a step the wave waits until at most LD + ST vector-memory operations are outstanding:
+  // those issued after the step's own operand loads are the other operand set's loads (LD, every
+  // one issued, clamped to the last edge) and the previous step's stores (ST). Operations of a
+  // wave complete in issue order, so the step's operands have then arrived, while the next
+  // edge's loads and the last stores stay in flight. (The compiler's own waits, placed where a
+  // loaded register is first used, count conservatively across the loop's paths and waited for
+  // the loads just issued.) A chunk boundary waits for everything: the coupling-matrix fill
+  // waits for its own loads, issued after all others.
+  constexpr int LD = D1 + NP, ST = NP + (NEED1 ? D1 : 0);
+  constexpr int VM_STEP = LD + ST < 63 ? LD + ST : 63;  // at most 63 can be outstanding
+  auto wait_operands = [&]() {
+    vm_wait_barrier();
+    __builtin_amdgcn_s_waitcnt(FC_VMCNT_IMM(VM_STEP));
   };
 
   auto step = [&](int64_t e, const EdgeOps<D1, D2, NP>& cur, const float* ae, int slot) {
@@ -552,28 +596,47 @@ __global__ void __launch_bounds__(C * EG, 2) tp_bwd_conv_kernel(TPArgs g) {
   };
 
   EdgeOps<D1, D2, NP> opa, opb;
-  if (EG == 1 || e0 + grp < e1) load(e0 + grp, opa);
+  {  // the first edge's operands, from the global indices (the fill below waits for them)
+    const int64_t ef = e0 + grp < e1 ? e0 + grp : e1 - 1;
+    load_rows(g.idx_j[ef], weight_row(g, ef), opa);
+  }
+  vm_wait_barrier();
+  fill_idx(e0, 0);
+  if (e0 + CH < e1) fill_idx(e0 + CH, 1);
   fill_amat<L1, L2, LO, SYM>(g.in2, e0, e1 - e0 < CH ? (int)(e1 - e0) : CH, a_lds, lane, wave, NW);
   __syncthreads();
-  int buf = 0;
+  vm_wait_barrier();
+  __builtin_amdgcn_s_waitcnt(FC_VMCNT_IMM(0));  // the first operands (fewer than LD + ST operations follow them)
+  int buf = 0, q = 0;
   // Every chunk but the last holds CH edges, an even number per group, so each chunk starts on
   // operand set a; group grp takes the chunk's slots grp, grp + EG, ...
-  for (int64_t c0 = e0; c0 < e1; c0 += CH) {
+  // (a load looks at most 2 EG <= CH edges ahead: into this chunk or the next)
+  auto load_at = [&](int64_t e, int64_t c0, EdgeOps<D1, D2, NP>& o) {
+    const int s = (int)(e - c0);
+    if (s < CH) load(e, q, s, o);
+    else load(e, q + 1, s - CH, o);
+  };
+  for (int64_t c0 = e0; c0 < e1; c0 += CH, ++q) {
     const int64_t c1 = c0 + CH < e1 ? c0 + CH : e1;
     const int n = (int)(c1 - c0);
     const int n_next = e1 - c1 < CH ? (int)(e1 - c1) : CH;
     const float* ab = a_lds + buf * CH * AL::total;
     for (int64_t e = c0 + grp; e < c1; e += 2 * EG) {
       const int slot = (int)(e - c0);
-      if (e + EG < e1) load(e + EG, opb);
+      load_at(e + EG < e1 ? e + EG : e1 - 1, c0, opb);
+      wait_operands();
       step(e, opa, ab + slot * AL::total, slot);
       if (e + EG < c1) {
-        if (e + 2 * EG < e1) load(e + 2 * EG, opa);
+        load_at(e + 2 * EG < e1 ? e + 2 * EG : e1 - 1, c0, opa);
+        wait_operands();
         step(e + EG, opb, ab + (slot + EG) * AL::total, slot + EG);
       }
     }
-    // the other buffer was last read in the previous chunk, before that chunk's barriers
+    vm_wait_barrier();
+    // the other buffer was last read in the previous chunk, before that chunk's barriers; index
+    // slot (q + 2) % 3 held chunk q - 1, whose last reads were in that chunk's loop
     if (n_next > 0) fill_amat<L1, L2, LO, SYM>(g.in2, c1, n_next, a_lds + (buf ^ 1) * CH * AL::total, lane, wave, NW);
+    if (c1 + CH < e1) fill_idx(c1 + CH, q + 2);
     __syncthreads();
     for (int k = t; k < n * D2; k += T) {
       const int slot = k / D2, u = k % D2;
@@ -642,6 +705,7 @@ __global__ void __launch_bounds__(C * EG, 2) tp_bwd_send_kernel(TPArgs g) {
   __shared__ __align__(16) float a_lds[2 * CH * AL::total];
   __shared__ float red_lds[CH * NWG * D2];
   __shared__ float gx_lds[(EG > 1 ? EG - 1 : 1) * D1 * C];
+  __shared__ int32_t ix_lds[3 * 3 * CH];  // edge, receiver and weight row of the edges of three chunks
 
   const int64_t row = xcd_row(g.n_rows);  // the sender
   if (row >= g.n_rows) return;
@@ -657,25 +721,44 @@ __global__ void __launch_bounds__(C * EG, 2) tp_bwd_send_kernel(TPArgs g) {
     gx[u] = 0.f;
   }
 
-  auto load = [&](int64_t k, SendOps<NOUT, NP>& o) {
-    const int64_t e = g.sperm[k];
-    const int64_t i = g.idx_i[e];
+  // Each out-edge's edge id, receiver and weight row are staged in LDS two chunks ahead (chunk
+  // q in slot q % 3), as in tp_bwd_conv_kernel: read from global memory in the loop they are
+  // vector loads whose waits also wait for the prefetched rows. The output-gradient rows are
+  // scaled where they are used, not as they are loaded, for the same reason.
+  auto fill_idx = [&](int64_t q0, int q) {
+    const int64_t n = k1 - q0 < CH ? k1 - q0 : CH;
+    if (t < n) {
+      const int32_t e = g.sperm[q0 + t];
+      int32_t* ix = ix_lds + (q % 3) * 3 * CH;
+      ix[t] = e;
+      ix[CH + t] = g.idx_i[e];
+      ix[2 * CH + t] = g.wslot ? (g.wslot[e] >> 1) : e;
+    }
+  };
+
+  // exactly LD vector loads on every path (row -1: the zero row)
+  static_assert(SW <= kZeroRowFloats, "zero row");
+  auto load_rows = [&](int64_t i, int64_t wrow, SendOps<NOUT, NP>& o) {
     const float* gr = g.grad_out + i * SO + f;
 #pragma unroll
-    for (int a = 0; a < NOUT; ++a) o.go[a] = alpha * gr[(int64_t)a * C];
-    const int64_t wrow = weight_row(g, e);
-    if (wrow < 0) {
-#pragma unroll
-      for (int p = 0; p < NP; ++p) o.w[p] = 0.f;
-      return;
-    }
-    const float* wr = g.w + wrow * SW + f;
+    for (int a = 0; a < NOUT; ++a) o.go[a] = gr[(int64_t)a * C];
+    const float* wr = (wrow < 0 ? zero_weight_row : g.w + wrow * SW) + f;
 #pragma unroll
     for (int p = 0; p < NP; ++p) o.w[p] = wr[p * C];
   };
+  auto load = [&](int q, int s, SendOps<NOUT, NP>& o) {
+    const int* ix = ix_lds + (q % 3) * 3 * CH;
+    load_rows(ix[CH + s], ix[2 * CH + s], o);
+  };
+  // explicit waits before each step, as in tp_bwd_conv_kernel: LD loads per edge, ST stores per step
+  constexpr int LD = NOUT + NP, ST = NP;
+  constexpr int VM_STEP = LD + ST < 63 ? LD + ST : 63;
+  auto wait_operands = [&]() {
+    vm_wait_barrier();
+    __builtin_amdgcn_s_waitcnt(FC_VMCNT_IMM(VM_STEP));
+  };
 
-  auto step = [&](int64_t k, const SendOps<NOUT, NP>& cur, const float* ae, int slot) {
-    const int64_t e = g.sperm[k];
+  auto step = [&](int64_t e, const SendOps<NOUT, NP>& cur, const float* ae, int slot) {
     float gy[R2];
 #pragma unroll
     for (int u = 0; u < R2; ++u) gy[u] = 0.f;
@@ -687,7 +770,7 @@ __global__ void __launch_bounds__(C * EG, 2) tp_bwd_send_kernel(TPArgs g) {
       const float* xp = x + P.r1 * P.r1;
       float gop[TP::NO];
 #pragma unroll
-      for (int a = 0; a < TP::NO; ++a) gop[a] = cur.go[PL::out_index(i, a)];
+      for (int a = 0; a < TP::NO; ++a) gop[a] = alpha * cur.go[PL::out_index(i, a)];
       float v[TP::N1];
 #pragma unroll
       for (int b = 0; b < TP::N1; ++b) v[b] = 0.f;
@@ -710,33 +793,49 @@ __global__ void __launch_bounds__(C * EG, 2) tp_bwd_send_kernel(TPArgs g) {
 
   if (k0 < k1) {  // uniform over the workgroup
     SendOps<NOUT, NP> opa, opb;
-    if (EG == 1 || k0 + grp < k1) load(k0 + grp, opa);
+    fill_idx(k0, 0);
+    if (k0 + CH < k1) fill_idx(k0 + CH, 1);
     fill_amat_perm<L1, L2, LO, SYM>(g.in2, g.sperm, k0, k1 - k0 < CH ? (int)(k1 - k0) : CH, a_lds, lane, wave, NW);
     __syncthreads();
-    int buf = 0;
-    for (int64_t c0 = k0; c0 < k1; c0 += CH) {
+    load(0, k0 + grp < k1 ? grp : (int)(k1 - 1 - k0), opa);
+    vm_wait_barrier();
+    __builtin_amdgcn_s_waitcnt(FC_VMCNT_IMM(0));  // the first operands
+    int buf = 0, q = 0;
+    // a load looks at most 2 EG <= CH edges ahead: into this chunk or the next
+    auto load_at = [&](int64_t k, int64_t c0, SendOps<NOUT, NP>& o) {
+      const int s = (int)(k - c0);
+      if (s < CH) load(q, s, o);
+      else load(q + 1, s - CH, o);
+    };
+    for (int64_t c0 = k0; c0 < k1; c0 += CH, ++q) {
       const int64_t c1 = c0 + CH < k1 ? c0 + CH : k1;
       const int n = (int)(c1 - c0);
       const int n_next = k1 - c1 < CH ? (int)(k1 - c1) : CH;
       const float* ab = a_lds + buf * CH * AL::total;
+      const int* ixe = ix_lds + (q % 3) * 3 * CH;  // this chunk's edge ids
       for (int64_t k = c0 + grp; k < c1; k += 2 * EG) {
         const int slot = (int)(k - c0);
-        if (k + EG < k1) load(k + EG, opb);
-        step(k, opa, ab + slot * AL::total, slot);
+        load_at(k + EG < k1 ? k + EG : k1 - 1, c0, opb);
+        wait_operands();
+        step(ixe[slot], opa, ab + slot * AL::total, slot);
         if (k + EG < c1) {
-          if (k + 2 * EG < k1) load(k + 2 * EG, opa);
-          step(k + EG, opb, ab + (slot + EG) * AL::total, slot + EG);
+          load_at(k + 2 * EG < k1 ? k + 2 * EG : k1 - 1, c0, opa);
+          wait_operands();
+          step(ixe[slot + EG], opb, ab + (slot + EG) * AL::total, slot + EG);
         }
       }
+      vm_wait_barrier();
       if (n_next > 0)
         fill_amat_perm<L1, L2, LO, SYM>(g.in2, g.sperm, c1, n_next, a_lds + (buf ^ 1) * CH * AL::total, lane, wave, NW);
+      // slot (q + 2) % 3 held chunk q - 1, whose last reads were in that chunk's loop
+      if (c1 + CH < k1) fill_idx(c1 + CH, q + 2);
       __syncthreads();
-      for (int q = t; q < n * D2; q += T) {
-        const int slot = q / D2, u = q % D2;
+      for (int r = t; r < n * D2; r += T) {
+        const int slot = r / D2, u = r % D2;
         float sum = 0.f;
 #pragma unroll
         for (int w = 0; w < NWG; ++w) sum += red_lds[(slot * NWG + w) * D2 + u];
-        g.grad_in2[(int64_t)g.sperm[c0 + slot] * D2 + u] = sum;
+        g.grad_in2[(int64_t)ixe[slot] * D2 + u] = sum;
       }
       __syncthreads();
       buf ^= 1;

@@ -167,7 +167,8 @@ class _GatedBlock(torch.autograd.Function):
         g_values, g_pre = _ops.gate_bwd(g_gated, values, pre, layer.l_max, act, True, True)
         gx = layer.value_linear.input_grad(g_values, residual=g)
         gl = layer.gate_linear
-        gx[:, : layer.in_features] += _ops.dense_bwd(g_pre, pre_act, gl.weight, gl._scale, act_gemm)
+        # add_ on the column view: `gx[:, :k] += y` would also copy the view onto itself (a second kernel)
+        gx[:, : layer.in_features].add_(_ops.dense_bwd(g_pre, pre_act, gl.weight, gl._scale, act_gemm))
         return gx, None
 
 
@@ -321,7 +322,7 @@ class _EntryMaps(torch.autograd.Function):
         if g is None and gs is not None:
             g = gs.new_zeros(gs.shape[0], layer.linear_first.in_dim)
         if g is not None and gs is not None:
-            g[:, : ctx.n_read] += gs
+            g[:, : ctx.n_read].add_(gs)
         return g, None, None
 
 
