@@ -621,16 +621,23 @@ __global__ void __launch_bounds__(C * EG, 2) tp_bwd_conv_kernel(TPArgs g) {
     const int n = (int)(c1 - c0);
     const int n_next = e1 - c1 < CH ? (int)(e1 - c1) : CH;
     const float* ab = a_lds + buf * CH * AL::total;
-    for (int64_t e = c0 + grp; e < c1; e += 2 * EG) {
+    // pairs of edges, then (last chunk only) an odd edge: the loop body has no branch around its
+    // loads, stores or waits
+    int64_t e = c0 + grp;
+    for (; e + EG < c1; e += 2 * EG) {
       const int slot = (int)(e - c0);
-      load_at(e + EG < e1 ? e + EG : e1 - 1, c0, opb);
+      load_at(e + EG, c0, opb);
       wait_operands();
       step(e, opa, ab + slot * AL::total, slot);
-      if (e + EG < c1) {
-        load_at(e + 2 * EG < e1 ? e + 2 * EG : e1 - 1, c0, opa);
-        wait_operands();
-        step(e + EG, opb, ab + (slot + EG) * AL::total, slot + EG);
-      }
+      load_at(e + 2 * EG < e1 ? e + 2 * EG : e1 - 1, c0, opa);
+      wait_operands();
+      step(e + EG, opb, ab + (slot + EG) * AL::total, slot + EG);
+    }
+    if (e < c1) {
+      // opa was loaded before the last step's ST stores (or before a full wait)
+      vm_wait_barrier();
+      __builtin_amdgcn_s_waitcnt(FC_VMCNT_IMM(ST < 63 ? ST : 63));
+      step(e, opa, ab + (int)(e - c0) * AL::total, (int)(e - c0));
     }
     vm_wait_barrier();
     // the other buffer was last read in the previous chunk, before that chunk's barriers; index
@@ -813,16 +820,21 @@ __global__ void __launch_bounds__(C * EG, 2) tp_bwd_send_kernel(TPArgs g) {
       const int n_next = k1 - c1 < CH ? (int)(k1 - c1) : CH;
       const float* ab = a_lds + buf * CH * AL::total;
       const int* ixe = ix_lds + (q % 3) * 3 * CH;  // this chunk's edge ids
-      for (int64_t k = c0 + grp; k < c1; k += 2 * EG) {
+      // pairs of edges, then (last chunk only) an odd edge, as in tp_bwd_conv_kernel
+      int64_t k = c0 + grp;
+      for (; k + EG < c1; k += 2 * EG) {
         const int slot = (int)(k - c0);
-        load_at(k + EG < k1 ? k + EG : k1 - 1, c0, opb);
+        load_at(k + EG, c0, opb);
         wait_operands();
         step(ixe[slot], opa, ab + slot * AL::total, slot);
-        if (k + EG < c1) {
-          load_at(k + 2 * EG < k1 ? k + 2 * EG : k1 - 1, c0, opa);
-          wait_operands();
-          step(ixe[slot + EG], opb, ab + (slot + EG) * AL::total, slot + EG);
-        }
+        load_at(k + 2 * EG < k1 ? k + 2 * EG : k1 - 1, c0, opa);
+        wait_operands();
+        step(ixe[slot + EG], opb, ab + (slot + EG) * AL::total, slot + EG);
+      }
+      if (k < c1) {
+        vm_wait_barrier();
+        __builtin_amdgcn_s_waitcnt(FC_VMCNT_IMM(ST < 63 ? ST : 63));
+        step(ixe[k - c0], opa, ab + (int)(k - c0) * AL::total, (int)(k - c0));
       }
       vm_wait_barrier();
       if (n_next > 0)
