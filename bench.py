@@ -43,7 +43,7 @@ HBM_PEAK_GBS = 8000.0
 # profiles/hbm_counter_method.md and profiles/tp_conv_l1_fcc25k_kernel_only.md.
 MEASURED_TRAFFIC_BYTES = 11.33e9
 # The same for the layer-1 backward op (tp_bwd_conv_kernel + segment_rows_kernel).
-MEASURED_TRAFFIC_BWD_BYTES = 32.07e9
+MEASURED_TRAFFIC_BWD_BYTES = 32.14e9
 from flashcart_amd.data.synthetic import FCC25K_R_MAX as R_MAX  # noqa: E402
 from flashcart_amd.data.synthetic import FCC25K_SIGMA_STEP as SIGMA_STEP  # noqa: E402
 from flashcart_amd.data.synthetic import FCC25K_SKIN as SKIN  # noqa: E402
