@@ -119,6 +119,16 @@ def test_tp_conv(case):
     _tp_case(*case, conv=True)
 
 
+@pytest.mark.parametrize("case", [(2, 3, 3, 128, 1), (2, 2, 2, 64, 1), (1, 2, 2, 64, 1), (2, 2, 2, 32, 1)],
+                         ids=lambda c: "x".join(map(str, c)))
+def test_tp_conv_chunk_boundaries(case):
+    """Receiver and sender edge counts around the backward kernels' 16-edge chunks and their
+    paired edge loop (odd last edges, a last edge on a chunk's first slot, one to three chunks),
+    for one edge group (128 channels) and several (32 and 64): the staged indices and the
+    operand waits keep every edge's result."""
+    _tp_case(*case, conv=True, seed=5, degrees=(1, 15, 16, 17, 31, 32, 33, 47), n=48)
+
+
 @pytest.mark.parametrize("need", [(True, True, False), (True, False, True), (False, True, True)])
 def test_tp_conv_bwd_gradient_subsets(need):
     """The interaction-layer backward asked for a subset of its gradients (the second derivative
