@@ -93,10 +93,11 @@ struct EdgeOps {
   float x[D1], y[D2], w[NP];
 };
 
-template <int D1, int D2, int NP, bool CONV, bool BC2, bool LOADY = true>
+// GIVEN: the caller passes the edge's sender j_given and weight row wrow_given (no index loads here).
+template <int D1, int D2, int NP, bool CONV, bool BC2, bool LOADY = true, bool GIVEN = false>
 __device__ __forceinline__ void load_edge(const TPArgs& g, int64_t e, int f1, int f2, int fw, bool active,
-                                          EdgeOps<D1, D2, NP>& o) {
-  const int64_t j = CONV ? (int64_t)g.idx_j[e] : e;
+                                          EdgeOps<D1, D2, NP>& o, int64_t j_given = 0, int64_t wrow_given = 0) {
+  const int64_t j = GIVEN ? j_given : CONV ? (int64_t)g.idx_j[e] : e;
   const int64_t s1 = (int64_t)D1 * g.F1;
 #pragma unroll
   for (int u = 0; u < D1; ++u) o.x[u] = active ? g.in1[j * s1 + u * g.F1 + f1] : 0.f;
@@ -109,7 +110,7 @@ __device__ __forceinline__ void load_edge(const TPArgs& g, int64_t e, int f1, in
 #pragma unroll
     for (int u = 0; u < D2; ++u) o.y[u] = active ? g.in2[e * s2 + u * g.F2 + f2] : 0.f;
   }
-  const int64_t wrow = g.shared_w ? 0 : weight_row(g, e);
+  const int64_t wrow = g.shared_w ? 0 : GIVEN ? wrow_given : weight_row(g, e);
   if (wrow < 0) {  // uniform over the workgroup
 #pragma unroll
     for (int i = 0; i < NP; ++i) o.w[i] = 0.f;
@@ -197,10 +198,39 @@ __global__ void __launch_bounds__(256) tp_fwd_kernel(TPArgs g) {
   int64_t e0 = row, e1 = row + 1;
   if constexpr (CONV) { e0 = g.rowptr[row] + grp; e1 = g.rowptr[row + 1]; }
   EdgeOps<D1, D2, NP> cur, nxt;
-  if (e0 < e1) load_edge<D1, D2, NP, CONV, BC2>(g, e0, f1, f2, f, true, nxt);
-  for (int64_t e = e0; e < e1; e += EG) {
+  // With edge groups an edge's index differs between groups, so idx_j[e] and its pair slot are
+  // vector loads that the row loads would wait for one edge at a time. Instead the group's lanes
+  // stage the senders and weight rows of its next C edges in LDS (one load each, C edges per wait)
+  // and the loop reads them from there.
+  __shared__ int32_t ix_lds[CONV && EG > 1 ? 2 * EG * 64 : 1];
+  auto stage_idx = [&](int64_t k0) {  // the group's edges k0 .. k0 + C - 1
+    if constexpr (CONV && EG > 1) {
+      const int64_t e = e0 + (k0 + f) * EG;
+      if (e < e1) {
+        ix_lds[grp * 128 + f] = g.idx_j[e];
+        ix_lds[grp * 128 + 64 + f] = g.shared_w ? 0 : (int32_t)weight_row(g, e);
+      }
+    }
+  };
+  auto load_k = [&](int64_t k, EdgeOps<D1, D2, NP>& o) {  // the group's edge k
+    const int64_t e = e0 + k * EG;
+    if constexpr (CONV && EG > 1) {
+      const int s = (int)(k & (C - 1));  // C is 32 or 64 with edge groups
+      load_edge<D1, D2, NP, CONV, BC2, true, true>(g, e, f1, f2, f, true, o, ix_lds[grp * 128 + s],
+                                                   ix_lds[grp * 128 + 64 + s]);
+    } else {
+      load_edge<D1, D2, NP, CONV, BC2>(g, e, f1, f2, f, true, o);
+    }
+  };
+  stage_idx(0);
+  if (e0 < e1) load_k(0, nxt);
+  int64_t k = 0;
+  for (int64_t e = e0; e < e1; e += EG, ++k) {
     cur = nxt;
-    if (e + EG < e1) load_edge<D1, D2, NP, CONV, BC2>(g, e + EG, f1, f2, f, true, nxt);
+    if (e + EG < e1) {
+      if (((k + 1) & (C - 1)) == 0) stage_idx(k + 1);
+      load_k(k + 1, nxt);
+    }
     static_for<NP>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
       constexpr PathDesc P = PL::at(i);
